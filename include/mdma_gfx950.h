@@ -1,0 +1,216 @@
+/*
+ * mdma_gfx950 — MI355X (gfx950, CDNA4) backend for mdma's quantized-weight path.
+ *
+ * A C ABI that carries the reference's `trait Backend`
+ * (/root/reference/src/backend.rs:190-601) one method per entry point, so a
+ * Rust `impl Backend for Gfx950Backend` can wrap it without glue logic
+ * (the binding is shown in INTEGRATION.md). Citations are path:line inside
+ * the reference checkout.
+ *
+ * Conventions
+ *  - Every entry point returns an mdma_status; on failure the message is
+ *    readable from mdma_gfx950_last_error() on the same thread.
+ *  - Buffers are opaque handles owned by the caller and sized in bytes; a
+ *    buffer's length defines the shape an op infers (token counts come from
+ *    x's length, as src/backend/shape.rs does). Inputs must be whole rows;
+ *    outputs only need to be large enough and are never written past the
+ *    result (src/backend/shape.rs:1-10).
+ *  - Kernels run asynchronously in stream order on one non-blocking stream
+ *    per context; upload/download synchronize before returning
+ *    (src/backend/rocm.rs:543-599). The context is internally locked.
+ *  - Weight dtypes use GGML type ids: F32 0, F16 1, Q8_0 8, Q4_K 12, Q6_K 14.
+ */
+#ifndef MDMA_GFX950_H
+#define MDMA_GFX950_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* backend::Error variants, src/backend.rs:52-93, in declaration order. */
+typedef enum {
+    MDMA_OK = 0,
+    MDMA_ERR_CONTEXT_LIMIT = 1,
+    MDMA_ERR_SHAPE_MISMATCH = 2,
+    MDMA_ERR_NOT_IMPLEMENTED = 3,
+    MDMA_ERR_UNSUPPORTED_MODEL = 4,
+    MDMA_ERR_MEMORY_BUDGET = 5,
+    MDMA_ERR_BUFFER_BUDGET = 6,
+    MDMA_ERR_INSUFFICIENT_MEMORY = 7,
+    MDMA_ERR_OUT_OF_MEMORY = 8,
+    MDMA_ERR_SIZE_OVERFLOW = 9,
+    MDMA_ERR_BACKEND = 10,
+    MDMA_ERR_IO = 11
+} mdma_status;
+
+/* Pool, src/backend.rs:108-113. */
+typedef enum { MDMA_POOL_WEIGHTS = 0, MDMA_POOL_KV = 1, MDMA_POOL_SCRATCH = 2 } mdma_pool;
+
+/* WeightLayout (src/cache/layout.rs:10-38): raw GGUF blocks, or this
+ * backend's lossless repack (same bytes per block; MDMA_LAYOUT_GFX950). */
+typedef enum { MDMA_LAYOUT_GGUF = 0, MDMA_LAYOUT_GFX950 = 1 } mdma_layout;
+
+/* Activation mode of the decode GEMV: f32 activations (exact parity mode) or
+ * int8 activations quantized per 256 with an f32 scale. The reference's
+ * counterpart is the MDMA_HIP_F32 switch (src/backend/select.rs:49). */
+typedef enum { MDMA_ACT_F32 = 0, MDMA_ACT_I8 = 1 } mdma_act_mode;
+
+typedef struct mdma_ctx mdma_ctx;
+typedef struct mdma_buf mdma_buf;
+
+/* QWeight (src/backend.rs:114-118): dtype + rank-2 shape [rows=n_out, cols=n_in]. */
+typedef struct {
+    int32_t dtype;
+    uint64_t rows;
+    uint64_t cols;
+    const mdma_buf *buf;
+} mdma_qweight;
+
+/* RopeSpec (src/backend.rs:120-123). */
+typedef struct {
+    uint64_t head_dim;
+    float theta;
+} mdma_rope_spec;
+
+/* AttnSpec (src/backend.rs:132-137). */
+typedef struct {
+    uint64_t head_dim;
+    uint64_t n_q_heads;
+    uint64_t n_kv_heads;
+} mdma_attn_spec;
+
+/* KvView (src/backend.rs:125-129). */
+typedef struct {
+    const mdma_buf *k;
+    const mdma_buf *v;
+    uint64_t len;
+} mdma_kv_view;
+
+/* ---- lifecycle and capability queries ---- */
+
+/* HipBackend::new / create (src/backend/rocm.rs:165-223). */
+int mdma_gfx950_create(int device, mdma_ctx **out);
+void mdma_gfx950_destroy(mdma_ctx *ctx);
+/* Thread-local message of the last failed call on this thread. */
+const char *mdma_gfx950_last_error(void);
+/* Backend::device_label (src/backend.rs:206). */
+int mdma_gfx950_device_label(mdma_ctx *ctx, char *out, size_t cap);
+/* Backend::total_device_bytes (:219) / available_device_bytes (:214). */
+uint64_t mdma_gfx950_total_device_bytes(mdma_ctx *ctx);
+int mdma_gfx950_available_device_bytes(mdma_ctx *ctx, uint64_t *out);
+/* Backend::supports_weight_dtype (:363). Q8_0, Q4_K, Q6_K, F32 and F16. */
+int mdma_gfx950_supports_weight_dtype(mdma_ctx *ctx, int32_t dtype);
+/* Backend::max_head_dim (:368). */
+uint64_t mdma_gfx950_max_head_dim(mdma_ctx *ctx);
+/* Backend::kv_elem_bytes (:427): 2, the cache stores f16. */
+uint64_t mdma_gfx950_kv_elem_bytes(mdma_ctx *ctx);
+/* Backend::join_execution (:197): wait for all queued device work. */
+int mdma_gfx950_join_execution(mdma_ctx *ctx);
+/* Backend::set_buffer_budget (:352) with BufferBudget's per-pool device
+ * quotas (src/memory/buffers.rs:32-99); UINT64_MAX = unlimited. */
+int mdma_gfx950_set_buffer_budget(mdma_ctx *ctx, uint64_t weights, uint64_t kv, uint64_t scratch);
+int mdma_gfx950_buffer_usage(mdma_ctx *ctx, int pool, uint64_t *used, uint64_t *limit);
+/* Extra: select the decode GEMV activation mode (default MDMA_ACT_F32). */
+int mdma_gfx950_set_act_mode(mdma_ctx *ctx, int mode);
+/* Extra: the HIP stream (hipStream_t) every launch of this context uses. */
+void *mdma_gfx950_stream(mdma_ctx *ctx);
+
+/* ---- buffers: Backend::alloc/upload/download/copy (src/backend.rs:383-399) ---- */
+
+int mdma_gfx950_alloc(mdma_ctx *ctx, uint64_t bytes, int pool, mdma_buf **out);
+/* Drop of a buffer; a failed hipFree keeps its budget charge (src/backend/rocm/memory.rs:36-55). */
+int mdma_gfx950_free(mdma_buf *buf);
+uint64_t mdma_gfx950_buf_len(const mdma_buf *buf);
+/* Extra: a non-owning window [offset, offset+len) of a buffer (freed with mdma_gfx950_free). */
+int mdma_gfx950_buf_view(mdma_buf *parent, uint64_t offset, uint64_t len, mdma_buf **out);
+int mdma_gfx950_upload(mdma_ctx *ctx, mdma_buf *dst, uint64_t offset, const void *src, uint64_t len);
+int mdma_gfx950_download(mdma_ctx *ctx, const mdma_buf *src, uint64_t offset, void *dst, uint64_t len);
+int mdma_gfx950_copy(mdma_ctx *ctx, const mdma_buf *src, uint64_t src_off, mdma_buf *dst,
+                     uint64_t dst_off, uint64_t len);
+/* Backend::upload_weight (src/backend.rs:228-237). The dtype and shape are
+ * passed so the gfx950 layout can be produced at upload. */
+int mdma_gfx950_upload_weight(mdma_ctx *ctx, const void *bytes, uint64_t len, int layout,
+                              int32_t dtype, uint64_t rows, uint64_t cols, mdma_buf **out);
+
+/* ---- the quantized-weight hot path ---- */
+
+/* Backend::qmatmul (src/backend.rs:469): y[t, r] = sum_i deq(W)[r, i] * x[t, i].
+ * x is [T, n_in] f32 (T inferred), y is [T, n_out] f32. */
+int mdma_gfx950_qmatmul(mdma_ctx *ctx, const mdma_qweight *w, const mdma_buf *x, mdma_buf *y);
+/* Backend::qmatmul_qkv (src/backend.rs:409-422): three projections of one x. */
+int mdma_gfx950_qmatmul_qkv(mdma_ctx *ctx, const mdma_qweight *wq, const mdma_qweight *wk,
+                            const mdma_qweight *wv, const mdma_buf *x, mdma_buf *q, mdma_buf *k,
+                            mdma_buf *v);
+/* Backend::ffn_gate_up (src/backend.rs:472-489): y = silu(gate*x) * (up*x).
+ * The scratch buffers have the output shape; their final contents are unspecified. */
+int mdma_gfx950_ffn_gate_up(mdma_ctx *ctx, const mdma_qweight *gate, const mdma_qweight *up,
+                            const mdma_buf *x, mdma_buf *gate_scratch, mdma_buf *up_scratch,
+                            mdma_buf *y);
+
+/* ---- per-token ops ---- */
+
+/* Backend::embed (src/backend.rs:494): dequantized rows of a [vocab, n_embd] table. */
+int mdma_gfx950_embed(mdma_ctx *ctx, const mdma_qweight *table, const uint32_t *ids, uint64_t n_ids,
+                      mdma_buf *out);
+/* Backend::rmsnorm (:500); rows of w's length. */
+int mdma_gfx950_rmsnorm(mdma_ctx *ctx, const mdma_buf *w, const mdma_buf *x, mdma_buf *y, float eps);
+/* Backend::add_rmsnorm (:502-513): sum = a + b; y = rmsnorm(sum) * w. */
+int mdma_gfx950_add_rmsnorm(mdma_ctx *ctx, const mdma_buf *w, const mdma_buf *a, const mdma_buf *b,
+                            mdma_buf *sum, mdma_buf *y, float eps);
+/* Backend::add (:515). */
+int mdma_gfx950_add(mdma_ctx *ctx, const mdma_buf *a, const mdma_buf *b, mdma_buf *y);
+/* Backend::silu_mul (:540). */
+int mdma_gfx950_silu_mul(mdma_ctx *ctx, const mdma_buf *gate, const mdma_buf *up, mdma_buf *y);
+/* Backend::rope (:518-526): interleaved pairs; token t at position pos + t. */
+int mdma_gfx950_rope(mdma_ctx *ctx, mdma_buf *q, mdma_buf *k, uint32_t pos, uint64_t n_tokens,
+                     const mdma_rope_spec *spec);
+/* Backend::kv_write (:434-445): f32 rows into the f16 caches at element elem_offset. */
+int mdma_gfx950_kv_write(mdma_ctx *ctx, const mdma_buf *k, const mdma_buf *v, mdma_buf *dst_k,
+                         mdma_buf *dst_v, uint64_t elem_offset, uint64_t n_elems);
+/* Backend::rope_kv_write (:452-467), fused: q rotated in place; rotated k and v stored. */
+int mdma_gfx950_rope_kv_write(mdma_ctx *ctx, mdma_buf *q, mdma_buf *k, const mdma_buf *v,
+                              mdma_buf *dst_k, mdma_buf *dst_v, uint64_t elem_offset, uint32_t pos,
+                              uint64_t n_tokens, const mdma_rope_spec *spec, uint64_t n_elems);
+/* Backend::attn (:527-539): causal GQA over the f16 cache, scale 1/sqrt(head_dim). */
+int mdma_gfx950_attn(mdma_ctx *ctx, const mdma_buf *q, const mdma_kv_view *kv,
+                     const mdma_attn_spec *spec, mdma_buf *o);
+
+/* ---- extras beside the trait ---- */
+
+/* Argmax with ties to the LAST index (sampler::greedy, src/sampler.rs:64-74)
+ * of n f32 logits at element offset `offset`; the id is written to host *out. */
+int mdma_gfx950_greedy(mdma_ctx *ctx, const mdma_buf *logits, uint64_t offset, uint64_t n,
+                       uint32_t *out);
+/* Int8 activation quantizer (the Q8_1 rule of src/backend/rocm/kernels/kernels.hip:1102-1133
+ * with an f32 scale): q int8 [n], d f32 [n/group], sum16 i32 [n/16]. group is 256 or 32. */
+int mdma_gfx950_quantize_act(mdma_ctx *ctx, const mdma_buf *x, uint64_t group, mdma_buf *q,
+                             mdma_buf *d, mdma_buf *sum16);
+/* Debug: int32 dot per (token, row, sub-block) of weight quants with int8
+ * activations qx [T, n_in]; sub-blocks are 32 wide (Q4_K, Q8_0) or 16 (Q6_K).
+ * out is int32 [T][n_out][n_in/sub]. */
+int mdma_gfx950_block_dot_i32(mdma_ctx *ctx, const mdma_qweight *w, const mdma_buf *qx,
+                              mdma_buf *out);
+/* Explicit-mode GEMVs, independent of the context's mode. */
+int mdma_gfx950_qmatmul_f32(mdma_ctx *ctx, const mdma_qweight *w, const mdma_buf *x, mdma_buf *y);
+int mdma_gfx950_qmatmul_i8(mdma_ctx *ctx, const mdma_qweight *w, const mdma_buf *x, mdma_buf *y);
+
+/* Stream capture into a replayable HIP graph (the reference's graph decode
+ * executor, src/backend/rocm/graph.rs:105-262, captures forward_device the
+ * same way). Between begin and end, launches are recorded, not run; calls
+ * that must synchronize (upload, download, scratch growth) fail with
+ * MDMA_ERR_BACKEND instead. */
+typedef struct mdma_graph mdma_graph;
+int mdma_gfx950_graph_begin(mdma_ctx *ctx);
+int mdma_gfx950_graph_end(mdma_ctx *ctx, mdma_graph **out);
+int mdma_gfx950_graph_launch(mdma_ctx *ctx, mdma_graph *graph);
+void mdma_gfx950_graph_destroy(mdma_graph *graph);
+/* Pre-size the context scratch (int8 activations) so a later capture needs no growth. */
+int mdma_gfx950_reserve_scratch(mdma_ctx *ctx, uint64_t bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,1028 @@
+// Decode GEMV for GGUF Q4_K / Q6_K / Q8_0 (and F32 / F16) weights on gfx950.
+//
+// y[t, r] = sum_i deq(W)[r, i] * x[t, i]   (reference Backend::qmatmul,
+// /root/reference/src/backend.rs:469; CPU oracle src/backend/cpu.rs:335-368)
+//
+// Design (wave64, CDNA4):
+//  - One wave owns R output rows of one weight; its 64 lanes stride over the
+//    row's 16-byte "units" of packed quants, so every load of a wave covers
+//    contiguous bytes of R rows. A Q4_K unit is 16 quant bytes = 32 weights
+//    (16 low nibbles of sub-block 2p, 16 high nibbles of sub-block 2p+1);
+//    a Q6_K unit is 8 columns of one 128-half across its 4 quarters; a Q8_0
+//    unit is half a block. Eight units per 256 weights for the K-quants.
+//  - f32 mode factorises the dequantisation: sum (d*sc*q - dmin*m) * x =
+//    d*sc * sum(q*x) - dmin*m * sum(x), so per weight the VALU does one byte
+//    -> float conversion and one FMA; scales are decoded once per unit.
+//    Unit partial sums are f32; the per-lane accumulator across units and the
+//    cross-lane reduction are f64 (full rate on CDNA), which keeps the result
+//    closer to the exact dot product than the CPU's sequential f32 sum.
+//  - int8 mode (activations quantized per 256 with an f32 scale, see
+//    quant.hip) does the integer dot with v_dot4_i32_i8 and keeps exact int32
+//    per-sub-block sums; the float epilogue runs once per unit.
+//  - Fused QKV: up to three jobs (same dtype) in one launch; waves are dealt
+//    out to jobs in order. Gated: the wave computes R rows of gate AND up,
+//    then writes silu(g) * u.
+#include "internal.h"
+
+namespace mdma {
+namespace {
+
+constexpr int WAVES = 4;  // waves per workgroup
+constexpr int R = 2;      // rows per wave
+
+struct Job {
+  const uint8_t *w;
+  float *y;
+  uint32_t n_out, n_in, waves;
+};
+struct JobSet {
+  Job j[3];
+  int n;
+};
+
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits16 & 0xffff));
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// Streaming 16-byte weight load (nontemporal: weights are read once per token).
+__device__ __forceinline__ uint4 ld16(const uint8_t *p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t ldu16(const uint8_t *p) {
+  return *reinterpret_cast<const uint16_t *>(p);
+}
+// A dword made of two 2-byte-aligned halves (Q6_K / Q8_0 blocks are only
+// 2-byte aligned inside a row).
+__device__ __forceinline__ uint32_t ld2x16(const uint8_t *p) { return ldu16(p) | (ldu16(p + 2) << 16); }
+
+__device__ __forceinline__ float ub(uint32_t v, int k) { return (float)((v >> (8 * k)) & 0xffu); }
+__device__ __forceinline__ float sb(uint32_t v, int k) { return (float)(int8_t)((v >> (8 * k)) & 0xffu); }
+
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Locate this wave's job and first row; false when the wave has no rows.
+__device__ __forceinline__ bool locate(const JobSet &js, int &jidx, uint32_t &row0) {
+  uint32_t gw = blockIdx.x * WAVES + (threadIdx.x >> 6);
+  jidx = 0;
+  while (jidx < js.n - 1 && gw >= js.j[jidx].waves) {
+    gw -= js.j[jidx].waves;
+    jidx++;
+  }
+  if (gw >= js.j[jidx].waves) return false;
+  row0 = gw * R;
+  return true;
+}
+
+// ---------------------------------------------------------------- Q4_K ----
+
+// Six-bit (scale, min) pairs of sub-blocks 2p and 2p+1 from the 12 scale
+// bytes (get_scale_min_k4 of reference kernels.hip:19-27, evaluated for four
+// sub-blocks at once in packed bytes).
+__device__ __forceinline__ void q4k_scales(uint4 hd, int p, float &sca, float &scb, float &ma, float &mb) {
+  uint32_t s0 = hd.y, s1 = hd.z, s2 = hd.w;
+  uint32_t scw = p < 2 ? (s0 & 0x3F3F3F3Fu) : ((s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u));
+  uint32_t mw = p < 2 ? (s1 & 0x3F3F3F3Fu) : (((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u));
+  int sh = (p & 1) * 16;
+  sca = ub(scw >> sh, 0);
+  scb = ub(scw >> sh, 1);
+  ma = ub(mw >> sh, 0);
+  mb = ub(mw >> sh, 1);
+}
+
+// Integer part of an int8-mode Q4_K unit: dots of the 16 low nibbles with
+// qa (16 int8) and of the 16 high nibbles with qb.
+__device__ __forceinline__ void q4k_unit_isum(uint4 qs, uint4 qa, uint4 qb, int &ia, int &ib) {
+  const uint32_t w[4] = {qs.x, qs.y, qs.z, qs.w};
+  const uint32_t a[4] = {qa.x, qa.y, qa.z, qa.w};
+  const uint32_t b[4] = {qb.x, qb.y, qb.z, qb.w};
+  ia = 0;
+  ib = 0;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    ia = __builtin_amdgcn_sdot4((int)(w[k] & 0x0F0F0F0Fu), (int)a[k], ia, false);
+    ib = __builtin_amdgcn_sdot4((int)((w[k] >> 4) & 0x0F0F0F0Fu), (int)b[k], ib, false);
+  }
+}
+
+// ---------------------------------------------------------------- Q6_K ----
+
+struct Q6Unit {
+  uint32_t qa[2], qb[2], qh[2];  // ql[l0..+8], ql[32+l0..+8], qh[l0..+8] of one half
+  uint32_t sc;                   // 4 sub-scales (quarters 0..3) as bytes
+  uint32_t d;                    // f16 bits
+};
+
+// Unit c in 0..7 of a block: half n = c>>2, column group g = c&3 (l0 = 8g).
+__device__ __forceinline__ Q6Unit q6_load(const uint8_t *blk, int c) {
+  const int n = c >> 2, g = c & 3, l0 = 8 * g;
+  Q6Unit u;
+  const uint8_t *ql = blk + 64 * n + l0, *qh = blk + 128 + 32 * n + l0;
+  u.qa[0] = ld2x16(ql);
+  u.qa[1] = ld2x16(ql + 4);
+  u.qb[0] = ld2x16(ql + 32);
+  u.qb[1] = ld2x16(ql + 36);
+  u.qh[0] = ld2x16(qh);
+  u.qh[1] = ld2x16(qh + 4);
+  // sc[8n + g/2 + 2r], r = 0..3: byte (g>>1) of the halfwords at 192+8n+2r.
+  const uint8_t *s = blk + 192 + 8 * n;
+  const int sh = (g >> 1) * 8;
+  u.sc = ((ldu16(s) >> sh) & 0xff) | (((ldu16(s + 2) >> sh) & 0xff) << 8) |
+         (((ldu16(s + 4) >> sh) & 0xff) << 16) | (((ldu16(s + 6) >> sh) & 0xff) << 24);
+  u.d = ldu16(blk + 208);
+  return u;
+}
+
+// Six-bit unsigned quants (0..63) of quarter r, word k (4 columns).
+__device__ __forceinline__ uint32_t q6_u(const Q6Unit &u, int r, int k) {
+  const uint32_t h = u.qh[k];
+  switch (r) {
+    case 0: return (u.qa[k] & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u);
+    case 1: return (u.qb[k] & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u);
+    case 2: return ((u.qa[k] >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u);
+    default: return ((u.qb[k] >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u);
+  }
+}
+
+// Integer dot of quarter r's 8 quants (q = u - 32) with 8 int8 activations.
+__device__ __forceinline__ int q6_quarter_isum(const Q6Unit &u, int r, uint32_t x0, uint32_t x1) {
+  int acc = __builtin_amdgcn_sdot4((int)q6_u(u, r, 0), (int)x0, 0, false);
+  acc = __builtin_amdgcn_sdot4((int)q6_u(u, r, 1), (int)x1, acc, false);
+  int sx = __builtin_amdgcn_sdot4((int)x0, 0x01010101, 0, false);
+  sx = __builtin_amdgcn_sdot4((int)x1, 0x01010101, sx, false);
+  return acc - 32 * sx;
+}
+
+// ---------------------------------------------------------------- Q8_0 ----
+
+struct Q8Unit {
+  uint32_t q[4];  // 16 int8 quants
+  uint32_t d;
+};
+// Unit c in 0..1 of a 34-byte block: quants [16c, 16c+16).
+__device__ __forceinline__ Q8Unit q8_load(const uint8_t *blk, int c) {
+  Q8Unit u;
+  const uint8_t *q = blk + 2 + 16 * c;
+#pragma unroll
+  for (int k = 0; k < 4; k++) u.q[k] = ld2x16(q + 4 * k);
+  u.d = ldu16(blk);
+  return u;
+}
+
+// ------------------------------------------------------- f32 mode kernel ----
+
+// Sum of q*x over one unit, returning the f32 unit contribution for row data
+// already loaded. TT tokens; xs holds the unit's 32 activations per token.
+template <int DT>
+struct Unit;
+
+template <>
+struct Unit<DT_Q4_K> {
+  static constexpr uint32_t BLOCK_BYTES = 144;
+  struct Data {
+    uint4 hd, qs;
+  };
+  __device__ static Data load(const uint8_t *blk, int c) { return Data{ld16(blk), ld16(blk + 16 + 16 * c)}; }
+  // Column indices (within the block) of the unit's 32 weights: two runs of 16.
+  __device__ static int col0(int c) { return ((c >> 1) << 6) + ((c & 1) << 4); }
+  __device__ static void cols(int c, int &a, int &b) {
+    a = col0(c);
+    b = a + 32;
+  }
+  // xa/xb: the 16 activations of each run; sums Xa/Xb precomputed.
+  __device__ static float dot(const Data &w, int c, const float *xa, const float *xb, float Xa, float Xb) {
+    const uint32_t qw[4] = {w.qs.x, w.qs.y, w.qs.z, w.qs.w};
+    float sa = 0.f, sb = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      uint32_t lo = qw[k] & 0x0F0F0F0Fu, hi = (qw[k] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        sa = fmaf(ub(lo, j), xa[4 * k + j], sa);
+        sb = fmaf(ub(hi, j), xb[4 * k + j], sb);
+      }
+    }
+    float sca, scb, ma, mb;
+    q4k_scales(w.hd, c >> 1, sca, scb, ma, mb);
+    const float d = h2f(w.hd.x), dmin = h2f(w.hd.x >> 16);
+    const float ca = fmaf(d * sca, sa, -(dmin * ma) * Xa);
+    const float cb = fmaf(d * scb, sb, -(dmin * mb) * Xb);
+    return ca + cb;
+  }
+};
+
+template <>
+struct Unit<DT_Q6_K> {
+  static constexpr uint32_t BLOCK_BYTES = 210;
+  using Data = Q6Unit;
+  __device__ static Data load(const uint8_t *blk, int c) { return q6_load(blk, c); }
+  // Quarter r of unit c covers columns 128n + 32r + [8g, 8g+8).
+  __device__ static int col(int c, int r) { return 128 * (c >> 2) + 32 * r + 8 * (c & 3); }
+  __device__ static float dot(const Data &u, const float (*x)[8]) {
+    float acc = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      float s = 0.f;
+#pragma unroll
+      for (int k = 0; k < 2; k++) {
+        uint32_t q = q6_u(u, r, k);
+#pragma unroll
+        for (int j = 0; j < 4; j++) s = fmaf(ub(q, j) - 32.f, x[r][4 * k + j], s);
+      }
+      acc = fmaf(sb(u.sc, r), s, acc);
+    }
+    return h2f(u.d) * acc;
+  }
+};
+
+template <int TT, bool GATED>
+__global__ __launch_bounds__(256) void gemv_q4k_f32(JobSet js, const float *__restrict__ x, uint32_t T,
+                                                    float *__restrict__ ygated) {
+  using U = Unit<DT_Q4_K>;
+  int ji;
+  uint32_t row0;
+  if (!locate(js, ji, row0)) return;
+  const Job &J = js.j[ji];
+  const Job &JU = js.j[GATED ? 1 : ji];
+  const int lane = threadIdx.x & 63;
+  const uint32_t n_in = J.n_in, nb = n_in >> 8, units = nb * 8;
+  const size_t rb = (size_t)nb * U::BLOCK_BYTES;
+  constexpr int NR = GATED ? 2 * R : R;
+  double acc[NR][TT];
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int t = 0; t < TT; t++) acc[r][t] = 0.0;
+
+  for (uint32_t u = lane; u < units; u += 64) {
+    const uint32_t b = u >> 3;
+    const int c = u & 7;
+    U::Data wd[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      const uint32_t row = row0 + (r % R);
+      const uint8_t *base = (r < R ? J.w : JU.w);
+      if (row < J.n_out)
+        wd[r] = U::load(base + row * rb + (size_t)b * U::BLOCK_BYTES, c);
+      else
+        wd[r] = U::Data{make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+    }
+    int ca, cb;
+    U::cols(c, ca, cb);
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+      if (t >= (int)T) break;
+      const float *xt = x + (size_t)t * n_in + (size_t)b * 256;
+      float xa[16], xb[16];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        float4 va = *reinterpret_cast<const float4 *>(xt + ca + 4 * k);
+        float4 vb = *reinterpret_cast<const float4 *>(xt + cb + 4 * k);
+        xa[4 * k] = va.x, xa[4 * k + 1] = va.y, xa[4 * k + 2] = va.z, xa[4 * k + 3] = va.w;
+        xb[4 * k] = vb.x, xb[4 * k + 1] = vb.y, xb[4 * k + 2] = vb.z, xb[4 * k + 3] = vb.w;
+      }
+      float Xa = 0.f, Xb = 0.f;
+#pragma unroll
+      for (int k = 0; k < 16; k++) {
+        Xa += xa[k];
+        Xb += xb[k];
+      }
+#pragma unroll
+      for (int r = 0; r < NR; r++) acc[r][t] += (double)U::dot(wd[r], c, xa, xb, Xa, Xb);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int t = 0; t < TT; t++) acc[r][t] = wave_sum(acc[r][t]);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const uint32_t row = row0 + r;
+      if (row >= J.n_out) break;
+#pragma unroll
+      for (int t = 0; t < TT; t++) {
+        if (t >= (int)T) break;
+        if (GATED) {
+          const float g = (float)acc[r][t], up = (float)acc[R + r][t];
+          ygated[(size_t)t * J.n_out + row] = g / (1.0f + expf(-g)) * up;
+        } else {
+          J.y[(size_t)t * J.n_out + row] = (float)acc[r][t];
+        }
+      }
+    }
+  }
+}
+
+template <int TT, bool GATED>
+__global__ __launch_bounds__(256) void gemv_q6k_f32(JobSet js, const float *__restrict__ x, uint32_t T,
+                                                    float *__restrict__ ygated) {
+  using U = Unit<DT_Q6_K>;
+  int ji;
+  uint32_t row0;
+  if (!locate(js, ji, row0)) return;
+  const Job &J = js.j[ji];
+  const Job &JU = js.j[GATED ? 1 : ji];
+  const int lane = threadIdx.x & 63;
+  const uint32_t n_in = J.n_in, nb = n_in >> 8, units = nb * 8;
+  const size_t rb = (size_t)nb * U::BLOCK_BYTES;
+  constexpr int NR = GATED ? 2 * R : R;
+  double acc[NR][TT];
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int t = 0; t < TT; t++) acc[r][t] = 0.0;
+
+  for (uint32_t u = lane; u < units; u += 64) {
+    const uint32_t b = u >> 3;
+    const int c = u & 7;
+    U::Data wd[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      const uint32_t row = row0 + (r % R);
+      const uint8_t *base = (r < R ? J.w : JU.w);
+      if (row < J.n_out)
+        wd[r] = U::load(base + row * rb + (size_t)b * U::BLOCK_BYTES, c);
+      else
+        wd[r] = Q6Unit{{0, 0}, {0, 0}, {0, 0}, 0, 0};
+    }
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+      if (t >= (int)T) break;
+      const float *xt = x + (size_t)t * n_in + (size_t)b * 256;
+      float xs[4][8];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const float *p = xt + U::col(c, q);
+        float4 v0 = *reinterpret_cast<const float4 *>(p), v1 = *reinterpret_cast<const float4 *>(p + 4);
+        xs[q][0] = v0.x, xs[q][1] = v0.y, xs[q][2] = v0.z, xs[q][3] = v0.w;
+        xs[q][4] = v1.x, xs[q][5] = v1.y, xs[q][6] = v1.z, xs[q][7] = v1.w;
+      }
+#pragma unroll
+      for (int r = 0; r < NR; r++) acc[r][t] += (double)U::dot(wd[r], xs);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int t = 0; t < TT; t++) acc[r][t] = wave_sum(acc[r][t]);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const uint32_t row = row0 + r;
+      if (row >= J.n_out) break;
+#pragma unroll
+      for (int t = 0; t < TT; t++) {
+        if (t >= (int)T) break;
+        if (GATED) {
+          const float g = (float)acc[r][t], up = (float)acc[R + r][t];
+          ygated[(size_t)t * J.n_out + row] = g / (1.0f + expf(-g)) * up;
+        } else {
+          J.y[(size_t)t * J.n_out + row] = (float)acc[r][t];
+        }
+      }
+    }
+  }
+}
+
+// Q8_0: unit = half block (16 weights); 2 units per 32 weights.
+template <int TT, bool GATED>
+__global__ __launch_bounds__(256) void gemv_q8_f32(JobSet js, const float *__restrict__ x, uint32_t T,
+                                                   float *__restrict__ ygated) {
+  int ji;
+  uint32_t row0;
+  if (!locate(js, ji, row0)) return;
+  const Job &J = js.j[ji];
+  const Job &JU = js.j[GATED ? 1 : ji];
+  const int lane = threadIdx.x & 63;
+  const uint32_t n_in = J.n_in, nb = n_in >> 5, units = nb * 2;
+  const size_t rb = (size_t)nb * 34;
+  constexpr int NR = GATED ? 2 * R : R;
+  double acc[NR][TT];
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int t = 0; t < TT; t++) acc[r][t] = 0.0;
+  for (uint32_t u = lane; u < units; u += 64) {
+    const uint32_t b = u >> 1;
+    const int c = u & 1;
+    Q8Unit wd[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      const uint32_t row = row0 + (r % R);
+      const uint8_t *base = (r < R ? J.w : JU.w);
+      if (row < J.n_out)
+        wd[r] = q8_load(base + row * rb + (size_t)b * 34, c);
+      else
+        wd[r] = Q8Unit{{0, 0, 0, 0}, 0};
+    }
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+      if (t >= (int)T) break;
+      const float *xt = x + (size_t)t * n_in + (size_t)b * 32 + 16 * c;
+      float xs[16];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        float4 v = *reinterpret_cast<const float4 *>(xt + 4 * k);
+        xs[4 * k] = v.x, xs[4 * k + 1] = v.y, xs[4 * k + 2] = v.z, xs[4 * k + 3] = v.w;
+      }
+#pragma unroll
+      for (int r = 0; r < NR; r++) {
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+#pragma unroll
+          for (int j = 0; j < 4; j++) s = fmaf(sb(wd[r].q[k], j), xs[4 * k + j], s);
+        acc[r][t] += (double)(h2f(wd[r].d) * s);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int t = 0; t < TT; t++) acc[r][t] = wave_sum(acc[r][t]);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const uint32_t row = row0 + r;
+      if (row >= J.n_out) break;
+#pragma unroll
+      for (int t = 0; t < TT; t++) {
+        if (t >= (int)T) break;
+        if (GATED) {
+          const float g = (float)acc[r][t], up = (float)acc[R + r][t];
+          ygated[(size_t)t * J.n_out + row] = g / (1.0f + expf(-g)) * up;
+        } else {
+          J.y[(size_t)t * J.n_out + row] = (float)acc[r][t];
+        }
+      }
+    }
+  }
+}
+
+// F32 / F16 weights: plain strided dot (not a hot path; kept for the trait's
+// full dtype set). One wave per row, lanes stride over columns.
+template <int DT, bool GATED>
+__global__ __launch_bounds__(256) void gemv_plain(JobSet js, const float *__restrict__ x, uint32_t T,
+                                                  float *__restrict__ ygated) {
+  const uint32_t gw = blockIdx.x * WAVES + (threadIdx.x >> 6);
+  uint32_t w = gw;
+  int ji = 0;
+  while (ji < js.n - 1 && w >= js.j[ji].n_out) {
+    w -= js.j[ji].n_out;
+    ji++;
+  }
+  const Job &J = js.j[ji];
+  if (w >= J.n_out) return;
+  const Job &JU = js.j[GATED ? 1 : ji];
+  const int lane = threadIdx.x & 63;
+  const uint32_t row = w, n_in = J.n_in;
+  for (uint32_t t = 0; t < T; t++) {
+    double a = 0.0, b = 0.0;
+    for (uint32_t i = lane; i < n_in; i += 64) {
+      float wv, uv = 0.f;
+      if (DT == DT_F32) {
+        wv = reinterpret_cast<const float *>(J.w)[(size_t)row * n_in + i];
+        if (GATED) uv = reinterpret_cast<const float *>(JU.w)[(size_t)row * n_in + i];
+      } else {
+        wv = h2f(reinterpret_cast<const uint16_t *>(J.w)[(size_t)row * n_in + i]);
+        if (GATED) uv = h2f(reinterpret_cast<const uint16_t *>(JU.w)[(size_t)row * n_in + i]);
+      }
+      const float xv = x[(size_t)t * n_in + i];
+      a += (double)(wv * xv);
+      if (GATED) b += (double)(uv * xv);
+    }
+    a = wave_sum(a);
+    if (GATED) b = wave_sum(b);
+    if (lane == 0) {
+      if (GATED) {
+        const float g = (float)a, up = (float)b;
+        ygated[(size_t)t * J.n_out + row] = g / (1.0f + expf(-g)) * up;
+      } else {
+        J.y[(size_t)t * J.n_out + row] = (float)a;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------ int8 mode kernel ----
+// qx: int8 [T, n_in]; dx: f32 [T, n_in/256]; s16: i32 [T, n_in/16].
+
+template <int TT, bool GATED>
+__global__ __launch_bounds__(256) void gemv_q4k_i8(JobSet js, const int8_t *__restrict__ qx,
+                                                   const float *__restrict__ dx, const int32_t *__restrict__ s16,
+                                                   uint32_t T, float *__restrict__ ygated) {
+  int ji;
+  uint32_t row0;
+  if (!locate(js, ji, row0)) return;
+  const Job &J = js.j[ji];
+  const Job &JU = js.j[GATED ? 1 : ji];
+  const int lane = threadIdx.x & 63;
+  const uint32_t n_in = J.n_in, nb = n_in >> 8, units = nb * 8;
+  const size_t rb = (size_t)nb * 144;
+  constexpr int NR = GATED ? 2 * R : R;
+  double acc[NR][TT];
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int t = 0; t < TT; t++) acc[r][t] = 0.0;
+  for (uint32_t u = lane; u < units; u += 64) {
+    const uint32_t b = u >> 3;
+    const int c = u & 7, p = c >> 1;
+    uint4 hd[NR], qs[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      const uint32_t row = row0 + (r % R);
+      const uint8_t *base = (r < R ? J.w : JU.w);
+      if (row < J.n_out) {
+        const uint8_t *blk = base + row * rb + (size_t)b * 144;
+        hd[r] = ld16(blk);
+        qs[r] = ld16(blk + 16 + 16 * c);
+      } else {
+        hd[r] = make_uint4(0, 0, 0, 0);
+        qs[r] = make_uint4(0, 0, 0, 0);
+      }
+    }
+    const uint32_t ca = b * 256 + (p << 6) + ((c & 1) << 4);
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+      if (t >= (int)T) break;
+      const int8_t *xt = qx + (size_t)t * n_in;
+      const uint4 qa = *reinterpret_cast<const uint4 *>(xt + ca);
+      const uint4 qb = *reinterpret_cast<const uint4 *>(xt + ca + 32);
+      const int sa = s16[(size_t)t * (n_in >> 4) + (ca >> 4)];
+      const int sbb = s16[(size_t)t * (n_in >> 4) + ((ca + 32) >> 4)];
+      const float d8 = dx[(size_t)t * nb + b];
+#pragma unroll
+      for (int r = 0; r < NR; r++) {
+        int ia, ib;
+        q4k_unit_isum(qs[r], qa, qb, ia, ib);
+        float sca, scb, ma, mb;
+        q4k_scales(hd[r], p, sca, scb, ma, mb);
+        const int A = (int)sca * ia + (int)scb * ib;
+        const int B = (int)ma * sa + (int)mb * sbb;
+        const float d = h2f(hd[r].x), dmin = h2f(hd[r].x >> 16);
+        acc[r][t] += (double)(d8 * fmaf(d, (float)A, -dmin * (float)B));
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int t = 0; t < TT; t++) acc[r][t] = wave_sum(acc[r][t]);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const uint32_t row = row0 + r;
+      if (row >= J.n_out) break;
+#pragma unroll
+      for (int t = 0; t < TT; t++) {
+        if (t >= (int)T) break;
+        if (GATED) {
+          const float g = (float)acc[r][t], up = (float)acc[R + r][t];
+          ygated[(size_t)t * J.n_out + row] = g / (1.0f + expf(-g)) * up;
+        } else {
+          J.y[(size_t)t * J.n_out + row] = (float)acc[r][t];
+        }
+      }
+    }
+  }
+}
+
+template <int TT, bool GATED>
+__global__ __launch_bounds__(256) void gemv_q6k_i8(JobSet js, const int8_t *__restrict__ qx,
+                                                   const float *__restrict__ dx, const int32_t *__restrict__ s16,
+                                                   uint32_t T, float *__restrict__ ygated) {
+  int ji;
+  uint32_t row0;
+  if (!locate(js, ji, row0)) return;
+  const Job &J = js.j[ji];
+  const Job &JU = js.j[GATED ? 1 : ji];
+  const int lane = threadIdx.x & 63;
+  const uint32_t n_in = J.n_in, nb = n_in >> 8, units = nb * 8;
+  const size_t rb = (size_t)nb * 210;
+  constexpr int NR = GATED ? 2 * R : R;
+  double acc[NR][TT];
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int t = 0; t < TT; t++) acc[r][t] = 0.0;
+  for (uint32_t u = lane; u < units; u += 64) {
+    const uint32_t b = u >> 3;
+    const int c = u & 7;
+    Q6Unit wd[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      const uint32_t row = row0 + (r % R);
+      const uint8_t *base = (r < R ? J.w : JU.w);
+      if (row < J.n_out)
+        wd[r] = q6_load(base + row * rb + (size_t)b * 210, c);
+      else
+        wd[r] = Q6Unit{{0, 0}, {0, 0}, {0, 0}, 0, 0};
+    }
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+      if (t >= (int)T) break;
+      const int8_t *xt = qx + (size_t)t * n_in + (size_t)b * 256;
+      uint32_t xq[4][2];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(xt + 128 * (c >> 2) + 32 * q + 8 * (c & 3));
+        xq[q][0] = v.x;
+        xq[q][1] = v.y;
+      }
+      const float d8 = dx[(size_t)t * nb + b];
+#pragma unroll
+      for (int r = 0; r < NR; r++) {
+        int A = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) A += (int)(int8_t)((wd[r].sc >> (8 * q)) & 0xff) *
+                                         q6_quarter_isum(wd[r], q, xq[q][0], xq[q][1]);
+        acc[r][t] += (double)(d8 * (h2f(wd[r].d) * (float)A));
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int t = 0; t < TT; t++) acc[r][t] = wave_sum(acc[r][t]);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const uint32_t row = row0 + r;
+      if (row >= J.n_out) break;
+#pragma unroll
+      for (int t = 0; t < TT; t++) {
+        if (t >= (int)T) break;
+        if (GATED) {
+          const float g = (float)acc[r][t], up = (float)acc[R + r][t];
+          ygated[(size_t)t * J.n_out + row] = g / (1.0f + expf(-g)) * up;
+        } else {
+          J.y[(size_t)t * J.n_out + row] = (float)acc[r][t];
+        }
+      }
+    }
+  }
+}
+
+template <int TT, bool GATED>
+__global__ __launch_bounds__(256) void gemv_q8_i8(JobSet js, const int8_t *__restrict__ qx,
+                                                  const float *__restrict__ dx, const int32_t *__restrict__ s16,
+                                                  uint32_t T, float *__restrict__ ygated) {
+  int ji;
+  uint32_t row0;
+  if (!locate(js, ji, row0)) return;
+  const Job &J = js.j[ji];
+  const Job &JU = js.j[GATED ? 1 : ji];
+  const int lane = threadIdx.x & 63;
+  const uint32_t n_in = J.n_in, nb = n_in >> 5, units = nb * 2;
+  const size_t rb = (size_t)nb * 34;
+  constexpr int NR = GATED ? 2 * R : R;
+  double acc[NR][TT];
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int t = 0; t < TT; t++) acc[r][t] = 0.0;
+  for (uint32_t u = lane; u < units; u += 64) {
+    const uint32_t b = u >> 1;
+    const int c = u & 1;
+    Q8Unit wd[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      const uint32_t row = row0 + (r % R);
+      const uint8_t *base = (r < R ? J.w : JU.w);
+      if (row < J.n_out)
+        wd[r] = q8_load(base + row * rb + (size_t)b * 34, c);
+      else
+        wd[r] = Q8Unit{{0, 0, 0, 0}, 0};
+    }
+    const uint32_t e0 = b * 32 + 16 * c;
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+      if (t >= (int)T) break;
+      const uint4 xv = *reinterpret_cast<const uint4 *>(qx + (size_t)t * n_in + e0);
+      const float d8 = dx[(size_t)t * (n_in >> 8) + (e0 >> 8)];
+#pragma unroll
+      for (int r = 0; r < NR; r++) {
+        int s = __builtin_amdgcn_sdot4((int)wd[r].q[0], (int)xv.x, 0, false);
+        s = __builtin_amdgcn_sdot4((int)wd[r].q[1], (int)xv.y, s, false);
+        s = __builtin_amdgcn_sdot4((int)wd[r].q[2], (int)xv.z, s, false);
+        s = __builtin_amdgcn_sdot4((int)wd[r].q[3], (int)xv.w, s, false);
+        acc[r][t] += (double)(d8 * (h2f(wd[r].d) * (float)s));
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int t = 0; t < TT; t++) acc[r][t] = wave_sum(acc[r][t]);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const uint32_t row = row0 + r;
+      if (row >= J.n_out) break;
+#pragma unroll
+      for (int t = 0; t < TT; t++) {
+        if (t >= (int)T) break;
+        if (GATED) {
+          const float g = (float)acc[r][t], up = (float)acc[R + r][t];
+          ygated[(size_t)t * J.n_out + row] = g / (1.0f + expf(-g)) * up;
+        } else {
+          J.y[(size_t)t * J.n_out + row] = (float)acc[r][t];
+        }
+      }
+    }
+  }
+}
+
+// --------------------------------------------------- int8 quantizer -------
+// One wave per group of `group` values (32 or 256): amax, d = amax/127,
+// q = round-half-away(x * 127/amax), and exact sums of every 16 quants.
+__global__ __launch_bounds__(256) void quantize_act_kernel(const float *__restrict__ x, uint32_t n_groups,
+                                                           uint32_t group, int8_t *__restrict__ q,
+                                                           float *__restrict__ d, int32_t *__restrict__ s16) {
+  const uint32_t g = blockIdx.x * WAVES + (threadIdx.x >> 6);
+  if (g >= n_groups) return;
+  const int lane = threadIdx.x & 63;
+  const float *xs = x + (size_t)g * group;
+  // Each lane holds up to 4 values (group <= 256).
+  float v[4];
+  float amax = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const uint32_t i = lane * 4 + k;
+    v[k] = i < group ? xs[i] : 0.f;
+    amax = fmaxf(amax, fabsf(v[k]));
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  const float inv = amax == 0.f ? 0.f : 127.0f / amax;
+  int qi[4];
+  int sum = 0;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    float r = roundf(v[k] * inv);
+    r = fminf(fmaxf(r, -127.f), 127.f);
+    qi[k] = (int)r;
+    sum += qi[k];
+  }
+  if (lane * 4 < group) {
+    const uint32_t packed = (uint32_t)(qi[0] & 0xff) | ((uint32_t)(qi[1] & 0xff) << 8) |
+                            ((uint32_t)(qi[2] & 0xff) << 16) | ((uint32_t)(qi[3] & 0xff) << 24);
+    *reinterpret_cast<uint32_t *>(q + (size_t)g * group + lane * 4) = packed;
+  }
+  // 16 values = 4 lanes.
+  sum += __shfl_xor(sum, 1, 64);
+  sum += __shfl_xor(sum, 2, 64);
+  if ((lane & 3) == 0 && lane * 4 < group) s16[((size_t)g * group + lane * 4) / 16] = sum;
+  if (lane == 0) d[g] = amax / 127.0f;
+}
+
+// --------------------------------------------------- block-dot debug ------
+// out[t][row][s] for sub-blocks of 32 (Q4_K, Q8_0) or 16 (Q6_K), through the
+// same unit functions the int8 GEMV uses.
+__global__ __launch_bounds__(256) void block_dot_kernel(int32_t dtype, const uint8_t *__restrict__ w,
+                                                        uint32_t n_out, uint32_t n_in, const int8_t *__restrict__ qx,
+                                                        uint32_t T, int32_t *__restrict__ out) {
+  const uint32_t sub = dtype == DT_Q6_K ? 16 : 32, nsub = n_in / sub;
+  const size_t total = (size_t)T * n_out * nsub;
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const uint32_t s = idx % nsub, row = (idx / nsub) % n_out, t = idx / ((size_t)nsub * n_out);
+  const int8_t *xt = qx + (size_t)t * n_in;
+  int32_t v = 0;
+  if (dtype == DT_Q4_K) {
+    // Sub-block s = 8b + j; units 2p, 2p+1 with p = j/2 hold its two halves,
+    // low nibbles for even j and high for odd j.
+    const uint32_t b = s / 8, j = s % 8, p = j / 2;
+    const uint8_t *blk = w + (size_t)row * (n_in / 256) * 144 + (size_t)b * 144;
+    for (int h = 0; h < 2; h++) {
+      const int c = 2 * p + h;
+      const uint32_t ca = b * 256 + (p << 6) + (h << 4);
+      int ia, ib;
+      q4k_unit_isum(ld16(blk + 16 + 16 * c), *reinterpret_cast<const uint4 *>(xt + ca),
+                    *reinterpret_cast<const uint4 *>(xt + ca + 32), ia, ib);
+      v += (j & 1) ? ib : ia;
+    }
+  } else if (dtype == DT_Q6_K) {
+    // Sub-block s = 16b + 8n + 2r + k2 covers l in [16 k2, 16 k2 + 16) of
+    // quarter r of half n: units with g = 2 k2 and 2 k2 + 1.
+    const uint32_t b = s / 16, i = s % 16, n = i / 8, r = (i % 8) / 2, k2 = i % 2;
+    const uint8_t *blk = w + (size_t)row * (n_in / 256) * 210 + (size_t)b * 210;
+    for (int gg = 0; gg < 2; gg++) {
+      const int g = 2 * k2 + gg, c = 4 * n + g;
+      Q6Unit u = q6_load(blk, c);
+      const uint2 xv = *reinterpret_cast<const uint2 *>(xt + b * 256 + 128 * n + 32 * r + 8 * g);
+      v += q6_quarter_isum(u, r, xv.x, xv.y);
+    }
+  } else {
+    const uint8_t *blk = w + (size_t)row * (n_in / 32) * 34 + (size_t)s * 34;
+    for (int c = 0; c < 2; c++) {
+      Q8Unit u = q8_load(blk, c);
+      const uint4 xv = *reinterpret_cast<const uint4 *>(xt + s * 32 + 16 * c);
+      v = __builtin_amdgcn_sdot4((int)u.q[0], (int)xv.x, v, false);
+      v = __builtin_amdgcn_sdot4((int)u.q[1], (int)xv.y, v, false);
+      v = __builtin_amdgcn_sdot4((int)u.q[2], (int)xv.z, v, false);
+      v = __builtin_amdgcn_sdot4((int)u.q[3], (int)xv.w, v, false);
+    }
+  }
+  out[idx] = v;
+}
+
+// ------------------------------------------------------------ launchers ----
+
+uint32_t waves_for(int32_t dtype, uint64_t n_out) {
+  if (dtype == DT_F32 || dtype == DT_F16) return (uint32_t)n_out;
+  return (uint32_t)((n_out + R - 1) / R);
+}
+
+JobSet make_set(const GemvJob *jobs, int n) {
+  JobSet js{};
+  js.n = n;
+  for (int i = 0; i < n; i++) {
+    js.j[i].w = jobs[i].w;
+    js.j[i].y = jobs[i].y;
+    js.j[i].n_out = (uint32_t)jobs[i].n_out;
+    js.j[i].n_in = (uint32_t)jobs[i].n_in;
+    js.j[i].waves = waves_for(jobs[i].dtype, jobs[i].n_out);
+  }
+  return js;
+}
+
+uint32_t grid_of(const JobSet &js) {
+  uint64_t w = 0;
+  for (int i = 0; i < js.n; i++) w += js.j[i].waves;
+  return (uint32_t)((w + WAVES - 1) / WAVES);
+}
+
+template <bool GATED>
+void dispatch_f32(mdma_ctx *ctx, int32_t dt, const JobSet &js, const float *x, uint32_t T, float *yg) {
+  const dim3 grid(grid_of(js)), block(64 * WAVES);
+#define MDMA_F32_CASE(TT)                                                                            \
+  switch (dt) {                                                                                      \
+    case DT_Q4_K: gemv_q4k_f32<TT, GATED><<<grid, block, 0, ctx->stream>>>(js, x, T, yg); break;     \
+    case DT_Q6_K: gemv_q6k_f32<TT, GATED><<<grid, block, 0, ctx->stream>>>(js, x, T, yg); break;     \
+    case DT_Q8_0: gemv_q8_f32<TT, GATED><<<grid, block, 0, ctx->stream>>>(js, x, T, yg); break;      \
+    case DT_F32: gemv_plain<DT_F32, GATED><<<grid, block, 0, ctx->stream>>>(js, x, T, yg); break;    \
+    case DT_F16: gemv_plain<DT_F16, GATED><<<grid, block, 0, ctx->stream>>>(js, x, T, yg); break;    \
+    default: fail(MDMA_ERR_NOT_IMPLEMENTED, "gemv: dtype");                                          \
+  }
+  if (T <= 1) { MDMA_F32_CASE(1) }
+  else if (T <= 2) { MDMA_F32_CASE(2) }
+  else if (T <= 4) { MDMA_F32_CASE(4) }
+  else { MDMA_F32_CASE(8) }
+#undef MDMA_F32_CASE
+  hip_check(hipGetLastError(), "gemv f32 launch");
+}
+
+template <bool GATED>
+void dispatch_i8(mdma_ctx *ctx, int32_t dt, const JobSet &js, const int8_t *qx, const float *dx,
+                 const int32_t *s16, uint32_t T, float *yg) {
+  const dim3 grid(grid_of(js)), block(64 * WAVES);
+#define MDMA_I8_CASE(TT)                                                                                   \
+  switch (dt) {                                                                                            \
+    case DT_Q4_K: gemv_q4k_i8<TT, GATED><<<grid, block, 0, ctx->stream>>>(js, qx, dx, s16, T, yg); break; \
+    case DT_Q6_K: gemv_q6k_i8<TT, GATED><<<grid, block, 0, ctx->stream>>>(js, qx, dx, s16, T, yg); break; \
+    case DT_Q8_0: gemv_q8_i8<TT, GATED><<<grid, block, 0, ctx->stream>>>(js, qx, dx, s16, T, yg); break;  \
+    default: fail(MDMA_ERR_NOT_IMPLEMENTED, "gemv i8: dtype");                                             \
+  }
+  if (T <= 1) { MDMA_I8_CASE(1) }
+  else if (T <= 2) { MDMA_I8_CASE(2) }
+  else if (T <= 4) { MDMA_I8_CASE(4) }
+  else { MDMA_I8_CASE(8) }
+#undef MDMA_I8_CASE
+  hip_check(hipGetLastError(), "gemv i8 launch");
+}
+
+bool same_dtype(const GemvJob *jobs, int n) {
+  for (int i = 1; i < n; i++)
+    if (jobs[i].dtype != jobs[0].dtype || jobs[i].n_in != jobs[0].n_in) return false;
+  return true;
+}
+
+// Token chunks of at most 8 per launch.
+template <class F>
+void by_chunks(uint64_t T, F &&f) {
+  for (uint64_t t0 = 0; t0 < T; t0 += 8) f(t0, T - t0 < 8 ? T - t0 : 8);
+}
+
+GemvJob offset_job(const GemvJob &j, uint64_t t0) {
+  GemvJob o = j;
+  if (o.y) o.y += t0 * j.n_out;
+  return o;
+}
+
+bool is_i8_dtype(int32_t dt) { return dt == DT_Q4_K || dt == DT_Q6_K || dt == DT_Q8_0; }
+
+// Quantize x [T, n_in] into the context scratch; returns pointers.
+void quantize_into_scratch(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in, int8_t **qx, float **dx,
+                           int32_t **s16) {
+  const uint64_t n = T * n_in;
+  const uint64_t qb = (n + 255) / 256 * 256, db = (n / 256 * 4 + 255) / 256 * 256;
+  char *s = scratch(ctx, qb + db + n / 16 * 4 + 256);
+  *qx = reinterpret_cast<int8_t *>(s);
+  *dx = reinterpret_cast<float *>(s + qb);
+  *s16 = reinterpret_cast<int32_t *>(s + qb + db);
+  launch_quantize_act(ctx, x, n, 256, *qx, *dx, *s16);
+}
+
+}  // namespace
+
+void launch_gemv_f32(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t T) {
+  if (!same_dtype(jobs, n_jobs)) {
+    for (int i = 0; i < n_jobs; i++) launch_gemv_f32(ctx, jobs + i, 1, x, T);
+    return;
+  }
+  by_chunks(T, [&](uint64_t t0, uint64_t tn) {
+    GemvJob js[3];
+    for (int i = 0; i < n_jobs; i++) js[i] = offset_job(jobs[i], t0);
+    dispatch_f32<false>(ctx, jobs[0].dtype, make_set(js, n_jobs), x + t0 * jobs[0].n_in, (uint32_t)tn, nullptr);
+  });
+}
+
+void launch_gemv_f32_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up, const float *x, uint64_t T,
+                           float *y) {
+  if (gate.dtype != up.dtype) {
+    launch_gemv_f32(ctx, &gate, 1, x, T);
+    launch_gemv_f32(ctx, &up, 1, x, T);
+    launch_silu_mul(ctx, gate.y, up.y, y, T * gate.n_out);
+    return;
+  }
+  by_chunks(T, [&](uint64_t t0, uint64_t tn) {
+    GemvJob js[2] = {offset_job(gate, t0), offset_job(up, t0)};
+    JobSet set = make_set(js, 2);
+    set.n = 1;  // waves cover the gate rows; each also reads up
+    dispatch_f32<true>(ctx, gate.dtype, set, x + t0 * gate.n_in, (uint32_t)tn, y + t0 * gate.n_out);
+  });
+}
+
+void launch_gemv_i8(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t T) {
+  for (int i = 0; i < n_jobs; i++)
+    if (!is_i8_dtype(jobs[i].dtype) || jobs[i].n_in % 256) {
+      // No int8 kernel for float weights (or rows that are not whole 256-groups):
+      // those run in f32 mode.
+      launch_gemv_f32(ctx, jobs, n_jobs, x, T);
+      return;
+    }
+  if (!same_dtype(jobs, n_jobs)) {
+    for (int i = 0; i < n_jobs; i++) launch_gemv_i8(ctx, jobs + i, 1, x, T);
+    return;
+  }
+  const uint64_t n_in = jobs[0].n_in;
+  int8_t *qx;
+  float *dx;
+  int32_t *s16;
+  quantize_into_scratch(ctx, x, T, n_in, &qx, &dx, &s16);
+  by_chunks(T, [&](uint64_t t0, uint64_t tn) {
+    GemvJob js[3];
+    for (int i = 0; i < n_jobs; i++) js[i] = offset_job(jobs[i], t0);
+    dispatch_i8<false>(ctx, jobs[0].dtype, make_set(js, n_jobs), qx + t0 * n_in, dx + t0 * (n_in / 256),
+                       s16 + t0 * (n_in / 16), (uint32_t)tn, nullptr);
+  });
+}
+
+void launch_gemv_i8_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up, const float *x, uint64_t T,
+                          float *y) {
+  if (gate.dtype != up.dtype || !is_i8_dtype(gate.dtype) || gate.n_in % 256) {
+    GemvJob js[2] = {gate, up};
+    launch_gemv_i8(ctx, js, 1, x, T);
+    launch_gemv_i8(ctx, js + 1, 1, x, T);
+    launch_silu_mul(ctx, gate.y, up.y, y, T * gate.n_out);
+    return;
+  }
+  const uint64_t n_in = gate.n_in;
+  int8_t *qx;
+  float *dx;
+  int32_t *s16;
+  quantize_into_scratch(ctx, x, T, n_in, &qx, &dx, &s16);
+  by_chunks(T, [&](uint64_t t0, uint64_t tn) {
+    GemvJob js[2] = {offset_job(gate, t0), offset_job(up, t0)};
+    JobSet set = make_set(js, 2);
+    set.n = 1;
+    dispatch_i8<true>(ctx, gate.dtype, set, qx + t0 * n_in, dx + t0 * (n_in / 256), s16 + t0 * (n_in / 16),
+                      (uint32_t)tn, y + t0 * gate.n_out);
+  });
+}
+
+void launch_quantize_act(mdma_ctx *ctx, const float *x, uint64_t n, uint64_t group, int8_t *q, float *d,
+                         int32_t *s16) {
+  const uint64_t groups = n / group;
+  quantize_act_kernel<<<dim3((uint32_t)((groups + WAVES - 1) / WAVES)), dim3(64 * WAVES), 0, ctx->stream>>>(
+      x, (uint32_t)groups, (uint32_t)group, q, d, s16);
+  hip_check(hipGetLastError(), "quantize_act launch");
+}
+
+void launch_block_dot(mdma_ctx *ctx, const GemvJob &w, const int8_t *qx, uint64_t T, int32_t *out) {
+  const uint64_t sub = w.dtype == DT_Q6_K ? 16 : 32, total = T * w.n_out * (w.n_in / sub);
+  if (!total) return;
+  block_dot_kernel<<<dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, ctx->stream>>>(
+      w.dtype, w.w, (uint32_t)w.n_out, (uint32_t)w.n_in, qx, (uint32_t)T, out);
+  hip_check(hipGetLastError(), "block_dot launch");
+}
+
+}  // namespace mdma

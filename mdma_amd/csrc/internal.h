@@ -1,0 +1,135 @@
+// Internal declarations shared by the gfx950 backend's host and kernel files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/mdma_gfx950.h"
+
+namespace mdma {
+
+enum : int32_t { DT_F32 = 0, DT_F16 = 1, DT_Q8_0 = 8, DT_Q4_K = 12, DT_Q6_K = 14 };
+
+inline uint64_t block_size(int32_t dt) {
+  switch (dt) {
+    case DT_F32: case DT_F16: return 1;
+    case DT_Q8_0: return 32;
+    case DT_Q4_K: case DT_Q6_K: return 256;
+    default: return 0;
+  }
+}
+inline uint64_t type_size(int32_t dt) {
+  switch (dt) {
+    case DT_F32: return 4;
+    case DT_F16: return 2;
+    case DT_Q8_0: return 34;
+    case DT_Q4_K: return 144;
+    case DT_Q6_K: return 210;
+    default: return 0;
+  }
+}
+
+// Status with message; thrown inside the library and turned into a status
+// code at the C boundary.
+struct Error {
+  int code;
+  std::string msg;
+};
+[[noreturn]] void fail(int code, const std::string &msg);
+[[noreturn]] inline void shape_fail(const std::string &msg) { fail(MDMA_ERR_SHAPE_MISMATCH, msg); }
+void hip_check(hipError_t e, const char *what);
+
+struct Pool {
+  uint64_t used = 0;
+  uint64_t limit = UINT64_MAX;
+};
+
+}  // namespace mdma
+
+struct mdma_buf {
+  mdma_ctx *ctx = nullptr;
+  char *ptr = nullptr;     // device address of element 0
+  uint64_t len = 0;        // bytes visible to ops
+  uint64_t charged = 0;    // bytes charged to the pool (0 for views)
+  int pool = MDMA_POOL_SCRATCH;
+  int layout = MDMA_LAYOUT_GGUF;
+  bool owner = true;       // false for views
+};
+
+struct mdma_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::recursive_mutex lock;
+  mdma::Pool pools[3];
+  int act_mode = MDMA_ACT_F32;
+  std::string label;
+  uint64_t total_bytes = 0;
+  int cu_count = 0;
+  // Scratch owned by the context (int8 activations, partial sums, RoPE tables).
+  char *scratch = nullptr;
+  uint64_t scratch_cap = 0;
+  // Device RoPE cos/sin table: [positions][head_dim/2] for one (head_dim, theta).
+  float *rope_tab = nullptr;
+  uint64_t rope_positions = 0, rope_hd = 0;
+  float rope_theta = 0.f;
+  uint32_t *host_ids = nullptr;  // pinned staging for token ids / argmax result
+  uint64_t host_ids_cap = 0;
+  bool capturing = false;        // stream capture in progress: no synchronizing calls
+};
+
+struct mdma_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
+namespace mdma {
+
+// Scratch space of at least `bytes` on the context's device; growing it
+// synchronizes the stream (callers hold the context lock).
+char *scratch(mdma_ctx *ctx, uint64_t bytes);
+// Device pointer to a cos/sin table covering positions [0, max_pos] for (hd, theta).
+const float *rope_table(mdma_ctx *ctx, uint64_t max_pos, uint64_t hd, float theta);
+
+// ---- kernel launchers (gemv.hip / quant.hip / ops.hip) ----
+struct GemvJob {
+  int32_t dtype;
+  const uint8_t *w;
+  uint64_t n_out, n_in;
+  float *y;        // [T, n_out], row stride n_out
+};
+// f32-activation GEMV for up to 3 independent weights sharing x (fused QKV).
+void launch_gemv_f32(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t T);
+// gate/up fused with SiLU: y = silu(gate x) * (up x); f32 activations.
+void launch_gemv_f32_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up, const float *x,
+                           uint64_t T, float *y);
+// int8 mode: quantize x per 256 then integer dots; same job conventions.
+void launch_gemv_i8(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t T);
+void launch_gemv_i8_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up, const float *x,
+                          uint64_t T, float *y);
+void launch_quantize_act(mdma_ctx *ctx, const float *x, uint64_t n, uint64_t group, int8_t *q,
+                         float *d, int32_t *sum16);
+void launch_block_dot(mdma_ctx *ctx, const GemvJob &w, const int8_t *qx, uint64_t T, int32_t *out);
+
+void launch_embed(mdma_ctx *ctx, int32_t dtype, const uint8_t *table, uint64_t n_embd,
+                  const uint32_t *ids_dev, uint64_t n_ids, float *out);
+void launch_rmsnorm(mdma_ctx *ctx, const float *w, uint64_t dim, const float *a, const float *b,
+                    float *sum, float *y, uint64_t rows, float eps);
+void launch_add(mdma_ctx *ctx, const float *a, const float *b, float *y, uint64_t n);
+void launch_silu_mul(mdma_ctx *ctx, const float *g, const float *u, float *y, uint64_t n);
+void launch_rope(mdma_ctx *ctx, float *x, uint64_t n_tokens, uint64_t heads, uint64_t hd,
+                 const float *tab, uint32_t pos);
+void launch_kv_write(mdma_ctx *ctx, const float *k, const float *v, uint16_t *dk, uint16_t *dv,
+                     uint64_t n);
+void launch_rope_kv_write(mdma_ctx *ctx, float *q, uint64_t q_heads, const float *k,
+                          const float *v, uint64_t kv_heads, uint64_t hd, uint64_t n_tokens,
+                          const float *tab, uint32_t pos, uint16_t *dk, uint16_t *dv);
+void launch_attn(mdma_ctx *ctx, const float *q, const uint16_t *k, const uint16_t *v, float *o,
+                 uint64_t n_q, uint64_t kv_len, uint64_t hd, uint64_t n_q_heads,
+                 uint64_t n_kv_heads);
+void launch_argmax(mdma_ctx *ctx, const float *x, uint64_t n, uint32_t *out_dev);
+
+}  // namespace mdma

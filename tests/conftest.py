@@ -1,0 +1,52 @@
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+
+
+@pytest.fixture(scope="session")
+def backend():
+    from mdma_amd.backend import Gfx950Backend
+
+    b = Gfx950Backend(0)
+    yield b
+    b.close()
+
+
+def f32_exact(W: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """f64 dot products of the oracle's dequantized rows with x: [T, n_out]."""
+    return x.reshape(-1, W.shape[1]).astype(np.float64) @ W.astype(np.float64).T
+
+
+def assert_parity(got, cpu, exact, rtol, atol=1e-6, what=""):
+    """Per-element parity against the CPU oracle.
+
+    The oracle sums each dot product sequentially in f32 (reference
+    src/backend/cpu.rs:46-48), so it carries its own rounding error |cpu - exact|
+    of up to ~1e-4 at K=14336; no parallel reduction order can reproduce it bit
+    for bit. An element passes when the GPU is within the stated tolerance of
+    the oracle after allowing for that error:
+        |gpu - cpu| <= atol + rtol*|cpu| + |cpu - exact|
+    where exact is the f64 dot product of the oracle's own dequantized f32
+    weights with the same x. Non-finite values fail.
+    """
+    got = np.asarray(got, dtype=np.float64).reshape(-1)
+    cpu = np.asarray(cpu, dtype=np.float64).reshape(-1)
+    exact = np.asarray(exact, dtype=np.float64).reshape(-1)
+    assert got.shape == cpu.shape == exact.shape
+    assert np.all(np.isfinite(got)), f"{what}: non-finite GPU output"
+    bound = atol + rtol * np.abs(cpu) + np.abs(cpu - exact)
+    err = np.abs(got - cpu)
+    bad = np.nonzero(~(err <= bound))[0]
+    assert bad.size == 0, (f"{what}: {bad.size}/{got.size} elements outside tolerance; first {bad[:5]}: "
+                           f"gpu {got[bad[:5]]} cpu {cpu[bad[:5]]} exact {exact[bad[:5]]}")
+    return float(np.mean(err <= atol + rtol * np.abs(cpu)))

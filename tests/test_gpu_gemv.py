@@ -1,0 +1,314 @@
+"""GPU parity of the quantized-weight hot path against the CPU oracle.
+
+f32-activation mode: per element within 1e-5 relative / 1e-6 absolute of the
+oracle, after allowing for the oracle's own sequential-f32 rounding error
+(see conftest.assert_parity). int8-activation mode: the reference's
+"requantize then CPU qmatmul" pattern (src/backend/rocm/decode/tests.rs:68-130)
+at 1e-3 relative, and the int32 block dots bit-exact. Outputs are allocated
+oversize with a canary tail that must survive (decode/tests.rs:98,123-126).
+"""
+import numpy as np
+import pytest
+
+from conftest import assert_parity, f32_exact
+from mdma_amd import synth
+from mdma_amd.backend import ShapeMismatch, QWeight
+from oracle import ffi
+
+pytestmark = pytest.mark.gpu
+Q8, Q4K, Q6K, F32, F16 = 8, 12, 14, 0, 1
+CANARY = np.float32(123456.25)
+
+
+def ref_weights(dtype, rows, k):
+    """The reference's synthetic blocks (src/backend/rocm/decode/tests.rs:47-66):
+    every byte varies, d in {1,2,3}/1024, dmin 1/512, Q6_K sub-scales -128/+127."""
+    tsz = synth.TYPE_SIZE[dtype]
+    nb = rows * (k // synth.BLOCK_SIZE[dtype])
+    raw = np.zeros((nb, tsz), np.uint8)
+    i = np.arange(tsz)
+    for b in range(nb):
+        raw[b] = (i * 73 + b * 31 + 19) & 255
+        d = np.frombuffer(np.float16((1 + b % 3) / 1024).tobytes(), np.uint8)
+        if dtype == Q4K:
+            raw[b, 0:2] = d
+            raw[b, 2:4] = np.frombuffer(np.float16(1 / 512).tobytes(), np.uint8)
+        elif dtype == Q6K:
+            raw[b, 208:210] = d
+            raw[b, 192], raw[b, 193] = 128, 127
+        else:
+            raw[b, 0:2] = d
+    return raw.reshape(-1)
+
+
+def x_kind(kind, n):
+    i = np.arange(n)
+    if kind == 0:
+        return (((i * 17) % 255).astype(np.float32) - 127.0) / 32.0
+    if kind == 1:
+        return -(((i * 7) % 31 + 1).astype(np.float32)) / 16.0
+    return np.zeros(n, np.float32)
+
+
+def run_qmatmul(be, dtype, raw, rows, k, x, mode="default", layout=0):
+    w = be.upload_weight(raw, dtype, (rows, k), layout)
+    T = x.size // k
+    xb = be.f32_buf(x)
+    yb = be.f32_buf(np.full(T * rows + 8, CANARY, np.float32))
+    {"default": be.qmatmul, "f32": be.qmatmul_f32, "i8": be.qmatmul_i8}[mode](w, xb, yb)
+    y = be.download_f32(yb)
+    assert np.all(y[T * rows:] == CANARY), "wrote past the output"
+    return y[:T * rows].reshape(T, rows)
+
+
+def oracle_f32(dtype, raw, rows, k, x):
+    cpu = ffi.qmatmul(dtype, raw, rows, k, x)
+    W = ffi.dequantize_row(dtype, raw, rows * k).reshape(rows, k)
+    return cpu, f32_exact(W, x)
+
+
+KS = {Q4K: (256, 512, 768), Q6K: (256, 512, 768), Q8: (32, 288, 768), F32: (3, 288), F16: (64, 288)}
+
+
+@pytest.mark.parametrize("dtype", [Q4K, Q6K, Q8])
+def test_f32_mode_reference_shapes_and_inputs(backend, dtype):
+    for rows in (1, 7, 9, 20):
+        for k in KS[dtype]:
+            raw = ref_weights(dtype, rows, k)
+            for kind in range(3):
+                x = x_kind(kind, k)
+                got = run_qmatmul(backend, dtype, raw, rows, k, x, "f32")
+                cpu, exact = oracle_f32(dtype, raw, rows, k, x)
+                assert_parity(got, cpu, exact, 1e-5, what=f"dtype={dtype} rows={rows} k={k} x={kind}")
+                if kind == 2:
+                    assert np.all(got == 0)
+
+
+@pytest.mark.parametrize("dtype", [F32, F16])
+def test_f32_mode_float_weights(backend, dtype):
+    for rows, k in ((2, 3), (5, 288), (33, 64)):
+        raw = synth.weight(dtype, rows, k, 3)
+        x = synth.normal_f32(2 * k, 4)
+        got = run_qmatmul(backend, dtype, raw, rows, k, x)
+        cpu, exact = oracle_f32(dtype, raw, rows, k, x)
+        assert_parity(got, cpu, exact, 1e-5, what=f"dtype={dtype}")
+    # src/backend/test_support.rs:254-268 hand-computed batch.
+    w = np.array([1.0, -2.0, 3.0, 4.0, 5.0, -6.0], np.float32).view(np.uint8)
+    got = run_qmatmul(backend, F32, w, 2, 3, np.array([2.0, -1.0, 0.5, -1.0, 2.0, 1.0], np.float32))
+    assert list(got.reshape(-1)) == [5.5, 0.0, -2.0, 0.0]
+
+
+@pytest.mark.parametrize("dtype", [Q4K, Q6K, Q8])
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 8, 9, 17])
+def test_f32_mode_batched_tokens(backend, dtype, T):
+    rows, k = 37, 1024
+    raw = synth.weight(dtype, rows, k, 100 + T)
+    x = synth.normal_f32(T * k, 200 + T)
+    got = run_qmatmul(backend, dtype, raw, rows, k, x, "f32")
+    cpu, exact = oracle_f32(dtype, raw, rows, k, x)
+    assert_parity(got, cpu, exact, 1e-5, what=f"dtype={dtype} T={T}")
+    # Batched rows equal single-token calls bit for bit.
+    one = run_qmatmul(backend, dtype, raw, rows, k, x[:k], "f32")
+    assert np.array_equal(one[0], got[0])
+
+
+SHAPES_8B = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]
+
+
+@pytest.mark.parametrize("shape", SHAPES_8B)
+def test_q4k_f32_mode_llama3_8b_shapes(backend, shape):
+    rows, k = shape
+    raw = synth.weight(Q4K, rows, k, 1)
+    x = synth.normal_f32(k, 2)
+    got = run_qmatmul(backend, Q4K, raw, rows, k, x, "f32")
+    cpu, exact = oracle_f32(Q4K, raw, rows, k, x)
+    rate = assert_parity(got, cpu, exact, 1e-5, what=f"Q4_K {shape}")
+    print(f"Q4_K {shape}: plain 1e-5/1e-6 pass rate vs sequential oracle {rate:.4f}")
+
+
+@pytest.mark.parametrize("shape,T", [((4096, 14336), 1), ((4096, 14336), 4), ((4096, 14336), 8),
+                                     ((128256, 4096), 1)])
+def test_q6k_f32_mode_config3_shapes(backend, shape, T):
+    rows, k = shape
+    raw = synth.weight(Q6K, rows, k, 3)
+    x = synth.normal_f32(T * k, 4)
+    got = run_qmatmul(backend, Q6K, raw, rows, k, x, "f32")
+    cpu = ffi.qmatmul(Q6K, raw, rows, k, x)
+    exact = np.empty_like(cpu, dtype=np.float64)
+    for r0 in range(0, rows, 8192):
+        r1 = min(rows, r0 + 8192)
+        W = ffi.dequantize_row(Q6K, raw[r0 * (k // 256) * 210:r1 * (k // 256) * 210], (r1 - r0) * k)
+        exact[:, r0:r1] = f32_exact(W.reshape(r1 - r0, k), x)
+    assert_parity(got, cpu, exact, 1e-5, what=f"Q6_K {shape} T={T}")
+
+
+# ------------------------------------------------------------ int8 mode ----
+
+def oracle_i8(dtype, raw, rows, k, x):
+    q, d, _ = ffi.quantize_act(x, 256)
+    xh = ffi.dequantize_act(q, d, 256)
+    return oracle_f32(dtype, raw, rows, k, xh)
+
+
+@pytest.mark.parametrize("dtype", [Q4K, Q6K, Q8])
+def test_i8_mode_reference_shapes(backend, dtype):
+    for rows in (1, 7, 9, 20):
+        for k in (256, 512, 768):
+            raw = ref_weights(dtype, rows, k)
+            for kind in range(3):
+                x = x_kind(kind, k)
+                got = run_qmatmul(backend, dtype, raw, rows, k, x, "i8")
+                cpu, exact = oracle_i8(dtype, raw, rows, k, x)
+                assert_parity(got, cpu, exact, 1e-3, what=f"i8 dtype={dtype} rows={rows} k={k} x={kind}")
+
+
+@pytest.mark.parametrize("dtype", [Q4K, Q6K, Q8])
+@pytest.mark.parametrize("shape", [(4096, 4096), (14336, 4096), (4096, 14336)])
+def test_i8_mode_llama3_8b_shapes(backend, dtype, shape):
+    rows, k = shape
+    raw = synth.weight(dtype, rows, k, 11)
+    x = synth.normal_f32(k, 12)
+    got = run_qmatmul(backend, dtype, raw, rows, k, x, "i8")
+    cpu, exact = oracle_i8(dtype, raw, rows, k, x)
+    assert_parity(got, cpu, exact, 1e-3, what=f"i8 {dtype} {shape}")
+    # Quantization error itself, against the unquantized f32 oracle
+    # (src/backend/rocm/tests.rs:306-376 requires rel-RMS below 0.03).
+    full = ffi.qmatmul(dtype, raw, rows, k, x)
+    rel_rms = np.sqrt(np.mean((got - full) ** 2) / np.mean(full ** 2))
+    assert rel_rms < 0.03, rel_rms
+
+
+@pytest.mark.parametrize("T", [2, 5, 8, 11])
+def test_i8_mode_batched(backend, T):
+    rows, k = 29, 2048
+    for dtype in (Q4K, Q6K, Q8):
+        raw = synth.weight(dtype, rows, k, T)
+        x = synth.normal_f32(T * k, 50 + T)
+        got = run_qmatmul(backend, dtype, raw, rows, k, x, "i8")
+        q = np.concatenate([ffi.quantize_act(x[t * k:(t + 1) * k], 256)[0] for t in range(T)])
+        d = np.concatenate([ffi.quantize_act(x[t * k:(t + 1) * k], 256)[1] for t in range(T)])
+        cpu, exact = oracle_f32(dtype, raw, rows, k, ffi.dequantize_act(q, d, 256))
+        assert_parity(got, cpu, exact, 1e-3, what=f"i8 batched {dtype} T={T}")
+
+
+@pytest.mark.parametrize("group", [32, 256])
+def test_quantize_act_bit_exact(backend, group):
+    x = synth.normal_f32(8 * 1024, 77) * 3
+    x[:group] = 0
+    x[group:2 * group] = np.linspace(-1, 1, group, dtype=np.float32) * 127  # .5 ties
+    n = x.size
+    xb = backend.f32_buf(x)
+    qb, db, sb = backend.alloc(n), backend.alloc(n // group * 4), backend.alloc(n // 16 * 4)
+    backend.quantize_act(xb, group, qb, db, sb)
+    q, d, s = ffi.quantize_act(x, group)
+    assert np.array_equal(backend.download(qb, 0, n).view(np.int8), q)
+    assert np.array_equal(backend.download(db, 0, n // group * 4).view(np.uint32), d.view(np.uint32))
+    assert np.array_equal(backend.download(sb, 0, n // 16 * 4).view(np.int32), s)
+
+
+@pytest.mark.parametrize("dtype", [Q4K, Q6K, Q8])
+def test_block_dot_i32_bit_exact(backend, dtype):
+    rows, k, T = 9, 1024, 3
+    raw = synth.weight(dtype, rows, k, 31)
+    q, _, _ = ffi.quantize_act(synth.normal_f32(T * k, 32), 256)
+    q = q.copy()
+    q[:64] = 127
+    q[64:128] = -128  # extremes the quantizer never emits, still exact
+    w = backend.upload_weight(raw, dtype, (rows, k))
+    qb = backend.alloc(q.size)
+    backend.upload(qb, 0, q)
+    sub = 16 if dtype == Q6K else 32
+    ob = backend.alloc(T * rows * (k // sub) * 4)
+    backend.block_dot_i32(w, qb, ob)
+    got = backend.download(ob, 0, ob.len).view(np.int32).reshape(T, rows, k // sub)
+    assert np.array_equal(got, ffi.block_dot_i32(dtype, raw, rows, k, q, T))
+
+
+# ------------------------------------------------------------- fusions ----
+
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("dtype", [Q4K, Q6K, Q8])
+def test_fused_qkv_equals_separate_calls(backend, dtype, mode):
+    backend.set_act_mode(mode)
+    try:
+        k_in = 512
+        shapes = [(96, k_in), (32, k_in), (32, k_in)]
+        for T in (1, 3):
+            x = backend.f32_buf(synth.normal_f32(T * k_in, 5))
+            ws = [backend.upload_weight(synth.weight(dtype, r, c, 40 + i), dtype, (r, c))
+                  for i, (r, c) in enumerate(shapes)]
+            outs = [backend.alloc(T * r * 4) for r, _ in shapes]
+            backend.qmatmul_qkv(ws[0], ws[1], ws[2], x, *outs)
+            for w, o, (r, _) in zip(ws, outs, shapes):
+                sep = backend.alloc(T * r * 4)
+                backend.qmatmul(w, x, sep)
+                assert np.array_equal(backend.download_f32(o), backend.download_f32(sep))
+    finally:
+        backend.set_act_mode(0)
+
+
+def test_fused_qkv_mixed_dtypes(backend):
+    k_in = 256
+    x_h = synth.normal_f32(k_in, 5)
+    x = backend.f32_buf(x_h)
+    specs = [(Q6K, 64), (Q4K, 16), (Q8, 16)]
+    ws = [backend.upload_weight(synth.weight(dt, r, k_in, i), dt, (r, k_in)) for i, (dt, r) in enumerate(specs)]
+    outs = [backend.alloc(r * 4) for _, r in specs]
+    backend.qmatmul_qkv(ws[0], ws[1], ws[2], x, *outs)
+    for (dt, r), o, i in zip(specs, outs, range(3)):
+        raw = synth.weight(dt, r, k_in, i)
+        cpu, exact = oracle_f32(dt, raw, r, k_in, x_h)
+        assert_parity(backend.download_f32(o), cpu, exact, 1e-5)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("dtype", [Q4K, Q6K, Q8])
+def test_ffn_gate_up_matches_oracle_and_unfused(backend, dtype, mode):
+    backend.set_act_mode(mode)
+    try:
+        rows, k, T = 300, 1024, 2
+        g_raw, u_raw = synth.weight(dtype, rows, k, 61), synth.weight(dtype, rows, k, 62)
+        x_h = synth.normal_f32(T * k, 63)
+        g = backend.upload_weight(g_raw, dtype, (rows, k))
+        u = backend.upload_weight(u_raw, dtype, (rows, k))
+        x = backend.f32_buf(x_h)
+        gs, us = backend.alloc(T * rows * 4), backend.alloc(T * rows * 4)
+        y = backend.f32_buf(np.full(T * rows + 8, CANARY, np.float32))
+        backend.ffn_gate_up(g, u, x, gs, us, y)
+        got = backend.download_f32(y)
+        assert np.all(got[T * rows:] == CANARY)
+        got = got[:T * rows]
+        # Unfused on the device: qmatmul, qmatmul, silu_mul (backend.rs:472-489).
+        backend.qmatmul(g, x, gs)
+        backend.qmatmul(u, x, us)
+        y2 = backend.alloc(T * rows * 4)
+        backend.silu_mul(gs, us, y2)
+        assert np.array_equal(got, backend.download_f32(y2))
+        # Oracle: CPU gate/up, CPU silu_mul; exact = f64 chain.
+        xx = x_h if mode == 0 else np.concatenate(
+            [ffi.dequantize_act(*ffi.quantize_act(x_h[t * k:(t + 1) * k], 256)[:2], 256) for t in range(T)])
+        cg, eg = oracle_f32(dtype, g_raw, rows, k, xx)
+        cu, eu = oracle_f32(dtype, u_raw, rows, k, xx)
+        cpu = ffi.silu_mul(cg.reshape(-1), cu.reshape(-1))
+        exact = (eg / (1 + np.exp(-eg)) * eu).reshape(-1)
+        assert_parity(got, cpu, exact, 1e-5 if mode == 0 else 1e-3, atol=1e-5, what=f"gate_up {dtype} mode {mode}")
+    finally:
+        backend.set_act_mode(0)
+
+
+# ---------------------------------------------------------- shape rules ----
+
+def test_qmatmul_shape_rules(backend):
+    raw = synth.weight(Q4K, 4, 512, 1)
+    w = backend.upload_weight(raw, Q4K, (4, 512))
+    with pytest.raises(ShapeMismatch):
+        backend.qmatmul(w, backend.alloc(300 * 4), backend.alloc(64))
+    with pytest.raises(ShapeMismatch):
+        backend.qmatmul(w, backend.alloc(512 * 4), backend.alloc(12))
+    with pytest.raises(ShapeMismatch):
+        backend.qmatmul(QWeight(Q4K, (4, 384), w.buf), backend.alloc(384 * 4), backend.alloc(64))
+    with pytest.raises(ShapeMismatch):
+        backend.qmatmul(QWeight(Q4K, (8, 512), w.buf), backend.alloc(512 * 4), backend.alloc(64))
+    with pytest.raises(ShapeMismatch):
+        backend.ffn_gate_up(w, QWeight(Q4K, (2, 512), w.buf), backend.alloc(2048), backend.alloc(16),
+                            backend.alloc(16), backend.alloc(16))
