@@ -207,7 +207,7 @@ int mdma_gfx950_graph_begin(mdma_ctx *ctx);
 int mdma_gfx950_graph_end(mdma_ctx *ctx, mdma_graph **out);
 int mdma_gfx950_graph_launch(mdma_ctx *ctx, mdma_graph *graph);
 void mdma_gfx950_graph_destroy(mdma_graph *graph);
-/* Pre-size the context scratch (int8 activations) so a later capture needs no growth. */
+/* Pre-size the context scratch and int8-activation buffers so a later capture needs no growth. */
 int mdma_gfx950_reserve_scratch(mdma_ctx *ctx, uint64_t bytes);
 
 #ifdef __cplusplus

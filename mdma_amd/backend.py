@@ -131,6 +131,8 @@ class Buf:
     def close(self):
         if self.handle:
             h, self.handle = self.handle, None
+            if self.backend.ctx is None:
+                return  # the context (and its device) is gone; the process reclaims it
             _check(lib().mdma_gfx950_free(h))
 
     def __del__(self):
@@ -357,8 +359,9 @@ class Graph:
 
     def close(self):
         if self.handle:
-            lib().mdma_gfx950_graph_destroy(self.handle)
-            self.handle = None
+            h, self.handle = self.handle, None
+            if self.backend.ctx is not None:
+                lib().mdma_gfx950_graph_destroy(h)
 
     def __del__(self):
         self.close()

@@ -123,6 +123,7 @@ int qmatmul_mode(mdma_ctx *ctx, const mdma_qweight *w, const mdma_buf *x, mdma_b
     same_ctx(ctx, y, "qmatmul");
     GemvJob j = job_of(w, y);
     run_gemv(ctx, mode < 0 ? ctx->act_mode : mode, &j, 1, reinterpret_cast<const float *>(x->ptr), T);
+    q8_invalidate_range(ctx, y->ptr, y->len);
   });
 }
 
@@ -189,6 +190,28 @@ char *scratch(mdma_ctx *ctx, uint64_t bytes) {
   ctx->scratch = static_cast<char *>(p);
   ctx->scratch_cap = cap;
   return ctx->scratch;
+}
+
+char *q8_buffer(mdma_ctx *ctx, uint64_t bytes) {
+  if (bytes <= ctx->q8_cap) return ctx->q8;
+  no_capture(ctx, "int8 activation buffer growth");
+  uint64_t cap = bytes < (1u << 20) ? (1u << 20) : bytes + bytes / 4;
+  hip_check(hipStreamSynchronize(ctx->stream), "q8 grow sync");
+  if (ctx->q8) hip_check(hipFree(ctx->q8), "q8 free");
+  ctx->q8 = nullptr;
+  ctx->q8_cap = 0;
+  ctx->q8_valid = false;
+  void *p = nullptr;
+  hip_check(hipMalloc(&p, cap), "q8 alloc");
+  ctx->q8 = static_cast<char *>(p);
+  ctx->q8_cap = cap;
+  return ctx->q8;
+}
+
+void q8_invalidate_range(mdma_ctx *ctx, const void *p, uint64_t bytes) {
+  if (!ctx->q8_valid) return;
+  const char *a = static_cast<const char *>(p), *x = reinterpret_cast<const char *>(ctx->q8_x);
+  if (a < x + ctx->q8_n * 4 && x < a + bytes) ctx->q8_valid = false;
 }
 
 const float *rope_table(mdma_ctx *ctx, uint64_t max_pos, uint64_t hd, float theta) {
@@ -259,6 +282,7 @@ void mdma_gfx950_destroy(mdma_ctx *ctx) {
   (void)hipSetDevice(ctx->device);
   (void)hipStreamSynchronize(ctx->stream);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
+  if (ctx->q8) (void)hipFree(ctx->q8);
   if (ctx->rope_tab) (void)hipFree(ctx->rope_tab);
   if (ctx->host_ids) (void)hipHostFree(ctx->host_ids);
   (void)hipStreamDestroy(ctx->stream);
@@ -376,6 +400,7 @@ int mdma_gfx950_free(mdma_buf *buf) {
     }
     mdma_ctx *ctx = buf->ctx;
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    q8_invalidate(ctx);
     no_capture(ctx, "free");
     // Kernels queued on the stream may still read the buffer.
     hip_check(hipStreamSynchronize(ctx->stream), "free: stream sync");
@@ -420,6 +445,7 @@ int mdma_gfx950_upload(mdma_ctx *ctx, mdma_buf *dst, uint64_t offset, const void
     if (!len) return;
     need(src, "upload");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    q8_invalidate(ctx);
     no_capture(ctx, "upload");
     hip_check(hipMemcpyAsync(dst->ptr + offset, src, len, hipMemcpyHostToDevice, ctx->stream), "upload");
     hip_check(hipStreamSynchronize(ctx->stream), "upload sync");
@@ -453,6 +479,7 @@ int mdma_gfx950_copy(mdma_ctx *ctx, const mdma_buf *src, uint64_t src_off, mdma_
     range("copy", dst_off, len, dst->len);
     if (!len) return;
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    q8_invalidate(ctx);
     hip_check(hipMemcpyAsync(dst->ptr + dst_off, src->ptr + src_off, len, hipMemcpyDeviceToDevice,
                              ctx->stream), "copy");
   });
@@ -510,6 +537,8 @@ int mdma_gfx950_qmatmul_qkv(mdma_ctx *ctx, const mdma_qweight *wq, const mdma_qw
       same_ctx(ctx, b, "qmatmul_qkv");
     GemvJob jobs[3] = {job_of(wq, q), job_of(wk, k), job_of(wv, v)};
     run_gemv(ctx, ctx->act_mode, jobs, 3, reinterpret_cast<const float *>(x->ptr), T);
+    for (const mdma_buf *o : {(const mdma_buf *)q, (const mdma_buf *)k, (const mdma_buf *)v})
+      q8_invalidate_range(ctx, o->ptr, o->len);
   });
 }
 
@@ -535,6 +564,13 @@ int mdma_gfx950_ffn_gate_up(mdma_ctx *ctx, const mdma_qweight *gate, const mdma_
     GemvJob gj = job_of(gate, gate_scratch), uj = job_of(up, up_scratch);
     const float *xp = reinterpret_cast<const float *>(x->ptr);
     float *yp = reinterpret_cast<float *>(y->ptr);
+    struct Inval {  // runs when the call returns, after the launches below
+      mdma_ctx *c;
+      const mdma_buf *bs[3];
+      ~Inval() {
+        for (const mdma_buf *b : bs) q8_invalidate_range(c, b->ptr, b->len);
+      }
+    } inval{ctx, {gate_scratch, up_scratch, y}};
     // The fused kernel writes only y; the scratch buffers stay unspecified,
     // as the trait allows. When the scratch is larger than T*n_out (the
     // default impl would then run silu_mul over the whole scratch length),
@@ -560,6 +596,7 @@ int mdma_gfx950_embed(mdma_ctx *ctx, const mdma_qweight *table, const uint32_t *
   return guarded([&] {
     need(ctx, "embed");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    q8_invalidate(ctx);
     weight_row_bytes(table, "embed");
     uint64_t oe = f32_elems("embed", out);
     // shape::embed (shape.rs:92-110).
@@ -588,6 +625,7 @@ int mdma_gfx950_rmsnorm(mdma_ctx *ctx, const mdma_buf *w, const mdma_buf *x, mdm
   return guarded([&] {
     need(ctx, "rmsnorm");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    q8_invalidate(ctx);
     uint64_t dim = f32_elems("rmsnorm", w), xe = f32_elems("rmsnorm", x), ye = f32_elems("rmsnorm", y);
     // shape::rows (shape.rs:113-124).
     if (!dim || !xe || xe % dim) shape_fail(fmt("rmsnorm: x has %llu elems, not whole rows of %llu",
@@ -604,6 +642,7 @@ int mdma_gfx950_add_rmsnorm(mdma_ctx *ctx, const mdma_buf *w, const mdma_buf *a,
   return guarded([&] {
     need(ctx, "add_rmsnorm");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    q8_invalidate(ctx);
     uint64_t dim = f32_elems("add_rmsnorm", w), ae = f32_elems("add_rmsnorm", a),
              be = f32_elems("add_rmsnorm", b), se = f32_elems("add_rmsnorm", sum),
              ye = f32_elems("add_rmsnorm", y);
@@ -632,6 +671,7 @@ int mdma_gfx950_add(mdma_ctx *ctx, const mdma_buf *a, const mdma_buf *b, mdma_bu
   return guarded([&] {
     need(ctx, "add");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    q8_invalidate(ctx);
     uint64_t ae = f32_elems("add", a), be = f32_elems("add", b), ye = f32_elems("add", y);
     if (ae != be) shape_fail("add: input lengths differ");
     if (ye < ae) shape_fail("add: output too small");
@@ -644,6 +684,7 @@ int mdma_gfx950_silu_mul(mdma_ctx *ctx, const mdma_buf *gate, const mdma_buf *up
   return guarded([&] {
     need(ctx, "silu_mul");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    q8_invalidate(ctx);
     uint64_t ge = f32_elems("silu_mul", gate), ue = f32_elems("silu_mul", up), ye = f32_elems("silu_mul", y);
     if (ge != ue) shape_fail("silu_mul: input lengths differ");
     if (ye < ge) shape_fail("silu_mul: output too small");
@@ -657,6 +698,7 @@ int mdma_gfx950_rope(mdma_ctx *ctx, mdma_buf *q, mdma_buf *k, uint32_t pos, uint
   return guarded([&] {
     need(ctx, "rope");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    q8_invalidate(ctx);
     uint64_t qh, kh;
     check_rope(spec, f32_elems("rope", q), f32_elems("rope", k), n_tokens, &qh, &kh);
     const float *tab = rope_table(ctx, pos + n_tokens - 1, spec->head_dim, spec->theta);
@@ -670,6 +712,7 @@ int mdma_gfx950_kv_write(mdma_ctx *ctx, const mdma_buf *k, const mdma_buf *v, md
   return guarded([&] {
     need(ctx, "kv_write");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    q8_invalidate(ctx);
     // The default impl's two copies: n_elems f32 from offset 0 of k/v to
     // element elem_offset of the caches (2-byte elements here).
     range("kv_write", 0, n_elems * 4, f32_elems("kv_write", k) * 4);
@@ -691,6 +734,7 @@ int mdma_gfx950_rope_kv_write(mdma_ctx *ctx, mdma_buf *q, mdma_buf *k, const mdm
   return guarded([&] {
     need(ctx, "rope_kv_write");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    q8_invalidate(ctx);
     uint64_t qh, kh, ke = f32_elems("rope_kv_write", k);
     check_rope(spec, f32_elems("rope_kv_write", q), ke, n_tokens, &qh, &kh);
     range("kv_write", 0, n_elems * 4, ke * 4);
@@ -727,6 +771,7 @@ int mdma_gfx950_attn(mdma_ctx *ctx, const mdma_buf *q, const mdma_kv_view *kv, c
     need(kv->k, "attn");
     need(kv->v, "attn");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    q8_invalidate(ctx);
     // shape::attn (shape.rs:291-330); K/V elements counted at 2 bytes.
     uint64_t per = spec->n_q_heads * spec->head_dim, qe = f32_elems("attn", q), oe = f32_elems("attn", o);
     if (!per || !qe || qe % per) shape_fail("attn: q is not whole tokens of n_q_heads*head_dim");
@@ -769,6 +814,7 @@ int mdma_gfx950_quantize_act(mdma_ctx *ctx, const mdma_buf *x, uint64_t group, m
   return guarded([&] {
     need(ctx, "quantize_act");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    q8_invalidate(ctx);
     uint64_t n = f32_elems("quantize_act", x);
     if (group != 256 && group != 32) shape_fail("quantize_act: group must be 32 or 256");
     if (!n || n % group) shape_fail("quantize_act: x is not whole groups");
@@ -787,6 +833,7 @@ int mdma_gfx950_block_dot_i32(mdma_ctx *ctx, const mdma_qweight *w, const mdma_b
   return guarded([&] {
     need(ctx, "block_dot_i32");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    q8_invalidate(ctx);
     weight_row_bytes(w, "block_dot_i32");
     if (w->dtype != DT_Q4_K && w->dtype != DT_Q6_K && w->dtype != DT_Q8_0)
       fail(MDMA_ERR_NOT_IMPLEMENTED, "block_dot_i32: quantized dtypes only");
@@ -846,6 +893,7 @@ int mdma_gfx950_graph_launch(mdma_ctx *ctx, mdma_graph *graph) {
     need(ctx, "graph_launch");
     need(graph, "graph_launch");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    q8_invalidate(ctx);
     no_capture(ctx, "graph_launch");
     hip_check(hipGraphLaunch(graph->exec, ctx->stream), "hipGraphLaunch");
   });
@@ -863,6 +911,7 @@ int mdma_gfx950_reserve_scratch(mdma_ctx *ctx, uint64_t bytes) {
     need(ctx, "reserve_scratch");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
     scratch(ctx, bytes);
+    q8_buffer(ctx, bytes);
   });
 }
 

@@ -27,8 +27,19 @@
 namespace mdma {
 namespace {
 
-constexpr int WAVES = 4;  // waves per workgroup
-constexpr int R = 2;      // rows per wave
+// Launch shape (tuned on MI355X; overridable at build time for sweeps).
+#ifndef MDMA_GEMV_R_F32
+#define MDMA_GEMV_R_F32 4
+#endif
+#ifndef MDMA_GEMV_R_I8
+#define MDMA_GEMV_R_I8 2
+#endif
+#ifndef MDMA_GEMV_NT
+#define MDMA_GEMV_NT 1
+#endif
+constexpr int WAVES = 4;                // waves per workgroup
+constexpr int R_F32 = MDMA_GEMV_R_F32;  // rows per wave, f32-activation kernels
+constexpr int R_I8 = MDMA_GEMV_R_I8;    // rows per wave, int8-activation kernels
 
 struct Job {
   const uint8_t *w;
@@ -47,7 +58,11 @@ __device__ __forceinline__ float h2f(uint32_t bits16) {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // Streaming 16-byte weight load (nontemporal: weights are read once per token).
 __device__ __forceinline__ uint4 ld16(const uint8_t *p) {
+#if MDMA_GEMV_NT
   const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+#else
+  const u32x4 v = *reinterpret_cast<const u32x4 *>(p);
+#endif
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 __device__ __forceinline__ uint32_t ldu16(const uint8_t *p) {
@@ -66,15 +81,27 @@ __device__ __forceinline__ double wave_sum(double v) {
   return v;
 }
 
-// Locate this wave's job and first row; false when the wave has no rows.
-__device__ __forceinline__ bool locate(const JobSet &js, int &jidx, uint32_t &row0) {
-  uint32_t gw = blockIdx.x * WAVES + (threadIdx.x >> 6);
-  jidx = 0;
-  while (jidx < js.n - 1 && gw >= js.j[jidx].waves) {
-    gw -= js.j[jidx].waves;
-    jidx++;
+// Locate this wave's job and first row (R rows per wave); false when the
+// wave has no rows. The wave index goes through readfirstlane so the job
+// choice and every job field stay in scalar registers: a per-lane index
+// into the kernel-argument struct would turn each use into a dependent
+// memory load in front of every weight load.
+template <int R>
+__device__ __forceinline__ bool locate(const JobSet &js, bool gated, Job &J, const uint8_t *&wu, uint32_t &row0) {
+  uint32_t gw = blockIdx.x * WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t w0 = js.j[0].waves, w1 = js.n > 1 ? js.j[1].waves : 0;
+  int ji = 0;
+  if (js.n > 1 && gw >= w0) {
+    gw -= w0;
+    ji = 1;
+    if (js.n > 2 && gw >= w1) {
+      gw -= w1;
+      ji = 2;
+    }
   }
-  if (gw >= js.j[jidx].waves) return false;
+  J = ji == 0 ? js.j[0] : (ji == 1 ? js.j[1] : js.j[2]);
+  if (gw >= J.waves) return false;
+  wu = gated ? js.j[1].w : J.w;
   row0 = gw * R;
   return true;
 }
@@ -175,83 +202,121 @@ __device__ __forceinline__ Q8Unit q8_load(const uint8_t *blk, int c) {
 }
 
 // ------------------------------------------------------- f32 mode kernel ----
+//
+// Exact products: a quant byte b (0..255) placed by one v_perm_b32 into
+// mantissa bits 40..47 of an f64 whose exponent is fixed gives the double
+// 2 + b/2048 with no conversion instruction. Its product with an activation
+// (converted once to f64 and reused by every row of the wave) is exact, and
+// the unit's 16- or 8-term chains accumulate in f64, so
+//     sum(q*x) = 2048*acc - (4096 + 2048*bias)*X,  X = sum(x)
+// where q = b - bias. Each weight costs one perm and one f64 FMA; the
+// result is the exact dot product up to f64 rounding, then one f32 rounding.
 
-// Sum of q*x over one unit, returning the f32 unit contribution for row data
-// already loaded. TT tokens; xs holds the unit's 32 activations per token.
+constexpr uint32_t F64_HI_TWO = 0x40000000u;  // high dword of 2.0
+
+// f64 value 2 + byte_k(w)/2048 (k compile-time).
+template <int K>
+__device__ __forceinline__ double byte_f64(uint32_t w) {
+  constexpr uint32_t sel = 0x070C000Cu | ((uint32_t)K << 8);
+  const uint32_t hi = __builtin_amdgcn_perm(F64_HI_TWO, w, sel);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32));
+}
+
+// acc += sum_k (2 + byte_k(w)/2048) * x[k] over the 4 bytes of w.
+__device__ __forceinline__ double fma4(uint32_t w, const double *x, double acc) {
+  acc = fma(byte_f64<0>(w), x[0], acc);
+  acc = fma(byte_f64<1>(w), x[1], acc);
+  acc = fma(byte_f64<2>(w), x[2], acc);
+  acc = fma(byte_f64<3>(w), x[3], acc);
+  return acc;
+}
+
 template <int DT>
-struct Unit;
+struct F32Fmt;
 
+// Q4_K unit c (0..7): 16 quant bytes; low nibbles are columns 64p+16h+[0,16)
+// of sub-block 2p, high nibbles the same columns +32 of sub-block 2p+1.
 template <>
-struct Unit<DT_Q4_K> {
-  static constexpr uint32_t BLOCK_BYTES = 144;
-  struct Data {
+struct F32Fmt<DT_Q4_K> {
+  static constexpr uint32_t ELEMS = 256, BYTES = 144, UNITS = 8, NX = 32, NG = 2;
+  struct W {
     uint4 hd, qs;
   };
-  __device__ static Data load(const uint8_t *blk, int c) { return Data{ld16(blk), ld16(blk + 16 + 16 * c)}; }
-  // Column indices (within the block) of the unit's 32 weights: two runs of 16.
-  __device__ static int col0(int c) { return ((c >> 1) << 6) + ((c & 1) << 4); }
-  __device__ static void cols(int c, int &a, int &b) {
-    a = col0(c);
-    b = a + 32;
-  }
-  // xa/xb: the 16 activations of each run; sums Xa/Xb precomputed.
-  __device__ static float dot(const Data &w, int c, const float *xa, const float *xb, float Xa, float Xb) {
-    const uint32_t qw[4] = {w.qs.x, w.qs.y, w.qs.z, w.qs.w};
-    float sa = 0.f, sb = 0.f;
+  __device__ static W load(const uint8_t *blk, int c) { return W{ld16(blk), ld16(blk + 16 + 16 * c)}; }
+  __device__ static W zero() { return W{make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)}; }
+  // x index i (0..31) -> column in the block; group of i.
+  __device__ static int col(int c, int i) { return ((c >> 1) << 6) + ((c & 1) << 4) + (i & 15) + ((i >> 4) << 5); }
+  __device__ static double dot(const W &w, int c, const double *xd, const double *X) {
+    const uint32_t q[4] = {w.qs.x, w.qs.y, w.qs.z, w.qs.w};
+    double aa = 0.0, ab = 0.0;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-      uint32_t lo = qw[k] & 0x0F0F0F0Fu, hi = (qw[k] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        sa = fmaf(ub(lo, j), xa[4 * k + j], sa);
-        sb = fmaf(ub(hi, j), xb[4 * k + j], sb);
-      }
+      aa = fma4(q[k] & 0x0F0F0F0Fu, xd + 4 * k, aa);
+      ab = fma4((q[k] >> 4) & 0x0F0F0F0Fu, xd + 16 + 4 * k, ab);
     }
     float sca, scb, ma, mb;
     q4k_scales(w.hd, c >> 1, sca, scb, ma, mb);
     const float d = h2f(w.hd.x), dmin = h2f(w.hd.x >> 16);
-    const float ca = fmaf(d * sca, sa, -(dmin * ma) * Xa);
-    const float cb = fmaf(d * scb, sb, -(dmin * mb) * Xb);
-    return ca + cb;
+    const double dsa = (double)(d * sca), dsb = (double)(d * scb);
+    const double dma = (double)(dmin * ma), dmb = (double)(dmin * mb);
+    // dsa*(2048*aa - 4096*Xa) - dma*Xa, likewise for b.
+    double r = fma(2048.0 * dsa, aa, -fma(4096.0, dsa, dma) * X[0]);
+    r += fma(2048.0 * dsb, ab, -fma(4096.0, dsb, dmb) * X[1]);
+    return r;
   }
 };
 
+// Q6_K unit c (0..7): half n = c>>2, columns 8g..8g+7 (g = c&3) of each of
+// the 4 quarters r (columns 128n + 32r + 8g + [0,8)); six-bit quants u, q = u - 32.
 template <>
-struct Unit<DT_Q6_K> {
-  static constexpr uint32_t BLOCK_BYTES = 210;
-  using Data = Q6Unit;
-  __device__ static Data load(const uint8_t *blk, int c) { return q6_load(blk, c); }
-  // Quarter r of unit c covers columns 128n + 32r + [8g, 8g+8).
-  __device__ static int col(int c, int r) { return 128 * (c >> 2) + 32 * r + 8 * (c & 3); }
-  __device__ static float dot(const Data &u, const float (*x)[8]) {
-    float acc = 0.f;
+struct F32Fmt<DT_Q6_K> {
+  static constexpr uint32_t ELEMS = 256, BYTES = 210, UNITS = 8, NX = 32, NG = 4;
+  using W = Q6Unit;
+  __device__ static W load(const uint8_t *blk, int c) { return q6_load(blk, c); }
+  __device__ static W zero() { return Q6Unit{{0, 0}, {0, 0}, {0, 0}, 0, 0}; }
+  __device__ static int col(int c, int i) { return 128 * (c >> 2) + 32 * (i >> 3) + 8 * (c & 3) + (i & 7); }
+  __device__ static double dot(const W &w, int c, const double *xd, const double *X) {
+    double r = 0.0;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      float s = 0.f;
-#pragma unroll
-      for (int k = 0; k < 2; k++) {
-        uint32_t q = q6_u(u, r, k);
-#pragma unroll
-        for (int j = 0; j < 4; j++) s = fmaf(ub(q, j) - 32.f, x[r][4 * k + j], s);
-      }
-      acc = fmaf(sb(u.sc, r), s, acc);
+    for (int q = 0; q < 4; q++) {
+      double a = fma4(q6_u(w, q, 0), xd + 8 * q, 0.0);
+      a = fma4(q6_u(w, q, 1), xd + 8 * q + 4, a);
+      const double s = (double)(int8_t)((w.sc >> (8 * q)) & 0xff);
+      r = fma(s, fma(2048.0, a, -4128.0 * X[q]), r);
     }
-    return h2f(u.d) * acc;
+    return (double)h2f(w.d) * r;
   }
 };
 
-template <int TT, bool GATED>
-__global__ __launch_bounds__(256) void gemv_q4k_f32(JobSet js, const float *__restrict__ x, uint32_t T,
-                                                    float *__restrict__ ygated) {
-  using U = Unit<DT_Q4_K>;
-  int ji;
+// Q8_0 unit c (0..1): quants 16c..16c+15 of a 34-byte block; bytes biased by
+// 128 so b = q + 128.
+template <>
+struct F32Fmt<DT_Q8_0> {
+  static constexpr uint32_t ELEMS = 32, BYTES = 34, UNITS = 2, NX = 16, NG = 1;
+  using W = Q8Unit;
+  __device__ static W load(const uint8_t *blk, int c) { return q8_load(blk, c); }
+  __device__ static W zero() { return Q8Unit{{0, 0, 0, 0}, 0}; }
+  __device__ static int col(int c, int i) { return 16 * c + i; }
+  __device__ static double dot(const W &w, int, const double *xd, const double *X) {
+    double a = 0.0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) a = fma4(w.q[k] ^ 0x80808080u, xd + 4 * k, a);
+    return (double)h2f(w.d) * fma(2048.0, a, -4224.0 * X[0]);
+  }
+};
+
+// One wave owns R rows (2R when gated: gate then up) of one job; lanes stride
+// over the row's units, x is read from global memory (L2-resident) per unit.
+template <class F, int R, int TT, bool GATED>
+__global__ __launch_bounds__(256) void gemv_f32(JobSet js, const float *__restrict__ x, uint32_t T,
+                                                float *__restrict__ ygated) {
+  Job J;
+  const uint8_t *wu;
   uint32_t row0;
-  if (!locate(js, ji, row0)) return;
-  const Job &J = js.j[ji];
-  const Job &JU = js.j[GATED ? 1 : ji];
+  if (!locate<R>(js, GATED, J, wu, row0)) return;
   const int lane = threadIdx.x & 63;
-  const uint32_t n_in = J.n_in, nb = n_in >> 8, units = nb * 8;
-  const size_t rb = (size_t)nb * U::BLOCK_BYTES;
+  const uint32_t n_in = J.n_in, nb = n_in / F::ELEMS, units = nb * F::UNITS;
+  const size_t rb = (size_t)nb * F::BYTES;
   constexpr int NR = GATED ? 2 * R : R;
   double acc[NR][TT];
 #pragma unroll
@@ -260,40 +325,35 @@ __global__ __launch_bounds__(256) void gemv_q4k_f32(JobSet js, const float *__re
     for (int t = 0; t < TT; t++) acc[r][t] = 0.0;
 
   for (uint32_t u = lane; u < units; u += 64) {
-    const uint32_t b = u >> 3;
-    const int c = u & 7;
-    U::Data wd[NR];
+    const uint32_t b = u / F::UNITS;
+    const int c = u % F::UNITS;
+    typename F::W wd[NR];
 #pragma unroll
     for (int r = 0; r < NR; r++) {
       const uint32_t row = row0 + (r % R);
-      const uint8_t *base = (r < R ? J.w : JU.w);
-      if (row < J.n_out)
-        wd[r] = U::load(base + row * rb + (size_t)b * U::BLOCK_BYTES, c);
-      else
-        wd[r] = U::Data{make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+      const uint8_t *base = (r < R ? J.w : wu);
+      wd[r] = row < J.n_out ? F::load(base + row * rb + (size_t)b * F::BYTES, c) : F::zero();
     }
-    int ca, cb;
-    U::cols(c, ca, cb);
 #pragma unroll
     for (int t = 0; t < TT; t++) {
       if (t >= (int)T) break;
-      const float *xt = x + (size_t)t * n_in + (size_t)b * 256;
-      float xa[16], xb[16];
+      const float *xt = x + (size_t)t * n_in + (size_t)b * F::ELEMS;
+      double xd[F::NX];
 #pragma unroll
-      for (int k = 0; k < 4; k++) {
-        float4 va = *reinterpret_cast<const float4 *>(xt + ca + 4 * k);
-        float4 vb = *reinterpret_cast<const float4 *>(xt + cb + 4 * k);
-        xa[4 * k] = va.x, xa[4 * k + 1] = va.y, xa[4 * k + 2] = va.z, xa[4 * k + 3] = va.w;
-        xb[4 * k] = vb.x, xb[4 * k + 1] = vb.y, xb[4 * k + 2] = vb.z, xb[4 * k + 3] = vb.w;
+      for (int i = 0; i < (int)F::NX; i += 4) {
+        const float4 v = *reinterpret_cast<const float4 *>(xt + F::col(c, i));
+        xd[i] = v.x, xd[i + 1] = v.y, xd[i + 2] = v.z, xd[i + 3] = v.w;
       }
-      float Xa = 0.f, Xb = 0.f;
+      double X[F::NG];
 #pragma unroll
-      for (int k = 0; k < 16; k++) {
-        Xa += xa[k];
-        Xb += xb[k];
+      for (int g = 0; g < (int)F::NG; g++) {
+        double s = 0.0;
+#pragma unroll
+        for (int i = 0; i < (int)(F::NX / F::NG); i++) s += xd[g * (F::NX / F::NG) + i];
+        X[g] = s;
       }
 #pragma unroll
-      for (int r = 0; r < NR; r++) acc[r][t] += (double)U::dot(wd[r], c, xa, xb, Xa, Xb);
+      for (int r = 0; r < NR; r++) acc[r][t] += F::dot(wd[r], c, xd, X);
     }
   }
 #pragma unroll
@@ -319,183 +379,31 @@ __global__ __launch_bounds__(256) void gemv_q4k_f32(JobSet js, const float *__re
   }
 }
 
-template <int TT, bool GATED>
-__global__ __launch_bounds__(256) void gemv_q6k_f32(JobSet js, const float *__restrict__ x, uint32_t T,
-                                                    float *__restrict__ ygated) {
-  using U = Unit<DT_Q6_K>;
-  int ji;
-  uint32_t row0;
-  if (!locate(js, ji, row0)) return;
-  const Job &J = js.j[ji];
-  const Job &JU = js.j[GATED ? 1 : ji];
-  const int lane = threadIdx.x & 63;
-  const uint32_t n_in = J.n_in, nb = n_in >> 8, units = nb * 8;
-  const size_t rb = (size_t)nb * U::BLOCK_BYTES;
-  constexpr int NR = GATED ? 2 * R : R;
-  double acc[NR][TT];
-#pragma unroll
-  for (int r = 0; r < NR; r++)
-#pragma unroll
-    for (int t = 0; t < TT; t++) acc[r][t] = 0.0;
-
-  for (uint32_t u = lane; u < units; u += 64) {
-    const uint32_t b = u >> 3;
-    const int c = u & 7;
-    U::Data wd[NR];
-#pragma unroll
-    for (int r = 0; r < NR; r++) {
-      const uint32_t row = row0 + (r % R);
-      const uint8_t *base = (r < R ? J.w : JU.w);
-      if (row < J.n_out)
-        wd[r] = U::load(base + row * rb + (size_t)b * U::BLOCK_BYTES, c);
-      else
-        wd[r] = Q6Unit{{0, 0}, {0, 0}, {0, 0}, 0, 0};
-    }
-#pragma unroll
-    for (int t = 0; t < TT; t++) {
-      if (t >= (int)T) break;
-      const float *xt = x + (size_t)t * n_in + (size_t)b * 256;
-      float xs[4][8];
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const float *p = xt + U::col(c, q);
-        float4 v0 = *reinterpret_cast<const float4 *>(p), v1 = *reinterpret_cast<const float4 *>(p + 4);
-        xs[q][0] = v0.x, xs[q][1] = v0.y, xs[q][2] = v0.z, xs[q][3] = v0.w;
-        xs[q][4] = v1.x, xs[q][5] = v1.y, xs[q][6] = v1.z, xs[q][7] = v1.w;
-      }
-#pragma unroll
-      for (int r = 0; r < NR; r++) acc[r][t] += (double)U::dot(wd[r], xs);
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < NR; r++)
-#pragma unroll
-    for (int t = 0; t < TT; t++) acc[r][t] = wave_sum(acc[r][t]);
-  if (lane == 0) {
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-      const uint32_t row = row0 + r;
-      if (row >= J.n_out) break;
-#pragma unroll
-      for (int t = 0; t < TT; t++) {
-        if (t >= (int)T) break;
-        if (GATED) {
-          const float g = (float)acc[r][t], up = (float)acc[R + r][t];
-          ygated[(size_t)t * J.n_out + row] = g / (1.0f + expf(-g)) * up;
-        } else {
-          J.y[(size_t)t * J.n_out + row] = (float)acc[r][t];
-        }
-      }
-    }
-  }
-}
-
-// Q8_0: unit = half block (16 weights); 2 units per 32 weights.
-template <int TT, bool GATED>
-__global__ __launch_bounds__(256) void gemv_q8_f32(JobSet js, const float *__restrict__ x, uint32_t T,
-                                                   float *__restrict__ ygated) {
-  int ji;
-  uint32_t row0;
-  if (!locate(js, ji, row0)) return;
-  const Job &J = js.j[ji];
-  const Job &JU = js.j[GATED ? 1 : ji];
-  const int lane = threadIdx.x & 63;
-  const uint32_t n_in = J.n_in, nb = n_in >> 5, units = nb * 2;
-  const size_t rb = (size_t)nb * 34;
-  constexpr int NR = GATED ? 2 * R : R;
-  double acc[NR][TT];
-#pragma unroll
-  for (int r = 0; r < NR; r++)
-#pragma unroll
-    for (int t = 0; t < TT; t++) acc[r][t] = 0.0;
-  for (uint32_t u = lane; u < units; u += 64) {
-    const uint32_t b = u >> 1;
-    const int c = u & 1;
-    Q8Unit wd[NR];
-#pragma unroll
-    for (int r = 0; r < NR; r++) {
-      const uint32_t row = row0 + (r % R);
-      const uint8_t *base = (r < R ? J.w : JU.w);
-      if (row < J.n_out)
-        wd[r] = q8_load(base + row * rb + (size_t)b * 34, c);
-      else
-        wd[r] = Q8Unit{{0, 0, 0, 0}, 0};
-    }
-#pragma unroll
-    for (int t = 0; t < TT; t++) {
-      if (t >= (int)T) break;
-      const float *xt = x + (size_t)t * n_in + (size_t)b * 32 + 16 * c;
-      float xs[16];
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        float4 v = *reinterpret_cast<const float4 *>(xt + 4 * k);
-        xs[4 * k] = v.x, xs[4 * k + 1] = v.y, xs[4 * k + 2] = v.z, xs[4 * k + 3] = v.w;
-      }
-#pragma unroll
-      for (int r = 0; r < NR; r++) {
-        float s = 0.f;
-#pragma unroll
-        for (int k = 0; k < 4; k++)
-#pragma unroll
-          for (int j = 0; j < 4; j++) s = fmaf(sb(wd[r].q[k], j), xs[4 * k + j], s);
-        acc[r][t] += (double)(h2f(wd[r].d) * s);
-      }
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < NR; r++)
-#pragma unroll
-    for (int t = 0; t < TT; t++) acc[r][t] = wave_sum(acc[r][t]);
-  if (lane == 0) {
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-      const uint32_t row = row0 + r;
-      if (row >= J.n_out) break;
-#pragma unroll
-      for (int t = 0; t < TT; t++) {
-        if (t >= (int)T) break;
-        if (GATED) {
-          const float g = (float)acc[r][t], up = (float)acc[R + r][t];
-          ygated[(size_t)t * J.n_out + row] = g / (1.0f + expf(-g)) * up;
-        } else {
-          J.y[(size_t)t * J.n_out + row] = (float)acc[r][t];
-        }
-      }
-    }
-  }
-}
-
-// F32 / F16 weights: plain strided dot (not a hot path; kept for the trait's
-// full dtype set). One wave per row, lanes stride over columns.
+// F32 / F16 weights: plain strided dot with exact f64 products (not a hot
+// path; kept for the trait's full dtype set). One wave per row.
 template <int DT, bool GATED>
 __global__ __launch_bounds__(256) void gemv_plain(JobSet js, const float *__restrict__ x, uint32_t T,
                                                   float *__restrict__ ygated) {
-  const uint32_t gw = blockIdx.x * WAVES + (threadIdx.x >> 6);
-  uint32_t w = gw;
-  int ji = 0;
-  while (ji < js.n - 1 && w >= js.j[ji].n_out) {
-    w -= js.j[ji].n_out;
-    ji++;
-  }
-  const Job &J = js.j[ji];
-  if (w >= J.n_out) return;
-  const Job &JU = js.j[GATED ? 1 : ji];
+  Job J;
+  const uint8_t *wu;
+  uint32_t row;
+  if (!locate<1>(js, GATED, J, wu, row)) return;
   const int lane = threadIdx.x & 63;
-  const uint32_t row = w, n_in = J.n_in;
+  const uint32_t n_in = J.n_in;
   for (uint32_t t = 0; t < T; t++) {
     double a = 0.0, b = 0.0;
     for (uint32_t i = lane; i < n_in; i += 64) {
       float wv, uv = 0.f;
       if (DT == DT_F32) {
         wv = reinterpret_cast<const float *>(J.w)[(size_t)row * n_in + i];
-        if (GATED) uv = reinterpret_cast<const float *>(JU.w)[(size_t)row * n_in + i];
+        if (GATED) uv = reinterpret_cast<const float *>(wu)[(size_t)row * n_in + i];
       } else {
         wv = h2f(reinterpret_cast<const uint16_t *>(J.w)[(size_t)row * n_in + i]);
-        if (GATED) uv = h2f(reinterpret_cast<const uint16_t *>(JU.w)[(size_t)row * n_in + i]);
+        if (GATED) uv = h2f(reinterpret_cast<const uint16_t *>(wu)[(size_t)row * n_in + i]);
       }
-      const float xv = x[(size_t)t * n_in + i];
-      a += (double)(wv * xv);
-      if (GATED) b += (double)(uv * xv);
+      const double xv = (double)x[(size_t)t * n_in + i];
+      a = fma((double)wv, xv, a);
+      if (GATED) b = fma((double)uv, xv, b);
     }
     a = wave_sum(a);
     if (GATED) b = wave_sum(b);
@@ -510,6 +418,7 @@ __global__ __launch_bounds__(256) void gemv_plain(JobSet js, const float *__rest
   }
 }
 
+
 // ------------------------------------------------------ int8 mode kernel ----
 // qx: int8 [T, n_in]; dx: f32 [T, n_in/256]; s16: i32 [T, n_in/16].
 
@@ -517,11 +426,11 @@ template <int TT, bool GATED>
 __global__ __launch_bounds__(256) void gemv_q4k_i8(JobSet js, const int8_t *__restrict__ qx,
                                                    const float *__restrict__ dx, const int32_t *__restrict__ s16,
                                                    uint32_t T, float *__restrict__ ygated) {
-  int ji;
+  Job J;
+  const uint8_t *wu;
   uint32_t row0;
-  if (!locate(js, ji, row0)) return;
-  const Job &J = js.j[ji];
-  const Job &JU = js.j[GATED ? 1 : ji];
+  constexpr int R = R_I8;
+  if (!locate<R>(js, GATED, J, wu, row0)) return;
   const int lane = threadIdx.x & 63;
   const uint32_t n_in = J.n_in, nb = n_in >> 8, units = nb * 8;
   const size_t rb = (size_t)nb * 144;
@@ -538,7 +447,7 @@ __global__ __launch_bounds__(256) void gemv_q4k_i8(JobSet js, const int8_t *__re
 #pragma unroll
     for (int r = 0; r < NR; r++) {
       const uint32_t row = row0 + (r % R);
-      const uint8_t *base = (r < R ? J.w : JU.w);
+      const uint8_t *base = (r < R ? J.w : wu);
       if (row < J.n_out) {
         const uint8_t *blk = base + row * rb + (size_t)b * 144;
         hd[r] = ld16(blk);
@@ -598,11 +507,11 @@ template <int TT, bool GATED>
 __global__ __launch_bounds__(256) void gemv_q6k_i8(JobSet js, const int8_t *__restrict__ qx,
                                                    const float *__restrict__ dx, const int32_t *__restrict__ s16,
                                                    uint32_t T, float *__restrict__ ygated) {
-  int ji;
+  Job J;
+  const uint8_t *wu;
   uint32_t row0;
-  if (!locate(js, ji, row0)) return;
-  const Job &J = js.j[ji];
-  const Job &JU = js.j[GATED ? 1 : ji];
+  constexpr int R = R_I8;
+  if (!locate<R>(js, GATED, J, wu, row0)) return;
   const int lane = threadIdx.x & 63;
   const uint32_t n_in = J.n_in, nb = n_in >> 8, units = nb * 8;
   const size_t rb = (size_t)nb * 210;
@@ -619,7 +528,7 @@ __global__ __launch_bounds__(256) void gemv_q6k_i8(JobSet js, const int8_t *__re
 #pragma unroll
     for (int r = 0; r < NR; r++) {
       const uint32_t row = row0 + (r % R);
-      const uint8_t *base = (r < R ? J.w : JU.w);
+      const uint8_t *base = (r < R ? J.w : wu);
       if (row < J.n_out)
         wd[r] = q6_load(base + row * rb + (size_t)b * 210, c);
       else
@@ -674,11 +583,11 @@ template <int TT, bool GATED>
 __global__ __launch_bounds__(256) void gemv_q8_i8(JobSet js, const int8_t *__restrict__ qx,
                                                   const float *__restrict__ dx, const int32_t *__restrict__ s16,
                                                   uint32_t T, float *__restrict__ ygated) {
-  int ji;
+  Job J;
+  const uint8_t *wu;
   uint32_t row0;
-  if (!locate(js, ji, row0)) return;
-  const Job &J = js.j[ji];
-  const Job &JU = js.j[GATED ? 1 : ji];
+  constexpr int R = R_I8;
+  if (!locate<R>(js, GATED, J, wu, row0)) return;
   const int lane = threadIdx.x & 63;
   const uint32_t n_in = J.n_in, nb = n_in >> 5, units = nb * 2;
   const size_t rb = (size_t)nb * 34;
@@ -695,7 +604,7 @@ __global__ __launch_bounds__(256) void gemv_q8_i8(JobSet js, const int8_t *__res
 #pragma unroll
     for (int r = 0; r < NR; r++) {
       const uint32_t row = row0 + (r % R);
-      const uint8_t *base = (r < R ? J.w : JU.w);
+      const uint8_t *base = (r < R ? J.w : wu);
       if (row < J.n_out)
         wd[r] = q8_load(base + row * rb + (size_t)b * 34, c);
       else
@@ -836,12 +745,12 @@ __global__ __launch_bounds__(256) void block_dot_kernel(int32_t dtype, const uin
 
 // ------------------------------------------------------------ launchers ----
 
-uint32_t waves_for(int32_t dtype, uint64_t n_out) {
+uint32_t waves_for(int32_t dtype, uint64_t n_out, int rows_per_wave) {
   if (dtype == DT_F32 || dtype == DT_F16) return (uint32_t)n_out;
-  return (uint32_t)((n_out + R - 1) / R);
+  return (uint32_t)((n_out + rows_per_wave - 1) / rows_per_wave);
 }
 
-JobSet make_set(const GemvJob *jobs, int n) {
+JobSet make_set(const GemvJob *jobs, int n, int rows_per_wave) {
   JobSet js{};
   js.n = n;
   for (int i = 0; i < n; i++) {
@@ -849,7 +758,7 @@ JobSet make_set(const GemvJob *jobs, int n) {
     js.j[i].y = jobs[i].y;
     js.j[i].n_out = (uint32_t)jobs[i].n_out;
     js.j[i].n_in = (uint32_t)jobs[i].n_in;
-    js.j[i].waves = waves_for(jobs[i].dtype, jobs[i].n_out);
+    js.j[i].waves = waves_for(jobs[i].dtype, jobs[i].n_out, rows_per_wave);
   }
   return js;
 }
@@ -863,14 +772,14 @@ uint32_t grid_of(const JobSet &js) {
 template <bool GATED>
 void dispatch_f32(mdma_ctx *ctx, int32_t dt, const JobSet &js, const float *x, uint32_t T, float *yg) {
   const dim3 grid(grid_of(js)), block(64 * WAVES);
-#define MDMA_F32_CASE(TT)                                                                            \
-  switch (dt) {                                                                                      \
-    case DT_Q4_K: gemv_q4k_f32<TT, GATED><<<grid, block, 0, ctx->stream>>>(js, x, T, yg); break;     \
-    case DT_Q6_K: gemv_q6k_f32<TT, GATED><<<grid, block, 0, ctx->stream>>>(js, x, T, yg); break;     \
-    case DT_Q8_0: gemv_q8_f32<TT, GATED><<<grid, block, 0, ctx->stream>>>(js, x, T, yg); break;      \
-    case DT_F32: gemv_plain<DT_F32, GATED><<<grid, block, 0, ctx->stream>>>(js, x, T, yg); break;    \
-    case DT_F16: gemv_plain<DT_F16, GATED><<<grid, block, 0, ctx->stream>>>(js, x, T, yg); break;    \
-    default: fail(MDMA_ERR_NOT_IMPLEMENTED, "gemv: dtype");                                          \
+#define MDMA_F32_CASE(TT)                                                                                          \
+  switch (dt) {                                                                                                    \
+    case DT_Q4_K: gemv_f32<F32Fmt<DT_Q4_K>, R_F32, TT, GATED><<<grid, block, 0, ctx->stream>>>(js, x, T, yg); break; \
+    case DT_Q6_K: gemv_f32<F32Fmt<DT_Q6_K>, R_F32, TT, GATED><<<grid, block, 0, ctx->stream>>>(js, x, T, yg); break; \
+    case DT_Q8_0: gemv_f32<F32Fmt<DT_Q8_0>, R_F32, TT, GATED><<<grid, block, 0, ctx->stream>>>(js, x, T, yg); break; \
+    case DT_F32: gemv_plain<DT_F32, GATED><<<grid, block, 0, ctx->stream>>>(js, x, T, yg); break;                  \
+    case DT_F16: gemv_plain<DT_F16, GATED><<<grid, block, 0, ctx->stream>>>(js, x, T, yg); break;                  \
+    default: fail(MDMA_ERR_NOT_IMPLEMENTED, "gemv: dtype");                                                        \
   }
   if (T <= 1) { MDMA_F32_CASE(1) }
   else if (T <= 2) { MDMA_F32_CASE(2) }
@@ -920,15 +829,23 @@ GemvJob offset_job(const GemvJob &j, uint64_t t0) {
 bool is_i8_dtype(int32_t dt) { return dt == DT_Q4_K || dt == DT_Q6_K || dt == DT_Q8_0; }
 
 // Quantize x [T, n_in] into the context scratch; returns pointers.
+// The int8 activations of x [T, n_in] in the context's activation buffer,
+// quantized now unless that buffer already holds exactly this x (same
+// pointer and shape, no write since; see q8_invalidate).
 void quantize_into_scratch(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in, int8_t **qx, float **dx,
                            int32_t **s16) {
   const uint64_t n = T * n_in;
   const uint64_t qb = (n + 255) / 256 * 256, db = (n / 256 * 4 + 255) / 256 * 256;
-  char *s = scratch(ctx, qb + db + n / 16 * 4 + 256);
+  char *s = q8_buffer(ctx, qb + db + n / 16 * 4 + 256);
   *qx = reinterpret_cast<int8_t *>(s);
   *dx = reinterpret_cast<float *>(s + qb);
   *s16 = reinterpret_cast<int32_t *>(s + qb + db);
+  if (ctx->q8_valid && ctx->q8_x == x && ctx->q8_n == n && ctx->q8_n_in == n_in) return;
   launch_quantize_act(ctx, x, n, 256, *qx, *dx, *s16);
+  ctx->q8_valid = true;
+  ctx->q8_x = x;
+  ctx->q8_n = n;
+  ctx->q8_n_in = n_in;
 }
 
 }  // namespace
@@ -941,7 +858,7 @@ void launch_gemv_f32(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float
   by_chunks(T, [&](uint64_t t0, uint64_t tn) {
     GemvJob js[3];
     for (int i = 0; i < n_jobs; i++) js[i] = offset_job(jobs[i], t0);
-    dispatch_f32<false>(ctx, jobs[0].dtype, make_set(js, n_jobs), x + t0 * jobs[0].n_in, (uint32_t)tn, nullptr);
+    dispatch_f32<false>(ctx, jobs[0].dtype, make_set(js, n_jobs, R_F32), x + t0 * jobs[0].n_in, (uint32_t)tn, nullptr);
   });
 }
 
@@ -955,7 +872,7 @@ void launch_gemv_f32_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up
   }
   by_chunks(T, [&](uint64_t t0, uint64_t tn) {
     GemvJob js[2] = {offset_job(gate, t0), offset_job(up, t0)};
-    JobSet set = make_set(js, 2);
+    JobSet set = make_set(js, 2, R_F32);
     set.n = 1;  // waves cover the gate rows; each also reads up
     dispatch_f32<true>(ctx, gate.dtype, set, x + t0 * gate.n_in, (uint32_t)tn, y + t0 * gate.n_out);
   });
@@ -981,7 +898,7 @@ void launch_gemv_i8(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float 
   by_chunks(T, [&](uint64_t t0, uint64_t tn) {
     GemvJob js[3];
     for (int i = 0; i < n_jobs; i++) js[i] = offset_job(jobs[i], t0);
-    dispatch_i8<false>(ctx, jobs[0].dtype, make_set(js, n_jobs), qx + t0 * n_in, dx + t0 * (n_in / 256),
+    dispatch_i8<false>(ctx, jobs[0].dtype, make_set(js, n_jobs, R_I8), qx + t0 * n_in, dx + t0 * (n_in / 256),
                        s16 + t0 * (n_in / 16), (uint32_t)tn, nullptr);
   });
 }
@@ -1002,7 +919,7 @@ void launch_gemv_i8_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up,
   quantize_into_scratch(ctx, x, T, n_in, &qx, &dx, &s16);
   by_chunks(T, [&](uint64_t t0, uint64_t tn) {
     GemvJob js[2] = {offset_job(gate, t0), offset_job(up, t0)};
-    JobSet set = make_set(js, 2);
+    JobSet set = make_set(js, 2, R_I8);
     set.n = 1;
     dispatch_i8<true>(ctx, gate.dtype, set, qx + t0 * n_in, dx + t0 * (n_in / 256), s16 + t0 * (n_in / 16),
                       (uint32_t)tn, y + t0 * gate.n_out);

@@ -72,6 +72,12 @@ struct mdma_ctx {
   // Scratch owned by the context (int8 activations, partial sums, RoPE tables).
   char *scratch = nullptr;
   uint64_t scratch_cap = 0;
+  // int8 activations of the last quantized x (int8 mode), reused while valid.
+  char *q8 = nullptr;
+  uint64_t q8_cap = 0;
+  bool q8_valid = false;
+  const float *q8_x = nullptr;
+  uint64_t q8_n = 0, q8_n_in = 0;
   // Device RoPE cos/sin table: [positions][head_dim/2] for one (head_dim, theta).
   float *rope_tab = nullptr;
   uint64_t rope_positions = 0, rope_hd = 0;
@@ -91,6 +97,12 @@ namespace mdma {
 // Scratch space of at least `bytes` on the context's device; growing it
 // synchronizes the stream (callers hold the context lock).
 char *scratch(mdma_ctx *ctx, uint64_t bytes);
+// The int8-activation buffer (grown like scratch; growth drops the cached x).
+char *q8_buffer(mdma_ctx *ctx, uint64_t bytes);
+// Forget the cached int8 activations: every entry point that writes device
+// memory calls this (a qmatmul only when its output overlaps the cached x).
+inline void q8_invalidate(mdma_ctx *ctx) { ctx->q8_valid = false; }
+void q8_invalidate_range(mdma_ctx *ctx, const void *p, uint64_t bytes);
 // Device pointer to a cos/sin table covering positions [0, max_pos] for (hd, theta).
 const float *rope_table(mdma_ctx *ctx, uint64_t max_pos, uint64_t hd, float theta);
 
@@ -124,12 +136,21 @@ void launch_rope(mdma_ctx *ctx, float *x, uint64_t n_tokens, uint64_t heads, uin
                  const float *tab, uint32_t pos);
 void launch_kv_write(mdma_ctx *ctx, const float *k, const float *v, uint16_t *dk, uint16_t *dv,
                      uint64_t n);
+// kv_stride: elements between consecutive tokens' cache rows (0 = kv_heads*hd,
+// contiguous); pos_step: position increment per token (1 in a sequence, 0
+// across the sequences of a decode batch).
 void launch_rope_kv_write(mdma_ctx *ctx, float *q, uint64_t q_heads, const float *k,
                           const float *v, uint64_t kv_heads, uint64_t hd, uint64_t n_tokens,
-                          const float *tab, uint32_t pos, uint16_t *dk, uint16_t *dv);
+                          const float *tab, uint32_t pos, uint16_t *dk, uint16_t *dv,
+                          uint64_t kv_stride = 0, uint32_t pos_step = 1);
+// seq_stride 0: causal over one sequence. Otherwise query i is sequence i's
+// single decode query over its own cache at k + i*seq_stride, kv_len keys.
 void launch_attn(mdma_ctx *ctx, const float *q, const uint16_t *k, const uint16_t *v, float *o,
                  uint64_t n_q, uint64_t kv_len, uint64_t hd, uint64_t n_q_heads,
-                 uint64_t n_kv_heads);
+                 uint64_t n_kv_heads, uint64_t seq_stride = 0);
 void launch_argmax(mdma_ctx *ctx, const float *x, uint64_t n, uint32_t *out_dev);
+// Greedy argmax of each row of x [rows, n] into idx[row]; flag[row] = any non-finite.
+void launch_argmax_rows(mdma_ctx *ctx, const float *x, uint64_t rows, uint64_t n, uint32_t *idx,
+                        uint32_t *flag);
 
 }  // namespace mdma

@@ -151,33 +151,38 @@ __global__ void kv_write_kernel(const float *__restrict__ k, const float *__rest
 }
 
 // Fused rope_kv_write (backend.rs:452-467): q rotated in place; k rotated and
-// stored with v as f16 rows.
+// stored with v as f16 rows. Token t sits at position pos + t*pos_step and
+// its cache row starts kv_stride elements after token t-1's (kv_stride =
+// the row width for one sequence; a cache-to-cache stride when each token
+// is a different sequence of a batch, with pos_step 0).
 __global__ void rope_kv_kernel(float *__restrict__ q, uint64_t q_pairs, uint32_t q_heads, const float *__restrict__ k,
                                const float *__restrict__ v, uint64_t k_pairs, uint32_t kv_heads, uint32_t hd,
-                               const float *__restrict__ tab, uint32_t pos, uint16_t *__restrict__ dk,
-                               uint16_t *__restrict__ dv) {
+                               const float *__restrict__ tab, uint32_t pos, uint32_t pos_step, uint64_t kv_stride,
+                               uint16_t *__restrict__ dk, uint16_t *__restrict__ dv) {
   const uint32_t half = hd / 2;
   for (uint64_t p = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; p < q_pairs + k_pairs;
        p += (uint64_t)gridDim.x * blockDim.x) {
     if (p < q_pairs) {
       const uint64_t t = p / ((uint64_t)q_heads * half);
       const uint32_t i = p % half;
-      const float2 cs = reinterpret_cast<const float2 *>(tab)[(pos + t) * half + i];
+      const float2 cs = reinterpret_cast<const float2 *>(tab)[(pos + t * pos_step) * half + i];
       float x0 = q[2 * p], x1 = q[2 * p + 1];
       rot(x0, x1, cs.x, cs.y);
       q[2 * p] = x0;
       q[2 * p + 1] = x1;
     } else {
       const uint64_t kp = p - q_pairs;
-      const uint64_t t = kp / ((uint64_t)kv_heads * half);
+      const uint64_t per_tok = (uint64_t)kv_heads * half;
+      const uint64_t t = kp / per_tok;
       const uint32_t i = kp % half;
-      const float2 cs = reinterpret_cast<const float2 *>(tab)[(pos + t) * half + i];
+      const float2 cs = reinterpret_cast<const float2 *>(tab)[(pos + t * pos_step) * half + i];
       float x0 = k[2 * kp], x1 = k[2 * kp + 1];
       rot(x0, x1, cs.x, cs.y);
-      dk[2 * kp] = f2h(x0);
-      dk[2 * kp + 1] = f2h(x1);
-      dv[2 * kp] = f2h(v[2 * kp]);
-      dv[2 * kp + 1] = f2h(v[2 * kp + 1]);
+      const uint64_t dst = t * kv_stride + 2 * (kp - t * per_tok);
+      dk[dst] = f2h(x0);
+      dk[dst + 1] = f2h(x1);
+      dv[dst] = f2h(v[2 * kp]);
+      dv[dst + 1] = f2h(v[2 * kp + 1]);
     }
   }
 }
@@ -203,17 +208,22 @@ __device__ float block_sumf(float v, float *sh) {
 
 // Causal GQA attention (cpu.rs:530-590) over an f16 cache: one workgroup per
 // (query token, q head). Keys are processed in chunks with an online softmax
-// (exact single pass when the visible keys fit one chunk).
+// (exact single pass when the visible keys fit one chunk). With seq_stride
+// 0, query i sees keys [0, prefix + i]; otherwise query i is the single
+// decode query of sequence i, whose cache starts seq_stride elements after
+// sequence i-1's, and sees keys [0, prefix].
 __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q, const uint16_t *__restrict__ K,
                                                    const uint16_t *__restrict__ V, float *__restrict__ o,
                                                    uint32_t prefix, uint32_t hd, uint32_t n_q_heads,
-                                                   uint32_t n_kv_heads, float scale) {
+                                                   uint32_t n_kv_heads, float scale, uint64_t seq_stride) {
   __shared__ float qs[256];
   __shared__ float sc[ATT_CHUNK];
   __shared__ float red[4];
   const uint32_t qh = blockIdx.x, i = blockIdx.y;
   const uint32_t kvh = qh / (n_q_heads / n_kv_heads), kv_row = n_kv_heads * hd;
-  const uint32_t visible = prefix + i + 1;
+  const uint32_t visible = seq_stride ? prefix + 1 : prefix + i + 1;
+  K += (size_t)i * seq_stride;
+  V += (size_t)i * seq_stride;
   const float *qv = q + ((size_t)i * n_q_heads + qh) * hd;
   for (uint32_t d = threadIdx.x; d < hd; d += 256) qs[d] = qv[d];
   __syncthreads();
@@ -258,6 +268,61 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q, 
 __device__ __forceinline__ int32_t total_key(float f) {
   const int32_t b = __builtin_bit_cast(int32_t, f);
   return b ^ (int32_t)(((uint32_t)(b >> 31)) >> 1);
+}
+
+// One workgroup per row of x [rows, n]; the index goes to idx[row], the
+// non-finite flag to flag[row].
+__global__ __launch_bounds__(1024) void argmax_rows_kernel(const float *__restrict__ x, uint64_t n,
+                                                           uint32_t *__restrict__ idx, uint32_t *__restrict__ flag) {
+  __shared__ int32_t sk[16];
+  __shared__ uint32_t si[16];
+  __shared__ uint32_t sbad[16];
+  x += (size_t)blockIdx.x * n;
+  int32_t bk = INT32_MIN;
+  uint32_t bi = 0, bad = 0;
+  bool have = false;
+  for (uint64_t i = threadIdx.x; i < n; i += 1024) {
+    const float v = x[i];
+    bad |= !isfinite(v);
+    const int32_t k = total_key(v);
+    if (!have || k >= bk) {
+      bk = k;
+      bi = (uint32_t)i;
+      have = true;
+    }
+  }
+  for (int o = 32; o >= 1; o >>= 1) {
+    const int32_t ok = __shfl_xor(bk, o, 64);
+    const uint32_t oi = __shfl_xor(bi, o, 64);
+    const int oh = __shfl_xor((int)have, o, 64);
+    if (oh && (!have || ok > bk || (ok == bk && oi > bi))) {
+      bk = ok;
+      bi = oi;
+      have = true;
+    }
+    bad |= __shfl_xor(bad, o, 64);
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    sk[w] = have ? bk : INT32_MIN;
+    si[w] = have ? bi : 0;
+    sbad[w] = bad;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int32_t k = sk[0];
+    uint32_t best = si[0], fl = sbad[0];
+    for (int j = 1; j < 16; j++) {
+      fl |= sbad[j];
+      if ((uint64_t)j * 64 >= n) continue;
+      if (sk[j] > k || (sk[j] == k && si[j] > best)) {
+        k = sk[j];
+        best = si[j];
+      }
+    }
+    idx[blockIdx.x] = best;
+    flag[blockIdx.x] = fl;
+  }
 }
 
 __global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ x, uint64_t n, uint32_t *out) {
@@ -361,26 +426,32 @@ void launch_kv_write(mdma_ctx *ctx, const float *k, const float *v, uint16_t *dk
 
 void launch_rope_kv_write(mdma_ctx *ctx, float *q, uint64_t q_heads, const float *k, const float *v,
                           uint64_t kv_heads, uint64_t hd, uint64_t n_tokens, const float *tab, uint32_t pos,
-                          uint16_t *dk, uint16_t *dv) {
+                          uint16_t *dk, uint16_t *dv, uint64_t kv_stride, uint32_t pos_step) {
   const uint64_t qp = n_tokens * q_heads * (hd / 2), kp = n_tokens * kv_heads * (hd / 2);
   if (!qp && !kp) return;
-  rope_kv_kernel<<<dim3(grid1d(qp + kp)), dim3(256), 0, ctx->stream>>>(q, qp, (uint32_t)q_heads, k, v, kp,
-                                                                       (uint32_t)kv_heads, (uint32_t)hd, tab, pos,
-                                                                       dk, dv);
+  if (!kv_stride) kv_stride = kv_heads * hd;
+  rope_kv_kernel<<<dim3(grid1d(qp + kp)), dim3(256), 0, ctx->stream>>>(
+      q, qp, (uint32_t)q_heads, k, v, kp, (uint32_t)kv_heads, (uint32_t)hd, tab, pos, pos_step, kv_stride, dk, dv);
   hip_check(hipGetLastError(), "rope_kv_write launch");
 }
 
 void launch_attn(mdma_ctx *ctx, const float *q, const uint16_t *k, const uint16_t *v, float *o, uint64_t n_q,
-                 uint64_t kv_len, uint64_t hd, uint64_t n_q_heads, uint64_t n_kv_heads) {
+                 uint64_t kv_len, uint64_t hd, uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride) {
   const float scale = 1.0f / sqrtf((float)hd);
+  const uint32_t prefix = (uint32_t)(seq_stride ? kv_len - 1 : kv_len - n_q);
   attn_kernel<<<dim3((uint32_t)n_q_heads, (uint32_t)n_q), dim3(256), 0, ctx->stream>>>(
-      q, k, v, o, (uint32_t)(kv_len - n_q), (uint32_t)hd, (uint32_t)n_q_heads, (uint32_t)n_kv_heads, scale);
+      q, k, v, o, prefix, (uint32_t)hd, (uint32_t)n_q_heads, (uint32_t)n_kv_heads, scale, seq_stride);
   hip_check(hipGetLastError(), "attn launch");
 }
 
 void launch_argmax(mdma_ctx *ctx, const float *x, uint64_t n, uint32_t *out_dev) {
   argmax_kernel<<<dim3(1), dim3(1024), 0, ctx->stream>>>(x, n, out_dev);
   hip_check(hipGetLastError(), "argmax launch");
+}
+
+void launch_argmax_rows(mdma_ctx *ctx, const float *x, uint64_t rows, uint64_t n, uint32_t *idx, uint32_t *flag) {
+  argmax_rows_kernel<<<dim3((uint32_t)rows), dim3(1024), 0, ctx->stream>>>(x, n, idx, flag);
+  hip_check(hipGetLastError(), "argmax_rows launch");
 }
 
 }  // namespace mdma
