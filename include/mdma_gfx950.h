@@ -210,6 +210,60 @@ void mdma_gfx950_graph_destroy(mdma_graph *graph);
 /* Pre-size the context scratch and int8-activation buffers so a later capture needs no growth. */
 int mdma_gfx950_reserve_scratch(mdma_ctx *ctx, uint64_t bytes);
 
+/* ---- Llama decoding: the hot path's caller ----
+ * Model / KvCache / Workspace / inference::generate (src/model.rs:41-468,
+ * src/kv_cache.rs:16-301, src/inference.rs:44-124). A session owns the f16 KV
+ * caches of `batch` sequences of up to `capacity` positions and a workspace
+ * of max(max_tokens, batch) token rows. */
+typedef struct mdma_model mdma_model;
+typedef struct mdma_session mdma_session;
+
+/* ModelConfig (src/model.rs:19-29) plus the vocabulary size. */
+typedef struct {
+    uint64_t n_layers, n_embd, n_ff, n_heads, n_kv_heads, head_dim, n_ctx, vocab;
+    float rope_theta, rms_eps;
+} mdma_model_config;
+
+/* Memory plan (src/model/memory.rs:16-63; headroom src/registry.rs:37):
+ * device bytes of the weights, of a KV cache for `batch` sequences of
+ * `capacity` positions and of a workspace, the headroom kept free, and the
+ * longest context the device still has room for at that batch. */
+typedef struct {
+    uint64_t weight_bytes, kv_bytes, workspace_bytes, headroom_bytes, total_bytes;
+    uint64_t device_bytes, available_bytes, max_context;
+} mdma_memory_plan;
+
+/* Model::load_with_budget (src/model.rs:141-149): preflight, reserve the
+ * weight bytes (budget_bytes = 0: unlimited; MDMA_ERR_MEMORY_BUDGET past it,
+ * MDMA_ERR_INSUFFICIENT_MEMORY past the device's free bytes less headroom),
+ * then upload every tensor of a llama GGUF file. */
+int mdma_gfx950_model_load(mdma_ctx *ctx, const char *gguf_path, uint64_t budget_bytes, mdma_model **out);
+void mdma_gfx950_model_free(mdma_model *m);
+int mdma_gfx950_model_config(const mdma_model *m, mdma_model_config *out);
+int mdma_gfx950_model_plan(const mdma_model *m, uint64_t capacity, uint64_t batch, uint64_t tokens,
+                           mdma_memory_plan *out);
+/* KvCache::new + Model::alloc_workspace, reserved like the weights. */
+int mdma_gfx950_session_new(mdma_model *m, uint64_t capacity, uint64_t batch, uint64_t max_tokens,
+                            mdma_session **out);
+void mdma_gfx950_session_free(mdma_session *s);
+/* KvCache::set_len(0) for every sequence. */
+int mdma_gfx950_session_reset(mdma_session *s);
+/* Model::prefill (src/model.rs:398-468) of sequence `seq`: n tokens at pos;
+ * the last row's logits (vocab f32) to host `logits` when non-null. */
+int mdma_gfx950_prefill(mdma_session *s, uint64_t seq, const uint32_t *tokens, uint64_t n, uint32_t pos,
+                        float *logits);
+/* Model::forward (src/model.rs:326-393): one decode step of sequence `seq`. */
+int mdma_gfx950_forward(mdma_session *s, uint64_t seq, uint32_t token, uint32_t pos, float *logits);
+/* Prefill + greedy decode of every sequence (inference::sample without EOS,
+ * src/inference.rs:102-124): prompts [batch][n_prompt], out_tokens
+ * [batch][n_gen]. With batch > 1 each decode step runs the batch's tokens
+ * through the weights together (one GEMV per matrix for all sequences).
+ * step_seconds[n_gen] (nullable): [0] = prefill of all sequences and the
+ * first token, [i] = decode step i. Non-finite logits fail with
+ * MDMA_ERR_BACKEND. */
+int mdma_gfx950_generate(mdma_session *s, const uint32_t *prompts, uint64_t n_prompt, uint64_t n_gen,
+                         uint32_t *out_tokens, double *step_seconds);
+
 #ifdef __cplusplus
 }
 #endif

@@ -166,6 +166,8 @@ namespace mdma {
 
 void fail(int code, const std::string &msg) { throw Error{code, msg}; }
 
+void set_last_error(const std::string &msg) { g_last_error = msg; }
+
 void hip_check(hipError_t e, const char *what) {
   if (e == hipSuccess) return;
   int code = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) ? MDMA_ERR_OUT_OF_MEMORY

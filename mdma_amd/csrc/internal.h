@@ -42,6 +42,8 @@ struct Error {
 [[noreturn]] void fail(int code, const std::string &msg);
 [[noreturn]] inline void shape_fail(const std::string &msg) { fail(MDMA_ERR_SHAPE_MISMATCH, msg); }
 void hip_check(hipError_t e, const char *what);
+// The thread-local message mdma_gfx950_last_error() returns.
+void set_last_error(const std::string &msg);
 
 struct Pool {
   uint64_t used = 0;

@@ -77,6 +77,29 @@ def write(path: str, metadata: dict, tensors: list) -> None:
             f.write(b"\0" * ((-b.nbytes) % ALIGN))
 
 
+def write_stream(path: str, metadata: dict, tensors: list) -> None:
+    """Like write(), with each payload given as a zero-argument function that is
+    called only when its bytes are written, so multi-GB models never sit in
+    memory whole. tensors: [(name, dtype, shape_rows_cols, make_payload)]."""
+    kv = b"".join(_str(k) + struct.pack("<I", _value(v)[0]) + _value(v)[1] for k, v in metadata.items())
+    infos, offset = [], 0
+    for name, dtype, shape, _ in tensors:
+        n = tensor_bytes(dtype, shape)
+        dims = list(reversed(shape))
+        infos.append(_str(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
+                     + struct.pack("<IQ", dtype, offset))
+        offset += (n + ALIGN - 1) // ALIGN * ALIGN
+    head = MAGIC + struct.pack("<IQQ", 3, len(tensors), len(metadata)) + kv + b"".join(infos)
+    with open(path, "wb") as f:
+        f.write(head + b"\0" * ((-len(head)) % ALIGN))
+        for name, dtype, shape, make in tensors:
+            b = np.ascontiguousarray(make()).view(np.uint8).reshape(-1)
+            if b.nbytes != tensor_bytes(dtype, shape):
+                raise ValueError(f"{name}: payload {b.nbytes} bytes, expected {tensor_bytes(dtype, shape)}")
+            f.write(b.tobytes())
+            f.write(b"\0" * ((-b.nbytes) % ALIGN))
+
+
 class Reader:
     def __init__(self, path: str):
         self.path = path

@@ -1,0 +1,116 @@
+"""End-to-end Llama decoding on the GPU against the CPU oracle.
+
+BASELINE config 1 (TinyStories-15M geometry, all linears Q8_0, random init,
+written as GGUF): 64-token greedy decode from a seeded 8-token prompt must give
+exactly the oracle's tokens in the f32-activation mode. The oracle stores K/V
+through f16 as the device cache does (the pattern of
+src/backend/test_support.rs:90-105). Batched multi-sequence decode must give
+each sequence's single-sequence tokens.
+"""
+import numpy as np
+import pytest
+
+from mdma_amd import gguf, llama_synth, synth
+from mdma_amd.backend import ACT_F32, ACT_I8, ContextLimit, MemoryBudget, ShapeMismatch
+from mdma_amd.model import Model
+from oracle import ffi
+
+pytestmark = pytest.mark.gpu
+N_PROMPT, N_GEN = 8, 64
+
+
+@pytest.fixture(scope="module")
+def tiny(tmp_path_factory):
+    paths = {}
+    for seed in (1, 2):
+        p = str(tmp_path_factory.mktemp("gguf") / f"tiny{seed}.gguf")
+        llama_synth.write(p, llama_synth.TINYSTORIES, llama_synth.Q8_ALL, seed)
+        paths[seed] = p
+    return paths
+
+
+def prompt(seed, vocab=32000):
+    return synth.tokens(N_PROMPT, vocab, 1000 + seed)
+
+
+@pytest.mark.parametrize("seed", [1, 2])
+def test_config1_greedy_tokens_match_oracle(backend, tiny, seed):
+    backend.set_act_mode(ACT_F32)
+    want, _ = ffi.llama_generate(gguf.Reader(tiny[seed]), prompt(seed), N_GEN, kv_f16=True)
+    m = Model(backend, tiny[seed])
+    s = m.session(N_PROMPT + N_GEN, 1, N_PROMPT)
+    got, secs = s.generate(prompt(seed)[None, :], N_GEN)
+    assert np.array_equal(got[0], want), (got[0].tolist(), want.tolist())
+    assert np.all(secs > 0)
+    s.close()
+    m.close()
+
+
+def test_prefill_and_forward_logits_match_oracle(backend, tiny):
+    backend.set_act_mode(ACT_F32)
+    r = gguf.Reader(tiny[1])
+    p = prompt(1)
+    m = Model(backend, tiny[1])
+    s = m.session(N_PROMPT + 4, 1, N_PROMPT)
+    logits = s.prefill(p, 0)
+    _, want = ffi.llama_generate(r, p, 1, kv_f16=True)
+    np.testing.assert_allclose(logits, want, rtol=1e-4, atol=1e-5)
+    tok = int(np.argmax(logits))
+    nxt = s.forward(tok, N_PROMPT)
+    _, want2 = ffi.llama_generate(r, p, 2, kv_f16=True)
+    # Both sides store K/V in f16; a value that differs by ~1e-7 relative can
+    # round to the neighbouring half (a 2^-11 relative step), so after the
+    # prefill the comparison is at the f16 cache's resolution.
+    np.testing.assert_allclose(nxt, want2, rtol=2e-3, atol=5e-4)
+    with pytest.raises(ShapeMismatch):
+        s.forward(40000, N_PROMPT + 1)  # token outside the vocabulary
+    s.close()
+    m.close()
+
+
+def test_batched_decode_equals_single_sequences(backend, tiny):
+    backend.set_act_mode(ACT_F32)
+    r = gguf.Reader(tiny[1])
+    prompts = np.stack([prompt(s) for s in (1, 5, 9)])
+    m = Model(backend, tiny[1])
+    s = m.session(N_PROMPT + 24, 3, N_PROMPT)
+    got, _ = s.generate(prompts, 24)
+    for b in range(3):
+        want, _ = ffi.llama_generate(r, prompts[b], 24, kv_f16=True)
+        assert np.array_equal(got[b], want), b
+    s.close()
+    m.close()
+
+
+def test_int8_mode_decodes(backend, tiny):
+    backend.set_act_mode(ACT_I8)
+    try:
+        m = Model(backend, tiny[1])
+        s = m.session(N_PROMPT + N_GEN, 1, N_PROMPT)
+        got, _ = s.generate(prompt(1)[None, :], N_GEN)
+        assert got.max() < 32000
+        want, _ = ffi.llama_generate(gguf.Reader(tiny[1]), prompt(1), N_GEN, kv_f16=True)
+        print(f"int8 mode: first {np.argmax(got[0] != want) if (got[0] != want).any() else N_GEN} tokens agree")
+        s.close()
+        m.close()
+    finally:
+        backend.set_act_mode(ACT_F32)
+
+
+def test_memory_plan_and_limits(backend, tiny):
+    m = Model(backend, tiny[1])
+    c = m.config
+    assert (c.n_layers, c.n_embd, c.n_heads, c.head_dim, c.n_ff, c.vocab, c.n_ctx) == (6, 288, 6, 48, 768, 32000, 256)
+    p = m.plan(256, 1, 8)
+    assert p.kv_bytes == 6 * 2 * 256 * 288 * 2
+    assert p.weight_bytes == sum(t.n_bytes for t in gguf.Reader(tiny[1]).tensors.values())
+    assert p.max_context == 256 and p.device_bytes > 250e9
+    with pytest.raises(ContextLimit):
+        m.session(257, 1, 8)
+    s = m.session(16, 1, 8)
+    with pytest.raises(ContextLimit):
+        s.generate(prompt(1)[None, :], 9)  # 8 + 9 > 16
+    s.close()
+    m.close()
+    with pytest.raises(MemoryBudget):
+        Model(backend, tiny[1], budget_bytes=1 << 20)
