@@ -142,6 +142,28 @@ def per_launch(be, ev, wl, mode, reps):
     return out
 
 
+def copy_probe(be, ev, nbytes=1 << 30, reps=10):
+    """Device-to-device copy rate (bytes read + bytes written per second) of
+    hipMemcpyAsync on the library's stream: the achievable-bandwidth
+    reference beside the 8 TB/s spec peak, and the plain copy of known size
+    that calibrates rocprof's FETCH_SIZE / WRITE_SIZE counters."""
+    from mdma_amd.backend import POOL_SCRATCH
+
+    a, b = be.alloc(nbytes, POOL_SCRATCH), be.alloc(nbytes, POOL_SCRATCH)
+    be.copy(a, 0, b, 0, nbytes)
+    be.join_execution()
+    e0, e1 = ev.event(), ev.event()
+    ev.record(e0, be.stream())
+    for _ in range(reps):
+        be.copy(a, 0, b, 0, nbytes)
+    ev.record(e1, be.stream())
+    ms = ev.elapsed_ms(e0, e1)
+    a.close()
+    b.close()
+    return {"bytes_per_copy": nbytes, "us_per_copy": round(ms * 1e3 / reps, 2),
+            "GBps_read_plus_write": round(2 * nbytes * reps / (ms * 1e-3) / 1e9, 1)}
+
+
 def cpu_baseline(raws, budget_s):
     from oracle import ffi
 
@@ -186,6 +208,7 @@ def main():
 
     be = Gfx950Backend(0)
     ev = HipEvents()
+    probe = copy_probe(be, ev)
     wl = Workload(be)
     be.reserve_scratch(64 << 20)
     results = {}
@@ -222,6 +245,7 @@ def main():
         "per_launch_i8": main_mode["per_launch"],
         "f32_mode": {"GBps": round(f["GBps"], 1), "ms_per_step": round(f["ms_per_step"], 5),
                      "pct_of_hbm_peak": round(100 * f["GBps"] / HBM_PEAK_GBS, 2), "per_launch": f["per_launch"]},
+        "copy_probe": probe,
         "device": be.device_label(),
     }
     print(json.dumps(line), flush=True)

@@ -258,7 +258,8 @@ int mdma_gfx950_create(int device, mdma_ctx **out) {
                                  prop.gcnArchName));
     auto *c = new mdma_ctx();
     c->device = device;
-    c->label = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+    c->label = std::string(prop.name[0] ? prop.name : "AMD Instinct (gfx950)") + " [" + prop.gcnArchName + ", " +
+               std::to_string(prop.multiProcessorCount) + " CUs]";
     c->total_bytes = prop.totalGlobalMem;
     c->cu_count = prop.multiProcessorCount;
     hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);

@@ -54,14 +54,18 @@ def test_prefill_and_forward_logits_match_oracle(backend, tiny):
     s = m.session(N_PROMPT + 4, 1, N_PROMPT)
     logits = s.prefill(p, 0)
     _, want = ffi.llama_generate(r, p, 1, kv_f16=True)
-    np.testing.assert_allclose(logits, want, rtol=1e-4, atol=1e-5)
+    # Both sides store K/V in f16 and the prompt's later tokens attend to the
+    # earlier ones through that cache: a K/V value that differs by ~1e-7
+    # relative can round to the neighbouring half (a 2^-11 relative step), so
+    # logits are compared at the f16 cache's resolution; the greedy choice
+    # must agree exactly.
+    np.testing.assert_allclose(logits, want, rtol=2e-3, atol=5e-4)
+    assert int(np.argmax(logits)) == int(np.argmax(want))
     tok = int(np.argmax(logits))
     nxt = s.forward(tok, N_PROMPT)
     _, want2 = ffi.llama_generate(r, p, 2, kv_f16=True)
-    # Both sides store K/V in f16; a value that differs by ~1e-7 relative can
-    # round to the neighbouring half (a 2^-11 relative step), so after the
-    # prefill the comparison is at the f16 cache's resolution.
     np.testing.assert_allclose(nxt, want2, rtol=2e-3, atol=5e-4)
+    assert int(np.argmax(nxt)) == int(np.argmax(want2))
     with pytest.raises(ShapeMismatch):
         s.forward(40000, N_PROMPT + 1)  # token outside the vocabulary
     s.close()
