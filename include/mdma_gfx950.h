@@ -50,7 +50,10 @@ typedef enum {
 typedef enum { MDMA_POOL_WEIGHTS = 0, MDMA_POOL_KV = 1, MDMA_POOL_SCRATCH = 2 } mdma_pool;
 
 /* WeightLayout (src/cache/layout.rs:10-38): raw GGUF blocks, or this
- * backend's lossless repack (same bytes per block; MDMA_LAYOUT_GFX950). */
+ * backend's prepared layout (MDMA_LAYOUT_GFX950): Q4_K / Q6_K / Q8_0 rows
+ * rearranged losslessly into 16-byte planes indexed by the 64-column unit
+ * (32 for Q8_0) a lane owns, so every wave load reads 1 KiB of contiguous
+ * memory. Each block keeps its byte count; rows are padded to 16 bytes. */
 typedef enum { MDMA_LAYOUT_GGUF = 0, MDMA_LAYOUT_GFX950 = 1 } mdma_layout;
 
 /* Activation mode of the decode GEMV: f32 activations (exact parity mode) or
@@ -130,10 +133,24 @@ int mdma_gfx950_upload(mdma_ctx *ctx, mdma_buf *dst, uint64_t offset, const void
 int mdma_gfx950_download(mdma_ctx *ctx, const mdma_buf *src, uint64_t offset, void *dst, uint64_t len);
 int mdma_gfx950_copy(mdma_ctx *ctx, const mdma_buf *src, uint64_t src_off, mdma_buf *dst,
                      uint64_t dst_off, uint64_t len);
-/* Backend::upload_weight (src/backend.rs:228-237). The dtype and shape are
- * passed so the gfx950 layout can be produced at upload. */
+/* Backend::upload_weight (src/backend.rs:228-237). `layout` names the format
+ * of `bytes`. GGUF Q4_K / Q6_K / Q8_0 bytes are packed into the prepared
+ * layout on the way (the buffer then holds prepared rows, as a buffer the
+ * reference's HIP backend uploads with its packed flag does,
+ * src/backend/rocm.rs:401-412); MDMA_LAYOUT_GFX950 bytes (from
+ * mdma_gfx950_pack_weight, e.g. a model cache) are stored as they are. The
+ * dtype and shape say what the bytes hold. */
 int mdma_gfx950_upload_weight(mdma_ctx *ctx, const void *bytes, uint64_t len, int layout,
                               int32_t dtype, uint64_t rows, uint64_t cols, mdma_buf **out);
+/* Host-side packing into / out of the prepared layout (pack_q4k of
+ * src/cache/layout.rs:40-79 is the reference's counterpart): bytes of a
+ * prepared [rows, cols] weight (0 if the dtype has no prepared layout), and
+ * the lossless conversions. Run on the CPU; no context needed. */
+uint64_t mdma_gfx950_prepared_bytes(int32_t dtype, uint64_t rows, uint64_t cols);
+int mdma_gfx950_pack_weight(int32_t dtype, uint64_t rows, uint64_t cols, const void *gguf, uint64_t len,
+                            void *out, uint64_t out_len);
+int mdma_gfx950_unpack_weight(int32_t dtype, uint64_t rows, uint64_t cols, const void *prepared, uint64_t len,
+                              void *out, uint64_t out_len);
 
 /* ---- the quantized-weight hot path ---- */
 

@@ -84,8 +84,11 @@ _SIGS = {
     "quantize_act": [_P, _P, _U64, _P, _P, _P], "block_dot_i32": [_P, _P, _P, _P],
     "graph_begin": [_P], "graph_end": [_P, _P], "graph_launch": [_P, _P], "graph_destroy": [_P],
     "reserve_scratch": [_P, _U64],
+    "prepared_bytes": [_I32, _U64, _U64],
+    "pack_weight": [_I32, _U64, _U64, _P, _U64, _P, _U64],
+    "unpack_weight": [_I32, _U64, _U64, _P, _U64, _P, _U64],
 }
-_RESTYPES = {"destroy": None, "graph_destroy": None, "last_error": C.c_char_p, "total_device_bytes": _U64, "max_head_dim": _U64,
+_RESTYPES = {"prepared_bytes": _U64, "destroy": None, "graph_destroy": None, "last_error": C.c_char_p, "total_device_bytes": _U64, "max_head_dim": _U64,
              "kv_elem_bytes": _U64, "stream": _P, "buf_len": _U64, "supports_weight_dtype": C.c_int}
 
 _lib = None
@@ -104,6 +107,29 @@ def lib():
             f.restype = _RESTYPES.get(name, C.c_int)
         _lib = L
     return _lib
+
+
+def prepared_bytes(dtype: int, rows: int, cols: int) -> int:
+    """Bytes of a [rows, cols] weight in the gfx950 prepared layout (0: none)."""
+    return int(lib().mdma_gfx950_prepared_bytes(dtype, rows, cols))
+
+
+def pack_weight(raw, dtype: int, shape) -> np.ndarray:
+    """GGUF blocks -> the gfx950 prepared layout (host side, lossless)."""
+    a = np.ascontiguousarray(np.frombuffer(bytes(raw) if not isinstance(raw, np.ndarray) else raw, np.uint8))
+    out = np.zeros(prepared_bytes(dtype, shape[0], shape[1]), np.uint8)
+    _check(lib().mdma_gfx950_pack_weight(dtype, shape[0], shape[1], a.ctypes.data, a.nbytes, out.ctypes.data,
+                                         out.nbytes))
+    return out
+
+
+def unpack_weight(prepared, dtype: int, shape) -> np.ndarray:
+    """The gfx950 prepared layout -> GGUF blocks (host side, lossless)."""
+    a = np.ascontiguousarray(np.frombuffer(prepared, np.uint8))
+    out = np.zeros(shape[0] * (shape[1] // BLOCK_SIZE[dtype]) * TYPE_SIZE[dtype], np.uint8)
+    _check(lib().mdma_gfx950_unpack_weight(dtype, shape[0], shape[1], a.ctypes.data, a.nbytes, out.ctypes.data,
+                                           out.nbytes))
+    return out
 
 
 def exported_symbols() -> list[str]:

@@ -75,7 +75,10 @@ uint64_t weight_row_bytes(const mdma_qweight *w, const char *op) {
   if (w->cols % bs)
     shape_fail(fmt("%s: width %llu is not a multiple of block size %llu", op,
                    (unsigned long long)w->cols, (unsigned long long)bs));
-  uint64_t rb = w->cols / bs * type_size(w->dtype);
+  const bool prepared = w->buf->layout == MDMA_LAYOUT_GFX950;
+  if (prepared && !gfx950_layout_dtype(w->dtype))
+    shape_fail(fmt("%s: buffer holds a prepared layout, weight dtype %d has none", op, w->dtype));
+  uint64_t rb = prepared ? gfx950_row_bytes(w->dtype, w->cols) : w->cols / bs * type_size(w->dtype);
   if (w->buf->len < rb * w->rows)
     shape_fail(fmt("%s: weight buffer %llu bytes, needs %llu", op, (unsigned long long)w->buf->len,
                    (unsigned long long)(rb * w->rows)));
@@ -103,7 +106,7 @@ uint64_t matmul_tokens(const mdma_qweight *w, const mdma_buf *x, const mdma_buf 
 
 GemvJob job_of(const mdma_qweight *w, mdma_buf *y) {
   return GemvJob{w->dtype, reinterpret_cast<const uint8_t *>(w->buf->ptr), w->rows, w->cols,
-                 reinterpret_cast<float *>(y->ptr)};
+                 reinterpret_cast<float *>(y->ptr), w->buf->layout};
 }
 
 void run_gemv(mdma_ctx *ctx, int mode, const GemvJob *jobs, int n, const float *x, uint64_t T) {
@@ -494,22 +497,40 @@ int mdma_gfx950_upload_weight(mdma_ctx *ctx, const void *bytes, uint64_t len, in
     need(ctx, "upload_weight");
     need(out, "upload_weight");
     *out = nullptr;
-    if (layout != MDMA_LAYOUT_GGUF)
-      fail(MDMA_ERR_NOT_IMPLEMENTED, "upload_weight: prepared weight layout for this backend");
+    if (layout != MDMA_LAYOUT_GGUF && layout != MDMA_LAYOUT_GFX950)
+      fail(MDMA_ERR_NOT_IMPLEMENTED, "upload_weight: unknown weight layout");
     uint64_t bs = block_size(dtype);
     if (!bs) fail(MDMA_ERR_NOT_IMPLEMENTED, fmt("upload_weight: dtype %d", dtype));
-    if (cols % bs || len != rows * (cols / bs) * type_size(dtype))
+    if (layout == MDMA_LAYOUT_GFX950 && !gfx950_layout_dtype(dtype))
+      fail(MDMA_ERR_NOT_IMPLEMENTED, fmt("upload_weight: dtype %d has no prepared layout", dtype));
+    const uint64_t raw = cols % bs ? 0 : rows * (cols / bs) * type_size(dtype);
+    const uint64_t want = layout == MDMA_LAYOUT_GFX950 ? rows * gfx950_row_bytes(dtype, cols) : raw;
+    if (cols % bs || len != want)
       shape_fail(fmt("upload_weight: %llu bytes do not hold a [%llu, %llu] weight", (unsigned long long)len,
                      (unsigned long long)rows, (unsigned long long)cols));
+    if (len) need(bytes, "upload_weight");
+    // GGUF Q4_K / Q6_K / Q8_0 rows are stored in the prepared layout, which
+    // every op on this backend reads; other dtypes keep their bytes.
+    const bool pack = layout == MDMA_LAYOUT_GGUF && gfx950_layout_dtype(dtype);
+    std::vector<uint8_t> packed;
+    const void *src = bytes;
+    uint64_t n = len;
+    if (pack) {
+      n = rows * gfx950_row_bytes(dtype, cols);
+      packed.resize(n);
+      pack_gfx950(dtype, rows, cols, static_cast<const uint8_t *>(bytes), packed.data());
+      src = packed.data();
+    }
     mdma_buf *b = nullptr;
-    int st = mdma_gfx950_alloc(ctx, len, MDMA_POOL_WEIGHTS, &b);
+    int st = mdma_gfx950_alloc(ctx, n, MDMA_POOL_WEIGHTS, &b);
     if (st) fail(st, g_last_error);
-    st = mdma_gfx950_upload(ctx, b, 0, bytes, len);
+    st = mdma_gfx950_upload(ctx, b, 0, src, n);
     if (st) {
       std::string m = g_last_error;
       mdma_gfx950_free(b);
       fail(st, m);
     }
+    b->layout = (pack || layout == MDMA_LAYOUT_GFX950) ? MDMA_LAYOUT_GFX950 : MDMA_LAYOUT_GGUF;
     *out = b;
   });
 }
@@ -617,7 +638,7 @@ int mdma_gfx950_embed(mdma_ctx *ctx, const mdma_qweight *table, const uint32_t *
     no_capture(ctx, "embed");
     uint32_t *dev_ids = reinterpret_cast<uint32_t *>(scratch(ctx, n_ids * 4));
     hip_check(hipMemcpyAsync(dev_ids, ids, n_ids * 4, hipMemcpyHostToDevice, ctx->stream), "embed ids");
-    launch_embed(ctx, table->dtype, reinterpret_cast<const uint8_t *>(table->buf->ptr), table->cols,
+    launch_embed(ctx, table->dtype, table->buf->layout, reinterpret_cast<const uint8_t *>(table->buf->ptr), table->cols,
                  dev_ids, n_ids, reinterpret_cast<float *>(out->ptr));
     // The ids live in scratch that a later call may overwrite.
     hip_check(hipStreamSynchronize(ctx->stream), "embed sync");
@@ -845,9 +866,43 @@ int mdma_gfx950_block_dot_i32(mdma_ctx *ctx, const mdma_qweight *w, const mdma_b
     if (!qx->len || qx->len % w->cols) shape_fail("block_dot_i32: qx is not whole rows");
     uint64_t T = qx->len / w->cols, sub = w->dtype == DT_Q6_K ? 16 : 32;
     if (out->len < T * w->rows * (w->cols / sub) * 4) shape_fail("block_dot_i32: out too small");
-    GemvJob j{w->dtype, reinterpret_cast<const uint8_t *>(w->buf->ptr), w->rows, w->cols, nullptr};
+    GemvJob j{w->dtype, reinterpret_cast<const uint8_t *>(w->buf->ptr), w->rows, w->cols, nullptr, w->buf->layout};
     launch_block_dot(ctx, j, reinterpret_cast<const int8_t *>(qx->ptr), T,
                      reinterpret_cast<int32_t *>(out->ptr));
+  });
+}
+
+uint64_t mdma_gfx950_prepared_bytes(int32_t dtype, uint64_t rows, uint64_t cols) {
+  if (!gfx950_layout_dtype(dtype)) return 0;
+  const uint64_t rb = gfx950_row_bytes(dtype, cols);
+  return rb && rows <= UINT64_MAX / rb ? rows * rb : 0;
+}
+
+int mdma_gfx950_pack_weight(int32_t dtype, uint64_t rows, uint64_t cols, const void *gguf, uint64_t len, void *out,
+                            uint64_t out_len) {
+  return guarded([&] {
+    if (!gfx950_layout_dtype(dtype)) fail(MDMA_ERR_NOT_IMPLEMENTED, fmt("pack_weight: dtype %d has no prepared layout", dtype));
+    const uint64_t bs = block_size(dtype);
+    if (!rows || !cols || cols % bs || len != rows * (cols / bs) * type_size(dtype))
+      shape_fail("pack_weight: bytes do not hold a [rows, cols] GGUF weight");
+    if (out_len != mdma_gfx950_prepared_bytes(dtype, rows, cols)) shape_fail("pack_weight: output size");
+    need(gguf, "pack_weight");
+    need(out, "pack_weight");
+    pack_gfx950(dtype, rows, cols, static_cast<const uint8_t *>(gguf), static_cast<uint8_t *>(out));
+  });
+}
+
+int mdma_gfx950_unpack_weight(int32_t dtype, uint64_t rows, uint64_t cols, const void *prepared, uint64_t len,
+                              void *out, uint64_t out_len) {
+  return guarded([&] {
+    if (!gfx950_layout_dtype(dtype)) fail(MDMA_ERR_NOT_IMPLEMENTED, fmt("unpack_weight: dtype %d has no prepared layout", dtype));
+    const uint64_t bs = block_size(dtype);
+    if (!rows || !cols || cols % bs || out_len != rows * (cols / bs) * type_size(dtype))
+      shape_fail("unpack_weight: output does not hold a [rows, cols] GGUF weight");
+    if (len != mdma_gfx950_prepared_bytes(dtype, rows, cols)) shape_fail("unpack_weight: input size");
+    need(prepared, "unpack_weight");
+    need(out, "unpack_weight");
+    unpack_gfx950(dtype, rows, cols, static_cast<const uint8_t *>(prepared), static_cast<uint8_t *>(out));
   });
 }
 

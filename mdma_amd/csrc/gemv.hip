@@ -22,7 +22,7 @@
 //  - Fused QKV: up to three jobs (same dtype) in one launch; waves are dealt
 //    out to jobs in order. Gated: the wave computes R rows of gate AND up,
 //    then writes silu(g) * u.
-#include "internal.h"
+#include "kernels.h"
 
 namespace mdma {
 namespace {
@@ -33,9 +33,6 @@ namespace {
 #endif
 #ifndef MDMA_GEMV_R_I8
 #define MDMA_GEMV_R_I8 2
-#endif
-#ifndef MDMA_GEMV_NT
-#define MDMA_GEMV_NT 1
 #endif
 constexpr int WAVES = 4;                // waves per workgroup
 constexpr int R_F32 = MDMA_GEMV_R_F32;  // rows per wave, f32-activation kernels
@@ -50,27 +47,6 @@ struct JobSet {
   Job j[3];
   int n;
 };
-
-__device__ __forceinline__ float h2f(uint32_t bits16) {
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits16 & 0xffff));
-}
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-// Streaming 16-byte weight load (nontemporal: weights are read once per token).
-__device__ __forceinline__ uint4 ld16(const uint8_t *p) {
-#if MDMA_GEMV_NT
-  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
-#else
-  const u32x4 v = *reinterpret_cast<const u32x4 *>(p);
-#endif
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
-__device__ __forceinline__ uint32_t ldu16(const uint8_t *p) {
-  return *reinterpret_cast<const uint16_t *>(p);
-}
-// A dword made of two 2-byte-aligned halves (Q6_K / Q8_0 blocks are only
-// 2-byte aligned inside a row).
-__device__ __forceinline__ uint32_t ld2x16(const uint8_t *p) { return ldu16(p) | (ldu16(p + 2) << 16); }
 
 __device__ __forceinline__ float ub(uint32_t v, int k) { return (float)((v >> (8 * k)) & 0xffu); }
 __device__ __forceinline__ float sb(uint32_t v, int k) { return (float)(int8_t)((v >> (8 * k)) & 0xffu); }
@@ -211,25 +187,6 @@ __device__ __forceinline__ Q8Unit q8_load(const uint8_t *blk, int c) {
 //     sum(q*x) = 2048*acc - (4096 + 2048*bias)*X,  X = sum(x)
 // where q = b - bias. Each weight costs one perm and one f64 FMA; the
 // result is the exact dot product up to f64 rounding, then one f32 rounding.
-
-constexpr uint32_t F64_HI_TWO = 0x40000000u;  // high dword of 2.0
-
-// f64 value 2 + byte_k(w)/2048 (k compile-time).
-template <int K>
-__device__ __forceinline__ double byte_f64(uint32_t w) {
-  constexpr uint32_t sel = 0x070C000Cu | ((uint32_t)K << 8);
-  const uint32_t hi = __builtin_amdgcn_perm(F64_HI_TWO, w, sel);
-  return __builtin_bit_cast(double, ((uint64_t)hi << 32));
-}
-
-// acc += sum_k (2 + byte_k(w)/2048) * x[k] over the 4 bytes of w.
-__device__ __forceinline__ double fma4(uint32_t w, const double *x, double acc) {
-  acc = fma(byte_f64<0>(w), x[0], acc);
-  acc = fma(byte_f64<1>(w), x[1], acc);
-  acc = fma(byte_f64<2>(w), x[2], acc);
-  acc = fma(byte_f64<3>(w), x[3], acc);
-  return acc;
-}
 
 template <int DT>
 struct F32Fmt;
@@ -828,7 +785,8 @@ GemvJob offset_job(const GemvJob &j, uint64_t t0) {
 
 bool is_i8_dtype(int32_t dt) { return dt == DT_Q4_K || dt == DT_Q6_K || dt == DT_Q8_0; }
 
-// Quantize x [T, n_in] into the context scratch; returns pointers.
+}  // namespace
+
 // The int8 activations of x [T, n_in] in the context's activation buffer,
 // quantized now unless that buffer already holds exactly this x (same
 // pointer and shape, no write since; see q8_invalidate).
@@ -848,10 +806,21 @@ void quantize_into_scratch(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n
   ctx->q8_n_in = n_in;
 }
 
-}  // namespace
+
+// Prepared-layout jobs go to the row-team kernels; a mix of layouts or
+// dtypes runs job by job; raw GGUF jobs use the kernels above.
+static bool any_prepared(const GemvJob *jobs, int n) {
+  for (int i = 0; i < n; i++)
+    if (jobs[i].layout == MDMA_LAYOUT_GFX950) return true;
+  return false;
+}
 
 void launch_gemv_f32(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t T) {
-  if (!same_dtype(jobs, n_jobs)) {
+  if (team_layout_ok(jobs, n_jobs)) {
+    launch_gemv_team(ctx, MDMA_ACT_F32, jobs, n_jobs, false, x, T, nullptr);
+    return;
+  }
+  if (!same_dtype(jobs, n_jobs) || any_prepared(jobs, n_jobs)) {
     for (int i = 0; i < n_jobs; i++) launch_gemv_f32(ctx, jobs + i, 1, x, T);
     return;
   }
@@ -864,7 +833,12 @@ void launch_gemv_f32(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float
 
 void launch_gemv_f32_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up, const float *x, uint64_t T,
                            float *y) {
-  if (gate.dtype != up.dtype) {
+  const GemvJob gu[2] = {gate, up};
+  if (team_layout_ok(gu, 2)) {
+    launch_gemv_team(ctx, MDMA_ACT_F32, gu, 2, true, x, T, y);
+    return;
+  }
+  if (gate.dtype != up.dtype || any_prepared(gu, 2)) {
     launch_gemv_f32(ctx, &gate, 1, x, T);
     launch_gemv_f32(ctx, &up, 1, x, T);
     launch_silu_mul(ctx, gate.y, up.y, y, T * gate.n_out);
@@ -886,7 +860,11 @@ void launch_gemv_i8(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float 
       launch_gemv_f32(ctx, jobs, n_jobs, x, T);
       return;
     }
-  if (!same_dtype(jobs, n_jobs)) {
+  if (team_layout_ok(jobs, n_jobs)) {
+    launch_gemv_team(ctx, MDMA_ACT_I8, jobs, n_jobs, false, x, T, nullptr);
+    return;
+  }
+  if (!same_dtype(jobs, n_jobs) || any_prepared(jobs, n_jobs)) {
     for (int i = 0; i < n_jobs; i++) launch_gemv_i8(ctx, jobs + i, 1, x, T);
     return;
   }
@@ -905,7 +883,12 @@ void launch_gemv_i8(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float 
 
 void launch_gemv_i8_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up, const float *x, uint64_t T,
                           float *y) {
-  if (gate.dtype != up.dtype || !is_i8_dtype(gate.dtype) || gate.n_in % 256) {
+  const GemvJob gu[2] = {gate, up};
+  if (team_layout_ok(gu, 2) && gate.n_in % 256 == 0) {
+    launch_gemv_team(ctx, MDMA_ACT_I8, gu, 2, true, x, T, y);
+    return;
+  }
+  if (gate.dtype != up.dtype || !is_i8_dtype(gate.dtype) || gate.n_in % 256 || any_prepared(gu, 2)) {
     GemvJob js[2] = {gate, up};
     launch_gemv_i8(ctx, js, 1, x, T);
     launch_gemv_i8(ctx, js + 1, 1, x, T);
@@ -935,6 +918,10 @@ void launch_quantize_act(mdma_ctx *ctx, const float *x, uint64_t n, uint64_t gro
 }
 
 void launch_block_dot(mdma_ctx *ctx, const GemvJob &w, const int8_t *qx, uint64_t T, int32_t *out) {
+  if (w.layout == MDMA_LAYOUT_GFX950) {
+    launch_block_dot_prepared(ctx, w, qx, T, out);
+    return;
+  }
   const uint64_t sub = w.dtype == DT_Q6_K ? 16 : 32, total = T * w.n_out * (w.n_in / sub);
   if (!total) return;
   block_dot_kernel<<<dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, ctx->stream>>>(

@@ -114,7 +114,15 @@ struct GemvJob {
   const uint8_t *w;
   uint64_t n_out, n_in;
   float *y;        // [T, n_out], row stride n_out
+  int layout = MDMA_LAYOUT_GGUF;  // MDMA_LAYOUT_GFX950: prepared rows (layout.cpp)
 };
+
+// ---- prepared weight layout (layout.cpp) ----
+// Bytes of one prepared row (0 if cols is not whole blocks).
+uint64_t gfx950_row_bytes(int32_t dtype, uint64_t cols);
+bool gfx950_layout_dtype(int32_t dtype);
+void pack_gfx950(int32_t dtype, uint64_t rows, uint64_t cols, const uint8_t *src, uint8_t *dst);
+void unpack_gfx950(int32_t dtype, uint64_t rows, uint64_t cols, const uint8_t *src, uint8_t *dst);
 // f32-activation GEMV for up to 3 independent weights sharing x (fused QKV).
 void launch_gemv_f32(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t T);
 // gate/up fused with SiLU: y = silu(gate x) * (up x); f32 activations.
@@ -124,11 +132,24 @@ void launch_gemv_f32_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up
 void launch_gemv_i8(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t T);
 void launch_gemv_i8_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up, const float *x,
                           uint64_t T, float *y);
+// Row-team GEMV over prepared layouts (gemv_team.hip): whether the jobs can
+// share one launch (all prepared, same dtype and n_in), and the launch in
+// mode MDMA_ACT_F32 or MDMA_ACT_I8 (I8 needs n_in % 256 == 0). Gated: jobs =
+// {gate, up}, output silu(gate x) * (up x) into ygated.
+bool team_layout_ok(const GemvJob *jobs, int n_jobs);
+void launch_gemv_team(mdma_ctx *ctx, int mode, const GemvJob *jobs, int n_jobs, bool gated, const float *x,
+                      uint64_t T, float *ygated);
+// The int8 activations of x [T, n_in] (per-256 f32 scales, per-16 sums) in
+// the context's activation buffer, quantized now unless it already holds
+// exactly this x.
+void quantize_into_scratch(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in, int8_t **qx, float **dx,
+                           int32_t **s16);
 void launch_quantize_act(mdma_ctx *ctx, const float *x, uint64_t n, uint64_t group, int8_t *q,
                          float *d, int32_t *sum16);
 void launch_block_dot(mdma_ctx *ctx, const GemvJob &w, const int8_t *qx, uint64_t T, int32_t *out);
+void launch_block_dot_prepared(mdma_ctx *ctx, const GemvJob &w, const int8_t *qx, uint64_t T, int32_t *out);
 
-void launch_embed(mdma_ctx *ctx, int32_t dtype, const uint8_t *table, uint64_t n_embd,
+void launch_embed(mdma_ctx *ctx, int32_t dtype, int layout, const uint8_t *table, uint64_t n_embd,
                   const uint32_t *ids_dev, uint64_t n_ids, float *out);
 void launch_rmsnorm(mdma_ctx *ctx, const float *w, uint64_t dim, const float *a, const float *b,
                     float *sum, float *y, uint64_t rows, float eps);

@@ -1,0 +1,98 @@
+// Device helpers shared by the gfx950 GEMV kernels: f16 conversion, 16-byte
+// streaming loads, DPP wave reductions and the Q4_K block pieces.
+#pragma once
+
+#include "internal.h"
+
+namespace mdma {
+namespace {
+
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits16 & 0xffff));
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// Streaming 16-byte weight load (nontemporal: weights are read once per token).
+__device__ __forceinline__ uint4 ld16(const uint8_t *p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+// Plain 16-byte load (activations: re-read by many waves, keep them cached).
+__device__ __forceinline__ uint4 ldx16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
+__device__ __forceinline__ uint32_t ldu16(const uint8_t *p) {
+  return *reinterpret_cast<const uint16_t *>(p);
+}
+// A dword made of two 2-byte-aligned halves (raw Q6_K / Q8_0 blocks are only
+// 2-byte aligned inside a row).
+__device__ __forceinline__ uint32_t ld2x16(const uint8_t *p) { return ldu16(p) | (ldu16(p + 2) << 16); }
+
+// Wave-wide sum through DPP lane moves (no LDS round trips): xor 1, xor 2,
+// half-row mirror, row mirror (16-lane sums in every lane), then row
+// broadcasts 15 and 31. The total is valid in lane 63 only.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xF, false);
+}
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_step(float v) {
+  return v + __builtin_bit_cast(float, dpp_u32<CTRL, ROWS>(__builtin_bit_cast(uint32_t, v)));
+}
+template <int CTRL, int ROWS>
+__device__ __forceinline__ double dpp_step(double v) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const uint64_t lo = dpp_u32<CTRL, ROWS>((uint32_t)b), hi = dpp_u32<CTRL, ROWS>((uint32_t)(b >> 32));
+  return v + __builtin_bit_cast(double, (hi << 32) | lo);
+}
+template <class V>
+__device__ __forceinline__ V wave_total63(V v) {
+  v = dpp_step<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+  v = dpp_step<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+  v = dpp_step<0x141, 0xF>(v);  // row_half_mirror
+  v = dpp_step<0x140, 0xF>(v);  // row_mirror
+  v = dpp_step<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+  v = dpp_step<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+  return v;
+}
+
+// Six-bit (scale, min) of Q4_K sub-blocks 2p and 2p+1 from the header's
+// 12 scale bytes (hd.y, hd.z, hd.w): get_scale_min_k4 of
+// /root/reference/src/backend/rocm/kernels/kernels.hip:19-27, evaluated for
+// two sub-blocks at once in packed bytes.
+__device__ __forceinline__ void q4k_scales_i(uint4 hd, int p, int &sca, int &scb, int &ma, int &mb) {
+  const uint32_t s0 = hd.y, s1 = hd.z, s2 = hd.w;
+  const uint32_t scw = p < 2 ? (s0 & 0x3F3F3F3Fu) : ((s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u));
+  const uint32_t mw = p < 2 ? (s1 & 0x3F3F3F3Fu) : (((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u));
+  const int sh = (p & 1) * 16;
+  sca = (scw >> sh) & 0xff;
+  scb = (scw >> (sh + 8)) & 0xff;
+  ma = (mw >> sh) & 0xff;
+  mb = (mw >> (sh + 8)) & 0xff;
+}
+
+// Exact products: a quant byte b (0..255) placed by one v_perm_b32 into
+// mantissa bits 40..47 of an f64 whose exponent is fixed gives the double
+// 2 + b/2048 with no conversion instruction. Its product with an activation
+// converted to f64 is exact, and short chains accumulate in f64, so
+//     sum(q*x) = 2048*acc - (4096 + 2048*bias)*X,  X = sum(x)
+// where q = b - bias.
+constexpr uint32_t F64_HI_TWO = 0x40000000u;  // high dword of 2.0
+
+// f64 value 2 + byte_k(w)/2048 (k compile-time).
+template <int K>
+__device__ __forceinline__ double byte_f64(uint32_t w) {
+  constexpr uint32_t sel = 0x070C000Cu | ((uint32_t)K << 8);
+  const uint32_t hi = __builtin_amdgcn_perm(F64_HI_TWO, w, sel);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32));
+}
+
+// acc += sum_k (2 + byte_k(w)/2048) * x[k] over the 4 bytes of w.
+__device__ __forceinline__ double fma4(uint32_t w, const double *x, double acc) {
+  acc = fma(byte_f64<0>(w), x[0], acc);
+  acc = fma(byte_f64<1>(w), x[1], acc);
+  acc = fma(byte_f64<2>(w), x[2], acc);
+  acc = fma(byte_f64<3>(w), x[3], acc);
+  return acc;
+}
+
+}  // namespace
+}  // namespace mdma

@@ -162,7 +162,9 @@ struct Weight {
   int32_t dtype = 0;
   uint64_t rows = 0, cols = 0;
   mdma_buf *buf = nullptr;
-  GemvJob job(float *y) const { return GemvJob{dtype, reinterpret_cast<const uint8_t *>(buf->ptr), rows, cols, y}; }
+  GemvJob job(float *y) const {
+    return GemvJob{dtype, reinterpret_cast<const uint8_t *>(buf->ptr), rows, cols, y, buf->layout};
+  }
 };
 
 struct Layer {
@@ -404,7 +406,8 @@ void run_layers(mdma_session *s, uint64_t T, uint32_t pos, uint64_t seq, bool ba
 
 void embed_dev(mdma_session *s, const uint32_t *ids_dev, uint64_t n) {
   const Weight &te = s->m->token_embd;
-  launch_embed(s->m->ctx, te.dtype, reinterpret_cast<const uint8_t *>(te.buf->ptr), te.cols, ids_dev, n, fp(s->x));
+  launch_embed(s->m->ctx, te.dtype, te.buf->layout, reinterpret_cast<const uint8_t *>(te.buf->ptr), te.cols, ids_dev, n,
+               fp(s->x));
 }
 
 // Output head on `rows` rows starting at row r0 of normed, logits to logits + out_row*vocab.

@@ -55,13 +55,54 @@ __device__ float deq_elem(int32_t dt, const uint8_t *row, uint32_t i) {
   return ds * (float)q;
 }
 
-__global__ __launch_bounds__(256) void embed_kernel(int32_t dt, const uint8_t *__restrict__ table, uint32_t n_embd,
-                                                    size_t row_bytes, const uint32_t *__restrict__ ids,
-                                                    float *__restrict__ out) {
+// The same element from a prepared row (layout.cpp): the same bytes, found
+// at their plane positions, with the same rounding sequence.
+__device__ float deq_elem_prepared(int32_t dt, const uint8_t *row, uint32_t i, uint32_t n_embd) {
+#pragma clang fp contract(off)
+  if (dt == DT_Q8_0) {
+    const uint32_t nb = n_embd / 32, b = i / 32, l = i % 32;
+    const float d = h2f((uint16_t)(row[32 * nb + 2 * b] | (row[32 * nb + 2 * b + 1] << 8)));
+    return (float)(int8_t)row[16 * (l < 16 ? b : nb + b) + l % 16] * d;
+  }
+  const uint32_t nb = n_embd / 256, U = 4 * nb, b = i / 256, e = i % 256;
+  if (dt == DT_Q4_K) {
+    const uint8_t *hd = row + 32 * U + 16 * b;
+    const uint32_t j = e / 32, p = e / 64, l = e % 32, u = 4 * b + p;
+    const float d = h2f((uint16_t)(hd[0] | (hd[1] << 8))), dmin = h2f((uint16_t)(hd[2] | (hd[3] << 8)));
+    const uint8_t *s = hd + 4;
+    uint32_t sc, m;
+    if (j < 4) {
+      sc = s[j] & 63;
+      m = s[j + 4] & 63;
+    } else {
+      sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4);
+      m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+    const uint8_t qb = row[16 * (l < 16 ? u : U + u) + l % 16];
+    const uint32_t q = (j & 1) ? (qb >> 4) : (qb & 0xF);
+    const float d1 = d * (float)sc, m1 = dmin * (float)m;
+    const float t = d1 * (float)q;
+    return t - m1;
+  }
+  // Q6_K
+  const uint32_t n = e / 128, r = (e % 128) / 32, l = e % 32, u = 4 * b + 2 * n + l / 16, ll = l % 16;
+  const uint8_t lq = row[16 * ((r & 1) ? U + u : u) + ll];
+  const int low = (r < 2) ? (lq & 0xF) : (lq >> 4);
+  const int high = (row[16 * (2 * U + u) + ll] >> (2 * r)) & 3;
+  const int q = (low | (high << 4)) - 32;
+  const int8_t sc = (int8_t)row[48 * U + 4 * u + r];
+  const float d = h2f((uint16_t)(row[52 * U + 2 * b] | (row[52 * U + 2 * b + 1] << 8)));
+  const float ds = d * (float)sc;
+  return ds * (float)q;
+}
+
+__global__ __launch_bounds__(256) void embed_kernel(int32_t dt, int prepared, const uint8_t *__restrict__ table,
+                                                    uint32_t n_embd, size_t row_bytes,
+                                                    const uint32_t *__restrict__ ids, float *__restrict__ out) {
   const uint32_t t = blockIdx.y;
   const uint8_t *row = table + (size_t)ids[t] * row_bytes;
   for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n_embd; i += gridDim.x * 256)
-    out[(size_t)t * n_embd + i] = deq_elem(dt, row, i);
+    out[(size_t)t * n_embd + i] = prepared ? deq_elem_prepared(dt, row, i, n_embd) : deq_elem(dt, row, i);
 }
 
 // Block-wide f64 sum (256 threads).
@@ -385,11 +426,12 @@ uint32_t grid1d(uint64_t n, uint32_t per = 256) {
 
 }  // namespace
 
-void launch_embed(mdma_ctx *ctx, int32_t dtype, const uint8_t *table, uint64_t n_embd, const uint32_t *ids,
-                  uint64_t n_ids, float *out) {
-  const size_t rb = n_embd / block_size(dtype) * type_size(dtype);
-  embed_kernel<<<dim3(grid1d(n_embd), (uint32_t)n_ids), dim3(256), 0, ctx->stream>>>(dtype, table,
-                                                                                     (uint32_t)n_embd, rb, ids, out);
+void launch_embed(mdma_ctx *ctx, int32_t dtype, int layout, const uint8_t *table, uint64_t n_embd,
+                  const uint32_t *ids, uint64_t n_ids, float *out) {
+  const bool prepared = layout == MDMA_LAYOUT_GFX950;
+  const size_t rb = prepared ? gfx950_row_bytes(dtype, n_embd) : n_embd / block_size(dtype) * type_size(dtype);
+  embed_kernel<<<dim3(grid1d(n_embd), (uint32_t)n_ids), dim3(256), 0, ctx->stream>>>(
+      dtype, prepared ? 1 : 0, table, (uint32_t)n_embd, rb, ids, out);
   hip_check(hipGetLastError(), "embed launch");
 }
 

@@ -12,7 +12,8 @@ import pytest
 
 from conftest import assert_parity, f32_exact
 from mdma_amd import synth
-from mdma_amd.backend import ShapeMismatch, QWeight
+from mdma_amd import backend as backend_mod
+from mdma_amd.backend import LAYOUT_GFX950, POOL_WEIGHTS, QWeight, ShapeMismatch, pack_weight
 from oracle import ffi
 
 pytestmark = pytest.mark.gpu
@@ -343,3 +344,56 @@ def test_qmatmul_shape_rules(backend):
     with pytest.raises(ShapeMismatch):
         backend.ffn_gate_up(w, QWeight(Q4K, (2, 512), w.buf), backend.alloc(2048), backend.alloc(16),
                             backend.alloc(16), backend.alloc(16))
+
+
+# ------------------------------------------------------ storage layouts ----
+
+def raw_weight(be, raw, dtype, shape):
+    """A weight buffer holding raw GGUF blocks (alloc + upload, as a caller of
+    the trait may build one): the backend's GGUF-layout kernels read it."""
+    a = np.ascontiguousarray(raw).view(np.uint8).reshape(-1)
+    b = be.alloc(a.nbytes, POOL_WEIGHTS)
+    be.upload(b, 0, a)
+    return QWeight(dtype, tuple(shape), b)
+
+
+@pytest.mark.parametrize("T", [1, 3])
+@pytest.mark.parametrize("dtype", [Q4K, Q6K, Q8])
+def test_raw_and_prepared_storage_agree_with_oracle(backend, dtype, T):
+    """upload_weight stores Q4_K/Q6_K/Q8_0 in the prepared layout; raw GGUF
+    buffers and pre-packed uploads (layout GFX950) must give the oracle's
+    results too, in both activation modes."""
+    rows, k = 37, 768
+    raw = synth.weight(dtype, rows, k, 90 + dtype)
+    x = synth.normal_f32(T * k, 91)
+    W = ffi.dequantize_row(dtype, raw, rows * k).reshape(rows, k)
+    cpu, exact = oracle_f32(dtype, raw, rows, k, x)
+    cpu8, exact8 = oracle_i8(dtype, raw, rows, k, x)
+    ws = {"prepared": backend.upload_weight(raw, dtype, (rows, k)),
+          "packed": backend.upload_weight(pack_weight(raw, dtype, (rows, k)), dtype, (rows, k), LAYOUT_GFX950),
+          "raw": raw_weight(backend, raw, dtype, (rows, k))}
+    xb = backend.f32_buf(x)
+    for name, w in ws.items():
+        for mode, fn in (("f32", backend.qmatmul_f32), ("i8", backend.qmatmul_i8)):
+            yb = backend.f32_buf(np.full(T * rows + 8, CANARY, np.float32))
+            fn(w, xb, yb)
+            y = backend.download_f32(yb)
+            assert np.all(y[T * rows:] == CANARY), (name, mode)
+            if mode == "f32":
+                assert_parity(y[:T * rows], cpu, exact, 1e-5, what=f"{name} f32 dtype={dtype} T={T}")
+            else:
+                assert_parity(y[:T * rows], cpu8, exact8, 1e-3, what=f"{name} i8 dtype={dtype} T={T}")
+    # The embedding gather reads every storage layout the same way.
+    ids = np.array([0, rows - 1, 5, 5], np.uint32)
+    for name, w in ws.items():
+        ob = backend.alloc(ids.size * k * 4)
+        backend.embed(w, ids, ob)
+        assert np.array_equal(backend.download_f32(ob), W[ids].reshape(-1)), name
+
+
+def test_packed_upload_rejects_wrong_sizes(backend):
+    raw = synth.weight(Q4K, 4, 256, 5)
+    with pytest.raises(ShapeMismatch):
+        backend.upload_weight(raw[:-16], Q4K, (4, 256), LAYOUT_GFX950)
+    with pytest.raises(backend_mod.NotImplemented):
+        backend.upload_weight(np.zeros(4 * 256 * 4, np.uint8), F32, (4, 256), LAYOUT_GFX950)
