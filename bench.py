@@ -18,10 +18,13 @@ reported beside it. Algorithmic bytes count each weight byte, each launch's
 input and each output once (int8 inputs: values, per-256 scales and per-16
 sums).
 
-Also reported: per-launch rates, the roofline of the dominant kernel (the
-fused gate/up GEMV, 66 MB per launch) and the CPU baseline (the C
-restatement of CpuBackend::qmatmul on this host's cores, on a bounded
-sample of the same step).
+Also reported: per-launch rates (kernel-only from the dispatch's own
+timestamps, and back to back in a graph), the roofline of the dominant
+kernel (the fused gate/up GEMV, 66 MB per launch), the Q6_K GEMVs of
+BASELINE config 3 (output head 128256x4096 and down 4096x14336 at batch 1, 4
+and 8), a device copy-bandwidth probe, and the CPU baseline (the C
+restatement of CpuBackend::qmatmul on this host's cores, on a bounded sample
+of the same step).
 """
 import argparse
 import ctypes as C
@@ -44,6 +47,11 @@ LAUNCHES = [("qkv", ("q", "k", "v"), 4096, 6144), ("o", ("o",), 4096, 4096),
             ("gate_up", ("gate", "up"), 4096, 14336), ("down", ("down",), 14336, 4096)]
 Q4K = 12
 SEED = 20261201
+# HBM bytes per launch of the dominant kernel from rocprofv3 --pmc FETCH_SIZE
+# and WRITE_SIZE (profiles/gemv_q4k_llama8b_layer.md), FETCH_SIZE scaled by
+# 2.0: a 1 GiB device copy reads 524,299 KiB on that counter on this
+# device, WRITE_SIZE reads 1,048,576 KiB (scale 1.0).
+TRAFFIC_GATE_UP = None
 
 
 def w_bytes(name):
@@ -73,6 +81,9 @@ class HipEvents:
 
     def record(self, e, stream):
         assert self.h.hipEventRecord(e, C.c_void_p(stream)) == 0
+
+    def destroy(self, e):
+        self.h.hipEventDestroy(e)
 
     def elapsed_ms(self, a, b):
         assert self.h.hipEventSynchronize(b) == 0
@@ -126,19 +137,86 @@ def time_graphs(be, ev, graphs, steps, warmup):
 
 
 def per_launch(be, ev, wl, mode, reps):
-    """Average duration of each launch kind: a graph of that launch over every
-    distinct weight copy (same input buffer, so in int8 mode the activations
-    are quantized once and the replays time the GEMV kernel itself)."""
+    """Per launch kind, over every distinct weight copy (same input buffer, so
+    in int8 mode the activations are quantized once and the GEMV kernel
+    itself is timed):
+      - us_kernel: kernel duration from the dispatch's own start/end
+        timestamps (hipExtLaunchKernel events, the figure a profiler's
+        kernel trace reports), averaged over reps * copies eager launches;
+      - us_graph: time per launch of a graph replaying that launch over every
+        copy back to back (includes the gap between graph nodes)."""
     out = {}
+    n = reps * len(wl.layers)
+    starts, stops = [ev.event() for _ in range(n)], [ev.event() for _ in range(n)]
     for launch in LAUNCHES:
         name = launch[0]
         g = be.capture(lambda: [wl.launch(be, L, name) for L in wl.layers])
         ms = time_graphs(be, ev, [g], reps, 2)
-        n = reps * len(wl.layers)
-        us = ms * 1e3 / n
-        out[name] = {"us_per_launch": round(us, 3), "bytes_per_launch": launch_bytes(launch, mode),
-                     "GBps": round(launch_bytes(launch, mode) / us / 1e3, 1), "launches_timed": n}
         g.close()
+        us_graph = ms * 1e3 / n
+        for L in wl.layers:  # warm: activations quantized, code loaded
+            wl.launch(be, L, name)
+        be.join_execution()
+        i = 0
+        for _ in range(reps):
+            for L in wl.layers:
+                be.time_next_gemv(starts[i].value, stops[i].value)
+                wl.launch(be, L, name)
+                i += 1
+        be.join_execution()
+        us = sum(ev.elapsed_ms(starts[k], stops[k]) for k in range(n)) * 1e3 / n
+        b = launch_bytes(launch, mode)
+        out[name] = {"us_kernel": round(us, 3), "GBps_kernel": round(b / us / 1e3, 1),
+                     "us_graph": round(us_graph, 3), "GBps_graph": round(b / us_graph / 1e3, 1),
+                     "bytes_per_launch": b, "launches_timed": n}
+    for e in starts + stops:
+        ev.destroy(e)
+    return out
+
+
+Q6K = 14
+# Q6_K GEMVs of BASELINE config 3: the output head and the down projection
+# of the Q4_K_M mix, at batch 1, 4 and 8.
+Q6_SHAPES = {"q6k_head": (128256, 4096), "q6k_down": (4096, 14336)}
+
+
+def q6k_gemvs(be, ev, reps):
+    """Kernel-only rates (dispatch timestamps) of the Q6_K GEMVs, weights
+    rotated over >= 1 GiB of copies; int8 mode at T = 1, 4, 8 and the f32
+    mode at T = 1. Bytes: weights + activations + outputs, each once."""
+    from mdma_amd import synth
+    from mdma_amd.backend import ACT_F32, ACT_I8
+
+    out = {}
+    for name, (rows, k) in Q6_SHAPES.items():
+        raw = synth.weight(Q6K, rows, k, SEED + 7)
+        copies = max(2, -(-MALL_DEFEAT_BYTES // len(raw)))
+        ws = [be.upload_weight(raw, Q6K, (rows, k)) for _ in range(copies)]
+        for T, mode in ((1, "i8"), (4, "i8"), (8, "i8"), (1, "f32")):
+            be.set_act_mode(ACT_I8 if mode == "i8" else ACT_F32)
+            x = be.f32_buf(synth.normal_f32(T * k, SEED + 8))
+            y = be.alloc(T * rows * 4)
+            for w in ws:
+                be.qmatmul(w, x, y)
+            be.join_execution()
+            n = reps * copies
+            st, sp = [ev.event() for _ in range(n)], [ev.event() for _ in range(n)]
+            for i in range(n):
+                be.time_next_gemv(st[i].value, sp[i].value)
+                be.qmatmul(ws[i % copies], x, y)
+            be.join_execution()
+            us = sum(ev.elapsed_ms(st[i], sp[i]) for i in range(n)) * 1e3 / n
+            for e in st + sp:
+                ev.destroy(e)
+            b = len(raw) + T * (x_bytes(k, mode)) + T * rows * 4
+            out[f"{name}_T{T}_{mode}"] = {"us_kernel": round(us, 3), "GBps_kernel": round(b / us / 1e3, 1),
+                                          "pct_of_hbm_peak": round(100 * b / us / 1e3 / HBM_PEAK_GBS, 1),
+                                          "bytes_per_launch": b, "launches_timed": n}
+            x.close()
+            y.close()
+        for w in ws:
+            w.buf.close()
+    be.set_act_mode(ACT_I8)
     return out
 
 
@@ -222,13 +300,14 @@ def main():
         results[mode] = {"ms_per_step": ms / args.steps, "GBps": step_bytes * args.steps / (ms * 1e-3) / 1e9,
                          "step_bytes": step_bytes, "per_launch": per_launch(be, ev, wl, mode, args.reps)}
     be.set_act_mode(ACT_I8)
+    q6 = q6k_gemvs(be, ev, max(2, args.reps // 4))
 
     main_mode = results["i8"]
     dom = main_mode["per_launch"]["gate_up"]
-    roof = {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "gemv_q4k_i8<1,true> (fused ffn gate/up + SiLU, 2 x 14336x4096 Q4_K)",
-            "bytes_per_launch": dom["bytes_per_launch"], "us_per_launch": dom["us_per_launch"]}
+    roof = {"bound": "hbm", "achieved": dom["GBps_kernel"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(dom["GBps_kernel"] / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_GATE_UP,
+            "kernel": "gemv_team<Q4G, int8, gated> (fused ffn gate/up + SiLU, 2 x 14336x4096 Q4_K)",
+            "bytes_per_launch": dom["bytes_per_launch"], "us_per_launch": dom["us_kernel"]}
     cpu = None if args.no_cpu else cpu_baseline(wl.raws, args.cpu_seconds)
     f = results["f32"]
     line = {
@@ -245,6 +324,7 @@ def main():
         "per_launch_i8": main_mode["per_launch"],
         "f32_mode": {"GBps": round(f["GBps"], 1), "ms_per_step": round(f["ms_per_step"], 5),
                      "pct_of_hbm_peak": round(100 * f["GBps"] / HBM_PEAK_GBS, 2), "per_launch": f["per_launch"]},
+        "q6k_gemv": q6,
         "copy_probe": probe,
         "device": be.device_label(),
     }

@@ -226,6 +226,12 @@ int mdma_gfx950_graph_launch(mdma_ctx *ctx, mdma_graph *graph);
 void mdma_gfx950_graph_destroy(mdma_graph *graph);
 /* Pre-size the context scratch and int8-activation buffers so a later capture needs no growth. */
 int mdma_gfx950_reserve_scratch(mdma_ctx *ctx, uint64_t bytes);
+/* Extra (no counterpart in the reference; for benchmarks and profiling):
+ * the next GEMV kernel this context launches on prepared weights is
+ * dispatched with these hipEvent_t handles (either may be NULL), which its
+ * dispatch packet timestamps at kernel start and end (hipExtLaunchKernel).
+ * Applies to one launch; not allowed during graph capture. */
+int mdma_gfx950_time_next_gemv(mdma_ctx *ctx, void *start_event, void *stop_event);
 
 /* ---- Llama decoding: the hot path's caller ----
  * Model / KvCache / Workspace / inference::generate (src/model.rs:41-468,

@@ -84,6 +84,7 @@ _SIGS = {
     "quantize_act": [_P, _P, _U64, _P, _P, _P], "block_dot_i32": [_P, _P, _P, _P],
     "graph_begin": [_P], "graph_end": [_P, _P], "graph_launch": [_P, _P], "graph_destroy": [_P],
     "reserve_scratch": [_P, _U64],
+    "time_next_gemv": [_P, _P, _P],
     "prepared_bytes": [_I32, _U64, _U64],
     "pack_weight": [_I32, _U64, _U64, _P, _U64, _P, _U64],
     "unpack_weight": [_I32, _U64, _U64, _P, _U64, _P, _U64],
@@ -359,6 +360,10 @@ class Gfx950Backend:
 
     def block_dot_i32(self, w: QWeight, qx: Buf, out: Buf):
         _check(lib().mdma_gfx950_block_dot_i32(self.ctx, C.byref(w.c()), qx.handle, out.handle))
+
+    def time_next_gemv(self, start_event: int, stop_event: int):
+        """Have the next GEMV kernel's dispatch timestamp these hipEvent_t handles."""
+        _check(lib().mdma_gfx950_time_next_gemv(self.ctx, start_event, stop_event))
 
     def reserve_scratch(self, nbytes: int):
         _check(lib().mdma_gfx950_reserve_scratch(self.ctx, nbytes))

@@ -964,6 +964,16 @@ void mdma_gfx950_graph_destroy(mdma_graph *graph) {
   delete graph;
 }
 
+int mdma_gfx950_time_next_gemv(mdma_ctx *ctx, void *start_event, void *stop_event) {
+  return guarded([&] {
+    need(ctx, "time_next_gemv");
+    std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    no_capture(ctx, "time_next_gemv");
+    ctx->time_start = static_cast<hipEvent_t>(start_event);
+    ctx->time_stop = static_cast<hipEvent_t>(stop_event);
+  });
+}
+
 int mdma_gfx950_reserve_scratch(mdma_ctx *ctx, uint64_t bytes) {
   return guarded([&] {
     need(ctx, "reserve_scratch");

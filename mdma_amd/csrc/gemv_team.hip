@@ -28,6 +28,8 @@
 //    Q8_0 d_x*d*isum; f32 partial sums.
 //  - f32: exact products (byte_f64) accumulated in f64, one f32 rounding at
 //    the end.
+#include <hip/hip_ext.h>
+
 #include <type_traits>
 
 #include "kernels.h"
@@ -343,23 +345,8 @@ __global__ __launch_bounds__(WG) void gemv_team(TeamSet ts, const float *__restr
     uok[p] = u < U;
     uid[p] = uok[p] ? u : U - 1;
   }
-  // Activations of the lane's units, loaded once.
   typename F::XI xi[F32 ? 1 : PL][F32 ? 1 : TT];
   typename F::XF xr[F32 && TT == 1 ? PL : 1];
-  if constexpr (!F32) {
-#pragma unroll
-    for (int p = 0; p < PL; p++)
-#pragma unroll
-      for (int t = 0; t < TT; t++) {
-        const uint32_t tc = t < (int)T ? t : 0;  // rows past T are never used
-        xi[p][t] = F::loadxi(qx + (size_t)tc * n_in, dx + (size_t)tc * (n_in / 256),
-                             s16 + (size_t)tc * (n_in / 16), uid[p]);
-      }
-  } else if constexpr (TT == 1) {
-#pragma unroll
-    for (int p = 0; p < PL; p++) xr[p] = F::loadxf(xf, uid[p]);
-  }
-
   // Weight loads are unconditional: a row past the team's run re-reads the
   // team's last row (a cache hit, not HBM traffic). A conditional load would
   // make the compiler's wait-count analysis treat the prefetch as pending
@@ -455,7 +442,24 @@ __global__ __launch_bounds__(WG) void gemv_team(TeamSet ts, const float *__restr
   };
 
   const uint32_t iters = ts.rpt / R;
+  // The first rows' weights go out before the activations: the weights come
+  // from HBM, the activations from L2.
   load(A, r_begin);
+  // Activations of the lane's units, loaded once.
+  if constexpr (!F32) {
+#pragma unroll
+    for (int p = 0; p < PL; p++)
+#pragma unroll
+      for (int t = 0; t < TT; t++) {
+        const uint32_t tc = t < (int)T ? t : 0;  // rows past T are never used
+        xi[p][t] = F::loadxi(qx + (size_t)tc * n_in, dx + (size_t)tc * (n_in / 256),
+                             s16 + (size_t)tc * (n_in / 16), uid[p]);
+      }
+  } else if constexpr (TT == 1) {
+#pragma unroll
+    for (int p = 0; p < PL; p++) xr[p] = F::loadxf(xf, uid[p]);
+  }
+
   for (uint32_t it = 0; it < iters; it += 2) {
     const uint32_t r0 = r_begin + it * R;
     load(B, r0 + R);
@@ -477,7 +481,7 @@ __global__ __launch_bounds__(WG) void gemv_team(TeamSet ts, const float *__restr
 #define MDMA_TEAM_RG 1
 #endif
 #ifndef MDMA_TEAM_WAVES_PER_CU
-#define MDMA_TEAM_WAVES_PER_CU 16
+#define MDMA_TEAM_WAVES_PER_CU 8
 #endif
 
 template <class F, bool F32, int R, int TT, bool GATED>
@@ -505,8 +509,18 @@ void launch_fmt(mdma_ctx *ctx, TeamSet ts, const float *xf, const int8_t *qx, co
   }
   const int tpw = WG / 64 / tw;
   const dim3 grid((uint32_t)((teams + tpw - 1) / tpw)), block(WG);
-#define MDMA_TEAM_LAUNCH(TW_, PL_) \
-  gemv_team<F, F32, R, TW_, PL_, TT, GATED><<<grid, block, 0, ctx->stream>>>(ts, xf, qx, dx, s16, T, yg)
+  // With timing events set, the dispatch itself timestamps them (kernel-only
+  // duration, as a profiler measures it); they apply to one launch.
+  hipEvent_t t0 = ctx->time_start, t1 = ctx->time_stop;
+  ctx->time_start = ctx->time_stop = nullptr;
+#define MDMA_TEAM_LAUNCH(TW_, PL_)                                                                             \
+  do {                                                                                                          \
+    if (t0 || t1)                                                                                               \
+      hipExtLaunchKernelGGL(gemv_team<F, F32, R, TW_, PL_, TT, GATED>, grid, block, 0, ctx->stream, t0, t1, 0, \
+                            ts, xf, qx, dx, s16, T, yg);                                                        \
+    else                                                                                                        \
+      gemv_team<F, F32, R, TW_, PL_, TT, GATED><<<grid, block, 0, ctx->stream>>>(ts, xf, qx, dx, s16, T, yg);  \
+  } while (0)
   if (tw == 1) MDMA_TEAM_LAUNCH(1, 1);
   else if (tw == 2) MDMA_TEAM_LAUNCH(2, 1);
   else if (pl == 1) MDMA_TEAM_LAUNCH(4, 1);

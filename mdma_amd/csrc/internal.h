@@ -87,6 +87,8 @@ struct mdma_ctx {
   uint32_t *host_ids = nullptr;  // pinned staging for token ids / argmax result
   uint64_t host_ids_cap = 0;
   bool capturing = false;        // stream capture in progress: no synchronizing calls
+  // Events the next GEMV kernel's dispatch timestamps (mdma_gfx950_time_next_gemv).
+  hipEvent_t time_start = nullptr, time_stop = nullptr;
 };
 
 struct mdma_graph {
