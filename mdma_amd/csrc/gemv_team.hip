@@ -1,555 +1,10 @@
-// Decode GEMV on gfx950 over the prepared weight layouts (layout.cpp): the
-// streaming "row team" kernels, in the int8-activation and the
-// f32-activation mode, for 1..8 tokens.
-//
-// y[t, r] = sum_i deq(W)[r, i] * x[t, i]   (reference Backend::qmatmul,
-// /root/reference/src/backend.rs:469; CPU oracle src/backend/cpu.rs:335-368)
-//
-// Layout of the work:
-//  - A lane owns fixed "units" of K (64 columns; 32 for Q8_0). The prepared
-//    layout stores each row as planes indexed by unit, so lane i of every
-//    16-byte load instruction reads bytes [16i, 16i+16) of a plane: a wave
-//    load is 1 KiB of contiguous HBM.
-//  - The lane's activations for its units stay in registers for the whole
-//    kernel (int8 values, their exact sub-block sums and the per-256 scale;
-//    or, in the f32 mode of one token, the f32 values and their f64 sums).
-//  - A team of TW waves (64*TW lanes) covers all units of a row, PL units
-//    per lane. A team owns a contiguous run of rows of one weight and walks
-//    it R rows at a time, loading the next R rows while it computes the
-//    current ones (ping-pong register buffers).
-//  - Lanes reduce with DPP moves; multi-wave teams add the waves' sums in LDS.
-//  - Fused QKV: up to three weights share x; teams are dealt out in order.
-//    Gated (ffn gate/up + SiLU): a team computes R rows of gate and the same
-//    rows of up and writes silu(g) * u.
-// Arithmetic per mode:
-//  - int8: exact int32 dot per sub-block with v_dot4_i32_i8, scales applied
-//    as in the reference's int8 decode (src/backend/rocm/kernels/decode.hip:47-108):
-//    Q4_K d_x*(d*sum sc*isum - dmin*sum m*xsum), Q6_K d_x*d*sum sc*isum,
-//    Q8_0 d_x*d*isum; f32 partial sums.
-//  - f32: exact products (byte_f64) accumulated in f64, one f32 rounding at
-//    the end.
-#include <hip/hip_ext.h>
-
-#include <type_traits>
-
-#include "kernels.h"
+// Host entry points of the row-team GEMV (kernels in gemv_team.h,
+// instantiated per format and activation mode in gemv_team_*.hip) and the
+// prepared-layout block-dot debug kernel.
+#include "gemv_team.h"
 
 namespace mdma {
 namespace {
-
-constexpr int WG = 256;  // threads per workgroup
-
-__device__ __forceinline__ uint32_t ld32(const uint8_t *p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p));
-}
-__device__ __forceinline__ uint32_t ld16b(const uint8_t *p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const uint16_t *>(p));
-}
-// Dword k of the quad (lanes 4j..4j+3 hold the four dwords of one header).
-template <int K>
-__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, K * 0x55, 0xF, 0xF, false);
-}
-__device__ __forceinline__ void f4(const float *p, float *o) {
-  const float4 v = *reinterpret_cast<const float4 *>(p);
-  o[0] = v.x, o[1] = v.y, o[2] = v.z, o[3] = v.w;
-}
-__device__ __forceinline__ double sum_f64(const float *v, int n) {
-  double s = 0.0;
-  for (int i = 0; i < n; i++) s += (double)v[i];
-  return s;
-}
-// acc += sum_k (2 + byte_k(w)/2048) * x[k] with f32 x converted on use.
-__device__ __forceinline__ double fma4f(uint32_t w, const float *x, double acc) {
-  acc = fma(byte_f64<0>(w), (double)x[0], acc);
-  acc = fma(byte_f64<1>(w), (double)x[1], acc);
-  acc = fma(byte_f64<2>(w), (double)x[2], acc);
-  acc = fma(byte_f64<3>(w), (double)x[3], acc);
-  return acc;
-}
-
-// ---------------------------------------------------------------- Q4_K ----
-// Unit u = sub-block pair p = u%4 of block u/4: 32 quant bytes (A, B planes)
-// whose low nibbles are columns 64u..64u+31 and high nibbles 64u+32..+63;
-// the 16-byte block header is spread over the quad (dword u%4 per lane).
-struct Q4G {
-  static constexpr uint32_t UCOLS = 64;
-  struct W {
-    uint4 a, b;
-    uint32_t h;
-  };
-  struct XI {
-    uint4 a0, a1, b0, b1;
-    int sa, sb;
-    float d8;
-  };
-  struct XF {
-    float xa[32], xb[32];
-    double sa, sb;
-  };
-  __device__ static uint32_t units(uint32_t n_in) { return n_in / 64; }
-  __device__ static size_t row_bytes(uint32_t n_in) { return (size_t)(n_in / 256) * 144; }
-  __device__ static W load(const uint8_t *row, uint32_t u, uint32_t U) {
-    return W{ld16(row + 16 * (size_t)u), ld16(row + 16 * (size_t)(U + u)), ld32(row + 32 * (size_t)U + 4 * u)};
-  }
-  __device__ static uint4 header(uint32_t h) {
-    return make_uint4(quad_bcast<0>(h), quad_bcast<1>(h), quad_bcast<2>(h), quad_bcast<3>(h));
-  }
-  __device__ static XI loadxi(const int8_t *qx, const float *dx, const int32_t *s16, uint32_t u) {
-    const int8_t *xt = qx + 64 * (size_t)u;
-    const int4 s = *reinterpret_cast<const int4 *>(s16 + 4 * (size_t)u);
-    return XI{ldx16(xt), ldx16(xt + 16), ldx16(xt + 32), ldx16(xt + 48), s.x + s.y, s.z + s.w, dx[u >> 2]};
-  }
-  __device__ static XF loadxf(const float *x, uint32_t u) {
-    XF r;
-#pragma unroll
-    for (int k = 0; k < 32; k += 4) {
-      f4(x + 64 * (size_t)u + k, r.xa + k);
-      f4(x + 64 * (size_t)u + 32 + k, r.xb + k);
-    }
-    r.sa = sum_f64(r.xa, 32);
-    r.sb = sum_f64(r.xb, 32);
-    return r;
-  }
-  __device__ static float dot_i8(const W &w, const XI &x, uint32_t u) {
-    const uint4 hd = header(w.h);
-    const uint32_t q[8] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w};
-    const uint32_t xa[8] = {x.a0.x, x.a0.y, x.a0.z, x.a0.w, x.a1.x, x.a1.y, x.a1.z, x.a1.w};
-    const uint32_t xb[8] = {x.b0.x, x.b0.y, x.b0.z, x.b0.w, x.b1.x, x.b1.y, x.b1.z, x.b1.w};
-    int ia = 0, ib = 0;
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      ia = __builtin_amdgcn_sdot4((int)(q[k] & 0x0F0F0F0Fu), (int)xa[k], ia, false);
-      ib = __builtin_amdgcn_sdot4((int)((q[k] >> 4) & 0x0F0F0F0Fu), (int)xb[k], ib, false);
-    }
-    int sca, scb, ma, mb;
-    q4k_scales_i(hd, u & 3, sca, scb, ma, mb);
-    const int A = sca * ia + scb * ib;
-    const int B = ma * x.sa + mb * x.sb;
-    const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
-    return x.d8 * fmaf(d, (float)A, -dmin * (float)B);
-  }
-  __device__ static double dot_f32(const W &w, const XF &x, uint32_t u) {
-    const uint4 hd = header(w.h);
-    const uint32_t q[8] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w};
-    double aa = 0.0, ab = 0.0;
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      aa = fma4f(q[k] & 0x0F0F0F0Fu, x.xa + 4 * k, aa);
-      ab = fma4f((q[k] >> 4) & 0x0F0F0F0Fu, x.xb + 4 * k, ab);
-    }
-    int sca, scb, ma, mb;
-    q4k_scales_i(hd, u & 3, sca, scb, ma, mb);
-    const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
-    const double dsa = (double)(d * (float)sca), dsb = (double)(d * (float)scb);
-    const double dma = (double)(dmin * (float)ma), dmb = (double)(dmin * (float)mb);
-    // sum (d*sc*q - dmin*m) * x with sum q*x = 2048*acc - 4096*X.
-    double r = fma(2048.0 * dsa, aa, -fma(4096.0, dsa, dma) * x.sa);
-    r += fma(2048.0 * dsb, ab, -fma(4096.0, dsb, dmb) * x.sb);
-    return r;
-  }
-};
-
-// ---------------------------------------------------------------- Q6_K ----
-// Unit u = (half n, column group h) of block u/4 (u%4 = 2n+h): columns
-// 128n + 32r + 16h + [0,16) of quarters r = 0..3 (16 six-bit quants each,
-// q = u6 - 32), with sub-scales sc[8n + 2r + h] and the block's f16 d.
-struct Q6G {
-  static constexpr uint32_t UCOLS = 64;
-  struct W {
-    uint4 a, b, q;
-    uint32_t sc, d;
-  };
-  struct XI {
-    uint4 xq[4];
-    int sq[4];
-    float d8;
-  };
-  struct XF {
-    float x[4][16];
-    double s[4];
-  };
-  __device__ static uint32_t units(uint32_t n_in) { return n_in / 64; }
-  __device__ static size_t row_bytes(uint32_t n_in) { return ((size_t)(n_in / 256) * 210 + 15) / 16 * 16; }
-  __device__ static W load(const uint8_t *row, uint32_t u, uint32_t U) {
-    return W{ld16(row + 16 * (size_t)u), ld16(row + 16 * (size_t)(U + u)), ld16(row + 16 * (size_t)(2 * U + u)),
-             ld32(row + 48 * (size_t)U + 4 * u), ld16b(row + 52 * (size_t)U + 2 * (u >> 2))};
-  }
-  // First column of quarter r of unit u.
-  __device__ static uint32_t col(uint32_t u, int r) {
-    return 256 * (u >> 2) + 128 * ((u >> 1) & 1) + 32 * r + 16 * (u & 1);
-  }
-  __device__ static XI loadxi(const int8_t *qx, const float *dx, const int32_t *s16, uint32_t u) {
-    XI r;
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      r.xq[q] = ldx16(qx + col(u, q));
-      r.sq[q] = s16[col(u, q) / 16];
-    }
-    r.d8 = dx[u >> 2];
-    return r;
-  }
-  __device__ static XF loadxf(const float *x, uint32_t u) {
-    XF r;
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-#pragma unroll
-      for (int k = 0; k < 16; k += 4) f4(x + col(u, q) + k, r.x[q] + k);
-      r.s[q] = sum_f64(r.x[q], 16);
-    }
-    return r;
-  }
-  // Six-bit quants of quarter r, dword k (4 columns).
-  __device__ static uint32_t u6(const W &w, int r, int k) {
-    const uint32_t qa = k == 0 ? w.a.x : k == 1 ? w.a.y : k == 2 ? w.a.z : w.a.w;
-    const uint32_t qb = k == 0 ? w.b.x : k == 1 ? w.b.y : k == 2 ? w.b.z : w.b.w;
-    const uint32_t h = k == 0 ? w.q.x : k == 1 ? w.q.y : k == 2 ? w.q.z : w.q.w;
-    switch (r) {
-      case 0: return (qa & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u);
-      case 1: return (qb & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u);
-      case 2: return ((qa >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u);
-      default: return ((qb >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u);
-    }
-  }
-  __device__ static float dot_i8(const W &w, const XI &x, uint32_t) {
-    int A = 0;
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const uint32_t xv[4] = {x.xq[r].x, x.xq[r].y, x.xq[r].z, x.xq[r].w};
-      int s = 0;
-#pragma unroll
-      for (int k = 0; k < 4; k++) s = __builtin_amdgcn_sdot4((int)u6(w, r, k), (int)xv[k], s, false);
-      A += (int)(int8_t)((w.sc >> (8 * r)) & 0xff) * (s - 32 * x.sq[r]);
-    }
-    return x.d8 * (h2f(w.d) * (float)A);
-  }
-  __device__ static double dot_f32(const W &w, const XF &x, uint32_t) {
-    double r = 0.0;
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      double a = 0.0;
-#pragma unroll
-      for (int k = 0; k < 4; k++) a = fma4f(u6(w, q, k), x.x[q] + 4 * k, a);
-      const double s = (double)(int8_t)((w.sc >> (8 * q)) & 0xff);
-      r = fma(s, fma(2048.0, a, -4128.0 * x.s[q]), r);
-    }
-    return (double)h2f(w.d) * r;
-  }
-};
-
-// ---------------------------------------------------------------- Q8_0 ----
-// Unit u = block u: 32 int8 quants (A, B planes) and the f16 d.
-struct Q8G {
-  static constexpr uint32_t UCOLS = 32;
-  struct W {
-    uint4 a, b;
-    uint32_t d;
-  };
-  struct XI {
-    uint4 x0, x1;
-    float d8;
-  };
-  struct XF {
-    float x[32];
-    double s;
-  };
-  __device__ static uint32_t units(uint32_t n_in) { return n_in / 32; }
-  __device__ static size_t row_bytes(uint32_t n_in) { return ((size_t)(n_in / 32) * 34 + 15) / 16 * 16; }
-  __device__ static W load(const uint8_t *row, uint32_t u, uint32_t U) {
-    return W{ld16(row + 16 * (size_t)u), ld16(row + 16 * (size_t)(U + u)), ld16b(row + 32 * (size_t)U + 2 * u)};
-  }
-  __device__ static XI loadxi(const int8_t *qx, const float *dx, const int32_t *, uint32_t u) {
-    return XI{ldx16(qx + 32 * (size_t)u), ldx16(qx + 32 * (size_t)u + 16), dx[u >> 3]};
-  }
-  __device__ static XF loadxf(const float *x, uint32_t u) {
-    XF r;
-#pragma unroll
-    for (int k = 0; k < 32; k += 4) f4(x + 32 * (size_t)u + k, r.x + k);
-    r.s = sum_f64(r.x, 32);
-    return r;
-  }
-  __device__ static float dot_i8(const W &w, const XI &x, uint32_t) {
-    int s = __builtin_amdgcn_sdot4((int)w.a.x, (int)x.x0.x, 0, false);
-    s = __builtin_amdgcn_sdot4((int)w.a.y, (int)x.x0.y, s, false);
-    s = __builtin_amdgcn_sdot4((int)w.a.z, (int)x.x0.z, s, false);
-    s = __builtin_amdgcn_sdot4((int)w.a.w, (int)x.x0.w, s, false);
-    s = __builtin_amdgcn_sdot4((int)w.b.x, (int)x.x1.x, s, false);
-    s = __builtin_amdgcn_sdot4((int)w.b.y, (int)x.x1.y, s, false);
-    s = __builtin_amdgcn_sdot4((int)w.b.z, (int)x.x1.z, s, false);
-    s = __builtin_amdgcn_sdot4((int)w.b.w, (int)x.x1.w, s, false);
-    return x.d8 * (h2f(w.d) * (float)s);
-  }
-  __device__ static double dot_f32(const W &w, const XF &x, uint32_t) {
-    const uint32_t q[8] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w};
-    double a = 0.0;
-#pragma unroll
-    for (int k = 0; k < 8; k++) a = fma4f(q[k] ^ 0x80808080u, x.x + 4 * k, a);
-    // bytes biased by 128: sum q*x = 2048*acc - (4096 + 128)*X.
-    return (double)h2f(w.d) * fma(2048.0, a, -4224.0 * x.s);
-  }
-};
-
-// ------------------------------------------------------------- kernel ----
-
-struct TeamJob {
-  const uint8_t *w;
-  float *y;
-  uint32_t n_out, teams;
-};
-struct TeamSet {
-  TeamJob j[3];
-  int n;
-  uint32_t n_in, rpt;  // shared row length; rows per team (a multiple of R)
-};
-
-template <class F, bool F32, int R, int TW, int PL, int TT, bool GATED>
-__global__ __launch_bounds__(WG) void gemv_team(TeamSet ts, const float *__restrict__ xf,
-                                                const int8_t *__restrict__ qx, const float *__restrict__ dx,
-                                                const int32_t *__restrict__ s16, uint32_t T,
-                                                float *__restrict__ ygated) {
-  // A lane's partial (at most PL unit terms) is f32 in the int8 mode and f64
-  // in the f32 mode; lane and wave partials are added in f64, so outputs
-  // that cancel (|y| << sum |w*x|) keep their relative accuracy.
-  using Acc = typename std::conditional<F32, double, float>::type;
-  constexpr int TPW = WG / 64 / TW;  // teams per workgroup
-  constexpr int NR = GATED ? 2 * R : R;
-  __shared__ double red[TPW][TW][NR * TT];
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int tw = wave % TW, slot = wave / TW;
-  // Team -> job (scalar, so every job field stays in SGPRs).
-  uint32_t team = blockIdx.x * TPW + slot;
-  int ji = 0;
-  if (ts.n > 1 && team >= ts.j[0].teams) {
-    team -= ts.j[0].teams;
-    ji = 1;
-    if (ts.n > 2 && team >= ts.j[1].teams) {
-      team -= ts.j[1].teams;
-      ji = 2;
-    }
-  }
-  const TeamJob J = ji == 0 ? ts.j[0] : (ji == 1 ? ts.j[1] : ts.j[2]);
-  // A team past its job's end (the grid's last workgroup) runs the loop for
-  // the barriers of its workgroup but stores nothing.
-  const bool team_live = team < J.teams;
-  const uint32_t n_in = ts.n_in, U = F::units(n_in), n_out = J.n_out;
-  const size_t rb = F::row_bytes(n_in);
-  const uint8_t *w_main = J.w, *w_up = GATED ? ts.j[1].w : J.w;
-  const uint32_t r_begin = min(team, J.teams - 1) * ts.rpt;
-  const uint32_t r_last = min(r_begin + ts.rpt, n_out) - 1;
-
-  uint32_t uid[PL];
-  bool uok[PL];
-#pragma unroll
-  for (int p = 0; p < PL; p++) {
-    const uint32_t u = (uint32_t)(p * TW + tw) * 64 + lane;
-    uok[p] = u < U;
-    uid[p] = uok[p] ? u : U - 1;
-  }
-  typename F::XI xi[F32 ? 1 : PL][F32 ? 1 : TT];
-  typename F::XF xr[F32 && TT == 1 ? PL : 1];
-  // Weight loads are unconditional: a row past the team's run re-reads the
-  // team's last row (a cache hit, not HBM traffic). A conditional load would
-  // make the compiler's wait-count analysis treat the prefetch as pending
-  // and wait for it before computing the current rows.
-  typename F::W A[PL][NR], B[PL][NR];
-  auto load = [&](typename F::W(&w)[PL][NR], uint32_t r0) {
-#pragma unroll
-    for (int r = 0; r < NR; r++) {
-      const uint32_t row = min(r0 + (r % R), r_last);
-      const uint8_t *rp = (r < R ? w_main : w_up) + row * rb;
-#pragma unroll
-      for (int p = 0; p < PL; p++) w[p][r] = F::load(rp, uid[p], U);
-    }
-  };
-  auto consume = [&](const typename F::W(&w)[PL][NR], uint32_t r0) {
-    Acc s[NR][TT];
-#pragma unroll
-    for (int r = 0; r < NR; r++)
-#pragma unroll
-      for (int t = 0; t < TT; t++) s[r][t] = 0;
-#pragma unroll
-    for (int p = 0; p < PL; p++) {
-      if constexpr (!F32) {
-#pragma unroll
-        for (int t = 0; t < TT; t++) {
-          if (t >= (int)T) break;
-#pragma unroll
-          for (int r = 0; r < NR; r++) {
-            const float v = F::dot_i8(w[p][r], xi[p][t], uid[p]);
-            s[r][t] += uok[p] ? v : 0.f;
-          }
-        }
-      } else if constexpr (TT == 1) {
-#pragma unroll
-        for (int r = 0; r < NR; r++) {
-          const double v = F::dot_f32(w[p][r], xr[p], uid[p]);
-          s[r][0] += uok[p] ? v : 0.0;
-        }
-      } else {
-#pragma unroll
-        for (int t = 0; t < TT; t++) {
-          if (t >= (int)T) break;
-          const typename F::XF xt = F::loadxf(xf + (size_t)t * n_in, uid[p]);
-#pragma unroll
-          for (int r = 0; r < NR; r++) {
-            const double v = F::dot_f32(w[p][r], xt, uid[p]);
-            s[r][t] += uok[p] ? v : 0.0;
-          }
-        }
-      }
-    }
-    double tot[NR][TT];
-#pragma unroll
-    for (int r = 0; r < NR; r++)
-#pragma unroll
-      for (int t = 0; t < TT; t++) tot[r][t] = (t < (int)T) ? wave_total63((double)s[r][t]) : 0.0;
-    if constexpr (TW > 1) {
-      if (lane == 63)
-#pragma unroll
-        for (int r = 0; r < NR; r++)
-#pragma unroll
-          for (int t = 0; t < TT; t++) red[slot][tw][r * TT + t] = tot[r][t];
-      __syncthreads();
-      if (tw == 0 && lane == 63)
-#pragma unroll
-        for (int r = 0; r < NR; r++)
-#pragma unroll
-          for (int t = 0; t < TT; t++) {
-            double v = 0;
-#pragma unroll
-            for (int k = 0; k < TW; k++) v += red[slot][k][r * TT + t];
-            tot[r][t] = v;
-          }
-      __syncthreads();
-    }
-    if (team_live && tw == 0 && lane == 63) {
-#pragma unroll
-      for (int r = 0; r < R; r++) {
-        const uint32_t row = r0 + r;
-        if (row > r_last) break;
-#pragma unroll
-        for (int t = 0; t < TT; t++) {
-          if (t >= (int)T) break;
-          if (GATED) {
-            const float g = (float)tot[r][t], up = (float)tot[R + r][t];
-            ygated[(size_t)t * n_out + row] = g / (1.0f + expf(-g)) * up;
-          } else {
-            J.y[(size_t)t * n_out + row] = (float)tot[r][t];
-          }
-        }
-      }
-    }
-  };
-
-  const uint32_t iters = ts.rpt / R;
-  // The first rows' weights go out before the activations: the weights come
-  // from HBM, the activations from L2.
-  load(A, r_begin);
-  // Activations of the lane's units, loaded once.
-  if constexpr (!F32) {
-#pragma unroll
-    for (int p = 0; p < PL; p++)
-#pragma unroll
-      for (int t = 0; t < TT; t++) {
-        const uint32_t tc = t < (int)T ? t : 0;  // rows past T are never used
-        xi[p][t] = F::loadxi(qx + (size_t)tc * n_in, dx + (size_t)tc * (n_in / 256),
-                             s16 + (size_t)tc * (n_in / 16), uid[p]);
-      }
-  } else if constexpr (TT == 1) {
-#pragma unroll
-    for (int p = 0; p < PL; p++) xr[p] = F::loadxf(xf, uid[p]);
-  }
-
-  for (uint32_t it = 0; it < iters; it += 2) {
-    const uint32_t r0 = r_begin + it * R;
-    load(B, r0 + R);
-    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
-    consume(A, r0);
-    if (it + 1 >= iters) break;
-    load(A, r0 + 2 * R);
-    __builtin_amdgcn_sched_barrier(0);
-    consume(B, r0 + R);
-  }
-}
-
-// ----------------------------------------------------------- launcher ----
-
-#ifndef MDMA_TEAM_R
-#define MDMA_TEAM_R 2
-#endif
-#ifndef MDMA_TEAM_RG
-#define MDMA_TEAM_RG 1
-#endif
-#ifndef MDMA_TEAM_WAVES_PER_CU
-#define MDMA_TEAM_WAVES_PER_CU 8
-#endif
-
-template <class F, bool F32, int R, int TT, bool GATED>
-void launch_fmt(mdma_ctx *ctx, TeamSet ts, const float *xf, const int8_t *qx, const float *dx, const int32_t *s16,
-                uint32_t T, float *yg) {
-  const uint32_t units = ts.n_in / F::UCOLS;
-  int tw, pl;
-  if (units <= 64) tw = 1, pl = 1;
-  else if (units <= 128) tw = 2, pl = 1;
-  else if (units <= 256) tw = 4, pl = 1;
-  else if (units <= 512) tw = 4, pl = 2;
-  else tw = 4, pl = 4;
-  // Rows per team: enough teams for MDMA_TEAM_WAVES_PER_CU waves per CU,
-  // whole multiples of R rows.
-  uint64_t rows = 0;
-  for (int i = 0; i < ts.n; i++) rows += ts.j[i].n_out;
-  const uint64_t want = (uint64_t)ctx->cu_count * MDMA_TEAM_WAVES_PER_CU / tw;
-  uint64_t rpt = (rows + want - 1) / want;
-  rpt = (rpt + R - 1) / R * R;
-  ts.rpt = (uint32_t)rpt;
-  uint64_t teams = 0;
-  for (int i = 0; i < ts.n; i++) {
-    ts.j[i].teams = (uint32_t)((ts.j[i].n_out + rpt - 1) / rpt);
-    teams += ts.j[i].teams;
-  }
-  const int tpw = WG / 64 / tw;
-  const dim3 grid((uint32_t)((teams + tpw - 1) / tpw)), block(WG);
-  // With timing events set, the dispatch itself timestamps them (kernel-only
-  // duration, as a profiler measures it); they apply to one launch.
-  hipEvent_t t0 = ctx->time_start, t1 = ctx->time_stop;
-  ctx->time_start = ctx->time_stop = nullptr;
-#define MDMA_TEAM_LAUNCH(TW_, PL_)                                                                             \
-  do {                                                                                                          \
-    if (t0 || t1)                                                                                               \
-      hipExtLaunchKernelGGL(gemv_team<F, F32, R, TW_, PL_, TT, GATED>, grid, block, 0, ctx->stream, t0, t1, 0, \
-                            ts, xf, qx, dx, s16, T, yg);                                                        \
-    else                                                                                                        \
-      gemv_team<F, F32, R, TW_, PL_, TT, GATED><<<grid, block, 0, ctx->stream>>>(ts, xf, qx, dx, s16, T, yg);  \
-  } while (0)
-  if (tw == 1) MDMA_TEAM_LAUNCH(1, 1);
-  else if (tw == 2) MDMA_TEAM_LAUNCH(2, 1);
-  else if (pl == 1) MDMA_TEAM_LAUNCH(4, 1);
-  else if (pl == 2) MDMA_TEAM_LAUNCH(4, 2);
-  else MDMA_TEAM_LAUNCH(4, 4);
-#undef MDMA_TEAM_LAUNCH
-  hip_check(hipGetLastError(), "gemv team launch");
-}
-
-template <bool F32, int TT, bool GATED>
-void launch_tt(mdma_ctx *ctx, int32_t dtype, const TeamSet &ts, const float *xf, const int8_t *qx, const float *dx,
-               const int32_t *s16, uint32_t T, float *yg) {
-  constexpr int R = GATED ? MDMA_TEAM_RG : MDMA_TEAM_R;
-  switch (dtype) {
-    case DT_Q4_K: launch_fmt<Q4G, F32, R, TT, GATED>(ctx, ts, xf, qx, dx, s16, T, yg); break;
-    case DT_Q6_K: launch_fmt<Q6G, F32, R, TT, GATED>(ctx, ts, xf, qx, dx, s16, T, yg); break;
-    case DT_Q8_0: launch_fmt<Q8G, F32, R, TT, GATED>(ctx, ts, xf, qx, dx, s16, T, yg); break;
-    default: fail(MDMA_ERR_NOT_IMPLEMENTED, "gemv: dtype has no prepared layout");
-  }
-}
-
-template <bool F32, bool GATED>
-void launch_t(mdma_ctx *ctx, int32_t dtype, const TeamSet &ts, const float *xf, const int8_t *qx, const float *dx,
-              const int32_t *s16, uint32_t T, float *yg) {
-  if (T <= 1) launch_tt<F32, 1, GATED>(ctx, dtype, ts, xf, qx, dx, s16, T, yg);
-  else if (T <= 2) launch_tt<F32, 2, GATED>(ctx, dtype, ts, xf, qx, dx, s16, T, yg);
-  else if (T <= 4) launch_tt<F32, 4, GATED>(ctx, dtype, ts, xf, qx, dx, s16, T, yg);
-  else launch_tt<F32, 8, GATED>(ctx, dtype, ts, xf, qx, dx, s16, T, yg);
-}
 
 // Debug: int32 dot per (token, row, sub-block) from prepared rows, one
 // thread per (token, row, unit), through the same plane loads as the GEMV.
@@ -621,6 +76,7 @@ void launch_gemv_team(mdma_ctx *ctx, int mode, const GemvJob *jobs, int n_jobs, 
   float *dx = nullptr;
   int32_t *s16 = nullptr;
   const bool f32 = mode != MDMA_ACT_I8;
+  const int32_t dt = jobs[0].dtype;
   if (!f32) quantize_into_scratch(ctx, x, T, n_in, &qx, &dx, &s16);
   for (uint64_t t0 = 0; t0 < T; t0 += 8) {
     const uint32_t tn = (uint32_t)(T - t0 < 8 ? T - t0 : 8);
@@ -634,16 +90,14 @@ void launch_gemv_team(mdma_ctx *ctx, int mode, const GemvJob *jobs, int n_jobs, 
     }
     const float *xt = x + t0 * n_in;
     const int8_t *qt = qx ? qx + t0 * n_in : nullptr;
-    const float *dt = dx ? dx + t0 * (n_in / 256) : nullptr;
+    const float *dt_ = dx ? dx + t0 * (n_in / 256) : nullptr;
     const int32_t *st = s16 ? s16 + t0 * (n_in / 16) : nullptr;
     float *yg = gated ? ygated + t0 * jobs[0].n_out : nullptr;
-    if (f32) {
-      if (gated) launch_t<true, true>(ctx, jobs[0].dtype, ts, xt, qt, dt, st, tn, yg);
-      else launch_t<true, false>(ctx, jobs[0].dtype, ts, xt, qt, dt, st, tn, yg);
-    } else {
-      if (gated) launch_t<false, true>(ctx, jobs[0].dtype, ts, xt, qt, dt, st, tn, yg);
-      else launch_t<false, false>(ctx, jobs[0].dtype, ts, xt, qt, dt, st, tn, yg);
-    }
+    const TeamSetArgs a{&ts, xt, qt, dt_, st, tn, yg};
+    if (dt == DT_Q4_K) (f32 ? team_launch_q4_f32 : team_launch_q4_i8)(ctx, gated, a);
+    else if (dt == DT_Q6_K) (f32 ? team_launch_q6_f32 : team_launch_q6_i8)(ctx, gated, a);
+    else if (dt == DT_Q8_0) (f32 ? team_launch_q8_f32 : team_launch_q8_i8)(ctx, gated, a);
+    else fail(MDMA_ERR_NOT_IMPLEMENTED, "gemv: dtype has no prepared layout");
   }
 }
 
