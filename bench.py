@@ -1,12 +1,12 @@
 #!/usr/bin/env python3
 """Headline benchmark: Q4_K decode GEMV at Llama-3-8B layer shapes on one MI355X.
 
-Workload: one step is one pass over a Llama-3-8B layer's
+Workload (the Q4_K decode-GEMV benchmark configuration): one step is one pass over a Llama-3-8B layer's
 seven Q4_K matrix-vector products at batch 1 (q and o 4096x4096, k and v
 1024x4096, gate and up 14336x4096, down 4096x14336), issued the way the decode
 path issues them: fused QKV, o, fused gate/up + SiLU, down -- four launches,
-each reading its own input buffer. Weights are synthetic with the BASELINE
-distribution and rotate over >= 1 GiB of distinct device copies so the 256 MB
+each reading its own input buffer. Weights are synthetic (f16 d, dmin = |N(0,1)|*1e-3,
+six-bit scales and mins uniform in [0,63], nibbles uniform in [0,15]) and rotate over >= 1 GiB of distinct device copies so the 256 MB
 Infinity Cache cannot serve them. Each step is one replay of a captured HIP
 graph; the timed region is bracketed by stream synchronisation and HIP events
 recorded on the library's own stream.
@@ -21,7 +21,7 @@ sums).
 Also reported: per-launch rates (kernel-only from the dispatch's own
 timestamps, and back to back in a graph), the roofline of the dominant
 kernel (the fused gate/up GEMV, 66 MB per launch), the Q6_K GEMVs of
-BASELINE config 3 (output head 128256x4096 and down 4096x14336 at batch 1, 4
+the Q6_K configuration (output head 128256x4096 and down 4096x14336 at batch 1, 4
 and 8), a device copy-bandwidth probe, and the CPU baseline (the C
 restatement of CpuBackend::qmatmul on this host's cores, on a bounded sample
 of the same step).
@@ -175,7 +175,7 @@ def per_launch(be, ev, wl, mode, reps):
 
 
 Q6K = 14
-# Q6_K GEMVs of BASELINE config 3: the output head and the down projection
+# Q6_K GEMVs of the Q4_K_M mix: the output head and the down projection
 # of the Q4_K_M mix, at batch 1, 4 and 8.
 Q6_SHAPES = {"q6k_head": (128256, 4096), "q6k_down": (4096, 14336)}
 

@@ -3,9 +3,8 @@
  *
  * A C ABI that carries the reference's `trait Backend`
  * (/root/reference/src/backend.rs:190-601) one method per entry point, so a
- * Rust `impl Backend for Gfx950Backend` can wrap it without glue logic
- * (the binding is shown in INTEGRATION.md). Citations are path:line inside
- * the reference checkout.
+ * Rust `impl Backend for Gfx950Backend` can wrap it without glue logic.
+ * Citations are path:line inside the reference checkout.
  *
  * Conventions
  *  - Every entry point returns an mdma_status; on failure the message is

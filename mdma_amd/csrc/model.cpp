@@ -468,7 +468,13 @@ int mdma_gfx950_model_load(mdma_ctx *ctx, const char *path, uint64_t budget_byte
     m->ctx = ctx;
     m->cfg = preflight(g);
     m->budget = budget_bytes;
-    for (auto &kv : g.tensors) m->weight_bytes += kv.second.bytes;
+    // Device bytes as allocated: Q4_K / Q6_K / Q8_0 matrices in the prepared
+    // layout (rows padded to 16 bytes), every buffer rounded to 256 bytes.
+    for (auto &kv : g.tensors) {
+      const GgufTensor &t = kv.second;
+      const uint64_t n = gfx950_layout_dtype(t.dtype) ? t.rows * gfx950_row_bytes(t.dtype, t.cols) : t.bytes;
+      m->weight_bytes += (n + 255) / 256 * 256;
+    }
     reserve(m.get(), m->weight_bytes);  // Model::load_reserved: before any upload
     std::vector<uint8_t> tmp;
     m->token_embd = load_weight(m.get(), g, "token_embd.weight", tmp);

@@ -1,4 +1,4 @@
-"""Synthetic Llama GGUF models with the BASELINE geometries and distributions.
+"""Synthetic Llama GGUF models with the benchmark geometries and distributions.
 
 config 1: TinyStories-15M geometry, every linear Q8_0 (d = f16(|N|*0.02),
           quants uniform in [-127, 127]), embeddings and norms f32 N(0, 0.02).

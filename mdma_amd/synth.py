@@ -1,4 +1,4 @@
-"""Seeded synthetic GGUF blocks and activations with the BASELINE distributions.
+"""Seeded synthetic GGUF blocks and activations with the benchmark distributions.
 
 One counter-based splitmix64 stream per (seed, purpose) feeds everything, so a
 JSON report that names the seed names the exact bytes. Normals come from
@@ -90,7 +90,7 @@ def pack_q4k_scales(sc: np.ndarray, m: np.ndarray) -> np.ndarray:
 
 
 def q4k_blocks(n_blocks: int, seed: int, d_scale: float = 1e-3) -> np.ndarray:
-    """d, dmin = f16(|N(0,1)|*1e-3), six-bit scales and
+    """Q4_K: d, dmin = f16(|N(0,1)|*1e-3), six-bit scales and
     mins uniform in [0,63], 4-bit quants uniform in [0,15]."""
     s = Stream(seed)
     d = np.abs(s.normal(n_blocks)) * d_scale
@@ -106,7 +106,7 @@ def q4k_blocks(n_blocks: int, seed: int, d_scale: float = 1e-3) -> np.ndarray:
 
 
 def q6k_blocks(n_blocks: int, seed: int, d_scale: float = 1e-3) -> np.ndarray:
-    """uniform ql/qh bytes, int8 sub-scales uniform in
+    """Q6_K: uniform ql/qh bytes, int8 sub-scales uniform in
     [-64,63], d = f16(|N(0,1)|*1e-3)."""
     s = Stream(seed)
     blk = np.empty((n_blocks, 210), dtype=np.uint8)
@@ -117,7 +117,7 @@ def q6k_blocks(n_blocks: int, seed: int, d_scale: float = 1e-3) -> np.ndarray:
 
 
 def q8_0_blocks(n_blocks: int, seed: int, d_scale: float = 0.02) -> np.ndarray:
-    """fp16 d = |N(0,1)|*0.02, int8 quants uniform in [-127,127]."""
+    """Q8_0: fp16 d = |N(0,1)|*0.02, int8 quants uniform in [-127,127]."""
     s = Stream(seed)
     blk = np.empty((n_blocks, 34), dtype=np.uint8)
     blk[:, 0:2] = f16_bytes(np.abs(s.normal(n_blocks)) * d_scale)
@@ -126,7 +126,7 @@ def q8_0_blocks(n_blocks: int, seed: int, d_scale: float = 0.02) -> np.ndarray:
 
 
 def weight(dtype: int, n_out: int, n_in: int, seed: int) -> np.ndarray:
-    """Raw GGUF bytes of an [n_out, n_in] weight with the BASELINE distribution."""
+    """Raw GGUF bytes of an [n_out, n_in] weight with the benchmark distribution of its dtype."""
     nb = n_out * (n_in // BLOCK_SIZE[dtype])
     if dtype == GGML_Q4_K:
         return q4k_blocks(nb, seed)

@@ -11,7 +11,7 @@
  * (Cargo.lock:465-468; called from src/backend/cpu/dequant.rs:36), which is
  * not vendored in the reference. Their formulas are pinned by the reference's
  * own known-answer test (src/cache/layout/tests.rs:8-55, restated in
- * tests/test_oracle.py) and by closed forms; see the pin table in DESIGN.md.
+ * tests/test_oracle.py) and by closed forms checked in tests/test_oracle.py.
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load
  * this library. The product library (mdma_amd/) never links or calls it.

@@ -48,13 +48,11 @@ int orc_attention(const float *q, size_t q_elems, const float *k, const float *v
                   float *o, size_t o_elems);
 uint32_t orc_greedy(const float *logits, size_t n);
 
-/* Int8 activation mode (BASELINE definition, built in the Q8_1 pattern of the reference). */
+/* Int8 activation mode: groups of 256 (decode) or 32 (prefill) with an f32
+ * scale, rounded by the Q8_1 rule of the reference. */
 int orc_quantize_act(const float *x, size_t n, size_t group, int8_t *q, float *d, int32_t *sum16);
 int orc_block_dot_i32(int dtype, const uint8_t *w, size_t w_bytes, size_t n_out, size_t n_in,
                       const int8_t *qx, size_t n_tokens, int32_t *out);
-int orc_qmatmul_i8_epilogue(int dtype, const uint8_t *w, size_t w_bytes, size_t n_out,
-                            size_t n_in, const int8_t *qx, const float *dx, const int32_t *sum16,
-                            size_t n_tokens, float *y);
 
 /* Llama decode (reference src/model/arch/llama.rs:158-246, src/model.rs:326-468). */
 typedef struct {

@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Writes the committed golden fixtures under tests/golden/ from the CPU oracle.
 
-- config1_tokens.json: 64 greedy tokens of the BASELINE config-1 model
+- config1_tokens.json: 64 greedy tokens of the TinyStories-15M-geometry model
   (TinyStories-15M geometry, Q8_0 linears, seeds 1 and 2, f16-rounded KV).
 - qmatmul_small.npz: raw blocks, x and oracle outputs for Q8_0 / Q4_K / Q6_K
   at the reference's test shapes (rows 1/7/9/20 x K 256/512/768 as in

@@ -1,6 +1,6 @@
 """End-to-end Llama decoding on the GPU against the CPU oracle.
 
-BASELINE config 1 (TinyStories-15M geometry, all linears Q8_0, random init,
+The TinyStories-15M configuration (geometry, all linears Q8_0, random init,
 written as GGUF): 64-token greedy decode from a seeded 8-token prompt must give
 exactly the oracle's tokens in the f32-activation mode. The oracle stores K/V
 through f16 as the device cache does (the pattern of
@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 from mdma_amd import gguf, llama_synth, synth
-from mdma_amd.backend import ACT_F32, ACT_I8, ContextLimit, MemoryBudget, ShapeMismatch
+from mdma_amd.backend import ACT_F32, ACT_I8, ContextLimit, MemoryBudget, ShapeMismatch, prepared_bytes
 from mdma_amd.model import Model
 from oracle import ffi
 
@@ -107,7 +107,10 @@ def test_memory_plan_and_limits(backend, tiny):
     assert (c.n_layers, c.n_embd, c.n_heads, c.head_dim, c.n_ff, c.vocab, c.n_ctx) == (6, 288, 6, 48, 768, 32000, 256)
     p = m.plan(256, 1, 8)
     assert p.kv_bytes == 6 * 2 * 256 * 288 * 2
-    assert p.weight_bytes == sum(t.n_bytes for t in gguf.Reader(tiny[1]).tensors.values())
+    # Device bytes: quantized matrices in the prepared layout, 256-byte allocations.
+    dev = [prepared_bytes(t.dtype, t.shape[0], t.shape[1]) if t.dtype in (8, 12, 14) else t.n_bytes
+           for t in gguf.Reader(tiny[1]).tensors.values()]
+    assert p.weight_bytes == sum(-(-n // 256) * 256 for n in dev)
     assert p.max_context == 256 and p.device_bytes > 250e9
     with pytest.raises(ContextLimit):
         m.session(257, 1, 8)
