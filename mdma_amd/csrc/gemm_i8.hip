@@ -1,0 +1,252 @@
+// Prefill GEMM on gfx950: int8 MFMA over Q8_0 / Q4_K weights in the prepared
+// layout, activations quantized per 32 to int8 with an f32 scale.
+//
+// Y[m, n] = sum_k X[m, k] * deq(W)[n, k]   (reference HipBackend::qmatmul_i8,
+// /root/reference/src/backend/rocm.rs:1759-1918, the WMMA prefill of
+// src/backend/rocm/kernels/kernels.hip:1158-2806; CPU oracle
+// src/backend/cpu.rs:335-368 on the requantized activations)
+//
+// Each 32-wide K block is one v_mfma_i32_32x32x32_i8 per 32x32 output tile:
+// the exact int32 block dot of int8 weights and int8 activations. The
+// epilogue applies that block's scales and accumulates in f64 (full rate on
+// CDNA, like non-packed f32), so outputs that cancel keep their accuracy:
+//   Q8_0: acc += (s_x[m] * d_w[n]) * I
+//   Q4_K: acc += (s_x[m] * d*sc[n]) * I - (dmin*m[n]) * (s_x[m] * sum_k qx[m, k])
+// Weights are unpacked to int8 (Q4_K nibbles 0..15) in LDS with their block
+// scales; activation rows and their scales are staged beside them.
+//
+// Tiling: a 256-thread workgroup computes a 64x128 tile of Y; each of its 4
+// waves owns 32x64 (1x2 MFMA tiles). K advances 128 columns (4 blocks) per
+// stage; the next stage's global loads are in registers while the current
+// stage computes. LDS rows of 32 bytes are padded to 48 so that the 16-byte
+// operand reads of 16 lanes hit all 64 banks once.
+#include <hip/hip_ext.h>
+
+#include "kernels.h"
+
+namespace mdma {
+namespace {
+
+constexpr int BM = 64, BN = 128, BK = 128, KB = BK / 32, LDR = 48;
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+struct GemmArgs {
+  const int8_t *qx;    // [M, K] int8
+  const float *sx;     // [M, K/32] per-32 activation scales
+  const int32_t *s16;  // [M, K/16] exact sums of 16 activations
+  const uint8_t *w;    // prepared rows, row_bytes apart
+  float *y;            // [M, N]
+  uint32_t M, N, K;
+  uint64_t row_bytes;
+};
+
+template <int DT>
+__global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) int8_t xs[KB][BM][LDR];
+  __shared__ __attribute__((aligned(16))) int8_t ws[KB][BN][LDR];
+  __shared__ __attribute__((aligned(16))) double sxs[KB][BM];  // s_x
+  __shared__ __attribute__((aligned(16))) float sws[KB][BN];   // d_w (Q8_0) or d*sc (Q4_K)
+  __shared__ __attribute__((aligned(16))) double sbs[KB][BM];  // Q4_K: s_x * sum of the block's 32 activations
+  __shared__ __attribute__((aligned(16))) float dms[KB][BN];   // Q4_K: dmin*m
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t bm = blockIdx.y * BM, bn = blockIdx.x * BN;
+  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 64;
+  const uint32_t K = a.K, nk32 = K / 32;
+
+  // ---- global -> register staging of one K stage ----
+  // X: 64 rows x 128 bytes = 512 chunks of 16 B, 2 per thread.
+  // W: Q8_0 128 rows x 4 blocks x 2 halves; Q4_K 128 rows x 2 pair units x 2 planes.
+  uint4 rx[2], rw[4];
+  uint32_t rh = 0, rh2 = 0, rh3 = 0, rh4 = 0;  // Q8_0 d (2 x f16 per dword) / Q4_K header dwords
+  float rsx;
+  int rsb = 0;
+  auto gload = [&](uint32_t k0) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int c = tid + 256 * i, row = c >> 3, part = c & 7;
+      const uint32_t gm = min(bm + row, a.M - 1);
+      rx[i] = ldx16(a.qx + (size_t)gm * K + k0 + 16 * part);
+    }
+    {  // scales: 64 rows x 4 blocks = 256, 1 per thread
+      const int row = tid >> 2, kb = tid & 3;
+      const uint32_t gm = min(bm + row, a.M - 1);
+      rsx = a.sx[(size_t)gm * nk32 + k0 / 32 + kb];
+      if (DT == DT_Q4_K) {
+        const int2 s = *reinterpret_cast<const int2 *>(a.s16 + (size_t)gm * (K / 16) + k0 / 16 + 2 * kb);
+        rsb = s.x + s.y;
+      }
+    }
+    if (DT == DT_Q8_0) {
+      const uint32_t nb = K / 32;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int c = tid + 256 * i, row = c >> 3, blk = (c >> 1) & 3, half = c & 1;
+        const uint32_t gn = min(bn + row, a.N - 1);
+        const uint8_t *rp = a.w + gn * a.row_bytes;
+        rw[i] = ld16(rp + 16 * ((half ? nb : 0) + k0 / 32 + blk));
+      }
+      // d: 128 rows x 4 blocks x 2 B = 256 dwords (two blocks per dword), 1 per thread.
+      const int row = tid >> 1, pairb = tid & 1;
+      const uint32_t gn = min(bn + row, a.N - 1);
+      rh = *reinterpret_cast<const uint32_t *>(a.w + gn * a.row_bytes + 32 * (size_t)nb + 2 * (k0 / 32) + 4 * pairb);
+    } else {
+      const uint32_t U = K / 64;
+#pragma unroll
+      for (int i = 0; i < 2; i++) {  // 128 rows x 2 units x 2 planes = 512 chunks
+        const int c = tid + 256 * i, row = c >> 2, unit = (c >> 1) & 1, plane = c & 1;
+        const uint32_t gn = min(bn + row, a.N - 1);
+        const uint8_t *rp = a.w + gn * a.row_bytes;
+        rw[i] = ld16(rp + 16 * ((plane ? U : 0) + k0 / 64 + unit));
+      }
+      // header of the stage's block: 128 rows x 16 B, threads 0..127 one each.
+      if (tid < 128) {
+        const uint32_t gn = min(bn + tid, a.N - 1);
+        const uint4 hd = ldx16(a.w + gn * a.row_bytes + 32 * (size_t)U + 16 * (k0 / 256));
+        rh = hd.x, rh2 = hd.y, rh3 = hd.z, rh4 = hd.w;
+      }
+    }
+  };
+  // ---- register -> LDS ----
+  auto lstore = [&](uint32_t k0) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int c = tid + 256 * i, row = c >> 3, part = c & 7;
+      *reinterpret_cast<uint4 *>(&xs[part >> 1][row][16 * (part & 1)]) = rx[i];
+    }
+    {
+      const int row = tid >> 2, kb = tid & 3;
+      sxs[kb][row] = (double)rsx;
+      if (DT == DT_Q4_K) sbs[kb][row] = (double)rsx * (double)rsb;
+    }
+    if (DT == DT_Q8_0) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int c = tid + 256 * i, row = c >> 3, blk = (c >> 1) & 3, half = c & 1;
+        *reinterpret_cast<uint4 *>(&ws[blk][row][16 * half]) = rw[i];
+      }
+      const int row = tid >> 1, pairb = tid & 1;
+      sws[2 * pairb][row] = h2f(rh);
+      sws[2 * pairb + 1][row] = h2f(rh >> 16);
+    } else {
+      // Pair unit (within the stage) -> sub-blocks 2*unit (low nibbles) and
+      // 2*unit+1 (high nibbles); plane -> bytes [16*plane, 16*plane+16).
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        const int c = tid + 256 * i, row = c >> 2, unit = (c >> 1) & 1, plane = c & 1;
+        const uint4 q = rw[i];
+        const uint4 lo = make_uint4(q.x & 0x0F0F0F0Fu, q.y & 0x0F0F0F0Fu, q.z & 0x0F0F0F0Fu, q.w & 0x0F0F0F0Fu);
+        const uint4 hi = make_uint4((q.x >> 4) & 0x0F0F0F0Fu, (q.y >> 4) & 0x0F0F0F0Fu, (q.z >> 4) & 0x0F0F0F0Fu,
+                                    (q.w >> 4) & 0x0F0F0F0Fu);
+        *reinterpret_cast<uint4 *>(&ws[2 * unit][row][16 * plane]) = lo;
+        *reinterpret_cast<uint4 *>(&ws[2 * unit + 1][row][16 * plane]) = hi;
+      }
+      if (tid < 128) {
+        const uint4 hd = make_uint4(rh, rh2, rh3, rh4);
+        const float d = h2f(rh), dmin = h2f(rh >> 16);
+        const int p0 = (k0 % 256) / 64;  // first pair of this stage in its block
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+          int sca, scb, ma, mb;
+          q4k_scales_i(hd, p0 + u, sca, scb, ma, mb);
+          sws[2 * u][tid] = d * (float)sca;
+          sws[2 * u + 1][tid] = d * (float)scb;
+          dms[2 * u][tid] = dmin * (float)ma;
+          dms[2 * u + 1][tid] = dmin * (float)mb;
+        }
+      }
+    }
+  };
+
+  double acc[2][16];
+#pragma unroll
+  for (int j = 0; j < 2; j++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[j][r] = 0.0;
+
+  const int lr = lane & 31, lk = lane >> 5;  // operand row/column, K half
+  gload(0);
+  for (uint32_t k0 = 0; k0 < K; k0 += BK) {
+    __syncthreads();  // the previous stage's reads of LDS are done
+    lstore(k0);
+    __syncthreads();
+    if (k0 + BK < K) gload(k0 + BK);
+#pragma unroll
+    for (int kb = 0; kb < KB; kb++) {
+      const uint4 t = *reinterpret_cast<const uint4 *>(&xs[kb][wm + lr][16 * lk]);
+      const v4i av = v4i{(int)t.x, (int)t.y, (int)t.z, (int)t.w};
+      v4i bv[2];
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const uint4 u = *reinterpret_cast<const uint4 *>(&ws[kb][wn + 32 * j + lr][16 * lk]);
+        bv[j] = v4i{(int)u.x, (int)u.y, (int)u.z, (int)u.w};
+      }
+      // Rows of result register r: (r&3) + 4*lk + 8*(r>>2) of the tile.
+      double sx[16], sb[16];
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+#pragma unroll
+        for (int e = 0; e < 4; e += 2) {
+          const double2 s2 = *reinterpret_cast<const double2 *>(&sxs[kb][wm + 8 * g + 4 * lk + e]);
+          sx[4 * g + e] = s2.x, sx[4 * g + e + 1] = s2.y;
+          if (DT == DT_Q4_K) {
+            const double2 b2 = *reinterpret_cast<const double2 *>(&sbs[kb][wm + 8 * g + 4 * lk + e]);
+            sb[4 * g + e] = b2.x, sb[4 * g + e + 1] = b2.y;
+          }
+        }
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        v16i c = {};
+        c = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[j], c, 0, 0, 0);
+        const double sw = (double)sws[kb][wn + 32 * j + lr];
+        const double dm = DT == DT_Q4_K ? (double)dms[kb][wn + 32 * j + lr] : 0.0;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          acc[j][r] = fma(sx[r] * sw, (double)c[r], acc[j][r]);
+          if (DT == DT_Q4_K) acc[j][r] = fma(-dm, sb[r], acc[j][r]);
+        }
+      }
+    }
+  }
+  // ---- store ----
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const uint32_t n = bn + wn + 32 * j + lr;
+    if (n >= a.N) continue;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const uint32_t m = bm + wm + (r & 3) + 4 * lk + 8 * (r >> 2);
+      if (m < a.M) a.y[(size_t)m * a.N + n] = (float)acc[j][r];
+    }
+  }
+}
+
+}  // namespace
+
+bool gemm_i8_supported(int32_t dtype, int layout, uint64_t n_in) {
+  if (layout != MDMA_LAYOUT_GFX950) return false;
+  if (dtype == DT_Q8_0) return n_in % BK == 0;
+  if (dtype == DT_Q4_K) return n_in % 256 == 0;
+  return false;
+}
+
+void launch_gemm_i8(mdma_ctx *ctx, const GemvJob &w, const int8_t *qx, const float *sx, const int32_t *s16,
+                    uint64_t M, float *y) {
+  GemmArgs a{qx, sx, s16, w.w, y, (uint32_t)M, (uint32_t)w.n_out, (uint32_t)w.n_in,
+             gfx950_row_bytes(w.dtype, w.n_in)};
+  const dim3 grid((uint32_t)((w.n_out + BN - 1) / BN), (uint32_t)((M + BM - 1) / BM)), block(256);
+  hipEvent_t t0 = ctx->time_start, t1 = ctx->time_stop;
+  ctx->time_start = ctx->time_stop = nullptr;
+  if (w.dtype == DT_Q8_0) {
+    if (t0 || t1) hipExtLaunchKernelGGL(gemm_i8_kernel<DT_Q8_0>, grid, block, 0, ctx->stream, t0, t1, 0, a);
+    else gemm_i8_kernel<DT_Q8_0><<<grid, block, 0, ctx->stream>>>(a);
+  } else {
+    if (t0 || t1) hipExtLaunchKernelGGL(gemm_i8_kernel<DT_Q4_K>, grid, block, 0, ctx->stream, t0, t1, 0, a);
+    else gemm_i8_kernel<DT_Q4_K><<<grid, block, 0, ctx->stream>>>(a);
+  }
+  hip_check(hipGetLastError(), "gemm i8 launch");
+}
+
+}  // namespace mdma

@@ -852,7 +852,27 @@ void launch_gemv_f32_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up
   });
 }
 
+// Prefill-sized int8 calls (T >= GEMM_MIN_TOKENS) on prepared Q8_0 / Q4_K
+// weights run the MFMA GEMM with activations quantized per 32 (quantized
+// once for every job sharing x). Returns false when a job is not covered.
+static bool try_gemm_i8(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t T) {
+  if (T < GEMM_MIN_TOKENS) return false;
+  for (int i = 0; i < n_jobs; i++)
+    if (!gemm_i8_supported(jobs[i].dtype, jobs[i].layout, jobs[i].n_in) || jobs[i].n_in != jobs[0].n_in)
+      return false;
+  const uint64_t n_in = jobs[0].n_in, n = T * n_in;
+  const uint64_t qb = (n + 255) / 256 * 256, db = (n / 32 * 4 + 255) / 256 * 256, sb = n / 16 * 4;
+  char *s = scratch(ctx, qb + db + sb);
+  int8_t *qx = reinterpret_cast<int8_t *>(s);
+  float *dx = reinterpret_cast<float *>(s + qb);
+  int32_t *s16 = reinterpret_cast<int32_t *>(s + qb + db);
+  launch_quantize_act(ctx, x, n, 32, qx, dx, s16);
+  for (int i = 0; i < n_jobs; i++) launch_gemm_i8(ctx, jobs[i], qx, dx, s16, T, jobs[i].y);
+  return true;
+}
+
 void launch_gemv_i8(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t T) {
+  if (try_gemm_i8(ctx, jobs, n_jobs, x, T)) return;
   for (int i = 0; i < n_jobs; i++)
     if (!is_i8_dtype(jobs[i].dtype) || jobs[i].n_in % 256) {
       // No int8 kernel for float weights (or rows that are not whole 256-groups):
@@ -884,6 +904,10 @@ void launch_gemv_i8(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float 
 void launch_gemv_i8_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up, const float *x, uint64_t T,
                           float *y) {
   const GemvJob gu[2] = {gate, up};
+  if (try_gemm_i8(ctx, gu, 2, x, T)) {
+    launch_silu_mul(ctx, gate.y, up.y, y, T * gate.n_out);
+    return;
+  }
   if (team_layout_ok(gu, 2) && gate.n_in % 256 == 0) {
     launch_gemv_team(ctx, MDMA_ACT_I8, gu, 2, true, x, T, y);
     return;

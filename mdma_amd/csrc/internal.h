@@ -146,6 +146,14 @@ void launch_gemv_team(mdma_ctx *ctx, int mode, const GemvJob *jobs, int n_jobs, 
 // exactly this x.
 void quantize_into_scratch(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in, int8_t **qx, float **dx,
                            int32_t **s16);
+// Prefill int8 MFMA GEMM (gemm_i8.hip) over prepared Q8_0 / Q4_K weights:
+// whether it covers (dtype, layout, n_in), and the launch for M tokens with
+// activations quantized per 32 (qx [M, K], sx [M, K/32], s16 [M, K/16]).
+bool gemm_i8_supported(int32_t dtype, int layout, uint64_t n_in);
+void launch_gemm_i8(mdma_ctx *ctx, const GemvJob &w, const int8_t *qx, const float *sx, const int32_t *s16,
+                    uint64_t M, float *y);
+// Token count from which the int8 mode runs the MFMA GEMM instead of the GEMV.
+constexpr uint64_t GEMM_MIN_TOKENS = 16;
 void launch_quantize_act(mdma_ctx *ctx, const float *x, uint64_t n, uint64_t group, int8_t *q,
                          float *d, int32_t *sum16);
 void launch_block_dot(mdma_ctx *ctx, const GemvJob &w, const int8_t *qx, uint64_t T, int32_t *out);

@@ -397,3 +397,69 @@ def test_packed_upload_rejects_wrong_sizes(backend):
         backend.upload_weight(raw[:-16], Q4K, (4, 256), LAYOUT_GFX950)
     with pytest.raises(backend_mod.NotImplemented):
         backend.upload_weight(np.zeros(4 * 256 * 4, np.uint8), F32, (4, 256), LAYOUT_GFX950)
+
+
+# ------------------------------------------------------- prefill GEMM ----
+# int8 mode with T >= 16 tokens on prepared Q8_0 / Q4_K weights runs the
+# int8 MFMA GEMM: activations quantized per 32 with an f32 scale. Oracle: the
+# reference's "requantize, then CPU qmatmul" (src/backend/rocm/decode/tests.rs:68-130).
+
+def oracle_i8_32(dtype, raw, rows, k, x):
+    q, d, _ = ffi.quantize_act(x, 32)
+    return oracle_f32(dtype, raw, rows, k, ffi.dequantize_act(q, d, 32))
+
+
+@pytest.mark.parametrize("shape", [(16, 256, 64), (37, 512, 200), (130, 1024, 257), (64, 4096, 384)])
+@pytest.mark.parametrize("dtype", [Q8, Q4K])
+def test_prefill_gemm_i8(backend, dtype, shape):
+    T, k, rows = shape
+    raw = synth.weight(dtype, rows, k, 300 + T)
+    x = synth.normal_f32(T * k, 301 + rows)
+    got = run_qmatmul(backend, dtype, raw, rows, k, x, "i8")
+    cpu, exact = oracle_i8_32(dtype, raw, rows, k, x)
+    assert_parity(got, cpu, exact, 1e-3, what=f"gemm dtype={dtype} T={T} k={k} rows={rows}")
+
+
+@pytest.mark.parametrize("dtype", [Q8, Q4K])
+def test_prefill_gemm_config4_shapes_sampled_rows(backend, dtype):
+    """Full config-4 shapes on the GPU; the oracle checks a sample of output
+    rows (the weight rows are contiguous, so a row slice is its own weight)."""
+    for T, k, rows in ((512, 4096, 14336), (2048, 14336, 4096)):
+        raw = synth.weight(dtype, rows, k, 400 + T)
+        x = synth.normal_f32(T * k, 401 + T)
+        w = backend.upload_weight(raw, dtype, (rows, k))
+        xb, yb = backend.f32_buf(x), backend.alloc(T * rows * 4)
+        backend.qmatmul_i8(w, xb, yb)
+        y = backend.download_f32(yb).reshape(T, rows)
+        rb = len(raw) // rows
+        for r0 in (0, rows // 2 + 13, rows - 16):
+            sl = raw[r0 * rb:(r0 + 16) * rb]
+            tok = np.r_[0:8, T - 8:T]
+            cpu, exact = oracle_i8_32(dtype, sl, 16, k, x.reshape(T, k)[tok].reshape(-1))
+            assert_parity(y[tok, r0:r0 + 16].reshape(-1), cpu, exact, 1e-3,
+                          what=f"gemm config4 dtype={dtype} T={T} rows {r0}..")
+        w.buf.close(), xb.close(), yb.close()
+
+
+@pytest.mark.parametrize("dtype", [Q8, Q4K])
+def test_prefill_gemm_fused_calls(backend, dtype):
+    backend.set_act_mode(1)
+    try:
+        T, k, n = 24, 512, 160
+        raws = [synth.weight(dtype, n, k, 500 + i) for i in range(3)]
+        ws = [backend.upload_weight(r, dtype, (n, k)) for r in raws]
+        x = synth.normal_f32(T * k, 510)
+        xb = backend.f32_buf(x)
+        outs = [backend.alloc(T * n * 4) for _ in range(3)]
+        backend.qmatmul_qkv(ws[0], ws[1], ws[2], xb, *outs)
+        for i in range(3):
+            cpu, exact = oracle_i8_32(dtype, raws[i], n, k, x)
+            assert_parity(backend.download_f32(outs[i]), cpu, exact, 1e-3, what=f"gemm qkv {i}")
+        y = backend.alloc(T * n * 4)
+        backend.ffn_gate_up(ws[0], ws[1], xb, outs[0], outs[1], y)
+        g = oracle_i8_32(dtype, raws[0], n, k, x)[0].astype(np.float32)
+        u = oracle_i8_32(dtype, raws[1], n, k, x)[0].astype(np.float32)
+        want = ffi.silu_mul(g.reshape(-1), u.reshape(-1))
+        np.testing.assert_allclose(backend.download_f32(y), want, rtol=2e-3, atol=1e-3)
+    finally:
+        backend.set_act_mode(0)
