@@ -20,7 +20,9 @@ sums).
 
 Also reported: per-launch rates (kernel-only from the dispatch's own
 timestamps, and back to back in a graph), the roofline of the dominant
-kernel (the fused gate/up GEMV, 66 MB per launch), the Q6_K GEMVs of
+kernel (the fused gate/up GEMV, 66 MB per launch), the prefill int8 MFMA
+GEMM (512x4096->14336 and 2048x14336->4096, Q4_K and Q8_0 weights; TOPS
+against the 5.0 POPS int8 peak), the Q6_K GEMVs of
 the Q6_K configuration (output head 128256x4096 and down 4096x14336 at batch 1, 4
 and 8), a device copy-bandwidth probe, and the CPU baseline (the C
 restatement of CpuBackend::qmatmul on this host's cores, on a bounded sample
@@ -220,6 +222,53 @@ def q6k_gemvs(be, ev, reps):
     return out
 
 
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POPS
+GEMM_SHAPES = [(512, 4096, 14336), (2048, 14336, 4096)]  # (M tokens, K, N)
+
+
+def prefill_gemms(be, ev, reps):
+    """Prefill int8 MFMA GEMM at the two prefill shapes, Q4_K and Q8_0
+    weights: kernel-only GEMM duration (dispatch timestamps) and the whole
+    qmatmul call (per-32 activation quantization + GEMM) timed by events on
+    the stream. TOPS = 2*M*N*K / time."""
+    from mdma_amd import synth
+    from mdma_amd.backend import ACT_I8
+
+    be.set_act_mode(ACT_I8)
+    out = {}
+    for M, K, N in GEMM_SHAPES:
+        x = be.f32_buf(synth.normal_f32(M * K, SEED + 20))
+        y = be.alloc(M * N * 4)
+        for dt, name in ((12, "q4k"), (8, "q8_0")):
+            raw = synth.weight(dt, N, K, SEED + 21)
+            w = be.upload_weight(raw, dt, (N, K))
+            be.qmatmul(w, x, y)
+            be.join_execution()
+            st, sp = [ev.event() for _ in range(reps)], [ev.event() for _ in range(reps)]
+            for i in range(reps):
+                be.time_next_gemv(st[i].value, sp[i].value)
+                be.qmatmul(w, x, y)
+            be.join_execution()
+            us = sum(ev.elapsed_ms(st[i], sp[i]) for i in range(reps)) * 1e3 / reps
+            a, b = ev.event(), ev.event()
+            ev.record(a, be.stream())
+            for i in range(reps):
+                be.qmatmul(w, x, y)
+            ev.record(b, be.stream())
+            us_call = ev.elapsed_ms(a, b) * 1e3 / reps
+            for e in st + sp + [a, b]:
+                ev.destroy(e)
+            ops = 2.0 * M * N * K
+            out[f"{name}_M{M}_K{K}_N{N}"] = {
+                "us_kernel": round(us, 2), "TOPS_kernel": round(ops / us / 1e6, 1),
+                "pct_of_int8_peak": round(100 * ops / us / 1e6 / INT8_PEAK_TOPS, 2),
+                "us_call": round(us_call, 2), "TOPS_call": round(ops / us_call / 1e6, 1), "launches_timed": reps}
+            w.buf.close()
+        x.close()
+        y.close()
+    return out
+
+
 def copy_probe(be, ev, nbytes=1 << 30, reps=10):
     """Device-to-device copy rate (bytes read + bytes written per second) of
     hipMemcpyAsync on the library's stream: the achievable-bandwidth
@@ -301,6 +350,7 @@ def main():
                          "step_bytes": step_bytes, "per_launch": per_launch(be, ev, wl, mode, args.reps)}
     be.set_act_mode(ACT_I8)
     q6 = q6k_gemvs(be, ev, max(2, args.reps // 4))
+    gemm = prefill_gemms(be, ev, max(2, args.reps // 4))
 
     main_mode = results["i8"]
     dom = main_mode["per_launch"]["gate_up"]
@@ -325,6 +375,7 @@ def main():
         "f32_mode": {"GBps": round(f["GBps"], 1), "ms_per_step": round(f["ms_per_step"], 5),
                      "pct_of_hbm_peak": round(100 * f["GBps"] / HBM_PEAK_GBS, 2), "per_launch": f["per_launch"]},
         "q6k_gemv": q6,
+        "prefill_gemm_i8": gemm,
         "copy_probe": probe,
         "device": be.device_label(),
     }
