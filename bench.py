@@ -269,6 +269,47 @@ def prefill_gemms(be, ev, reps):
     return out
 
 
+def e2e_decode(be, n_prompt=512, n_gen=256, batches=(1, 8), path="/tmp/mdma_bench_llama3_8b_q4km.gguf"):
+    """Llama-3-8B geometry, Q4_K_M mix (attention and down Q6_K, gate/up and
+    token_embd Q4_K, head Q6_K), random init written as GGUF; a 512-token
+    random prompt prefill, then greedy decode at batch 1 and 8, int8
+    activations, f16 KV. Step times come from HIP events recorded on the
+    stream between steps (the whole generation is queued on the device;
+    tokens feed back through device memory)."""
+    from mdma_amd import llama_synth
+    from mdma_amd.backend import ACT_I8
+    from mdma_amd.model import Model
+
+    t0 = time.perf_counter()
+    if not os.path.exists(path):
+        llama_synth.write(path, llama_synth.LLAMA3_8B, llama_synth.Q4_K_M, SEED, fast=True)
+    print(f"[bench] e2e: model written in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+    be.set_act_mode(ACT_I8)
+    t0 = time.perf_counter()
+    m = Model(be, path)
+    load_s = time.perf_counter() - t0
+    out = {"model": "Llama-3-8B geometry, Q4_K_M mix, random init", "weight_bytes": int(m.plan(1).weight_bytes),
+           "load_seconds": round(load_s, 2), "prompt_tokens": n_prompt, "decode_tokens": n_gen}
+    from mdma_amd import synth
+    for B in batches:
+        s = m.session(n_prompt + n_gen, B, n_prompt)
+        prompts = np.stack([synth.tokens(n_prompt, 128256, SEED + 50 + b) for b in range(B)])
+        s.generate(prompts, 4)  # warm: code paths, activation buffers, RoPE table
+        s.reset()
+        toks, secs = s.generate(prompts, n_gen)
+        dec = secs[1:]
+        out[f"batch{B}"] = {"prefill_and_first_token_ms": round(secs[0] * 1e3, 2),
+                            "prefill_tok_s": round(B * n_prompt / secs[0], 1),
+                            "decode_tok_s": round(B * len(dec) / dec.sum(), 1),
+                            "decode_ms_per_step_p50": round(float(np.median(dec)) * 1e3, 3),
+                            "decode_ms_per_step_p90": round(float(np.percentile(dec, 90)) * 1e3, 3),
+                            "weight_stream_GBps": round(out["weight_bytes"] / float(np.median(dec)) / 1e9, 1)}
+        print(f"[bench] e2e batch {B}: {out[f'batch{B}']}", file=sys.stderr, flush=True)
+        s.close()
+    m.close()
+    return out
+
+
 def copy_probe(be, ev, nbytes=1 << 30, reps=10):
     """Device-to-device copy rate (bytes read + bytes written per second) of
     hipMemcpyAsync on the library's stream: the achievable-bandwidth
@@ -325,6 +366,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--reps", type=int, default=40, help="graph replays per launch kind in the roofline probe")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the Llama-3-8B end-to-end decode")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU's share of the workload; --gpus {args.gpus} is not supported "
@@ -351,6 +393,7 @@ def main():
     be.set_act_mode(ACT_I8)
     q6 = q6k_gemvs(be, ev, max(2, args.reps // 4))
     gemm = prefill_gemms(be, ev, max(2, args.reps // 4))
+    print("[bench] GEMV, GEMM legs done", file=sys.stderr, flush=True)
 
     main_mode = results["i8"]
     dom = main_mode["per_launch"]["gate_up"]
@@ -358,6 +401,10 @@ def main():
             "frac": round(dom["GBps_kernel"] / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_GATE_UP,
             "kernel": "gemv_team<Q4G, int8, gated> (fused ffn gate/up + SiLU, 2 x 14336x4096 Q4_K)",
             "bytes_per_launch": dom["bytes_per_launch"], "us_per_launch": dom["us_kernel"]}
+    for L in wl.layers:  # free the rotated layer copies before the 8B model loads
+        for w in L.values():
+            w.buf.close()
+    e2e = None if args.no_e2e else e2e_decode(be)
     cpu = None if args.no_cpu else cpu_baseline(wl.raws, args.cpu_seconds)
     f = results["f32"]
     line = {
@@ -376,6 +423,7 @@ def main():
                      "pct_of_hbm_peak": round(100 * f["GBps"] / HBM_PEAK_GBS, 2), "per_launch": f["per_launch"]},
         "q6k_gemv": q6,
         "prefill_gemm_i8": gemm,
+        "e2e_llama3_8b": e2e,
         "copy_probe": probe,
         "device": be.device_label(),
     }

@@ -213,6 +213,37 @@ char *q8_buffer(mdma_ctx *ctx, uint64_t bytes) {
   return ctx->q8;
 }
 
+char *argmax_parts(mdma_ctx *ctx, uint64_t chunks) {
+  if (chunks <= ctx->argmax_part_cap) return ctx->argmax_part;
+  no_capture(ctx, "argmax buffer growth");
+  const uint64_t cap = chunks < 4096 ? 4096 : chunks + chunks / 4;
+  hip_check(hipStreamSynchronize(ctx->stream), "argmax buffer grow sync");
+  if (ctx->argmax_part) hip_check(hipFree(ctx->argmax_part), "argmax buffer free");
+  ctx->argmax_part = nullptr;
+  ctx->argmax_part_cap = 0;
+  void *p = nullptr;
+  hip_check(hipMalloc(&p, cap * 12), "argmax buffer alloc");
+  ctx->argmax_part = static_cast<char *>(p);
+  ctx->argmax_part_cap = cap;
+  return ctx->argmax_part;
+}
+
+uint32_t *attn_counters(mdma_ctx *ctx, uint64_t n) {
+  if (n <= ctx->attn_cnt_cap) return ctx->attn_cnt;
+  no_capture(ctx, "attention counter growth");
+  const uint64_t cap = n < 4096 ? 4096 : n + n / 4;
+  hip_check(hipStreamSynchronize(ctx->stream), "attention counter grow sync");
+  if (ctx->attn_cnt) hip_check(hipFree(ctx->attn_cnt), "attention counter free");
+  ctx->attn_cnt = nullptr;
+  ctx->attn_cnt_cap = 0;
+  void *p = nullptr;
+  hip_check(hipMalloc(&p, cap * 4), "attention counter alloc");
+  hip_check(hipMemset(p, 0, cap * 4), "attention counter clear");
+  ctx->attn_cnt = static_cast<uint32_t *>(p);
+  ctx->attn_cnt_cap = cap;
+  return ctx->attn_cnt;
+}
+
 void q8_invalidate_range(mdma_ctx *ctx, const void *p, uint64_t bytes) {
   if (!ctx->q8_valid) return;
   const char *a = static_cast<const char *>(p), *x = reinterpret_cast<const char *>(ctx->q8_x);
@@ -289,6 +320,8 @@ void mdma_gfx950_destroy(mdma_ctx *ctx) {
   (void)hipStreamSynchronize(ctx->stream);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
   if (ctx->q8) (void)hipFree(ctx->q8);
+  if (ctx->argmax_part) (void)hipFree(ctx->argmax_part);
+  if (ctx->attn_cnt) (void)hipFree(ctx->attn_cnt);
   if (ctx->rope_tab) (void)hipFree(ctx->rope_tab);
   if (ctx->host_ids) (void)hipHostFree(ctx->host_ids);
   (void)hipStreamDestroy(ctx->stream);
@@ -645,6 +678,16 @@ int mdma_gfx950_embed(mdma_ctx *ctx, const mdma_qweight *table, const uint32_t *
   });
 }
 
+// In the int8 mode, decode-sized rows also leave their int8 form in the
+// activation cache, so a qmatmul that reads y next does not quantize again
+// (the same values bit for bit as quantizing y there).
+static void rmsnorm_rows(mdma_ctx *ctx, const float *w, uint64_t dim, const float *a, const float *b, float *sum,
+                         float *y, uint64_t rows, float eps) {
+  if (ctx->act_mode == MDMA_ACT_I8 && rows < GEMM_MIN_TOKENS && launch_rmsnorm_q8(ctx, w, dim, a, b, sum, y, rows, eps))
+    return;
+  launch_rmsnorm(ctx, w, dim, a, b, sum, y, rows, eps);
+}
+
 int mdma_gfx950_rmsnorm(mdma_ctx *ctx, const mdma_buf *w, const mdma_buf *x, mdma_buf *y, float eps) {
   return guarded([&] {
     need(ctx, "rmsnorm");
@@ -655,9 +698,8 @@ int mdma_gfx950_rmsnorm(mdma_ctx *ctx, const mdma_buf *w, const mdma_buf *x, mdm
     if (!dim || !xe || xe % dim) shape_fail(fmt("rmsnorm: x has %llu elems, not whole rows of %llu",
                                                 (unsigned long long)xe, (unsigned long long)dim));
     if (ye < xe) shape_fail("rmsnorm: y too small");
-    launch_rmsnorm(ctx, reinterpret_cast<const float *>(w->ptr), dim,
-                   reinterpret_cast<const float *>(x->ptr), nullptr, nullptr,
-                   reinterpret_cast<float *>(y->ptr), xe / dim, eps);
+    rmsnorm_rows(ctx, reinterpret_cast<const float *>(w->ptr), dim, reinterpret_cast<const float *>(x->ptr),
+                 nullptr, nullptr, reinterpret_cast<float *>(y->ptr), xe / dim, eps);
   });
 }
 
@@ -685,9 +727,9 @@ int mdma_gfx950_add_rmsnorm(mdma_ctx *ctx, const mdma_buf *w, const mdma_buf *a,
                      reinterpret_cast<float *>(y->ptr), se / dim, eps);
       return;
     }
-    launch_rmsnorm(ctx, reinterpret_cast<const float *>(w->ptr), dim, reinterpret_cast<const float *>(a->ptr),
-                   reinterpret_cast<const float *>(b->ptr), reinterpret_cast<float *>(sum->ptr),
-                   reinterpret_cast<float *>(y->ptr), se / dim, eps);
+    rmsnorm_rows(ctx, reinterpret_cast<const float *>(w->ptr), dim, reinterpret_cast<const float *>(a->ptr),
+                 reinterpret_cast<const float *>(b->ptr), reinterpret_cast<float *>(sum->ptr),
+                 reinterpret_cast<float *>(y->ptr), se / dim, eps);
   });
 }
 
@@ -807,9 +849,15 @@ int mdma_gfx950_attn(mdma_ctx *ctx, const mdma_buf *q, const mdma_kv_view *kv, c
     uint64_t need_e = kv->len * spec->n_kv_heads * spec->head_dim;
     if (kv->k->len / 2 < need_e || kv->v->len / 2 < need_e) shape_fail("attn: K/V too short for kv.len");
     if (oe < qe) shape_fail("attn: o too small");
-    launch_attn(ctx, reinterpret_cast<const float *>(q->ptr), reinterpret_cast<const uint16_t *>(kv->k->ptr),
-                reinterpret_cast<const uint16_t *>(kv->v->ptr), reinterpret_cast<float *>(o->ptr), n_q, kv->len,
-                spec->head_dim, spec->n_q_heads, spec->n_kv_heads);
+    const float *qp = reinterpret_cast<const float *>(q->ptr);
+    const uint16_t *kp = reinterpret_cast<const uint16_t *>(kv->k->ptr), *vp = reinterpret_cast<const uint16_t *>(kv->v->ptr);
+    float *op = reinterpret_cast<float *>(o->ptr);
+    // In the int8 mode, decode-sized outputs also leave their int8 form in
+    // the activation cache for a qmatmul that reads o next.
+    if (ctx->act_mode == MDMA_ACT_I8 && n_q < GEMM_MIN_TOKENS &&
+        launch_attn_q8(ctx, qp, kp, vp, op, n_q, kv->len, spec->head_dim, spec->n_q_heads, spec->n_kv_heads))
+      return;
+    launch_attn(ctx, qp, kp, vp, op, n_q, kv->len, spec->head_dim, spec->n_q_heads, spec->n_kv_heads);
   });
 }
 
@@ -825,7 +873,7 @@ int mdma_gfx950_greedy(mdma_ctx *ctx, const mdma_buf *logits, uint64_t offset, u
       return;
     }
     uint32_t *dev = reinterpret_cast<uint32_t *>(scratch(ctx, 256));
-    launch_argmax(ctx, reinterpret_cast<const float *>(logits->ptr) + offset, n, dev);
+    launch_argmax_rows(ctx, reinterpret_cast<const float *>(logits->ptr) + offset, 1, n, dev, dev + 1);
     hip_check(hipMemcpyAsync(ctx->host_ids, dev, 8, hipMemcpyDeviceToHost, ctx->stream), "greedy d2h");
     hip_check(hipStreamSynchronize(ctx->stream), "greedy sync");
     if (ctx->host_ids[1]) fail(MDMA_ERR_BACKEND, "empty or nonfinite logits");

@@ -607,29 +607,27 @@ __global__ __launch_bounds__(256) void gemv_q8_i8(JobSet js, const int8_t *__res
 }
 
 // --------------------------------------------------- int8 quantizer -------
-// One wave per group of `group` values (32 or 256): amax, d = amax/127,
-// q = round-half-away(x * 127/amax), and exact sums of every 16 quants.
-__global__ __launch_bounds__(256) void quantize_act_kernel(const float *__restrict__ x, uint32_t n_groups,
-                                                           uint32_t group, int8_t *__restrict__ q,
-                                                           float *__restrict__ d, int32_t *__restrict__ s16) {
-  const uint32_t g = blockIdx.x * WAVES + (threadIdx.x >> 6);
-  if (g >= n_groups) return;
-  const int lane = threadIdx.x & 63;
-  const float *xs = x + (size_t)g * group;
-  // Each lane holds up to 4 values (group <= 256).
-  float v[4];
-  float amax = 0.f;
-#pragma unroll
-  for (int k = 0; k < 4; k++) {
-    const uint32_t i = lane * 4 + k;
-    v[k] = i < group ? xs[i] : 0.f;
-    amax = fmaxf(amax, fabsf(v[k]));
+// Groups of G values (32 or 256) get amax, d = amax/127 and
+// q = round-half-away(x * 127/amax); exact sums of every 16 quants are kept.
+// A lane quantizes 4 consecutive values, so a wave covers 256 values: one
+// group of 256 or eight groups of 32 (G/4 lanes each).
+template <int G>
+__global__ __launch_bounds__(256) void quantize_act_kernel(const float *__restrict__ x, uint64_t n,
+                                                           int8_t *__restrict__ q, float *__restrict__ d,
+                                                           int32_t *__restrict__ s16) {
+  constexpr int LPG = G / 4;  // lanes per group
+  const uint64_t base = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  const bool live = base < n;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  if (live) {
+    const float4 t = *reinterpret_cast<const float4 *>(x + base);
+    v[0] = t.x, v[1] = t.y, v[2] = t.z, v[3] = t.w;
   }
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  for (int o = LPG / 2; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
   const float inv = amax == 0.f ? 0.f : 127.0f / amax;
-  int qi[4];
-  int sum = 0;
+  int qi[4], sum = 0;
 #pragma unroll
   for (int k = 0; k < 4; k++) {
     float r = roundf(v[k] * inv);
@@ -637,16 +635,14 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const float *__restri
     qi[k] = (int)r;
     sum += qi[k];
   }
-  if (lane * 4 < group) {
-    const uint32_t packed = (uint32_t)(qi[0] & 0xff) | ((uint32_t)(qi[1] & 0xff) << 8) |
-                            ((uint32_t)(qi[2] & 0xff) << 16) | ((uint32_t)(qi[3] & 0xff) << 24);
-    *reinterpret_cast<uint32_t *>(q + (size_t)g * group + lane * 4) = packed;
-  }
-  // 16 values = 4 lanes.
-  sum += __shfl_xor(sum, 1, 64);
+  sum += __shfl_xor(sum, 1, 64);  // 16 values = 4 lanes
   sum += __shfl_xor(sum, 2, 64);
-  if ((lane & 3) == 0 && lane * 4 < group) s16[((size_t)g * group + lane * 4) / 16] = sum;
-  if (lane == 0) d[g] = amax / 127.0f;
+  if (!live) return;
+  *reinterpret_cast<uint32_t *>(q + base) = (uint32_t)(qi[0] & 0xff) | ((uint32_t)(qi[1] & 0xff) << 8) |
+                                            ((uint32_t)(qi[2] & 0xff) << 16) | ((uint32_t)(qi[3] & 0xff) << 24);
+  const int lane = threadIdx.x & 63;
+  if ((lane & 3) == 0) s16[base / 16] = sum;
+  if ((lane & (LPG - 1)) == 0) d[base / G] = amax / 127.0f;
 }
 
 // --------------------------------------------------- block-dot debug ------
@@ -790,20 +786,29 @@ bool is_i8_dtype(int32_t dt) { return dt == DT_Q4_K || dt == DT_Q6_K || dt == DT
 // The int8 activations of x [T, n_in] in the context's activation buffer,
 // quantized now unless that buffer already holds exactly this x (same
 // pointer and shape, no write since; see q8_invalidate).
-void quantize_into_scratch(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in, int8_t **qx, float **dx,
-                           int32_t **s16) {
+void q8_slots(mdma_ctx *ctx, uint64_t T, uint64_t n_in, int8_t **qx, float **dx, int32_t **s16) {
   const uint64_t n = T * n_in;
   const uint64_t qb = (n + 255) / 256 * 256, db = (n / 256 * 4 + 255) / 256 * 256;
   char *s = q8_buffer(ctx, qb + db + n / 16 * 4 + 256);
   *qx = reinterpret_cast<int8_t *>(s);
   *dx = reinterpret_cast<float *>(s + qb);
   *s16 = reinterpret_cast<int32_t *>(s + qb + db);
-  if (ctx->q8_valid && ctx->q8_x == x && ctx->q8_n == n && ctx->q8_n_in == n_in) return;
-  launch_quantize_act(ctx, x, n, 256, *qx, *dx, *s16);
+}
+
+void q8_mark(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in) {
   ctx->q8_valid = true;
   ctx->q8_x = x;
-  ctx->q8_n = n;
+  ctx->q8_n = T * n_in;
   ctx->q8_n_in = n_in;
+}
+
+void quantize_into_scratch(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in, int8_t **qx, float **dx,
+                           int32_t **s16) {
+  q8_slots(ctx, T, n_in, qx, dx, s16);
+  const uint64_t n = T * n_in;
+  if (ctx->q8_valid && ctx->q8_x == x && ctx->q8_n == n && ctx->q8_n_in == n_in) return;
+  launch_quantize_act(ctx, x, n, 256, *qx, *dx, *s16);
+  q8_mark(ctx, x, T, n_in);
 }
 
 
@@ -935,9 +940,11 @@ void launch_gemv_i8_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up,
 
 void launch_quantize_act(mdma_ctx *ctx, const float *x, uint64_t n, uint64_t group, int8_t *q, float *d,
                          int32_t *s16) {
-  const uint64_t groups = n / group;
-  quantize_act_kernel<<<dim3((uint32_t)((groups + WAVES - 1) / WAVES)), dim3(64 * WAVES), 0, ctx->stream>>>(
-      x, (uint32_t)groups, (uint32_t)group, q, d, s16);
+  const dim3 grid((uint32_t)((n + 1023) / 1024)), block(256);
+  if (group == 32)
+    quantize_act_kernel<32><<<grid, block, 0, ctx->stream>>>(x, n, q, d, s16);
+  else
+    quantize_act_kernel<256><<<grid, block, 0, ctx->stream>>>(x, n, q, d, s16);
   hip_check(hipGetLastError(), "quantize_act launch");
 }
 

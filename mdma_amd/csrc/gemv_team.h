@@ -17,7 +17,7 @@
 //  - A team of TW waves (64*TW lanes) covers all units of a row, PL units
 //    per lane. A team owns a contiguous run of rows of one weight and walks
 //    it R rows at a time, loading the next R rows while it computes the
-//    current ones (ping-pong register buffers).
+//    current ones (NBUF rotating register buffers).
 //  - Lanes reduce with DPP moves; multi-wave teams add the waves' sums in LDS.
 //  - Fused QKV: up to three weights share x; teams are dealt out in order.
 //    Gated (ffn gate/up + SiLU): a team computes R rows of gate and the same
@@ -305,6 +305,18 @@ struct TeamSet {
   uint32_t n_in, rpt;  // shared row length; rows per team (a multiple of R)
 };
 
+// Row groups in flight per wave (loads issued NBUF-1 groups ahead): three
+// for one-wave teams in the int8 mode, whose short compute leaves the loads
+// exposed; two elsewhere, where a third costs occupancy or registers.
+template <bool F32, int TW>
+constexpr int nbuf() {
+#ifdef MDMA_TEAM_NBUF
+  return MDMA_TEAM_NBUF;
+#else
+  return !F32 && TW == 1 ? 3 : 2;
+#endif
+}
+
 template <class F, bool F32, int R, int ITERS, int TW, int PL, int TT, bool GATED>
 __global__ __launch_bounds__(WG) void gemv_team(TeamSet ts, const float *__restrict__ xf,
                                                 const int8_t *__restrict__ qx, const float *__restrict__ dx,
@@ -316,6 +328,7 @@ __global__ __launch_bounds__(WG) void gemv_team(TeamSet ts, const float *__restr
   using Acc = typename std::conditional<F32, double, float>::type;
   constexpr int TPW = WG / 64 / TW;  // teams per workgroup
   constexpr int NR = GATED ? 2 * R : R;
+  constexpr int NBUF = nbuf<F32, TW>();
   // Multi-wave teams: each wave's per-row totals for the whole run, added
   // across the team's waves once, after the run (one barrier per kernel).
   __shared__ double red[TW > 1 ? TPW : 1][TW > 1 ? TW : 1][TW > 1 ? ITERS * NR * TT : 1];
@@ -354,7 +367,7 @@ __global__ __launch_bounds__(WG) void gemv_team(TeamSet ts, const float *__restr
   typename F::XF xr[F32 && TT == 1 ? PL : 1];
   // Rows past the weight's end (last team of a job) re-read its last row;
   // their sums are not stored.
-  typename F::W buf[2][PL][NR];  // ping-pong row groups
+  typename F::W buf[NBUF][PL][NR];  // rotating row-group buffers
   auto load = [&](typename F::W(&w)[PL][NR], uint32_t r0) {
 #pragma unroll
     for (int r = 0; r < NR; r++) {
@@ -434,7 +447,8 @@ __global__ __launch_bounds__(WG) void gemv_team(TeamSet ts, const float *__restr
 
   // The first rows' weights go out before the activations: the weights come
   // from HBM, the activations from L2.
-  load(buf[0], r_begin);
+#pragma unroll
+  for (int it = 0; it < NBUF - 1 && it < ITERS; it++) load(buf[it], r_begin + it * R);
   // Activations of the lane's units, loaded once.
   if constexpr (!F32) {
 #pragma unroll
@@ -452,13 +466,13 @@ __global__ __launch_bounds__(WG) void gemv_team(TeamSet ts, const float *__restr
 
   // The team's run is ITERS row groups, fully unrolled: straight-line code
   // gives the compiler exact wait counts (each group waits only for its own
-  // loads while the next group's are in flight) and nothing is loaded past
-  // the run.
+  // loads while the next NBUF-1 groups' are in flight) and nothing is loaded
+  // past the run.
 #pragma unroll
   for (int it = 0; it < ITERS; it++) {
-    if (it + 1 < ITERS) load(buf[(it + 1) & 1], r_begin + (it + 1) * R);
+    if (it + NBUF - 1 < ITERS) load(buf[(it + NBUF - 1) % NBUF], r_begin + (it + NBUF - 1) * R);
     __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
-    consume(buf[it & 1], it);
+    consume(buf[it % NBUF], it);
   }
   if constexpr (TW > 1) {
     __syncthreads();
@@ -494,7 +508,7 @@ __global__ __launch_bounds__(WG) void gemv_team(TeamSet ts, const float *__restr
 #define MDMA_TEAM_RG 1
 #endif
 #ifndef MDMA_TEAM_WAVES_PER_CU
-#define MDMA_TEAM_WAVES_PER_CU 8
+#define MDMA_TEAM_WAVES_PER_CU 12
 #endif
 
 template <class F, bool F32, int R, int ITERS, int TT, bool GATED>

@@ -89,6 +89,11 @@ struct mdma_ctx {
   bool capturing = false;        // stream capture in progress: no synchronizing calls
   // Events the next GEMV kernel's dispatch timestamps (mdma_gfx950_time_next_gemv).
   hipEvent_t time_start = nullptr, time_stop = nullptr;
+  // Per-chunk partial results of the two-pass argmax (12 bytes per chunk).
+  char *argmax_part = nullptr;
+  uint64_t argmax_part_cap = 0;  // chunks
+  uint32_t *attn_cnt = nullptr;
+  uint64_t attn_cnt_cap = 0;
 };
 
 struct mdma_graph {
@@ -103,6 +108,12 @@ namespace mdma {
 char *scratch(mdma_ctx *ctx, uint64_t bytes);
 // The int8-activation buffer (grown like scratch; growth drops the cached x).
 char *q8_buffer(mdma_ctx *ctx, uint64_t bytes);
+// Device space for `chunks` partial results of the two-pass argmax (grown
+// like scratch).
+char *argmax_parts(mdma_ctx *ctx, uint64_t chunks);
+// At least n zeroed arrival counters for split attention; each launch leaves
+// the counters it used at zero.
+uint32_t *attn_counters(mdma_ctx *ctx, uint64_t n);
 // Forget the cached int8 activations: every entry point that writes device
 // memory calls this (a qmatmul only when its output overlaps the cached x).
 inline void q8_invalidate(mdma_ctx *ctx) { ctx->q8_valid = false; }
@@ -144,6 +155,10 @@ void launch_gemv_team(mdma_ctx *ctx, int mode, const GemvJob *jobs, int n_jobs, 
 // The int8 activations of x [T, n_in] (per-256 f32 scales, per-16 sums) in
 // the context's activation buffer, quantized now unless it already holds
 // exactly this x.
+// Slots of the int8-activation buffer for x [T, n_in] (int8 values, per-256
+// scales, sums of 16), and marking them as holding x's quantization.
+void q8_slots(mdma_ctx *ctx, uint64_t T, uint64_t n_in, int8_t **qx, float **dx, int32_t **s16);
+void q8_mark(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in);
 void quantize_into_scratch(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in, int8_t **qx, float **dx,
                            int32_t **s16);
 // Prefill int8 MFMA GEMM (gemm_i8.hip) over prepared Q8_0 / Q4_K weights:
@@ -163,6 +178,12 @@ void launch_embed(mdma_ctx *ctx, int32_t dtype, int layout, const uint8_t *table
                   const uint32_t *ids_dev, uint64_t n_ids, float *out);
 void launch_rmsnorm(mdma_ctx *ctx, const float *w, uint64_t dim, const float *a, const float *b,
                     float *sum, float *y, uint64_t rows, float eps);
+// rmsnorm that also leaves y's int8 per-256 quantization in the
+// int8-activation buffer, marked as holding y (so the int8 GEMV that reads y
+// next does not quantize it again). False, launching nothing, when dim is not
+// whole groups of 256 or exceeds 16384.
+bool launch_rmsnorm_q8(mdma_ctx *ctx, const float *w, uint64_t dim, const float *a, const float *b, float *sum,
+                       float *y, uint64_t rows, float eps);
 void launch_add(mdma_ctx *ctx, const float *a, const float *b, float *y, uint64_t n);
 void launch_silu_mul(mdma_ctx *ctx, const float *g, const float *u, float *y, uint64_t n);
 void launch_rope(mdma_ctx *ctx, float *x, uint64_t n_tokens, uint64_t heads, uint64_t hd,
@@ -181,8 +202,13 @@ void launch_rope_kv_write(mdma_ctx *ctx, float *q, uint64_t q_heads, const float
 void launch_attn(mdma_ctx *ctx, const float *q, const uint16_t *k, const uint16_t *v, float *o,
                  uint64_t n_q, uint64_t kv_len, uint64_t hd, uint64_t n_q_heads,
                  uint64_t n_kv_heads, uint64_t seq_stride = 0);
-void launch_argmax(mdma_ctx *ctx, const float *x, uint64_t n, uint32_t *out_dev);
 // Greedy argmax of each row of x [rows, n] into idx[row]; flag[row] = any non-finite.
+// launch_attn that also leaves the int8 form of o (per 256) in the
+// int8-activation buffer, marked as holding o. False, launching nothing, when
+// the shape has no such variant (needs hd % 8 == 0, hd <= 256, a power-of-two
+// group of at most 8 query heads per KV head, group outputs whole 256s).
+bool launch_attn_q8(mdma_ctx *ctx, const float *q, const uint16_t *k, const uint16_t *v, float *o, uint64_t n_q,
+                    uint64_t kv_len, uint64_t hd, uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride = 0);
 void launch_argmax_rows(mdma_ctx *ctx, const float *x, uint64_t rows, uint64_t n, uint32_t *idx,
                         uint32_t *flag);
 

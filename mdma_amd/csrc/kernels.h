@@ -7,6 +7,14 @@
 namespace mdma {
 namespace {
 
+// Workgroup barrier ordering LDS only: unlike __syncthreads it does not wait
+// for this wave's global loads, so a prefetch stays in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ float h2f(uint32_t bits16) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits16 & 0xffff));
 }

@@ -337,18 +337,20 @@ mdma_buf *load_norm(mdma_model *m, Gguf &g, const std::string &name, std::vector
   return b;
 }
 
-void gemv(mdma_ctx *ctx, const GemvJob *jobs, int n, const float *x, uint64_t T) {
-  // Inputs here are rewritten between calls without passing through the
-  // C entry points, so cached int8 activations are never reused.
-  q8_invalidate(ctx);
+// fresh: x's int8 form was just written by launch_rmsnorm_q8 (kept);
+// otherwise inputs here are rewritten between calls without passing through
+// the C entry points, so cached int8 activations are not reused.
+void gemv(mdma_ctx *ctx, const GemvJob *jobs, int n, const float *x, uint64_t T, bool fresh = false) {
+  if (!fresh) q8_invalidate(ctx);
   if (ctx->act_mode == MDMA_ACT_I8)
     launch_gemv_i8(ctx, jobs, n, x, T);
   else
     launch_gemv_f32(ctx, jobs, n, x, T);
 }
 
-void gemv_gated(mdma_ctx *ctx, const GemvJob &g, const GemvJob &u, const float *x, uint64_t T, float *y) {
-  q8_invalidate(ctx);
+void gemv_gated(mdma_ctx *ctx, const GemvJob &g, const GemvJob &u, const float *x, uint64_t T, float *y,
+                bool fresh = false) {
+  if (!fresh) q8_invalidate(ctx);
   if (ctx->act_mode == MDMA_ACT_I8)
     launch_gemv_i8_gated(ctx, g, u, x, T, y);
   else
@@ -368,36 +370,55 @@ void run_layers(mdma_session *s, uint64_t T, uint32_t pos, uint64_t seq, bool ba
   const float *tab = rope_table(ctx, pos + (batched ? 0 : T - 1), hd, c.rope_theta);
   mdma_buf *x = s->x, *x_alt = s->x_alt;
   const uint64_t cache_stride = s->capacity * kvw;
+  // In the int8 mode, decode-sized rows get their int8 form from the
+  // rmsnorm that produces them (prefill-sized ones go to the int8 GEMM,
+  // which quantizes per 32 itself).
+  const bool fuse_q8 = ctx->act_mode == MDMA_ACT_I8 && T < GEMM_MIN_TOKENS;
+  auto norm = [&](const mdma_buf *w, const float *a, const float *b, float *sum) {
+    q8_invalidate(ctx);
+    if (fuse_q8 && launch_rmsnorm_q8(ctx, fp(w), E, a, b, sum, fp(s->normed), T, c.rms_eps)) return true;
+    launch_rmsnorm(ctx, fp(w), E, a, b, sum, fp(s->normed), T, c.rms_eps);
+    return false;
+  };
+  bool fresh = false;
+  auto attend = [&](const uint16_t *kc, const uint16_t *vc, uint64_t n_q, uint64_t kv_len, uint64_t stride) {
+    q8_invalidate(ctx);
+    fresh = fuse_q8 && launch_attn_q8(ctx, fp(s->q), kc, vc, fp(s->attn_out), n_q, kv_len, hd, c.n_heads,
+                                      c.n_kv_heads, stride);
+    if (!fresh) launch_attn(ctx, fp(s->q), kc, vc, fp(s->attn_out), n_q, kv_len, hd, c.n_heads, c.n_kv_heads, stride);
+  };
   for (uint64_t i = 0; i < c.n_layers; i++) {
     const Layer &L = m->layers[i];
     if (i == 0) {
-      launch_rmsnorm(ctx, fp(L.attn_norm), E, fp(x), nullptr, nullptr, fp(s->normed), T, c.rms_eps);
+      fresh = norm(L.attn_norm, fp(x), nullptr, nullptr);
     } else {
-      launch_rmsnorm(ctx, fp(L.attn_norm), E, fp(x), fp(s->proj), fp(x_alt), fp(s->normed), T, c.rms_eps);
+      fresh = norm(L.attn_norm, fp(x), fp(s->proj), fp(x_alt));
       std::swap(x, x_alt);
     }
     GemvJob qkv[3] = {L.wq.job(fp(s->q)), L.wk.job(fp(s->k)), L.wv.job(fp(s->v))};
-    gemv(ctx, qkv, 3, fp(s->normed), T);
+    gemv(ctx, qkv, 3, fp(s->normed), T, fresh);
     // KvCache::rope_write (src/kv_cache.rs:212-244): rotate q, store rotated k and v.
     uint16_t *kb = reinterpret_cast<uint16_t *>(s->kc[i]->ptr), *vb = reinterpret_cast<uint16_t *>(s->vc[i]->ptr);
     if (batched) {
       launch_rope_kv_write(ctx, fp(s->q), c.n_heads, fp(s->k), fp(s->v), c.n_kv_heads, hd, T, tab, pos,
                            kb + pos * kvw, vb + pos * kvw, cache_stride, 0);
-      launch_attn(ctx, fp(s->q), kb, vb, fp(s->attn_out), T, pos + 1, hd, c.n_heads, c.n_kv_heads, cache_stride);
+      attend(kb, vb, T, pos + 1, cache_stride);
     } else {
       uint16_t *ks = kb + seq * cache_stride, *vs = vb + seq * cache_stride;
       launch_rope_kv_write(ctx, fp(s->q), c.n_heads, fp(s->k), fp(s->v), c.n_kv_heads, hd, T, tab, pos,
                            ks + pos * kvw, vs + pos * kvw);
-      launch_attn(ctx, fp(s->q), ks, vs, fp(s->attn_out), T, pos + T, hd, c.n_heads, c.n_kv_heads);
+      attend(ks, vs, T, pos + T, 0);
     }
     GemvJob wo = L.wo.job(fp(s->proj));
-    gemv(ctx, &wo, 1, fp(s->attn_out), T);
-    launch_rmsnorm(ctx, fp(L.ffn_norm), E, fp(x), fp(s->proj), fp(x_alt), fp(s->normed), T, c.rms_eps);
+    gemv(ctx, &wo, 1, fp(s->attn_out), T, fresh);
+    fresh = norm(L.ffn_norm, fp(x), fp(s->proj), fp(x_alt));
     std::swap(x, x_alt);
-    gemv_gated(ctx, L.gate.job(fp(s->gate)), L.up.job(fp(s->up)), fp(s->normed), T, fp(s->act));
+    gemv_gated(ctx, L.gate.job(fp(s->gate)), L.up.job(fp(s->up)), fp(s->normed), T, fp(s->act), fresh);
     GemvJob dn = L.down.job(fp(s->proj));
     gemv(ctx, &dn, 1, fp(s->act), T);
   }
+  // The head GEMV quantizes the final-normed rows itself when it needs
+  // them (only the rows it reads, which may be a subset).
   launch_rmsnorm(ctx, fp(m->output_norm), E, fp(x), fp(s->proj), fp(x_alt), fp(s->normed), T, c.rms_eps);
   std::swap(x, x_alt);
   // Keep s->x as the buffer holding the residual stream.

@@ -5,6 +5,7 @@
 // (/root/reference/src/backend/cpu.rs) op for op; these are simple, correct
 // kernels, not the hot path.
 #include "internal.h"
+#include "kernels.h"
 
 namespace mdma {
 namespace {
@@ -141,6 +142,88 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ 
     const float v = b ? sum[base + i] : a[base + i];
     const float t = v * scale;
     y[base + i] = t * w[i];
+  }
+}
+
+// rmsnorm for rows of up to 16384 values (dim % 4 == 0), one 1024-thread
+// workgroup per row with the row held in registers (a single pass over
+// memory); same arithmetic as rmsnorm_kernel: f32 squares summed in f64,
+// scale = 1/sqrt(mean + eps) in f32, y = (x*scale)*w. With QUANT (dim % 256
+// == 0) it also writes y's int8 form for the int8-activation GEMV: groups of
+// 256 (one wave each), d = amax/127, q = round-half-away(y*127/amax), exact
+// sums of 16 -- the arithmetic of quantize_act_kernel, so the result is the
+// same bit for bit.
+template <bool QUANT>
+__global__ __launch_bounds__(1024) void rmsnorm_row_kernel(const float *__restrict__ w, uint32_t dim,
+                                                           const float *__restrict__ a, const float *__restrict__ b,
+                                                           float *__restrict__ sum, float *__restrict__ y, float eps,
+                                                           int8_t *__restrict__ q, float *__restrict__ qd,
+                                                           int32_t *__restrict__ qs16) {
+#pragma clang fp contract(off)
+  __shared__ double sh[16];
+  const size_t base = (size_t)blockIdx.x * dim;
+  const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  float v[4][4];
+  float4 wv[4];
+  double ss = 0.0;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const uint32_t i = 4 * t + 4096 * c;
+    if (i >= dim) break;
+    wv[c] = *reinterpret_cast<const float4 *>(w + i);
+    float4 av = *reinterpret_cast<const float4 *>(a + base + i);
+    if (b) {
+      const float4 bv = *reinterpret_cast<const float4 *>(b + base + i);
+      av.x = av.x + bv.x, av.y = av.y + bv.y, av.z = av.z + bv.z, av.w = av.w + bv.w;
+      *reinterpret_cast<float4 *>(sum + base + i) = av;
+    }
+    v[c][0] = av.x, v[c][1] = av.y, v[c][2] = av.z, v[c][3] = av.w;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const float sq = v[c][k] * v[c][k];
+      ss += (double)sq;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  if (lane == 0) sh[wave] = ss;
+  __syncthreads();
+  double tot = 0.0;
+  for (int k = 0; k < 16; k++) tot += sh[k];
+  const float mean_sq = (float)tot / (float)dim;
+  const float scale = 1.0f / sqrtf(mean_sq + eps);
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const uint32_t i = 4 * t + 4096 * c;
+    if (i >= dim) break;
+    const float wk[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
+    float r[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const float s1 = v[c][k] * scale;
+      r[k] = s1 * wk[k];
+    }
+    *reinterpret_cast<float4 *>(y + base + i) = make_float4(r[0], r[1], r[2], r[3]);
+    if (QUANT) {
+      float amax = fmaxf(fmaxf(fabsf(r[0]), fabsf(r[1])), fmaxf(fabsf(r[2]), fabsf(r[3])));
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+      const float inv = amax == 0.f ? 0.f : 127.0f / amax;
+      int qi[4], sm = 0;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        float rr = roundf(r[k] * inv);
+        rr = fminf(fmaxf(rr, -127.f), 127.f);
+        qi[k] = (int)rr;
+        sm += qi[k];
+      }
+      sm += __shfl_xor(sm, 1, 64);
+      sm += __shfl_xor(sm, 2, 64);
+      *reinterpret_cast<uint32_t *>(q + base + i) = (uint32_t)(qi[0] & 0xff) | ((uint32_t)(qi[1] & 0xff) << 8) |
+                                                    ((uint32_t)(qi[2] & 0xff) << 16) | ((uint32_t)(qi[3] & 0xff) << 24);
+      if ((lane & 3) == 0) qs16[(base + i) / 16] = sm;
+      if (lane == 0) qd[(base + i) / 256] = amax / 127.0f;
+    }
   }
 }
 
@@ -304,11 +387,395 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q, 
   if (threadIdx.x < hd) o[((size_t)i * n_q_heads + qh) * hd + threadIdx.x] = acc / l;
 }
 
-// Greedy argmax (sampler.rs:64-74): largest by total order, ties to the last
-// index; out[1] flags any non-finite logit.
+// Split-key attention (flash-decoding). A workgroup takes one query, one KV
+// head with all G query heads of its group (each f16 K/V row is read once
+// for the group) and a run of `tpw` tiles of ATT_TILE keys, with an online
+// softmax across its tiles and the next tile's K/V loaded while the current
+// one is computed. Scores: a quad of lanes per key, each lane 8-wide 16-byte
+// slices 32 apart, summed over the quad with DPP. P.V: each lane owns two
+// adjacent dims of a 128-wide slice over 16 keys per wave, so no cross-lane
+// sums; the four waves' partial outputs meet in LDS. A run leaves, per query
+// head, its max m, its sum l of exp(s - m) and its unnormalised output in
+// part [query][q head][split][hd + 2]; the run that arrives last for its
+// (query, KV head) -- a device-scope counter, reset by that run -- merges
+// them (weights exp(m_s - M)). A single run writes o directly. Scores and
+// exponentials are f32: s = (q.k) * scale, p = expf(s - m).
+// With QUANT (G*hd a multiple of 256) the finishing workgroup also writes
+// the int8 form of its G heads' output (groups of 256, the arithmetic of
+// quantize_act_kernel) into q8 at the output's element offsets.
+constexpr uint32_t ATT_TILE = 64;
+constexpr uint32_t ATT_MAX_RUNS = 16;  // runs merged per (query, KV head)
+#ifndef MDMA_ATT_WG_TARGET
+#define MDMA_ATT_WG_TARGET 1024
+#endif
+struct AttnQ8 {
+  int8_t *q;
+  float *d;
+  int32_t *s16;
+};
+
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_max(float v) {
+  const float o = __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, -INFINITY), __builtin_bit_cast(int, v), CTRL, ROWS,
+                                         0xF, false));
+  return fmaxf(v, o);
+}
+// Max / sum over the 64 lanes, the result in every lane.
+__device__ __forceinline__ float wave_max_all(float v) {
+  v = dpp_max<0xB1, 0xF>(v);
+  v = dpp_max<0x4E, 0xF>(v);
+  v = dpp_max<0x141, 0xF>(v);
+  v = dpp_max<0x140, 0xF>(v);
+  v = dpp_max<0x142, 0xA>(v);
+  v = dpp_max<0x143, 0xC>(v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ __forceinline__ float wave_sum_all(float v) {
+  v = wave_total63(v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+template <int C>
+struct AttnTile {
+  uint4 k[4 * C];     // K slices of this lane's key
+  uint32_t v[16][C];  // V dim pairs of this wave's 16 keys
+};
+
+template <int C>
+__device__ __forceinline__ void attn_load(AttnTile<C> &t, const uint16_t *__restrict__ K,
+                                          const uint16_t *__restrict__ V, uint32_t tile, uint32_t visible,
+                                          uint32_t kv_row, uint32_t hd, uint32_t lane, uint32_t wave) {
+  const uint32_t jk = tile * ATT_TILE + wave * 16 + (lane >> 2), l4 = lane & 3;
+#pragma unroll
+  for (int m = 0; m < 4 * C; m++) {
+    const uint32_t d0 = 8 * l4 + 32 * m;
+    t.k[m] = jk < visible && d0 < hd ? *reinterpret_cast<const uint4 *>(K + (size_t)jk * kv_row + d0)
+                                     : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const uint32_t jv = tile * ATT_TILE + wave * 16 + r;
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+      const uint32_t d = 2 * lane + 128 * c;
+      t.v[r][c] = jv < visible && d < hd ? *reinterpret_cast<const uint32_t *>(V + (size_t)jv * kv_row + d) : 0u;
+    }
+  }
+}
+
+template <int G, int C, bool QUANT>
+__global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict__ q, const uint16_t *__restrict__ K,
+                                                         const uint16_t *__restrict__ V, float *__restrict__ o,
+                                                         float *__restrict__ part, uint32_t *__restrict__ cnt,
+                                                         uint32_t prefix, uint32_t hd, uint32_t n_q_heads,
+                                                         uint32_t n_kv_heads, float scale, uint64_t seq_stride,
+                                                         uint32_t tpw, AttnQ8 q8) {
+  __shared__ float qs[G][128 * C];
+  __shared__ float sc[G][ATT_TILE];
+  __shared__ float mrun[G], lrun[G], alph[G];
+  __shared__ float red[4][G][128 * C];
+  __shared__ float gmax[4];
+  __shared__ float wml[G][ATT_MAX_RUNS][2];
+  __shared__ uint32_t last;
+  const uint32_t kvh = blockIdx.x, split = blockIdx.y, i = blockIdx.z, n_splits = gridDim.y;
+  const uint32_t visible = seq_stride ? prefix + 1 : prefix + i + 1;
+  const uint32_t tiles = (visible + ATT_TILE - 1) / ATT_TILE, t0 = split * tpw;
+  if (t0 >= tiles) return;  // this query's keys end before the run
+  const uint32_t t1 = min(t0 + tpw, tiles), live = (tiles + tpw - 1) / tpw;
+  const uint32_t kv_row = n_kv_heads * hd, qh0 = kvh * G;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l4 = lane & 3;
+  K += (size_t)i * seq_stride + (size_t)kvh * hd;
+  V += (size_t)i * seq_stride + (size_t)kvh * hd;
+  // Ping-pong tile buffers: the loads for tile+1 go out before tile is
+  // computed (clamped to the run's last tile, so every load is in bounds and
+  // the wait counts are fixed).
+  AttnTile<C> ta, tb;
+  attn_load<C>(ta, K, V, t0, visible, kv_row, hd, lane, wave);
+  const float *qv = q + ((size_t)i * n_q_heads + qh0) * hd;
+  for (uint32_t t = tid; t < G * hd; t += 256) qs[t / hd][t % hd] = qv[t];
+  if (tid < G) mrun[tid] = -INFINITY, lrun[tid] = 0.f;
+  float acc[G][C][2];
+#pragma unroll
+  for (int h = 0; h < G; h++)
+#pragma unroll
+    for (int c = 0; c < C; c++) acc[h][c][0] = acc[h][c][1] = 0.f;
+  lds_barrier();
+  auto process = [&](const AttnTile<C> &cur, uint32_t tile) {
+    float s[G];
+#pragma unroll
+    for (int h = 0; h < G; h++) s[h] = 0.f;
+#pragma unroll
+    for (int m = 0; m < 4 * C; m++) {
+      const uint32_t d0 = 8 * l4 + 32 * m;
+      if (d0 < hd) {
+        const uint32_t kk[4] = {cur.k[m].x, cur.k[m].y, cur.k[m].z, cur.k[m].w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const float kf = h2f((uint16_t)(kk[e >> 1] >> (16 * (e & 1))));
+#pragma unroll
+          for (int h = 0; h < G; h++) s[h] = fmaf(qs[h][d0 + e], kf, s[h]);
+        }
+      }
+    }
+    const uint32_t jl = wave * 16 + (lane >> 2);
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+      float v = dpp_step<0xB1, 0xF>(s[h]);
+      v = dpp_step<0x4E, 0xF>(v);
+      if (l4 == 0) sc[h][jl] = tile * ATT_TILE + jl < visible ? v * scale : -INFINITY;
+    }
+    lds_barrier();
+    for (int h = wave; h < G; h += 4) {
+      const float v = sc[h][lane];
+      const float mo = mrun[h], mn = fmaxf(mo, wave_max_all(v));
+      const float pj = expf(v - mn);  // 0 for masked keys (v = -inf)
+      const float l = wave_sum_all(pj);
+      sc[h][lane] = pj;
+      if (lane == 0) {
+        const float a = expf(mo - mn);  // 0 on the first tile (mo = -inf)
+        lrun[h] = lrun[h] * a + l;
+        mrun[h] = mn;
+        alph[h] = a;
+      }
+    }
+    lds_barrier();
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+      const float a = alph[h];
+#pragma unroll
+      for (int c = 0; c < C; c++) acc[h][c][0] *= a, acc[h][c][1] *= a;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+#pragma unroll
+      for (int h = 0; h < G; h++) {
+        const float ph = sc[h][wave * 16 + r];
+#pragma unroll
+        for (int c = 0; c < C; c++) {
+          acc[h][c][0] = fmaf(ph, h2f(cur.v[r][c] & 0xffffu), acc[h][c][0]);
+          acc[h][c][1] = fmaf(ph, h2f(cur.v[r][c] >> 16), acc[h][c][1]);
+        }
+      }
+    }
+    lds_barrier();  // sc is rewritten by the next tile
+  };
+  if (t1 - t0 == 1) {
+    process(ta, t0);
+  } else {
+    for (uint32_t tile = t0; tile < t1; tile += 2) {
+      attn_load<C>(tb, K, V, min(tile + 1, t1 - 1), visible, kv_row, hd, lane, wave);
+      process(ta, tile);
+      if (tile + 1 >= t1) break;
+      attn_load<C>(ta, K, V, min(tile + 2, t1 - 1), visible, kv_row, hd, lane, wave);
+      process(tb, tile + 1);
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < C; c++) {
+    const uint32_t d = 2 * lane + 128 * c;
+    if (d < hd) {
+#pragma unroll
+      for (int h = 0; h < G; h++) red[wave][h][d] = acc[h][c][0], red[wave][h][d + 1] = acc[h][c][1];
+    }
+  }
+  lds_barrier();
+  // Outputs t = tid + 256*k of the group's G*hd values (heads contiguous).
+  constexpr int NO = (G * 128 * C + 255) / 256;
+  float out[NO];
+  const size_t orow = ((size_t)i * n_q_heads + qh0) * hd;
+  if (n_splits == 1) {
+#pragma unroll
+    for (int k = 0; k < NO; k++) {
+      const uint32_t t = tid + 256 * k;
+      if (t < G * hd) {
+        const uint32_t h = t / hd, d = t % hd;
+        out[k] = (((red[0][h][d] + red[1][h][d]) + red[2][h][d]) + red[3][h][d]) / lrun[h];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < NO; k++) {
+      const uint32_t t = tid + 256 * k;
+      if (t < G * hd) {
+        const uint32_t h = t / hd, d = t % hd;
+        part[((orow / hd + h) * n_splits + split) * (hd + 2) + d] =
+            ((red[0][h][d] + red[1][h][d]) + red[2][h][d]) + red[3][h][d];
+      }
+    }
+    if (tid < G) {
+      float *pp = part + ((orow / hd + tid) * n_splits + split) * (hd + 2) + hd;
+      pp[0] = mrun[tid];
+      pp[1] = lrun[tid];
+    }
+    // The barrier orders every wave's partial stores before thread 0's
+    // device-scope release; thread 0's acquire (in the last run) orders the
+    // merge's loads, which the second barrier extends to every wave.
+    __syncthreads();
+    if (tid == 0) {
+      __threadfence();
+      uint32_t *c = cnt + (size_t)i * n_kv_heads + kvh;
+      const uint32_t prev = atomicAdd(c, 1u);
+      last = prev == live - 1;
+      if (last) {
+        *c = 0u;  // every run of this (query, KV head) has arrived
+        __threadfence();
+      }
+    }
+    __syncthreads();
+    if (!last) return;
+    // Merge weights w[h][s] = exp(m_s - M) / L with M = max m_s and
+    // L = sum l_s exp(m_s - M); then out = sum_s w[h][s] * partial_s.
+    for (uint32_t e = tid; e < G * live; e += 256) {
+      const uint32_t h = e / live, s2 = e % live;
+      const float *pp = part + ((orow / hd + h) * n_splits + s2) * (hd + 2) + hd;
+      wml[h][s2][0] = pp[0];
+      wml[h][s2][1] = pp[1];
+    }
+    __syncthreads();
+    if (tid < G) {
+      float M = -INFINITY;
+      for (uint32_t s2 = 0; s2 < live; s2++) M = fmaxf(M, wml[tid][s2][0]);
+      float L = 0.f;
+      for (uint32_t s2 = 0; s2 < live; s2++) {
+        const float w = expf(wml[tid][s2][0] - M);
+        wml[tid][s2][0] = w;
+        L = fmaf(wml[tid][s2][1], w, L);
+      }
+      lrun[tid] = L;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < NO; k++) {
+      const uint32_t t = tid + 256 * k;
+      if (t < G * hd) {
+        const uint32_t h = t / hd, d = t % hd;
+        const float *pb = part + (orow / hd + h) * n_splits * (hd + 2) + d;
+        float pv[ATT_MAX_RUNS];
+#pragma unroll
+        for (uint32_t s2 = 0; s2 < ATT_MAX_RUNS; s2++) pv[s2] = s2 < live ? pb[s2 * (hd + 2)] : 0.f;
+        float a = 0.f;
+#pragma unroll
+        for (uint32_t s2 = 0; s2 < ATT_MAX_RUNS; s2++)
+          if (s2 < live) a = fmaf(pv[s2], wml[h][s2][0], a);
+        out[k] = a / lrun[h];
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < NO; k++) {
+    const uint32_t t = tid + 256 * k;
+    if (t < G * hd) o[orow + t] = out[k];
+  }
+  if (QUANT) {
+    // G*hd is whole groups of 256: output k of every thread is group k.
+#pragma unroll
+    for (int k = 0; k < NO; k++) {
+      if (256 * k >= G * hd) break;
+      float amax = wave_max_all(fabsf(out[k]));
+      __syncthreads();
+      if (lane == 0) gmax[wave] = amax;
+      __syncthreads();
+      amax = fmaxf(fmaxf(gmax[0], gmax[1]), fmaxf(gmax[2], gmax[3]));
+      const float inv = amax == 0.f ? 0.f : 127.0f / amax;
+      float r = roundf(out[k] * inv);
+      r = fminf(fmaxf(r, -127.f), 127.f);
+      const int qi = (int)r;
+      int sm = qi;
+#pragma unroll
+      for (int off = 8; off >= 1; off >>= 1) sm += __shfl_xor(sm, off, 64);
+      const size_t e = orow + tid + 256 * k;
+      q8.q[e] = (int8_t)qi;
+      if ((lane & 15) == 0) q8.s16[e / 16] = sm;
+      if (tid == 0) q8.d[e / 256] = amax / 127.0f;
+    }
+  }
+}
+
+// Greedy argmax (sampler.rs:64-74): largest by the total order of floats,
+// ties to the last index; non-finite logits are flagged.
 __device__ __forceinline__ int32_t total_key(float f) {
   const int32_t b = __builtin_bit_cast(int32_t, f);
   return b ^ (int32_t)(((uint32_t)(b >> 31)) >> 1);
+}
+
+// Greedy argmax in two passes: argmax_part_kernel reduces chunks of 4096
+// logits of each row to (key, index, non-finite flag), argmax_final_kernel
+// the chunks of a row; ties go to the larger index (max_by keeps the last
+// maximum, src/sampler.rs:64-74) at both levels.
+constexpr uint32_t ARGMAX_CHUNK = 4096;
+struct ArgPart {
+  int32_t key;
+  uint32_t idx, bad;
+};
+__global__ __launch_bounds__(256) void argmax_part_kernel(const float *__restrict__ x, uint64_t n,
+                                                          ArgPart *__restrict__ part) {
+  __shared__ ArgPart sp[4];
+  const uint32_t chunk = blockIdx.x, row = blockIdx.y, nchunks = gridDim.x;
+  const float *xr = x + (size_t)row * n;
+  const uint64_t c0 = (uint64_t)chunk * ARGMAX_CHUNK, c1 = min(c0 + ARGMAX_CHUNK, n);
+  int32_t bk = INT32_MIN;
+  uint32_t bi = 0, bad = 0;
+  bool have = false;
+  for (uint64_t i = c0 + threadIdx.x; i < c1; i += 256) {
+    const float v = xr[i];
+    bad |= !isfinite(v);
+    const int32_t k = total_key(v);
+    if (!have || k >= bk) {
+      bk = k;
+      bi = (uint32_t)i;
+      have = true;
+    }
+  }
+  for (int o = 32; o >= 1; o >>= 1) {
+    const int32_t ok = __shfl_xor(bk, o, 64);
+    const uint32_t oi = __shfl_xor(bi, o, 64);
+    const int oh = __shfl_xor((int)have, o, 64);
+    if (oh && (!have || ok > bk || (ok == bk && oi > bi))) {
+      bk = ok;
+      bi = oi;
+      have = true;
+    }
+    bad |= __shfl_xor(bad, o, 64);
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) sp[w] = ArgPart{have ? bk : INT32_MIN, have ? bi : 0u, bad | (have ? 0u : 2u)};
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    ArgPart r = sp[0];
+    for (int j = 1; j < 4; j++) {
+      const ArgPart &c = sp[j];
+      const bool rh = !(r.bad & 2u), ch = !(c.bad & 2u);
+      if (ch && (!rh || c.key > r.key || (c.key == r.key && c.idx > r.idx))) r = ArgPart{c.key, c.idx, r.bad & 1u};
+      r.bad = (r.bad & 2u ? (ch ? 0u : 2u) : 0u) | ((r.bad | c.bad) & 1u);
+    }
+    part[(size_t)row * nchunks + chunk] = r;
+  }
+}
+
+__global__ __launch_bounds__(64) void argmax_final_kernel(const ArgPart *__restrict__ part, uint32_t nchunks,
+                                                          uint32_t *__restrict__ idx, uint32_t *__restrict__ flag) {
+  const uint32_t row = blockIdx.x;
+  ArgPart r{INT32_MIN, 0, 2u};
+  for (uint32_t c = threadIdx.x; c < nchunks; c += 64) {
+    const ArgPart p = part[(size_t)row * nchunks + c];
+    const bool rh = !(r.bad & 2u), ph = !(p.bad & 2u);
+    const uint32_t nb = (r.bad | p.bad) & 1u;
+    if (ph && (!rh || p.key > r.key || (p.key == r.key && p.idx > r.idx))) r = ArgPart{p.key, p.idx, nb};
+    else r.bad = (r.bad & 2u) | nb;
+  }
+  for (int o = 32; o >= 1; o >>= 1) {
+    const int32_t ok = __shfl_xor(r.key, o, 64);
+    const uint32_t oi = __shfl_xor(r.idx, o, 64), ob = __shfl_xor(r.bad, o, 64);
+    const bool rh = !(r.bad & 2u), oh = !(ob & 2u);
+    const uint32_t nb = (r.bad | ob) & 1u;
+    if (oh && (!rh || ok > r.key || (ok == r.key && oi > r.idx))) r = ArgPart{ok, oi, nb};
+    else r.bad = (r.bad & 2u) | nb;
+  }
+  if (threadIdx.x == 0) {
+    idx[row] = r.idx;
+    flag[row] = (r.bad & 1u) || (r.bad & 2u) ? 1u : 0u;  // non-finite, or an empty row
+  }
 }
 
 // One workgroup per row of x [rows, n]; the index goes to idx[row], the
@@ -366,58 +833,6 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(const float *__restri
   }
 }
 
-__global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ x, uint64_t n, uint32_t *out) {
-  __shared__ int32_t sk[16];
-  __shared__ uint32_t si[16];
-  __shared__ uint32_t sbad[16];
-  int32_t bk = INT32_MIN;
-  uint32_t bi = 0, bad = 0;
-  bool have = false;
-  for (uint64_t i = threadIdx.x; i < n; i += 1024) {
-    const float v = x[i];
-    bad |= !isfinite(v);
-    const int32_t k = total_key(v);
-    if (!have || k >= bk) {
-      bk = k;
-      bi = (uint32_t)i;
-      have = true;
-    }
-  }
-  // Reduce (key, index): larger key wins; equal keys keep the larger index.
-  for (int o = 32; o >= 1; o >>= 1) {
-    const int32_t ok = __shfl_xor(bk, o, 64);
-    const uint32_t oi = __shfl_xor(bi, o, 64);
-    const int oh = __shfl_xor((int)have, o, 64);
-    if (oh && (!have || ok > bk || (ok == bk && oi > bi))) {
-      bk = ok;
-      bi = oi;
-      have = true;
-    }
-    bad |= __shfl_xor(bad, o, 64);
-  }
-  const int w = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) {
-    sk[w] = have ? bk : INT32_MIN;
-    si[w] = have ? bi : 0;
-    sbad[w] = bad;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int32_t k = sk[0];
-    uint32_t idx = si[0], fl = sbad[0];
-    for (int j = 1; j < 16; j++) {
-      fl |= sbad[j];
-      if ((uint64_t)j * 64 >= n) continue;
-      if (sk[j] > k || (sk[j] == k && si[j] > idx)) {
-        k = sk[j];
-        idx = si[j];
-      }
-    }
-    out[0] = idx;
-    out[1] = fl;
-  }
-}
-
 uint32_t grid1d(uint64_t n, uint32_t per = 256) {
   uint64_t g = (n + per - 1) / per;
   if (g > 65536) g = 65536;
@@ -437,8 +852,26 @@ void launch_embed(mdma_ctx *ctx, int32_t dtype, int layout, const uint8_t *table
 
 void launch_rmsnorm(mdma_ctx *ctx, const float *w, uint64_t dim, const float *a, const float *b, float *sum,
                     float *y, uint64_t rows, float eps) {
-  rmsnorm_kernel<<<dim3((uint32_t)rows), dim3(256), 0, ctx->stream>>>(w, (uint32_t)dim, a, b, sum, y, eps);
+  if (dim % 4 == 0 && dim <= 16384)
+    rmsnorm_row_kernel<false><<<dim3((uint32_t)rows), dim3(1024), 0, ctx->stream>>>(w, (uint32_t)dim, a, b, sum, y,
+                                                                                     eps, nullptr, nullptr, nullptr);
+  else
+    rmsnorm_kernel<<<dim3((uint32_t)rows), dim3(256), 0, ctx->stream>>>(w, (uint32_t)dim, a, b, sum, y, eps);
   hip_check(hipGetLastError(), "rmsnorm launch");
+}
+
+bool launch_rmsnorm_q8(mdma_ctx *ctx, const float *w, uint64_t dim, const float *a, const float *b, float *sum,
+                       float *y, uint64_t rows, float eps) {
+  if (dim % 256 || dim > 16384) return false;
+  int8_t *q;
+  float *d;
+  int32_t *s16;
+  q8_slots(ctx, rows, dim, &q, &d, &s16);
+  rmsnorm_row_kernel<true><<<dim3((uint32_t)rows), dim3(1024), 0, ctx->stream>>>(w, (uint32_t)dim, a, b, sum, y,
+                                                                                  eps, q, d, s16);
+  hip_check(hipGetLastError(), "rmsnorm launch");
+  q8_mark(ctx, y, rows, dim);
+  return true;
 }
 
 void launch_add(mdma_ctx *ctx, const float *a, const float *b, float *y, uint64_t n) {
@@ -477,22 +910,89 @@ void launch_rope_kv_write(mdma_ctx *ctx, float *q, uint64_t q_heads, const float
   hip_check(hipGetLastError(), "rope_kv_write launch");
 }
 
-void launch_attn(mdma_ctx *ctx, const float *q, const uint16_t *k, const uint16_t *v, float *o, uint64_t n_q,
-                 uint64_t kv_len, uint64_t hd, uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride) {
+namespace {
+bool attn_impl(mdma_ctx *ctx, const float *q, const uint16_t *k, const uint16_t *v, float *o, uint64_t n_q,
+               uint64_t kv_len, uint64_t hd, uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride,
+               const AttnQ8 *q8) {
   const float scale = 1.0f / sqrtf((float)hd);
   const uint32_t prefix = (uint32_t)(seq_stride ? kv_len - 1 : kv_len - n_q);
+  const uint64_t G = n_kv_heads ? n_q_heads / n_kv_heads : 0, C = (hd + 127) / 128;
+  // Runs of tiles per (query, KV head): enough workgroups to cover the chip
+  // (about MDMA_ATT_WG_TARGET), at least one tile and at most ATT_MAX_RUNS
+  // runs each; long prompts use one run per query.
+  const uint64_t tiles = (kv_len + ATT_TILE - 1) / ATT_TILE, pairs = n_q * n_kv_heads;
+  uint64_t n_splits = pairs ? (MDMA_ATT_WG_TARGET + pairs - 1) / pairs : 1;
+  if (n_splits > ATT_MAX_RUNS) n_splits = ATT_MAX_RUNS;
+  if (n_splits > tiles) n_splits = tiles;
+  if (!n_splits) n_splits = 1;
+  const uint64_t tpw = (tiles + n_splits - 1) / n_splits;
+  n_splits = tiles ? (tiles + tpw - 1) / tpw : 1;
+  const uint64_t part_bytes = n_splits > 1 ? n_q * n_q_heads * n_splits * (hd + 2) * 4 : 0;
+  const bool split_ok = hd % 8 == 0 && hd <= 256 && (G == 1 || G == 2 || G == 4 || G == 8) && G * C <= 8 &&
+                        n_splits < 65536 && n_q < 65536 && part_bytes <= (256ull << 20);
+  if (q8 && !(split_ok && (G * hd) % 256 == 0)) return false;
+  if (split_ok && n_q && kv_len) {
+    float *part = part_bytes ? reinterpret_cast<float *>(scratch(ctx, part_bytes)) : nullptr;
+    uint32_t *cnt = part_bytes ? attn_counters(ctx, n_q * n_kv_heads) : nullptr;
+    const AttnQ8 a8 = q8 ? *q8 : AttnQ8{nullptr, nullptr, nullptr};
+    const dim3 grid((uint32_t)n_kv_heads, (uint32_t)n_splits, (uint32_t)n_q);
+#define MDMA_ATT(GG, CC)                                                                                       \
+  do {                                                                                                         \
+    if (q8)                                                                                                    \
+      attn_split_kernel<GG, CC, true><<<grid, dim3(256), 0, ctx->stream>>>(                                    \
+          q, k, v, o, part, cnt, prefix, (uint32_t)hd, (uint32_t)n_q_heads, (uint32_t)n_kv_heads, scale,      \
+          seq_stride, (uint32_t)tpw, a8);                                                                      \
+    else                                                                                                       \
+      attn_split_kernel<GG, CC, false><<<grid, dim3(256), 0, ctx->stream>>>(                                   \
+          q, k, v, o, part, cnt, prefix, (uint32_t)hd, (uint32_t)n_q_heads, (uint32_t)n_kv_heads, scale,      \
+          seq_stride, (uint32_t)tpw, a8);                                                                      \
+  } while (0)
+    if (C == 1) {
+      if (G == 1) MDMA_ATT(1, 1);
+      else if (G == 2) MDMA_ATT(2, 1);
+      else if (G == 4) MDMA_ATT(4, 1);
+      else MDMA_ATT(8, 1);
+    } else {
+      if (G == 1) MDMA_ATT(1, 2);
+      else if (G == 2) MDMA_ATT(2, 2);
+      else MDMA_ATT(4, 2);
+    }
+#undef MDMA_ATT
+    hip_check(hipGetLastError(), "attn launch");
+    return true;
+  }
   attn_kernel<<<dim3((uint32_t)n_q_heads, (uint32_t)n_q), dim3(256), 0, ctx->stream>>>(
       q, k, v, o, prefix, (uint32_t)hd, (uint32_t)n_q_heads, (uint32_t)n_kv_heads, scale, seq_stride);
   hip_check(hipGetLastError(), "attn launch");
+  return true;
+}
+}  // namespace
+
+void launch_attn(mdma_ctx *ctx, const float *q, const uint16_t *k, const uint16_t *v, float *o, uint64_t n_q,
+                 uint64_t kv_len, uint64_t hd, uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride) {
+  attn_impl(ctx, q, k, v, o, n_q, kv_len, hd, n_q_heads, n_kv_heads, seq_stride, nullptr);
 }
 
-void launch_argmax(mdma_ctx *ctx, const float *x, uint64_t n, uint32_t *out_dev) {
-  argmax_kernel<<<dim3(1), dim3(1024), 0, ctx->stream>>>(x, n, out_dev);
-  hip_check(hipGetLastError(), "argmax launch");
+bool launch_attn_q8(mdma_ctx *ctx, const float *q, const uint16_t *k, const uint16_t *v, float *o, uint64_t n_q,
+                    uint64_t kv_len, uint64_t hd, uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride) {
+  const uint64_t n_in = n_q_heads * hd;
+  if (!n_q || !kv_len || n_in % 256) return false;
+  AttnQ8 a8;
+  q8_slots(ctx, n_q, n_in, &a8.q, &a8.d, &a8.s16);
+  if (!attn_impl(ctx, q, k, v, o, n_q, kv_len, hd, n_q_heads, n_kv_heads, seq_stride, &a8)) return false;
+  q8_mark(ctx, o, n_q, n_in);
+  return true;
 }
 
 void launch_argmax_rows(mdma_ctx *ctx, const float *x, uint64_t rows, uint64_t n, uint32_t *idx, uint32_t *flag) {
-  argmax_rows_kernel<<<dim3((uint32_t)rows), dim3(1024), 0, ctx->stream>>>(x, n, idx, flag);
+  const uint32_t nchunks = (uint32_t)((n + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK);
+  if (nchunks <= 1 || rows > 65535) {
+    argmax_rows_kernel<<<dim3((uint32_t)rows), dim3(1024), 0, ctx->stream>>>(x, n, idx, flag);
+  } else {
+    ArgPart *part = reinterpret_cast<ArgPart *>(argmax_parts(ctx, rows * nchunks));
+    argmax_part_kernel<<<dim3(nchunks, (uint32_t)rows), dim3(256), 0, ctx->stream>>>(x, n, part);
+    argmax_final_kernel<<<dim3((uint32_t)rows), dim3(64), 0, ctx->stream>>>(part, nchunks, idx, flag);
+  }
   hip_check(hipGetLastError(), "argmax_rows launch");
 }
 

@@ -28,13 +28,13 @@ Q4_K_M = {"attn_q": GGML_Q6_K, "attn_k": GGML_Q6_K, "attn_v": GGML_Q6_K, "attn_o
           "token_embd": GGML_Q4_K}
 
 
-def _weight(dtype, rows, cols, seed):
+def _weight(dtype, rows, cols, seed, fast=False):
     if dtype == GGML_F32:
         return synth.normal_f32(rows * cols, seed, 0.02).view(np.uint8)
-    return synth.weight(dtype, rows, cols, seed)
+    return synth.weight(dtype, rows, cols, seed, fast)
 
 
-def tensors(geom: dict, dtypes: dict, seed: int):
+def tensors(geom: dict, dtypes: dict, seed: int, fast: bool = False):
     """Yields (name, dtype, [rows, cols] or [n], make_payload) in load order; the
     payload is generated only when make_payload() is called."""
     E, F, V = geom["n_embd"], geom["n_ff"], geom["vocab"]
@@ -52,7 +52,7 @@ def tensors(geom: dict, dtypes: dict, seed: int):
 
     def mat(dtype, rows, cols):
         s = nxt()
-        return lambda: _weight(dtype, rows, cols, s)
+        return lambda: _weight(dtype, rows, cols, s, fast)
 
     yield "token_embd.weight", dtypes["token_embd"], (V, E), mat(dtypes["token_embd"], V, E)
     for i in range(geom["n_layers"]):
@@ -76,5 +76,5 @@ def metadata(geom: dict) -> dict:
             "llama.rope.freq_base": float(geom["rope_theta"])}
 
 
-def write(path: str, geom: dict, dtypes: dict, seed: int) -> None:
-    gguf.write_stream(path, metadata(geom), list(tensors(geom, dtypes, seed)))
+def write(path: str, geom: dict, dtypes: dict, seed: int, fast: bool = False) -> None:
+    gguf.write_stream(path, metadata(geom), list(tensors(geom, dtypes, seed, fast)))

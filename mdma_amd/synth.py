@@ -73,6 +73,26 @@ class Stream:
         return z[:n]
 
 
+class FastStream:
+    """Same interface and distributions as Stream, from numpy's PCG64: for
+    large synthetic models whose bytes no test recomputes (about 30x faster)."""
+
+    def __init__(self, seed: int):
+        self.rng = np.random.Generator(np.random.PCG64(seed & 0xFFFFFFFFFFFFFFFF))
+
+    def uniform(self, n: int) -> np.ndarray:
+        return self.rng.random(n)
+
+    def ints(self, n: int, lo: int, hi: int) -> np.ndarray:
+        return self.rng.integers(lo, hi + 1, n, dtype=np.int64)
+
+    def bytes(self, n: int) -> np.ndarray:
+        return np.frombuffer(self.rng.bytes(n), dtype=np.uint8).copy()
+
+    def normal(self, n: int) -> np.ndarray:
+        return self.rng.standard_normal(n)
+
+
 def f16_bytes(v: np.ndarray) -> np.ndarray:
     return np.asarray(v, dtype=np.float32).astype(np.float16).view(np.uint8).reshape(-1, 2)
 
@@ -89,10 +109,10 @@ def pack_q4k_scales(sc: np.ndarray, m: np.ndarray) -> np.ndarray:
     return out
 
 
-def q4k_blocks(n_blocks: int, seed: int, d_scale: float = 1e-3) -> np.ndarray:
+def q4k_blocks(n_blocks: int, seed: int, fast: bool = False, d_scale: float = 1e-3) -> np.ndarray:
     """Q4_K: d, dmin = f16(|N(0,1)|*1e-3), six-bit scales and
     mins uniform in [0,63], 4-bit quants uniform in [0,15]."""
-    s = Stream(seed)
+    s = (FastStream if fast else Stream)(seed)
     d = np.abs(s.normal(n_blocks)) * d_scale
     dmin = np.abs(s.normal(n_blocks)) * d_scale
     sc = s.ints(n_blocks * 8, 0, 63).reshape(n_blocks, 8)
@@ -105,10 +125,10 @@ def q4k_blocks(n_blocks: int, seed: int, d_scale: float = 1e-3) -> np.ndarray:
     return blk.reshape(-1)
 
 
-def q6k_blocks(n_blocks: int, seed: int, d_scale: float = 1e-3) -> np.ndarray:
+def q6k_blocks(n_blocks: int, seed: int, fast: bool = False, d_scale: float = 1e-3) -> np.ndarray:
     """Q6_K: uniform ql/qh bytes, int8 sub-scales uniform in
     [-64,63], d = f16(|N(0,1)|*1e-3)."""
-    s = Stream(seed)
+    s = (FastStream if fast else Stream)(seed)
     blk = np.empty((n_blocks, 210), dtype=np.uint8)
     blk[:, 0:192] = s.bytes(n_blocks * 192).reshape(n_blocks, 192)
     blk[:, 192:208] = s.ints(n_blocks * 16, -64, 63).astype(np.int8).view(np.uint8).reshape(n_blocks, 16)
@@ -116,24 +136,25 @@ def q6k_blocks(n_blocks: int, seed: int, d_scale: float = 1e-3) -> np.ndarray:
     return blk.reshape(-1)
 
 
-def q8_0_blocks(n_blocks: int, seed: int, d_scale: float = 0.02) -> np.ndarray:
+def q8_0_blocks(n_blocks: int, seed: int, fast: bool = False, d_scale: float = 0.02) -> np.ndarray:
     """Q8_0: fp16 d = |N(0,1)|*0.02, int8 quants uniform in [-127,127]."""
-    s = Stream(seed)
+    s = (FastStream if fast else Stream)(seed)
     blk = np.empty((n_blocks, 34), dtype=np.uint8)
     blk[:, 0:2] = f16_bytes(np.abs(s.normal(n_blocks)) * d_scale)
     blk[:, 2:34] = s.ints(n_blocks * 32, -127, 127).astype(np.int8).view(np.uint8).reshape(n_blocks, 32)
     return blk.reshape(-1)
 
 
-def weight(dtype: int, n_out: int, n_in: int, seed: int) -> np.ndarray:
-    """Raw GGUF bytes of an [n_out, n_in] weight with the benchmark distribution of its dtype."""
+def weight(dtype: int, n_out: int, n_in: int, seed: int, fast: bool = False) -> np.ndarray:
+    """Raw GGUF bytes of an [n_out, n_in] weight with the benchmark distribution
+    of its dtype (fast: PCG64 stream, see FastStream)."""
     nb = n_out * (n_in // BLOCK_SIZE[dtype])
     if dtype == GGML_Q4_K:
-        return q4k_blocks(nb, seed)
+        return q4k_blocks(nb, seed, fast)
     if dtype == GGML_Q6_K:
-        return q6k_blocks(nb, seed)
+        return q6k_blocks(nb, seed, fast)
     if dtype == GGML_Q8_0:
-        return q8_0_blocks(nb, seed)
+        return q8_0_blocks(nb, seed, fast)
     if dtype == GGML_F32:
         return normal_f32(n_out * n_in, seed).view(np.uint8)
     if dtype == GGML_F16:

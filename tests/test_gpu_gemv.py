@@ -328,6 +328,63 @@ def test_i8_activation_cache_reuses_and_invalidates(backend):
     assert np.array_equal(backend.download_f32(y), backend.download_f32(want))
 
 
+@pytest.mark.parametrize("T", [1, 3, 15, 16])
+def test_rmsnorm_int8_activations_bit_exact(backend, T):
+    # In the int8 mode an rmsnorm of fewer than 16 rows also leaves the int8
+    # form of its output in the activation cache; a qmatmul reading y must
+    # give the bits of one reading an identical copy of y quantized afresh.
+    k, rows = 4096, 40
+    w = backend.upload_weight(synth.weight(Q4K, rows, k, 3), Q4K, (rows, k))
+    w6 = backend.upload_weight(synth.weight(Q6K, rows, k, 4), Q6K, (rows, k))
+    g = backend.f32_buf(synth.normal_f32(k, 5))
+    a, b = backend.f32_buf(synth.normal_f32(T * k, 6)), backend.f32_buf(synth.normal_f32(T * k, 7))
+    y, s = backend.alloc(T * k * 4), backend.alloc(T * k * 4)
+    out, ref = backend.alloc(T * rows * 4), backend.alloc(T * rows * 4)
+    backend.set_act_mode(backend_mod.ACT_I8)
+    try:
+        for fused in (lambda: backend.rmsnorm(g, a, y, 1e-5), lambda: backend.add_rmsnorm(g, a, b, s, y, 1e-5)):
+            fused()
+            for wt in (w, w6):
+                backend.qmatmul(wt, y, out)
+                backend.qmatmul(wt, backend.f32_buf(backend.download_f32(y)), ref)
+                assert np.array_equal(backend.download_f32(out), backend.download_f32(ref))
+        # The normalized values themselves are those of the f32 mode.
+        backend.rmsnorm(g, a, y, 1e-5)
+        got = backend.download_f32(y)
+    finally:
+        backend.set_act_mode(backend_mod.ACT_F32)
+    backend.rmsnorm(g, a, y, 1e-5)
+    assert np.array_equal(got, backend.download_f32(y))
+
+
+@pytest.mark.parametrize("n_q,kv_len", [(1, 40), (1, 700), (3, 130), (15, 15)])
+def test_attention_int8_activations_bit_exact(backend, n_q, kv_len):
+    # Same for attention's output (Llama-3-8B heads: 32 query, 8 KV, 128 wide),
+    # which then feeds the output projection.
+    from mdma_amd.backend import AttnSpec, KvView
+    hd, nq, nkv, rows = 128, 32, 8, 40
+    k = synth.normal_f32(kv_len * nkv * hd, 8).astype(np.float16)
+    v = synth.normal_f32(kv_len * nkv * hd, 9).astype(np.float16)
+    kb, vb = backend.alloc(k.size * 2), backend.alloc(v.size * 2)
+    backend.upload(kb, 0, k)
+    backend.upload(vb, 0, v)
+    q = backend.f32_buf(synth.normal_f32(n_q * nq * hd, 10))
+    o = backend.alloc(n_q * nq * hd * 4)
+    w = backend.upload_weight(synth.weight(Q6K, rows, nq * hd, 11), Q6K, (rows, nq * hd))
+    out, ref = backend.alloc(n_q * rows * 4), backend.alloc(n_q * rows * 4)
+    backend.set_act_mode(backend_mod.ACT_I8)
+    try:
+        backend.attn(q, KvView(kb, vb, kv_len), AttnSpec(hd, nq, nkv), o)
+        got = backend.download_f32(o)
+        backend.qmatmul(w, o, out)
+        backend.qmatmul(w, backend.f32_buf(got), ref)
+        assert np.array_equal(backend.download_f32(out), backend.download_f32(ref))
+    finally:
+        backend.set_act_mode(backend_mod.ACT_F32)
+    backend.attn(q, KvView(kb, vb, kv_len), AttnSpec(hd, nq, nkv), o)
+    assert np.array_equal(got, backend.download_f32(o))
+
+
 # ---------------------------------------------------------- shape rules ----
 
 def test_qmatmul_shape_rules(backend):

@@ -47,7 +47,7 @@ def test_embed_q4k_known_answer_blocks(backend):
         assert np.array_equal(backend.download_f32(out), ffi.embed(Q4K, raw.reshape(-1), 3, 256, [0, 1, 2]).reshape(-1))
 
 
-@pytest.mark.parametrize("dim,rows", [(2, 1), (288, 8), (4096, 3), (1000, 2)])
+@pytest.mark.parametrize("dim,rows", [(2, 1), (288, 8), (4096, 3), (1000, 2), (16384, 2), (4098, 2), (5120, 1)])
 def test_rmsnorm_and_add_rmsnorm(backend, dim, rows):
     w = synth.normal_f32(dim, 1)
     a = synth.normal_f32(dim * rows, 2)
@@ -119,7 +119,10 @@ def test_kv_write_and_fused_rope_kv_write(backend):
 
 
 @pytest.mark.parametrize("hd,nq,nkv,n_q,kv_len", [(2, 1, 1, 1, 2), (48, 6, 6, 1, 9), (48, 6, 6, 8, 8),
-                                                  (128, 32, 8, 1, 700), (128, 32, 8, 4, 2500), (64, 4, 1, 5, 5)])
+                                                  (128, 32, 8, 1, 700), (128, 32, 8, 4, 2500), (64, 4, 1, 5, 5),
+                                                  (128, 32, 8, 1, 64), (128, 32, 8, 1, 65), (128, 32, 8, 70, 70),
+                                                  (128, 16, 2, 3, 300), (256, 8, 2, 2, 130), (96, 6, 3, 1, 200),
+                                                  (64, 12, 4, 2, 129)])
 def test_attention_over_f16_cache(backend, hd, nq, nkv, n_q, kv_len):
     q = synth.normal_f32(n_q * nq * hd, 1)
     k = f16r(synth.normal_f32(kv_len * nkv * hd, 2))
@@ -149,10 +152,23 @@ def test_attention_hand_computed(backend):
 
 def test_greedy(backend):
     for x in (np.array([1.0, 3.0, 2.0, 3.0, -1.0], np.float32), np.array([-0.0, 0.0, -0.0], np.float32),
-              synth.normal_f32(32000, 1), synth.normal_f32(128256, 2), np.full(5000, 2.5, np.float32)):
+              synth.normal_f32(32000, 1), synth.normal_f32(128256, 2), np.full(5000, 2.5, np.float32),
+              np.full(12289, -np.float32(3e38), np.float32)):
         assert backend.greedy(backend.f32_buf(x)) == ffi.greedy(x)
+    # The maximum, and a tie for it, in different chunks of 4096.
+    x = synth.normal_f32(20000, 4)
+    x[5000] = x[17000] = 9.0
+    assert backend.greedy(backend.f32_buf(x)) == ffi.greedy(x) == 17000
+    x[17000] = 8.0
+    assert backend.greedy(backend.f32_buf(x)) == 5000
+    # Sub-range of a buffer (offset, n).
+    assert backend.greedy(backend.f32_buf(x), 4097, 9000) == 5000 - 4097
     from mdma_amd.backend import BackendError
     bad = synth.normal_f32(100, 3)
     bad[17] = np.inf
+    with pytest.raises(BackendError):
+        backend.greedy(backend.f32_buf(bad))
+    bad = synth.normal_f32(10000, 5)
+    bad[9999] = np.nan
     with pytest.raises(BackendError):
         backend.greedy(backend.f32_buf(bad))
