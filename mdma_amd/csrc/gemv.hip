@@ -812,6 +812,11 @@ void quantize_into_scratch(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n
 }
 
 
+// Tokens from which int8-mode GEMVs of prepared rows go to the matrix-core
+// batch kernel (below: the row-team kernels, which keep each token's
+// activations in registers).
+constexpr uint64_t BATCH_MIN_TOKENS = 5;
+
 // Prepared-layout jobs go to the row-team kernels; a mix of layouts or
 // dtypes runs job by job; raw GGUF jobs use the kernels above.
 static bool any_prepared(const GemvJob *jobs, int n) {
@@ -885,6 +890,19 @@ void launch_gemv_i8(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float 
       launch_gemv_f32(ctx, jobs, n_jobs, x, T);
       return;
     }
+  if (T >= BATCH_MIN_TOKENS && gemv_batch_ok(jobs, n_jobs, 16)) {
+    // Up to 16 tokens per matrix-core launch (a short remainder: row teams).
+    for (uint64_t t0 = 0; t0 < T; t0 += 16) {
+      const uint64_t tn = T - t0 < 16 ? T - t0 : 16;
+      GemvJob js[3];
+      for (int i = 0; i < n_jobs; i++) js[i] = offset_job(jobs[i], t0);
+      if (tn < BATCH_MIN_TOKENS)
+        launch_gemv_team(ctx, MDMA_ACT_I8, js, n_jobs, false, x + t0 * jobs[0].n_in, tn, nullptr);
+      else
+        launch_gemv_batch(ctx, js, n_jobs, false, x + t0 * jobs[0].n_in, tn, nullptr);
+    }
+    return;
+  }
   if (team_layout_ok(jobs, n_jobs)) {
     launch_gemv_team(ctx, MDMA_ACT_I8, jobs, n_jobs, false, x, T, nullptr);
     return;
@@ -911,6 +929,19 @@ void launch_gemv_i8_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up,
   const GemvJob gu[2] = {gate, up};
   if (try_gemm_i8(ctx, gu, 2, x, T)) {
     launch_silu_mul(ctx, gate.y, up.y, y, T * gate.n_out);
+    return;
+  }
+  if (T >= BATCH_MIN_TOKENS && gemv_batch_ok(gu, 2, 16)) {
+    for (uint64_t t0 = 0; t0 < T; t0 += 16) {
+      const uint64_t tn = T - t0 < 16 ? T - t0 : 16;
+      const GemvJob js[2] = {offset_job(gate, t0), offset_job(up, t0)};
+      const float *xt = x + t0 * gate.n_in;
+      float *yt = y + t0 * gate.n_out;
+      if (tn < BATCH_MIN_TOKENS)
+        launch_gemv_team(ctx, MDMA_ACT_I8, js, 2, true, xt, tn, yt);
+      else
+        launch_gemv_batch(ctx, js, 2, true, xt, tn, yt);
+    }
     return;
   }
   if (team_layout_ok(gu, 2) && gate.n_in % 256 == 0) {

@@ -127,8 +127,9 @@ struct Q4G {
     }
     int sca, scb, ma, mb;
     q4k_scales_i(hd, u & 3, sca, scb, ma, mb);
-    const int A = sca * ia + scb * ib;
-    const int B = ma * x.sa + mb * x.sb;
+    // 24-bit multiplies (full rate): |isum| <= 15*127*32, |xsum| <= 127*32.
+    const int A = __mul24(sca, ia) + __mul24(scb, ib);
+    const int B = __mul24(ma, x.sa) + __mul24(mb, x.sb);
     const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
     return x.d8 * fmaf(d, (float)A, -dmin * (float)B);
   }
@@ -222,7 +223,8 @@ struct Q6G {
       int s = 0;
 #pragma unroll
       for (int k = 0; k < 4; k++) s = __builtin_amdgcn_sdot4((int)u6(w, r, k), (int)xv[k], s, false);
-      A += (int)(int8_t)((w.sc >> (8 * r)) & 0xff) * (s - 32 * x.sq[r]);
+      // 24-bit multiply (full rate): |s - 32*xsum| <= 63*127*16 + 32*127*16.
+      A += __mul24((int)(int8_t)((w.sc >> (8 * r)) & 0xff), s - 32 * x.sq[r]);
     }
     return x.d8 * (h2f(w.d) * (float)A);
   }

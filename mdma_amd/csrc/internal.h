@@ -150,6 +150,11 @@ void launch_gemv_i8_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up,
 // mode MDMA_ACT_F32 or MDMA_ACT_I8 (I8 needs n_in % 256 == 0). Gated: jobs =
 // {gate, up}, output silu(gate x) * (up x) into ygated.
 bool team_layout_ok(const GemvJob *jobs, int n_jobs);
+// Batched decode (2..16 tokens, int8 mode) on the matrix cores for prepared
+// Q4_K / Q6_K / Q8_0 rows of whole 256-column groups (gemv_batch.hip).
+bool gemv_batch_ok(const GemvJob *jobs, int n_jobs, uint64_t T);
+void launch_gemv_batch(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, bool gated, const float *x, uint64_t T,
+                       float *ygated);
 void launch_gemv_team(mdma_ctx *ctx, int mode, const GemvJob *jobs, int n_jobs, bool gated, const float *x,
                       uint64_t T, float *ygated);
 // The int8 activations of x [T, n_in] (per-256 f32 scales, per-16 sums) in

@@ -179,17 +179,38 @@ def test_i8_mode_llama3_8b_shapes(backend, dtype, shape):
     assert rel_rms < 0.03, rel_rms
 
 
-@pytest.mark.parametrize("T", [2, 5, 8, 11])
+@pytest.mark.parametrize("T", [2, 5, 8, 11, 16, 17, 35])
 def test_i8_mode_batched(backend, T):
     rows, k = 29, 2048
     for dtype in (Q4K, Q6K, Q8):
         raw = synth.weight(dtype, rows, k, T)
         x = synth.normal_f32(T * k, 50 + T)
         got = run_qmatmul(backend, dtype, raw, rows, k, x, "i8")
-        q = np.concatenate([ffi.quantize_act(x[t * k:(t + 1) * k], 256)[0] for t in range(T)])
-        d = np.concatenate([ffi.quantize_act(x[t * k:(t + 1) * k], 256)[1] for t in range(T)])
-        cpu, exact = oracle_f32(dtype, raw, rows, k, ffi.dequantize_act(q, d, 256))
+        # From 16 tokens, Q4_K and Q8_0 go to the prefill GEMM, whose
+        # activations are quantized per 32.
+        g = 32 if T >= 16 and dtype != Q6K else 256
+        q = np.concatenate([ffi.quantize_act(x[t * k:(t + 1) * k], g)[0] for t in range(T)])
+        d = np.concatenate([ffi.quantize_act(x[t * k:(t + 1) * k], g)[1] for t in range(T)])
+        cpu, exact = oracle_f32(dtype, raw, rows, k, ffi.dequantize_act(q, d, g))
         assert_parity(got, cpu, exact, 1e-3, what=f"i8 batched {dtype} T={T}")
+
+
+@pytest.mark.parametrize("dtype,shape,T", [(Q6K, (4096, 14336), 4), (Q6K, (4096, 14336), 8),
+                                           (Q4K, (14336, 4096), 8), (Q8, (4096, 4096), 3)])
+def test_i8_mode_batched_llama3_8b_shapes(backend, dtype, shape, T):
+    # The decode-batching case (batch 4 and 8) at Llama-3-8B shapes.
+    rows, k = shape
+    raw = synth.weight(dtype, rows, k, 21)
+    x = synth.normal_f32(T * k, 22)
+    got = run_qmatmul(backend, dtype, raw, rows, k, x, "i8")
+    xh = np.concatenate([ffi.dequantize_act(*ffi.quantize_act(x[t * k:(t + 1) * k], 256)[:2], 256) for t in range(T)])
+    cpu, exact = oracle_f32(dtype, raw, rows, k, xh)
+    # atol 1e-5: outputs near zero are differences of per-256 terms of order
+    # one, each rounded once in f32 by the single-token kernel.
+    assert_parity(got, cpu, exact, 1e-3, atol=1e-5, what=f"i8 batched {dtype} {shape} T={T}")
+    # Each token's row equals that token decoded alone, within the same bar.
+    one = run_qmatmul(backend, dtype, raw, rows, k, x[(T - 1) * k:], "i8")
+    assert_parity(one[0], cpu[T - 1], exact[T - 1], 1e-3, atol=1e-5, what="single token")
 
 
 @pytest.mark.parametrize("group", [32, 256])
