@@ -802,6 +802,10 @@ void q8_mark(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in) {
   ctx->q8_n_in = n_in;
 }
 
+bool q8_holds(mdma_ctx *ctx, const float *x, uint64_t n) {
+  return ctx->q8_valid && ctx->q8_x == x && ctx->q8_n == n && ctx->q8_n_in == n;
+}
+
 void quantize_into_scratch(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in, int8_t **qx, float **dx,
                            int32_t **s16) {
   q8_slots(ctx, T, n_in, qx, dx, s16);
@@ -890,6 +894,10 @@ void launch_gemv_i8(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float 
       launch_gemv_f32(ctx, jobs, n_jobs, x, T);
       return;
     }
+  if (T == 1 && !q8_holds(ctx, x, n_jobs ? jobs[0].n_in : 0)) {
+    // One token: quantized in the GEMV's own prologue (one launch).
+    if (launch_gemv_i8_x(ctx, jobs, n_jobs, false, x, nullptr)) return;
+  }
   if (T >= BATCH_MIN_TOKENS && gemv_batch_ok(jobs, n_jobs, 16)) {
     // Up to 16 tokens per matrix-core launch (a short remainder: row teams).
     for (uint64_t t0 = 0; t0 < T; t0 += 16) {
@@ -930,6 +938,9 @@ void launch_gemv_i8_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up,
   if (try_gemm_i8(ctx, gu, 2, x, T)) {
     launch_silu_mul(ctx, gate.y, up.y, y, T * gate.n_out);
     return;
+  }
+  if (T == 1 && !q8_holds(ctx, x, gate.n_in)) {
+    if (launch_gemv_i8_x(ctx, gu, 2, true, x, y)) return;
   }
   if (T >= BATCH_MIN_TOKENS && gemv_batch_ok(gu, 2, 16)) {
     for (uint64_t t0 = 0; t0 < T; t0 += 16) {

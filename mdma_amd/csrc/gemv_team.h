@@ -48,6 +48,11 @@ __device__ __forceinline__ uint32_t ld32(const uint8_t *p) {
 __device__ __forceinline__ uint32_t ld16b(const uint8_t *p) {
   return __builtin_nontemporal_load(reinterpret_cast<const uint16_t *>(p));
 }
+// The value of another lane of the quad (DPP quad_perm).
+template <int PERM>
+__device__ __forceinline__ uint32_t quad_perm_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, PERM, 0xF, 0xF, false);
+}
 // Dword k of the quad (lanes 4j..4j+3 hold the four dwords of one header).
 template <int K>
 __device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
@@ -97,6 +102,12 @@ struct Q4G {
   }
   __device__ static uint4 header(uint32_t h) {
     return make_uint4(quad_bcast<0>(h), quad_bcast<1>(h), quad_bcast<2>(h), quad_bcast<3>(h));
+  }
+  // First column of chunk c (16 columns) of unit u, and the activations of
+  // a unit from its four chunks (int8 bytes, their sums) and its scale.
+  __device__ static uint32_t chunk_col(uint32_t u, int c) { return 64 * u + 16 * c; }
+  __device__ static XI make_xi(const uint4 *q, const int *s, float d8) {
+    return XI{q[0], q[1], q[2], q[3], s[0] + s[1], s[2] + s[3], d8};
   }
   __device__ static XI loadxi(const int8_t *qx, const float *dx, const int32_t *s16, uint32_t u) {
     const int8_t *xt = qx + 64 * (size_t)u;
@@ -182,6 +193,10 @@ struct Q6G {
   // First column of quarter r of unit u.
   __device__ static uint32_t col(uint32_t u, int r) {
     return 256 * (u >> 2) + 128 * ((u >> 1) & 1) + 32 * r + 16 * (u & 1);
+  }
+  __device__ static uint32_t chunk_col(uint32_t u, int c) { return col(u, c); }
+  __device__ static XI make_xi(const uint4 *q, const int *s, float d8) {
+    return XI{{q[0], q[1], q[2], q[3]}, {s[0], s[1], s[2], s[3]}, d8};
   }
   __device__ static XI loadxi(const int8_t *qx, const float *dx, const int32_t *s16, uint32_t u) {
     XI r;
@@ -294,6 +309,50 @@ struct Q8G {
   }
 };
 
+// ----------------------------------------------------------- prologue ----
+// The int8 activations of unit u quantized from f32 x inside the GEMV, per
+// 256 columns (the four units of a quad): the arithmetic of
+// quantize_act_kernel, bit for bit.
+template <class F>
+__device__ typename F::XI prologue_xi(const float *__restrict__ x, uint32_t u, bool ok) {
+  float v[4][16];
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const uint32_t col = F::chunk_col(u, c);
+#pragma unroll
+    for (int k = 0; k < 16; k += 4) {
+      const float4 xv = ok ? *reinterpret_cast<const float4 *>(x + col + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+      v[c][k] = xv.x, v[c][k + 1] = xv.y, v[c][k + 2] = xv.z, v[c][k + 3] = xv.w;
+    }
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int c = 0; c < 4; c++)
+#pragma unroll
+    for (int k = 0; k < 16; k++) amax = fmaxf(amax, fabsf(v[c][k]));
+  amax = fmaxf(amax, __builtin_bit_cast(float, quad_perm_u32<0xB1>(__builtin_bit_cast(uint32_t, amax))));
+  amax = fmaxf(amax, __builtin_bit_cast(float, quad_perm_u32<0x4E>(__builtin_bit_cast(uint32_t, amax))));
+  const float inv = amax == 0.f ? 0.f : 127.0f / amax;
+  uint4 q[4];
+  int sums[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    uint32_t w4[4] = {0u, 0u, 0u, 0u};
+    int sm = 0;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      float r = roundf(v[c][k] * inv);
+      r = fminf(fmaxf(r, -127.f), 127.f);
+      const int qi = (int)r;
+      sm += qi;
+      w4[k >> 2] |= (uint32_t)(qi & 0xff) << (8 * (k & 3));
+    }
+    q[c] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+    sums[c] = sm;
+  }
+  return F::make_xi(q, sums, amax / 127.0f);
+}
+
 // ------------------------------------------------------------- kernel ----
 
 struct TeamJob {
@@ -305,6 +364,7 @@ struct TeamSet {
   TeamJob j[3];
   int n;
   uint32_t n_in, rpt;  // shared row length; rows per team (a multiple of R)
+  bool pro;            // one token, int8: x (f32) quantized in the prologue
 };
 
 // Row groups in flight per wave (loads issued NBUF-1 groups ahead): three
@@ -319,7 +379,11 @@ constexpr int nbuf() {
 #endif
 }
 
-template <class F, bool F32, int R, int ITERS, int TW, int PL, int TT, bool GATED>
+// PRO: one token whose int8 activations the kernel quantizes from f32 x
+// itself instead of reading the quantized-x buffers (a separate
+// instantiation: the prologue's registers would otherwise lower every
+// launch's occupancy).
+template <class F, bool F32, int R, int ITERS, int TW, int PL, int TT, bool GATED, bool PRO = false>
 __global__ __launch_bounds__(WG) void gemv_team(TeamSet ts, const float *__restrict__ xf,
                                                 const int8_t *__restrict__ qx, const float *__restrict__ dx,
                                                 const int32_t *__restrict__ s16, uint32_t T,
@@ -447,12 +511,19 @@ __global__ __launch_bounds__(WG) void gemv_team(TeamSet ts, const float *__restr
     }
   };
 
-  // The first rows' weights go out before the activations: the weights come
-  // from HBM, the activations from L2.
+  auto first_loads = [&]() {
 #pragma unroll
-  for (int it = 0; it < NBUF - 1 && it < ITERS; it++) load(buf[it], r_begin + it * R);
-  // Activations of the lane's units, loaded once.
-  if constexpr (!F32) {
+    for (int it = 0; it < NBUF - 1 && it < ITERS; it++) load(buf[it], r_begin + it * R);
+  };
+  // Activations of the lane's units, loaded once. The first rows' weights
+  // go out before them: the weights come from HBM, the activations from L2.
+  if constexpr (PRO) {
+    // The weights go out first, then each wave quantizes its lanes' x.
+    first_loads();
+#pragma unroll
+    for (int p = 0; p < PL; p++) xi[p][0] = prologue_xi<F>(xf, uid[p], uok[p]);
+  } else if constexpr (!F32) {
+    first_loads();
 #pragma unroll
     for (int p = 0; p < PL; p++)
 #pragma unroll
@@ -462,8 +533,11 @@ __global__ __launch_bounds__(WG) void gemv_team(TeamSet ts, const float *__restr
                              s16 + (size_t)tc * (n_in / 16), uid[p]);
       }
   } else if constexpr (TT == 1) {
+    first_loads();
 #pragma unroll
     for (int p = 0; p < PL; p++) xr[p] = F::loadxf(xf, uid[p]);
+  } else {
+    first_loads();
   }
 
   // The team's run is ITERS row groups, fully unrolled: straight-line code
@@ -528,14 +602,24 @@ void launch_iters(mdma_ctx *ctx, TeamSet ts, int tw, int pl, const float *xf, co
   // duration, as a profiler measures it); they apply to one launch.
   hipEvent_t t0 = ctx->time_start, t1 = ctx->time_stop;
   ctx->time_start = ctx->time_stop = nullptr;
-#define MDMA_TEAM_LAUNCH(TW_, PL_)                                                                                 \
-  do {                                                                                                              \
-    if (t0 || t1)                                                                                                   \
-      hipExtLaunchKernelGGL(gemv_team<F, F32, R, ITERS, TW_, PL_, TT, GATED>, grid, block, 0, ctx->stream, t0, t1, \
-                            0, ts, xf, qx, dx, s16, T, yg);                                                         \
-    else                                                                                                            \
-      gemv_team<F, F32, R, ITERS, TW_, PL_, TT, GATED><<<grid, block, 0, ctx->stream>>>(ts, xf, qx, dx, s16, T,  \
-                                                                                       yg);                       \
+  constexpr bool PRO_OK = !F32 && TT == 1 && !std::is_same<F, Q8G>::value;
+#define MDMA_TEAM_GO(TW_, PL_, PRO_)                                                                              \
+  do {                                                                                                            \
+    if (t0 || t1)                                                                                                 \
+      hipExtLaunchKernelGGL(gemv_team<F, F32, R, ITERS, TW_, PL_, TT, GATED, PRO_>, grid, block, 0, ctx->stream,  \
+                            t0, t1, 0, ts, xf, qx, dx, s16, T, yg);                                               \
+    else                                                                                                          \
+      gemv_team<F, F32, R, ITERS, TW_, PL_, TT, GATED, PRO_><<<grid, block, 0, ctx->stream>>>(ts, xf, qx, dx,   \
+                                                                                              s16, T, yg);      \
+  } while (0)
+#define MDMA_TEAM_LAUNCH(TW_, PL_)                             \
+  do {                                                         \
+    if constexpr (PRO_OK) {                                    \
+      if (ts.pro) MDMA_TEAM_GO(TW_, PL_, true);                \
+      else MDMA_TEAM_GO(TW_, PL_, false);                      \
+    } else {                                                   \
+      MDMA_TEAM_GO(TW_, PL_, false);                           \
+    }                                                          \
   } while (0)
   if (tw == 1) MDMA_TEAM_LAUNCH(1, 1);
   else if (tw == 2) MDMA_TEAM_LAUNCH(2, 1);
@@ -543,6 +627,7 @@ void launch_iters(mdma_ctx *ctx, TeamSet ts, int tw, int pl, const float *xf, co
   else if (pl == 2) MDMA_TEAM_LAUNCH(4, 2);
   else MDMA_TEAM_LAUNCH(4, 4);
 #undef MDMA_TEAM_LAUNCH
+#undef MDMA_TEAM_GO
   hip_check(hipGetLastError(), "gemv team launch");
 }
 

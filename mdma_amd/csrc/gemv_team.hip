@@ -60,6 +60,14 @@ void launch_block_dot_prepared(mdma_ctx *ctx, const GemvJob &w, const int8_t *qx
   hip_check(hipGetLastError(), "block_dot launch");
 }
 
+bool launch_gemv_i8_x(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, bool gated, const float *x, float *ygated) {
+  if (!team_layout_ok(jobs, gated ? 2 : n_jobs)) return false;
+  const int32_t dt = jobs[0].dtype;
+  if ((dt != DT_Q4_K && dt != DT_Q6_K) || jobs[0].n_in % 256) return false;
+  launch_gemv_team(ctx, MDMA_ACT_I8, jobs, n_jobs, gated, x, 1, ygated, true);
+  return true;
+}
+
 bool team_layout_ok(const GemvJob *jobs, int n_jobs) {
   for (int i = 0; i < n_jobs; i++)
     if (jobs[i].layout != MDMA_LAYOUT_GFX950 || jobs[i].dtype != jobs[0].dtype || jobs[i].n_in != jobs[0].n_in)
@@ -70,17 +78,18 @@ bool team_layout_ok(const GemvJob *jobs, int n_jobs) {
 }
 
 void launch_gemv_team(mdma_ctx *ctx, int mode, const GemvJob *jobs, int n_jobs, bool gated, const float *x,
-                      uint64_t T, float *ygated) {
+                      uint64_t T, float *ygated, bool pro) {
   const uint64_t n_in = jobs[0].n_in;
   int8_t *qx = nullptr;
   float *dx = nullptr;
   int32_t *s16 = nullptr;
   const bool f32 = mode != MDMA_ACT_I8;
   const int32_t dt = jobs[0].dtype;
-  if (!f32) quantize_into_scratch(ctx, x, T, n_in, &qx, &dx, &s16);
+  if (!f32 && !pro) quantize_into_scratch(ctx, x, T, n_in, &qx, &dx, &s16);
   for (uint64_t t0 = 0; t0 < T; t0 += 8) {
     const uint32_t tn = (uint32_t)(T - t0 < 8 ? T - t0 : 8);
     TeamSet ts{};
+    ts.pro = pro;
     ts.n = gated ? 1 : n_jobs;  // gated: teams cover the gate rows and also read up
     ts.n_in = (uint32_t)n_in;
     for (int i = 0; i < (gated ? 2 : n_jobs); i++) {

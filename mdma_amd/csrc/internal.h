@@ -150,13 +150,20 @@ void launch_gemv_i8_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up,
 // mode MDMA_ACT_F32 or MDMA_ACT_I8 (I8 needs n_in % 256 == 0). Gated: jobs =
 // {gate, up}, output silu(gate x) * (up x) into ygated.
 bool team_layout_ok(const GemvJob *jobs, int n_jobs);
+// One token, int8 mode, prepared Q4_K / Q6_K rows: the GEMV quantizes f32 x
+// itself in its prologue (per 256, as launch_quantize_act, bit for bit) --
+// one launch instead of two. False (nothing launched) when the shape has no
+// such variant.
+bool launch_gemv_i8_x(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, bool gated, const float *x, float *ygated);
+
 // Batched decode (2..16 tokens, int8 mode) on the matrix cores for prepared
 // Q4_K / Q6_K / Q8_0 rows of whole 256-column groups (gemv_batch.hip).
 bool gemv_batch_ok(const GemvJob *jobs, int n_jobs, uint64_t T);
 void launch_gemv_batch(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, bool gated, const float *x, uint64_t T,
                        float *ygated);
+// pro: one token in the int8 mode, x quantized by the GEMV's prologue.
 void launch_gemv_team(mdma_ctx *ctx, int mode, const GemvJob *jobs, int n_jobs, bool gated, const float *x,
-                      uint64_t T, float *ygated);
+                      uint64_t T, float *ygated, bool pro = false);
 // The int8 activations of x [T, n_in] (per-256 f32 scales, per-16 sums) in
 // the context's activation buffer, quantized now unless it already holds
 // exactly this x.
@@ -164,6 +171,8 @@ void launch_gemv_team(mdma_ctx *ctx, int mode, const GemvJob *jobs, int n_jobs, 
 // scales, sums of 16), and marking them as holding x's quantization.
 void q8_slots(mdma_ctx *ctx, uint64_t T, uint64_t n_in, int8_t **qx, float **dx, int32_t **s16);
 void q8_mark(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in);
+// The buffer holds the int8 form of the one row x of n values.
+bool q8_holds(mdma_ctx *ctx, const float *x, uint64_t n);
 void quantize_into_scratch(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in, int8_t **qx, float **dx,
                            int32_t **s16);
 // Prefill int8 MFMA GEMM (gemm_i8.hip) over prepared Q8_0 / Q4_K weights:

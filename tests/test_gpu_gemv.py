@@ -406,6 +406,34 @@ def test_attention_int8_activations_bit_exact(backend, n_q, kv_len):
     assert np.array_equal(got, backend.download_f32(o))
 
 
+@pytest.mark.parametrize("dtype", [Q4K, Q6K])
+@pytest.mark.parametrize("k", [256, 4096, 14336])
+def test_one_token_in_kernel_quantization_bit_exact(backend, dtype, k):
+    # One int8 token: the GEMV quantizes x itself; the result must be the
+    # bits of the GEMV over separately quantized x (x cached by rmsnorm).
+    rows = 48
+    w = backend.upload_weight(synth.weight(dtype, rows, k, 41), dtype, (rows, k))
+    x = synth.normal_f32(k, 42) * 3
+    x[:256] = 0  # an all-zero group
+    xb = backend.f32_buf(x)
+    y1, y2, yn = backend.alloc(rows * 4), backend.alloc(rows * 4), backend.alloc(k * 4)
+    backend.set_act_mode(backend_mod.ACT_I8)
+    try:
+        backend.qmatmul(w, xb, y1)  # in-kernel quantization
+        # rmsnorm with unit weights and eps 0 of (x / rms) reproduces x up to
+        # rounding, so quantize explicitly instead: the cache holds yn's int8 form.
+        backend.rmsnorm(backend.f32_buf(np.ones(k, np.float32)), xb, yn, 1e-5)
+        backend.qmatmul(w, yn, y2)  # reads the cached int8 activations of yn
+        yv = backend.download_f32(yn)
+        y3 = backend.alloc(rows * 4)
+        backend.qmatmul(w, backend.f32_buf(yv), y3)  # in-kernel quantization of the same values
+        assert np.array_equal(backend.download_f32(y2), backend.download_f32(y3))
+        cpu, exact = oracle_i8(dtype, synth.weight(dtype, rows, k, 41), rows, k, x)
+        assert_parity(backend.download_f32(y1), cpu, exact, 1e-3, atol=1e-5)
+    finally:
+        backend.set_act_mode(backend_mod.ACT_F32)
+
+
 # ---------------------------------------------------------- shape rules ----
 
 def test_qmatmul_shape_rules(backend):
