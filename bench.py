@@ -141,7 +141,9 @@ def time_graphs(be, ev, graphs, steps, warmup):
 def per_launch(be, ev, wl, mode, reps):
     """Per launch kind, over every distinct weight copy (same input buffer, so
     in int8 mode the activations are quantized once and the GEMV kernel
-    itself is timed):
+    itself is timed -- except the down projection (rows of 14336), whose
+    one-token GEMV quantizes x in its own prologue, so its time includes
+    that quantization):
       - us_kernel: kernel duration from the dispatch's own start/end
         timestamps (hipExtLaunchKernel events, the figure a profiler's
         kernel trace reports), averaged over reps * copies eager launches;

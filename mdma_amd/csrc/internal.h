@@ -152,8 +152,9 @@ void launch_gemv_i8_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up,
 bool team_layout_ok(const GemvJob *jobs, int n_jobs);
 // One token, int8 mode, prepared Q4_K / Q6_K rows: the GEMV quantizes f32 x
 // itself in its prologue (per 256, as launch_quantize_act, bit for bit) --
-// one launch instead of two. False (nothing launched) when the shape has no
-// such variant.
+// one launch instead of two. False (nothing launched) where that variant is
+// not available or not faster (rows of at most 4096 columns, fewer than
+// 65536 rows).
 bool launch_gemv_i8_x(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, bool gated, const float *x, float *ygated);
 
 // Batched decode (2..16 tokens, int8 mode) on the matrix cores for prepared
