@@ -50,10 +50,11 @@ LAUNCHES = [("qkv", ("q", "k", "v"), 4096, 6144), ("o", ("o",), 4096, 4096),
 Q4K = 12
 SEED = 20261201
 # HBM bytes per launch of the dominant kernel from rocprofv3 --pmc FETCH_SIZE
-# and WRITE_SIZE (profiles/gemv_q4k_llama8b_layer.md), FETCH_SIZE scaled by
-# 2.0: a 1 GiB device copy reads 524,299 KiB on that counter on this
-# device, WRITE_SIZE reads 1,048,576 KiB (scale 1.0).
-TRAFFIC_GATE_UP = None
+# (32,404.6 KiB per dispatch) and WRITE_SIZE (56.2 KiB) over 50 dispatches,
+# FETCH_SIZE scaled by 2.0 and WRITE_SIZE by 1.0: a 1 GiB device copy reads
+# 524,301 KiB on FETCH_SIZE and 1,048,576 KiB on WRITE_SIZE on this device.
+# Algorithmic bytes per launch: 66,122,816 (0.45% below).
+TRAFFIC_GATE_UP = 66_422_156
 
 
 def w_bytes(name):
@@ -369,6 +370,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--reps", type=int, default=40, help="graph replays per launch kind in the roofline probe")
     ap.add_argument("--no-e2e", action="store_true", help="skip the Llama-3-8B end-to-end decode")
+    ap.add_argument("--e2e-only", action="store_true",
+                    help="only the Llama-3-8B end-to-end leg (for a profiler's kernel trace of decode steps)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU's share of the workload; --gpus {args.gpus} is not supported "
@@ -378,6 +381,9 @@ def main():
     from mdma_amd.backend import ACT_F32, ACT_I8, Gfx950Backend
 
     be = Gfx950Backend(0)
+    if args.e2e_only:
+        print(json.dumps({"e2e_llama3_8b": e2e_decode(be), "device": be.device_label()}), flush=True)
+        return
     ev = HipEvents()
     probe = copy_probe(be, ev)
     wl = Workload(be)
