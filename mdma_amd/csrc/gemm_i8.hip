@@ -8,10 +8,12 @@
 //
 // Each 32-wide K block is one v_mfma_i32_32x32x32_i8 per 32x32 output tile:
 // the exact int32 block dot of int8 weights and int8 activations. The
-// epilogue applies that block's scales and accumulates in f64 (full rate on
-// CDNA, like non-packed f32), so outputs that cancel keep their accuracy:
-//   Q8_0: acc += (s_x[m] * d_w[n]) * I
-//   Q4_K: acc += (s_x[m] * d*sc[n]) * I - (dmin*m[n]) * (s_x[m] * sum_k qx[m, k])
+// epilogue applies that block's scales in f32 over the stage's four blocks
+// and adds each stage's partial into an f64 total, so outputs that cancel
+// across K keep their accuracy while the per-block work stays f32:
+//   Q8_0: part += (s_x[m] * d_w[n]) * I
+//   Q4_K: part += (s_x[m] * d*sc[n]) * I - (dmin*m[n]) * (s_x[m] * sum_k qx[m, k])
+//   per stage: acc += part
 // Weights are unpacked to int8 (Q4_K nibbles 0..15) in LDS with their block
 // scales; activation rows and their scales are staged beside them.
 //
@@ -46,9 +48,9 @@ template <int DT>
 __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(16))) int8_t xs[KB][BM][LDR];
   __shared__ __attribute__((aligned(16))) int8_t ws[KB][BN][LDR];
-  __shared__ __attribute__((aligned(16))) double sxs[KB][BM];  // s_x
+  __shared__ __attribute__((aligned(16))) float sxs[KB][BM];   // s_x
   __shared__ __attribute__((aligned(16))) float sws[KB][BN];   // d_w (Q8_0) or d*sc (Q4_K)
-  __shared__ __attribute__((aligned(16))) double sbs[KB][BM];  // Q4_K: s_x * sum of the block's 32 activations
+  __shared__ __attribute__((aligned(16))) float sbs[KB][BM];   // Q4_K: s_x * sum of the block's 32 activations
   __shared__ __attribute__((aligned(16))) float dms[KB][BN];   // Q4_K: dmin*m
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -118,8 +120,8 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
     }
     {
       const int row = tid >> 2, kb = tid & 3;
-      sxs[kb][row] = (double)rsx;
-      if (DT == DT_Q4_K) sbs[kb][row] = (double)rsx * (double)rsb;
+      sxs[kb][row] = rsx;
+      if (DT == DT_Q4_K) sbs[kb][row] = rsx * (float)rsb;  // |sum| <= 127*32: exact in f32
     }
     if (DT == DT_Q8_0) {
 #pragma unroll
@@ -173,6 +175,11 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
     lstore(k0);
     __syncthreads();
     if (k0 + BK < K) gload(k0 + BK);
+    float part[2][16];
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) part[j][r] = 0.f;
 #pragma unroll
     for (int kb = 0; kb < KB; kb++) {
       const uint4 t = *reinterpret_cast<const uint4 *>(&xs[kb][wm + lr][16 * lk]);
@@ -184,31 +191,33 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
         bv[j] = v4i{(int)u.x, (int)u.y, (int)u.z, (int)u.w};
       }
       // Rows of result register r: (r&3) + 4*lk + 8*(r>>2) of the tile.
-      double sx[16], sb[16];
+      float sx[16], sb[16];
 #pragma unroll
-      for (int g = 0; g < 4; g++)
-#pragma unroll
-        for (int e = 0; e < 4; e += 2) {
-          const double2 s2 = *reinterpret_cast<const double2 *>(&sxs[kb][wm + 8 * g + 4 * lk + e]);
-          sx[4 * g + e] = s2.x, sx[4 * g + e + 1] = s2.y;
-          if (DT == DT_Q4_K) {
-            const double2 b2 = *reinterpret_cast<const double2 *>(&sbs[kb][wm + 8 * g + 4 * lk + e]);
-            sb[4 * g + e] = b2.x, sb[4 * g + e + 1] = b2.y;
-          }
+      for (int g = 0; g < 4; g++) {
+        const float4 s4 = *reinterpret_cast<const float4 *>(&sxs[kb][wm + 8 * g + 4 * lk]);
+        sx[4 * g] = s4.x, sx[4 * g + 1] = s4.y, sx[4 * g + 2] = s4.z, sx[4 * g + 3] = s4.w;
+        if (DT == DT_Q4_K) {
+          const float4 b4 = *reinterpret_cast<const float4 *>(&sbs[kb][wm + 8 * g + 4 * lk]);
+          sb[4 * g] = b4.x, sb[4 * g + 1] = b4.y, sb[4 * g + 2] = b4.z, sb[4 * g + 3] = b4.w;
         }
+      }
 #pragma unroll
       for (int j = 0; j < 2; j++) {
         v16i c = {};
         c = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[j], c, 0, 0, 0);
-        const double sw = (double)sws[kb][wn + 32 * j + lr];
-        const double dm = DT == DT_Q4_K ? (double)dms[kb][wn + 32 * j + lr] : 0.0;
+        const float sw = sws[kb][wn + 32 * j + lr];
+        const float dm = DT == DT_Q4_K ? dms[kb][wn + 32 * j + lr] : 0.f;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-          acc[j][r] = fma(sx[r] * sw, (double)c[r], acc[j][r]);
-          if (DT == DT_Q4_K) acc[j][r] = fma(-dm, sb[r], acc[j][r]);
+          part[j][r] = fmaf(sx[r] * sw, (float)c[r], part[j][r]);
+          if (DT == DT_Q4_K) part[j][r] = fmaf(-dm, sb[r], part[j][r]);
         }
       }
     }
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[j][r] += (double)part[j][r];
   }
   // ---- store ----
 #pragma unroll
