@@ -52,37 +52,49 @@ __device__ __forceinline__ v4i mma(uint64_t x, uint64_t w, v4i c) {
   return __builtin_amdgcn_mfma_i32_16x16x32_i8((long)x, (long)w, c, 0, 0, 0);
 }
 
-// Activation bytes of the lane's token at column col (zero rows past T).
+// Activation bytes of the lane's token at column col.
 struct XRow {
   const int8_t *p;
-  __device__ uint64_t operator()(uint32_t col) const {
-    return p ? *reinterpret_cast<const uint64_t *>(p + col) : 0ull;
-  }
+  __device__ uint64_t operator()(uint32_t col) const { return *reinterpret_cast<const uint64_t *>(p + col); }
 };
 
-// Each format: W = the weight bytes of one row's 256-column block for the
-// lane, X = the lane's activation bytes for that block; load / loadx issue
-// the loads, compute turns them into the block's contributions c[j]
-// (before the activation scale) for the lane's row and tokens.
+// The weights of a wave's 16-row tile come in per 256-column block with
+// 16-byte loads, four lanes per row reading 64 contiguous bytes of a row
+// plane (plus one 16-byte per-row piece: Q4_K header, Q6_K scales, Q8_0
+// scales), are staged in the wave's own LDS region, and are read back in
+// the MFMA operand layout. Each format: Raw = one block's loads of a lane;
+// gload issues them (prow: the lane's row for plane loads, row l/4; hrow:
+// row l%16 for the per-row piece); lstore writes them to the wave's LDS;
+// compute reads the operands back and returns the block's contributions
+// c[j] (before the activation scale) for row l%16 and tokens 4*(l/16)+j.
 
 // Q4_K: unit u = 64 columns, 32 quant bytes (16 in plane A, 16 in plane B);
-// lane group g takes bytes 8g..8g+7 of A|B: low nibbles are columns
-// 64u + 8g + [0,8) (sub-block 2(u%4)), high nibbles 64u + 32 + 8g + [0,8).
+// LDS per row: 4 units x [A 16 | B 16]; lane group g reads bytes 8g..8g+7:
+// low nibbles are columns 64u + 8g + [0,8) (sub-block 2(u%4)), high
+// nibbles 64u + 32 + 8g + [0,8).
 struct BQ4 {
   static constexpr uint32_t UCOLS = 64;
+  static constexpr uint32_t RS = 144;                 // LDS row stride (128 + pad)
+  static constexpr uint32_t LDS = 16 * RS + 16 * 16;  // + headers
   __device__ static size_t row_bytes(uint32_t n_in) { return (size_t)(n_in / 256) * 144; }
-  struct W {
-    uint4 h;
-    uint64_t q[4];
+  struct Raw {
+    uint4 a, b, h;
   };
   struct X {
     uint64_t lo[4], hi[4];
   };
-  __device__ static void load(const uint8_t *row, uint32_t U, uint32_t b, uint32_t g, W &w) {
-    const uint8_t *plane = row + (g < 2 ? 0 : 16 * (size_t)U) + 8 * (g & 1);
-#pragma unroll
-    for (int p = 0; p < 4; p++) w.q[p] = ldw8(plane + 16 * (size_t)(4 * b + p));
-    w.h = *reinterpret_cast<const uint4 *>(row + 32 * (size_t)U + 16 * (size_t)b);
+  __device__ static void gload(const uint8_t *prow, const uint8_t *hrow, uint32_t U, uint32_t b, uint32_t l,
+                               Raw &r) {
+    const size_t o = 16 * (size_t)(4 * b + (l & 3));
+    r.a = ld16(prow + o);
+    r.b = ld16(prow + 16 * (size_t)U + o);
+    r.h = ld16(hrow + 32 * (size_t)U + 16 * (size_t)b);
+  }
+  __device__ static void lstore(const Raw &r, uint8_t *lds, uint32_t l) {
+    uint8_t *p = lds + (l >> 2) * RS + 32 * (l & 3);
+    *reinterpret_cast<uint4 *>(p) = r.a;
+    *reinterpret_cast<uint4 *>(p + 16) = r.b;
+    if (l < 16) *reinterpret_cast<uint4 *>(lds + 16 * RS + 16 * l) = r.h;
   }
   __device__ static void loadx(const XRow &xr, uint32_t b, uint32_t g, X &x) {
 #pragma unroll
@@ -92,34 +104,40 @@ struct BQ4 {
       x.hi[p] = xr(col + 32);
     }
   }
-  __device__ static void compute(const W &w, const X &x, uint32_t, double *c) {
+  __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, double *c) {
+    const uint32_t n = l & 15, g = l >> 4;
+    const uint4 h = *reinterpret_cast<const uint4 *>(lds + 16 * RS + 16 * n);
     constexpr uint64_t M4 = 0x0F0F0F0F0F0F0F0Full, ONES = 0x0101010101010101ull;
     v4i ai = {}, dm = {};
 #pragma unroll
     for (int p = 0; p < 4; p++) {
+      const uint64_t w = *reinterpret_cast<const uint64_t *>(lds + n * RS + 32 * p + 8 * g);
       const v4i z = {};
-      const v4i da = mma(x.lo[p], w.q[p] & M4, z);
-      const v4i db = mma(x.hi[p], (w.q[p] >> 4) & M4, z);
+      const v4i da = mma(x.lo[p], w & M4, z);
+      const v4i db = mma(x.hi[p], (w >> 4) & M4, z);
       int sca, scb, ma, mb;
-      q4k_scales_i(w.h, p, sca, scb, ma, mb);
+      q4k_scales_i(h, p, sca, scb, ma, mb);
       // 24-bit multiplies (full rate): |isum| <= 15*127*32.
 #pragma unroll
       for (int j = 0; j < 4; j++) ai[j] += __mul24(sca, da[j]) + __mul24(scb, db[j]);
       dm = mma(x.lo[p], (uint64_t)ma * ONES, dm);
       dm = mma(x.hi[p], (uint64_t)mb * ONES, dm);
     }
-    const double d = (double)h2f(w.h.x), dmin = (double)h2f(w.h.x >> 16);
+    const double d = (double)h2f(h.x), dmin = (double)h2f(h.x >> 16);
 #pragma unroll
     for (int j = 0; j < 4; j++) c[j] = d * (double)ai[j] - dmin * (double)dm[j];
   }
 };
 
 // Q6_K: unit u = (half n, group column h) of block u/4, quarters r = 0..3
-// of 16 columns each (col below), one int8 scale per quarter. Lanes g and
-// g+2 (g = 0,1) hold dwords 2g, 2g+1 of the A, B and high-bit planes of
-// units 2v and 2v+1: columns col(u, r) + 8g + [0,8).
+// of 16 columns each (col below), one int8 scale per quarter. LDS per row:
+// 4 units x [A 16 | B 16 | high bits 16], then the 16 scale bytes and d.
+// Lanes g and g+2 (g = 0,1) take dwords 2g, 2g+1 of units 2v and 2v+1:
+// columns col(u, r) + 8g + [0,8); each MFMA zeroes the other pair's x.
 struct BQ6 {
   static constexpr uint32_t UCOLS = 64;
+  static constexpr uint32_t RS = 208;  // 192 + pad
+  static constexpr uint32_t LDS = 16 * RS + 16 * 16 + 16 * 4;
   __device__ static size_t row_bytes(uint32_t n_in) { return ((size_t)(n_in / 256) * 210 + 15) / 16 * 16; }
   __device__ static uint32_t u6(uint32_t a, uint32_t b, uint32_t h, int r) {
     switch (r) {
@@ -137,27 +155,31 @@ struct BQ6 {
   __device__ static uint32_t col(uint32_t u, int r) {
     return 256 * (u >> 2) + 128 * ((u >> 1) & 1) + 32 * r + 16 * (u & 1);
   }
-  struct W {
-    uint64_t a[2], b[2], q[2];
-    uint32_t sc[2][2];
+  struct Raw {
+    uint4 a, b, q, s;
     uint32_t d;
   };
   struct X {
     uint64_t q[2][4];  // [unit pair][quarter]
   };
-  __device__ static void load(const uint8_t *row, uint32_t U, uint32_t b, uint32_t g, W &w) {
-#pragma unroll
-    for (int v = 0; v < 2; v++) {
-      const uint32_t u = 4 * b + 2 * v + (g >> 1);
-      const size_t o = 16 * (size_t)u + 8 * (g & 1);
-      w.a[v] = ldw8(row + o);
-      w.b[v] = ldw8(row + 16 * (size_t)U + o);
-      w.q[v] = ldw8(row + 32 * (size_t)U + o);
-      // Scales of both units of the pair (each lane pair multiplies by its own).
-      w.sc[v][0] = ldw4(row + 48 * (size_t)U + 4 * (size_t)(4 * b + 2 * v));
-      w.sc[v][1] = ldw4(row + 48 * (size_t)U + 4 * (size_t)(4 * b + 2 * v + 1));
+  __device__ static void gload(const uint8_t *prow, const uint8_t *hrow, uint32_t U, uint32_t b, uint32_t l,
+                               Raw &r) {
+    const size_t o = 16 * (size_t)(4 * b + (l & 3));
+    r.a = ld16(prow + o);
+    r.b = ld16(prow + 16 * (size_t)U + o);
+    r.q = ld16(prow + 32 * (size_t)U + o);
+    r.s = ld16(hrow + 48 * (size_t)U + 16 * (size_t)b);
+    r.d = ldw2(hrow + 52 * (size_t)U + 2 * (size_t)b);
+  }
+  __device__ static void lstore(const Raw &r, uint8_t *lds, uint32_t l) {
+    uint8_t *p = lds + (l >> 2) * RS + 48 * (l & 3);
+    *reinterpret_cast<uint4 *>(p) = r.a;
+    *reinterpret_cast<uint4 *>(p + 16) = r.b;
+    *reinterpret_cast<uint4 *>(p + 32) = r.q;
+    if (l < 16) {
+      *reinterpret_cast<uint4 *>(lds + 16 * RS + 16 * l) = r.s;
+      *reinterpret_cast<float *>(lds + 16 * RS + 256 + 4 * l) = h2f(r.d);
     }
-    w.d = ldw2(row + 52 * (size_t)U + 2 * (size_t)b);
   }
   __device__ static void loadx(const XRow &xr, uint32_t b, uint32_t g, X &x) {
 #pragma unroll
@@ -165,65 +187,88 @@ struct BQ6 {
 #pragma unroll
       for (int r = 0; r < 4; r++) x.q[v][r] = xr(col(4 * b + 2 * v + (g >> 1), r) + 8 * (g & 1));
   }
-  __device__ static void compute(const W &w, const X &x, uint32_t g, double *c) {
+  __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, double *c) {
+    const uint32_t n = l & 15, g = l >> 4;
+    const uint4 sc4 = *reinterpret_cast<const uint4 *>(lds + 16 * RS + 16 * n);
+    const uint32_t scw[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
     v4i ai = {};
 #pragma unroll
     for (int v = 0; v < 2; v++) {
+      const uint8_t *p = lds + n * RS + 48 * (2 * v + (g >> 1)) + 8 * (g & 1);
+      const uint64_t wa = *reinterpret_cast<const uint64_t *>(p);
+      const uint64_t wb = *reinterpret_cast<const uint64_t *>(p + 16);
+      const uint64_t wq = *reinterpret_cast<const uint64_t *>(p + 32);
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        const uint32_t lo = centred(u6((uint32_t)w.a[v], (uint32_t)w.b[v], (uint32_t)w.q[v], r));
-        const uint32_t hi =
-            centred(u6((uint32_t)(w.a[v] >> 32), (uint32_t)(w.b[v] >> 32), (uint32_t)(w.q[v] >> 32), r));
+        const uint32_t lo = centred(u6((uint32_t)wa, (uint32_t)wb, (uint32_t)wq, r));
+        const uint32_t hi = centred(u6((uint32_t)(wa >> 32), (uint32_t)(wb >> 32), (uint32_t)(wq >> 32), r));
         const uint64_t wv = (uint64_t)lo | ((uint64_t)hi << 32);
         // Unit 2v: lanes g < 2; unit 2v+1: lanes g >= 2.
         const v4i z = {};
         const v4i d0 = mma(g < 2 ? x.q[v][r] : 0ull, wv, z);
         const v4i d1 = mma(g < 2 ? 0ull : x.q[v][r], wv, z);
-        const int s0 = (int)(int8_t)((w.sc[v][0] >> (8 * r)) & 0xff);
-        const int s1 = (int)(int8_t)((w.sc[v][1] >> (8 * r)) & 0xff);
+        const int s0 = (int)(int8_t)((scw[2 * v] >> (8 * r)) & 0xff);
+        const int s1 = (int)(int8_t)((scw[2 * v + 1] >> (8 * r)) & 0xff);
         // 24-bit multiplies (full rate): |isum| <= 32*127*16.
 #pragma unroll
         for (int j = 0; j < 4; j++) ai[j] += __mul24(s0, d0[j]) + __mul24(s1, d1[j]);
       }
     }
-    const double d = (double)h2f(w.d);
+    const double d = (double)*reinterpret_cast<const float *>(lds + 16 * RS + 256 + 4 * n);
 #pragma unroll
     for (int j = 0; j < 4; j++) c[j] = d * (double)ai[j];
   }
 };
 
 // Q8_0: 32-column blocks (U = n_in/32 units), 16 bytes in plane A and 16 in
-// plane B; lane group g takes bytes 8g..8g+7 of A|B = columns 32u + 8g + [0,8).
+// plane B; LDS per row: 8 units x [A 16 | B 16], then the 8 f16 scales.
+// Lane group g reads bytes 8g..8g+7 of A|B = columns 32u + 8g + [0,8).
 struct BQ8 {
   static constexpr uint32_t UCOLS = 32;
+  static constexpr uint32_t RS = 272;  // 256 + pad
+  static constexpr uint32_t LDS = 16 * RS + 16 * 16;
   __device__ static size_t row_bytes(uint32_t n_in) { return ((size_t)(n_in / 32) * 34 + 15) / 16 * 16; }
-  struct W {
-    uint64_t q[8];
-    uint32_t d[8];
+  struct Raw {
+    uint4 a[2], b[2], d;
   };
   struct X {
     uint64_t q[8];
   };
-  __device__ static void load(const uint8_t *row, uint32_t U, uint32_t b, uint32_t g, W &w) {
-    const uint8_t *plane = row + (g < 2 ? 0 : 16 * (size_t)U) + 8 * (g & 1);
+  __device__ static void gload(const uint8_t *prow, const uint8_t *hrow, uint32_t U, uint32_t b, uint32_t l,
+                               Raw &r) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      w.q[i] = ldw8(plane + 16 * (size_t)(8 * b + i));
-      w.d[i] = ldw2(row + 32 * (size_t)U + 2 * (size_t)(8 * b + i));
+    for (int i = 0; i < 2; i++) {
+      const size_t o = 16 * (size_t)(8 * b + (l & 3) + 4 * i);
+      r.a[i] = ld16(prow + o);
+      r.b[i] = ld16(prow + 16 * (size_t)U + o);
     }
+    r.d = ld16(hrow + 32 * (size_t)U + 16 * (size_t)b);
+  }
+  __device__ static void lstore(const Raw &r, uint8_t *lds, uint32_t l) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      uint8_t *p = lds + (l >> 2) * RS + 32 * ((l & 3) + 4 * i);
+      *reinterpret_cast<uint4 *>(p) = r.a[i];
+      *reinterpret_cast<uint4 *>(p + 16) = r.b[i];
+    }
+    if (l < 16) *reinterpret_cast<uint4 *>(lds + 16 * RS + 16 * l) = r.d;
   }
   __device__ static void loadx(const XRow &xr, uint32_t b, uint32_t g, X &x) {
 #pragma unroll
     for (int i = 0; i < 8; i++) x.q[i] = xr(256 * b + 32 * i + 8 * g);
   }
-  __device__ static void compute(const W &w, const X &x, uint32_t, double *c) {
+  __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, double *c) {
+    const uint32_t n = l & 15, g = l >> 4;
+    const uint4 d4 = *reinterpret_cast<const uint4 *>(lds + 16 * RS + 16 * n);
+    const uint32_t dw[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
     for (int j = 0; j < 4; j++) c[j] = 0.0;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
+      const uint64_t w = *reinterpret_cast<const uint64_t *>(lds + n * RS + 32 * i + 8 * g);
       const v4i z = {};
-      const v4i dq = mma(x.q[i], w.q[i], z);
-      const double d = (double)h2f(w.d[i]);
+      const v4i dq = mma(x.q[i], w, z);
+      const double d = (double)h2f(dw[i >> 1] >> (16 * (i & 1)));
 #pragma unroll
       for (int j = 0; j < 4; j++) c[j] = fma(d, (double)dq[j], c[j]);
     }
@@ -269,39 +314,48 @@ __global__ __launch_bounds__(64 * TW) void gemv_batch(BatchSet bs, const int8_t 
   const uint32_t n_in = bs.n_in, nb = n_in / 256, n_out = J.n_out, U = n_in / F::UCOLS;
   const uint32_t nch = nb < NCHMAX ? nb : NCHMAX;
   const uint32_t g = lane >> 4, r_lane = tile * TROWS + (lane & 15);
-  const uint32_t row = min(r_lane, n_out - 1);  // rows past the end re-read the last row, not stored
   const size_t rb = F::row_bytes(n_in);
-  const uint8_t *wrow[NR];
-  wrow[0] = J.w + row * rb;
-  if (GATED) wrow[NR - 1] = bs.j[1].w + row * rb;
-  const uint32_t tok = lane & 15;
-  const XRow xr{tok < T ? qx + (size_t)tok * n_in : nullptr};
+  // Rows read by the lane: l/4 for the plane loads, l%16 for the per-row
+  // piece (rows past the end re-read the last row; their sums are not stored).
+  const uint32_t prow_i = min(tile * TROWS + (lane >> 2), n_out - 1), hrow_i = min(r_lane, n_out - 1);
+  const uint8_t *prow[NR], *hrow[NR];
+  prow[0] = J.w + prow_i * rb, hrow[0] = J.w + hrow_i * rb;
+  if (GATED) prow[NR - 1] = bs.j[1].w + prow_i * rb, hrow[NR - 1] = bs.j[1].w + hrow_i * rb;
+  __shared__ __attribute__((aligned(16))) uint8_t stage[TW][NR][F::LDS];
+  // Token rows past T read row T-1 again: their results are never stored.
+  const uint32_t tok = min((uint32_t)(lane & 15), T - 1);
+  const XRow xr{qx + (size_t)tok * n_in};
   // Token of result slot j.
   constexpr int NJ = 4;
   uint32_t tj[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; j++) tj[j] = 4 * (lane >> 4) + j;
   double acc[NR][NJ], tot[NR][NJ];
-  // Ping-pong slots: the next block's loads go out before a block is
-  // computed (clamped to the wave's last block, so every load is in bounds
-  // and the wait counts are fixed).
+  // A block's loads in flight: the weights (to be staged) and the lane's x.
   struct Slot {
+    typename F::Raw w[NR];
     typename F::X x;
-    typename F::W w[NR];
     float s[NJ];
   };
   auto fill = [&](Slot &sl, uint32_t b) {
 #pragma unroll
-    for (int r = 0; r < NR; r++) F::load(wrow[r], U, b, g, sl.w[r]);
+    for (int r = 0; r < NR; r++) F::gload(prow[r], hrow[r], U, b, lane, sl.w[r]);
     F::loadx(xr, b, g, sl.x);
 #pragma unroll
     for (int j = 0; j < NJ; j++) sl.s[j] = tj[j] < T ? dx[(size_t)tj[j] * nb + b] : 0.f;
   };
+  // Stage the weights in the wave's LDS, read them back as operands. The
+  // LDS-only waits order the stores before the reads (and the previous
+  // block's reads before the stores) without waiting for loads in flight.
   auto use = [&](const Slot &sl) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int r = 0; r < NR; r++) F::lstore(sl.w[r], stage[wave][r], lane);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
     for (int r = 0; r < NR; r++) {
       double c[NJ];
-      F::compute(sl.w[r], sl.x, g, c);
+      F::compute(stage[wave][r], sl.x, lane, c);
 #pragma unroll
       for (int j = 0; j < NJ; j++) acc[r][j] = fma((double)sl.s[j], c[j], acc[r][j]);
     }
@@ -330,17 +384,25 @@ __global__ __launch_bounds__(64 * TW) void gemv_batch(BatchSet bs, const int8_t 
   for (int r = 0; r < NR; r++)
 #pragma unroll
     for (int j = 0; j < NJ; j++) acc[r][j] = tot[r][j] = 0.0;
+  // Three slots in rotation: blocks b+1 and b+2 are in flight while block
+  // b is computed (loads clamped to the wave's last block: in bounds, fixed
+  // wait counts).
   if (b0 < b1) {
-    Slot sa, sb;
-    fill(sa, b0);
-    for (uint32_t b = b0; b < b1; b += 2) {
-      fill(sb, min(b + 1, b1 - 1));
-      use(sa);
+    Slot s0, s1, s2;
+    fill(s0, b0);
+    fill(s1, min(b0 + 1, b1 - 1));
+    for (uint32_t b = b0; b < b1; b += 3) {
+      fill(s2, min(b + 2, b1 - 1));
+      use(s0);
       chunk_done(b);
       if (b + 1 >= b1) break;
-      fill(sa, min(b + 2, b1 - 1));
-      use(sb);
+      fill(s0, min(b + 3, b1 - 1));
+      use(s1);
       chunk_done(b + 1);
+      if (b + 2 >= b1) break;
+      fill(s1, min(b + 4, b1 - 1));
+      use(s2);
+      chunk_done(b + 2);
     }
   }
   if constexpr (TW > 1) {
