@@ -1,21 +1,26 @@
-// Prefill GEMM on gfx950: int8 MFMA over Q8_0 / Q4_K weights in the prepared
-// layout, activations quantized per 32 to int8 with an f32 scale.
+// Prefill GEMM on gfx950: int8 MFMA over Q8_0 / Q4_K / Q6_K weights in the
+// prepared layout, activations quantized per 32 to int8 with an f32 scale.
 //
 // Y[m, n] = sum_k X[m, k] * deq(W)[n, k]   (reference HipBackend::qmatmul_i8,
 // /root/reference/src/backend/rocm.rs:1759-1918, the WMMA prefill of
 // src/backend/rocm/kernels/kernels.hip:1158-2806; CPU oracle
 // src/backend/cpu.rs:335-368 on the requantized activations)
 //
-// Each 32-wide K block is one v_mfma_i32_32x32x32_i8 per 32x32 output tile:
-// the exact int32 block dot of int8 weights and int8 activations. The
-// epilogue applies that block's scales in f32 over the stage's four blocks
-// and adds each stage's partial into an f64 total, so outputs that cancel
-// across K keep their accuracy while the per-block work stays f32:
+// Each 32-wide K block is one v_mfma_i32_32x32x32_i8 per 32x32 output tile
+// (Q6_K: two v_mfma_i32_32x32x16_i8, one per 16-column sub-block, whose
+// int8 scales differ): the exact int32 block dots of int8 weights and int8
+// activations. The epilogue applies that block's scales in f32 over the
+// stage's four blocks and adds each stage's partial into an f64 total, so
+// outputs that cancel across K keep their accuracy while the per-block work
+// stays f32:
 //   Q8_0: part += (s_x[m] * d_w[n]) * I
 //   Q4_K: part += (s_x[m] * d*sc[n]) * I - (dmin*m[n]) * (s_x[m] * sum_k qx[m, k])
-//   per stage: acc += part
-// Weights are unpacked to int8 (Q4_K nibbles 0..15) in LDS with their block
-// scales; activation rows and their scales are staged beside them.
+//   Q6_K: part += s_x[m] * (sc_lo[n] * I_lo + sc_hi[n] * I_hi)   (exact int32)
+//   per stage: acc += part (Q6_K: acc += d[n] * part; a stage is 128 columns
+//   of one super-block, so d is constant over it)
+// Weights are unpacked to int8 (Q4_K nibbles 0..15, Q6_K values centred to
+// -32..31) in LDS with their block scales; activation rows and their scales
+// are staged beside them.
 //
 // Tiling: a 256-thread workgroup computes a 64x128 tile of Y; each of its 4
 // waves owns 32x64 (1x2 MFMA tiles). K advances 128 columns (4 blocks) per
@@ -30,6 +35,22 @@ namespace mdma {
 namespace {
 
 constexpr int BM = 64, BN = 128, BK = 128, KB = BK / 32, LDR = 48;
+
+// Q6_K: the 6-bit values of quarter r (0..3) of a unit from its ql bytes a
+// (quarters 0, 2), b (quarters 1, 3) and qh bytes h, four per dword, and
+// those values (0..63) as signed int8 v - 32.
+__device__ __forceinline__ uint32_t q6_bytes(uint32_t a, uint32_t b, uint32_t h, int r) {
+  switch (r) {
+    case 0: return (a & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u);
+    case 1: return (b & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u);
+    case 2: return ((a >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u);
+    default: return ((b >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u);
+  }
+}
+__device__ __forceinline__ uint32_t q6_centred(uint32_t v) {
+  const uint32_t s = ~v & 0x20202020u;  // bytes below 32 become negative
+  return (v ^ 0x20202020u) | (s << 1) | (s << 2);
+}
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -52,6 +73,8 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(16))) float sws[KB][BN];   // d_w (Q8_0) or d*sc (Q4_K)
   __shared__ __attribute__((aligned(16))) float sbs[KB][BM];   // Q4_K: s_x * sum of the block's 32 activations
   __shared__ __attribute__((aligned(16))) float dms[KB][BN];   // Q4_K: dmin*m
+  __shared__ __attribute__((aligned(16))) int2 s6[KB][BN];      // Q6_K: the two 16-column scales
+  __shared__ __attribute__((aligned(16))) float d6[BN];         // Q6_K: d
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t bm = blockIdx.y * BM, bn = blockIdx.x * BN;
@@ -62,7 +85,8 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
   // X: 64 rows x 128 bytes = 512 chunks of 16 B, 2 per thread.
   // W: Q8_0 128 rows x 4 blocks x 2 halves; Q4_K 128 rows x 2 pair units x 2 planes.
   uint4 rx[2], rw[4];
-  uint32_t rh = 0, rh2 = 0, rh3 = 0, rh4 = 0;  // Q8_0 d (2 x f16 per dword) / Q4_K header dwords
+  // Q8_0 d (2 x f16 per dword) / Q4_K header dwords / Q6_K scale dwords and d
+  uint32_t rh = 0, rh2 = 0, rh3 = 0, rh4 = 0;
   float rsx;
   int rsb = 0;
   auto gload = [&](uint32_t k0) {
@@ -94,6 +118,27 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
       const int row = tid >> 1, pairb = tid & 1;
       const uint32_t gn = min(bn + row, a.N - 1);
       rh = *reinterpret_cast<const uint32_t *>(a.w + gn * a.row_bytes + 32 * (size_t)nb + 2 * (k0 / 32) + 4 * pairb);
+    } else if (DT == DT_Q6_K) {
+      // The stage is half hn of super-block sb: units u = 4*sb + 2*hn + h
+      // (h = 0, 1), each with planes A, B, Q; thread = (row, h), one chunk
+      // per plane.
+      const uint32_t U = K / 64, sb = k0 / 256, hn = (k0 / 128) & 1;
+      {
+        const int row = tid >> 1, h = tid & 1;
+        const uint32_t gn = min(bn + row, a.N - 1);
+        const uint8_t *rp = a.w + gn * a.row_bytes;
+        const size_t u = 4 * sb + 2 * hn + h;
+        rw[0] = ld16(rp + 16 * u);
+        rw[1] = ld16(rp + 16 * ((size_t)U + u));
+        rw[2] = ld16(rp + 16 * (2 * (size_t)U + u));
+      }
+      if (tid < 128) {  // S of both units (8 bytes) and d, one row each
+        const uint32_t gn = min(bn + tid, a.N - 1);
+        const uint8_t *rp = a.w + gn * a.row_bytes;
+        const uint2 sc = *reinterpret_cast<const uint2 *>(rp + 48 * (size_t)U + 4 * (4 * sb + 2 * hn));
+        rh = sc.x, rh2 = sc.y;
+        rh3 = *reinterpret_cast<const uint16_t *>(rp + 52 * (size_t)U + 2 * sb);
+      }
     } else {
       const uint32_t U = K / 64;
 #pragma unroll
@@ -132,6 +177,22 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
       const int row = tid >> 1, pairb = tid & 1;
       sws[2 * pairb][row] = h2f(rh);
       sws[2 * pairb + 1][row] = h2f(rh >> 16);
+    } else if (DT == DT_Q6_K) {
+      // Quarter r of unit h is columns [16h, 16h+16) of the stage's block r.
+      const int row = tid >> 1, h = tid & 1;
+      const uint4 A = rw[0], B = rw[1], Q = rw[2];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const uint4 v = make_uint4(q6_centred(q6_bytes(A.x, B.x, Q.x, r)), q6_centred(q6_bytes(A.y, B.y, Q.y, r)),
+                                   q6_centred(q6_bytes(A.z, B.z, Q.z, r)), q6_centred(q6_bytes(A.w, B.w, Q.w, r)));
+        *reinterpret_cast<uint4 *>(&ws[r][row][16 * h]) = v;
+      }
+      if (tid < 128) {
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          s6[r][tid] = make_int2((int)(int8_t)(rh >> (8 * r)), (int)(int8_t)(rh2 >> (8 * r)));
+        d6[tid] = h2f(rh3);
+      }
     } else {
       // Pair unit (within the stage) -> sub-blocks 2*unit (low nibbles) and
       // 2*unit+1 (high nibbles); plane -> bytes [16*plane, 16*plane+16).
@@ -182,6 +243,37 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
       for (int r = 0; r < 16; r++) part[j][r] = 0.f;
 #pragma unroll
     for (int kb = 0; kb < KB; kb++) {
+      if (DT == DT_Q6_K) {
+        float sx[16];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const float4 s4 = *reinterpret_cast<const float4 *>(&sxs[kb][wm + 8 * g + 4 * lk]);
+          sx[4 * g] = s4.x, sx[4 * g + 1] = s4.y, sx[4 * g + 2] = s4.z, sx[4 * g + 3] = s4.w;
+        }
+        v16i c[2][2];
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+          // K = 16 operands: lane l holds k = 8*(l/32) .. +8 of row l%32.
+          const long av = *reinterpret_cast<const long *>(&xs[kb][wm + lr][16 * hh + 8 * lk]);
+#pragma unroll
+          for (int j = 0; j < 2; j++) {
+            const long bv = *reinterpret_cast<const long *>(&ws[kb][wn + 32 * j + lr][16 * hh + 8 * lk]);
+            c[hh][j] = __builtin_amdgcn_mfma_i32_32x32x16_i8(av, bv, v16i{}, 0, 0, 0);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+          const int2 sc = s6[kb][wn + 32 * j + lr];
+#pragma unroll
+          for (int r = 0; r < 16; r++) {
+            // |I_lo|, |I_hi| <= 16*127*32 and |sc| <= 128: 24-bit multiplies
+            // are exact, and so is the sum (< 2^24) as an f32.
+            const int isum = __mul24(sc.x, c[0][j][r]) + __mul24(sc.y, c[1][j][r]);
+            part[j][r] = fmaf(sx[r], (float)isum, part[j][r]);
+          }
+        }
+        continue;
+      }
       const uint4 t = *reinterpret_cast<const uint4 *>(&xs[kb][wm + lr][16 * lk]);
       const v4i av = v4i{(int)t.x, (int)t.y, (int)t.z, (int)t.w};
       v4i bv[2];
@@ -215,9 +307,11 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
       }
     }
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int j = 0; j < 2; j++) {
+      const double dd = DT == DT_Q6_K ? (double)d6[wn + 32 * j + lr] : 1.0;
 #pragma unroll
-      for (int r = 0; r < 16; r++) acc[j][r] += (double)part[j][r];
+      for (int r = 0; r < 16; r++) acc[j][r] = fma((double)part[j][r], dd, acc[j][r]);
+    }
   }
   // ---- store ----
 #pragma unroll
@@ -237,7 +331,7 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
 bool gemm_i8_supported(int32_t dtype, int layout, uint64_t n_in) {
   if (layout != MDMA_LAYOUT_GFX950) return false;
   if (dtype == DT_Q8_0) return n_in % BK == 0;
-  if (dtype == DT_Q4_K) return n_in % 256 == 0;
+  if (dtype == DT_Q4_K || dtype == DT_Q6_K) return n_in % 256 == 0;
   return false;
 }
 
@@ -251,6 +345,9 @@ void launch_gemm_i8(mdma_ctx *ctx, const GemvJob &w, const int8_t *qx, const flo
   if (w.dtype == DT_Q8_0) {
     if (t0 || t1) hipExtLaunchKernelGGL(gemm_i8_kernel<DT_Q8_0>, grid, block, 0, ctx->stream, t0, t1, 0, a);
     else gemm_i8_kernel<DT_Q8_0><<<grid, block, 0, ctx->stream>>>(a);
+  } else if (w.dtype == DT_Q6_K) {
+    if (t0 || t1) hipExtLaunchKernelGGL(gemm_i8_kernel<DT_Q6_K>, grid, block, 0, ctx->stream, t0, t1, 0, a);
+    else gemm_i8_kernel<DT_Q6_K><<<grid, block, 0, ctx->stream>>>(a);
   } else {
     if (t0 || t1) hipExtLaunchKernelGGL(gemm_i8_kernel<DT_Q4_K>, grid, block, 0, ctx->stream, t0, t1, 0, a);
     else gemm_i8_kernel<DT_Q4_K><<<grid, block, 0, ctx->stream>>>(a);

@@ -436,6 +436,14 @@ __device__ __forceinline__ float wave_sum_all(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// Device-scope (all XCDs) coherent store and load of one float.
+__device__ __forceinline__ void store_dev(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_dev(const float *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int C>
 struct AttnTile {
   uint4 k[4 * C];     // K slices of this lane's key
@@ -599,38 +607,51 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
       const uint32_t t = tid + 256 * k;
       if (t < G * hd) {
         const uint32_t h = t / hd, d = t % hd;
-        part[((orow / hd + h) * n_splits + split) * (hd + 2) + d] =
-            ((red[0][h][d] + red[1][h][d]) + red[2][h][d]) + red[3][h][d];
+        store_dev(part + ((orow / hd + h) * n_splits + split) * (hd + 2) + d,
+                  ((red[0][h][d] + red[1][h][d]) + red[2][h][d]) + red[3][h][d]);
       }
     }
     if (tid < G) {
       float *pp = part + ((orow / hd + tid) * n_splits + split) * (hd + 2) + hd;
-      pp[0] = mrun[tid];
-      pp[1] = lrun[tid];
+      store_dev(pp, mrun[tid]);
+      store_dev(pp + 1, lrun[tid]);
     }
-    // The barrier orders every wave's partial stores before thread 0's
-    // device-scope release; thread 0's acquire (in the last run) orders the
-    // merge's loads, which the second barrier extends to every wave.
+    // Partials move between workgroups (possibly on different XCDs, whose
+    // L2s are not coherent with each other) only through device-scope
+    // stores and loads, which write through and read from the coherence
+    // point. Each wave waits for its stores to be acknowledged before the
+    // barrier; the counter's device-scope add comes after the barrier, so a
+    // run that sees every other run's add also sees their partials. This
+    // avoids the whole-L2 write-back and invalidate of a device-scope fence.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (tid == 0) {
-      __threadfence();
       uint32_t *c = cnt + (size_t)i * n_kv_heads + kvh;
-      const uint32_t prev = atomicAdd(c, 1u);
+      const uint32_t prev = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       last = prev == live - 1;
-      if (last) {
-        *c = 0u;  // every run of this (query, KV head) has arrived
-        __threadfence();
-      }
+      // every run of this (query, KV head) has arrived: ready for the next call
+      if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!last) return;
     // Merge weights w[h][s] = exp(m_s - M) / L with M = max m_s and
     // L = sum l_s exp(m_s - M); then out = sum_s w[h][s] * partial_s.
+    // The partial vectors are loaded first, so both loads overlap.
+    float pv[NO][ATT_MAX_RUNS];
+#pragma unroll
+    for (int k = 0; k < NO; k++) {
+      const uint32_t t = tid + 256 * k;
+      const uint32_t h = t / hd, d = t % hd;
+      const float *pb = part + (orow / hd + h) * n_splits * (hd + 2) + d;
+#pragma unroll
+      for (uint32_t s2 = 0; s2 < ATT_MAX_RUNS; s2++)
+        pv[k][s2] = t < G * hd && s2 < live ? load_dev(pb + s2 * (hd + 2)) : 0.f;
+    }
     for (uint32_t e = tid; e < G * live; e += 256) {
       const uint32_t h = e / live, s2 = e % live;
       const float *pp = part + ((orow / hd + h) * n_splits + s2) * (hd + 2) + hd;
-      wml[h][s2][0] = pp[0];
-      wml[h][s2][1] = pp[1];
+      wml[h][s2][0] = load_dev(pp);
+      wml[h][s2][1] = load_dev(pp + 1);
     }
     __syncthreads();
     if (tid < G) {
@@ -649,15 +670,11 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
     for (int k = 0; k < NO; k++) {
       const uint32_t t = tid + 256 * k;
       if (t < G * hd) {
-        const uint32_t h = t / hd, d = t % hd;
-        const float *pb = part + (orow / hd + h) * n_splits * (hd + 2) + d;
-        float pv[ATT_MAX_RUNS];
-#pragma unroll
-        for (uint32_t s2 = 0; s2 < ATT_MAX_RUNS; s2++) pv[s2] = s2 < live ? pb[s2 * (hd + 2)] : 0.f;
+        const uint32_t h = t / hd;
         float a = 0.f;
 #pragma unroll
         for (uint32_t s2 = 0; s2 < ATT_MAX_RUNS; s2++)
-          if (s2 < live) a = fmaf(pv[s2], wml[h][s2][0], a);
+          if (s2 < live) a = fmaf(pv[k][s2], wml[h][s2][0], a);
         out[k] = a / lrun[h];
       }
     }
