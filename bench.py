@@ -231,7 +231,7 @@ GEMM_SHAPES = [(512, 4096, 14336), (2048, 14336, 4096)]  # (M tokens, K, N)
 
 def prefill_gemms(be, ev, reps):
     """Prefill int8 MFMA GEMM at the two prefill shapes, Q4_K and Q8_0
-    weights: kernel-only GEMM duration (dispatch timestamps) and the whole
+    weights (and Q6_K, the Q4_K_M mix's attention and down type): kernel-only GEMM duration (dispatch timestamps) and the whole
     qmatmul call (per-32 activation quantization + GEMM) timed by events on
     the stream. TOPS = 2*M*N*K / time."""
     from mdma_amd import synth
@@ -242,7 +242,7 @@ def prefill_gemms(be, ev, reps):
     for M, K, N in GEMM_SHAPES:
         x = be.f32_buf(synth.normal_f32(M * K, SEED + 20))
         y = be.alloc(M * N * 4)
-        for dt, name in ((12, "q4k"), (8, "q8_0")):
+        for dt, name in ((12, "q4k"), (8, "q8_0"), (14, "q6k")):
             raw = synth.weight(dt, N, K, SEED + 21)
             w = be.upload_weight(raw, dt, (N, K))
             be.qmatmul(w, x, y)

@@ -228,20 +228,30 @@ char *argmax_parts(mdma_ctx *ctx, uint64_t chunks) {
   return ctx->argmax_part;
 }
 
-uint32_t *attn_counters(mdma_ctx *ctx, uint64_t n) {
-  if (n <= ctx->attn_cnt_cap) return ctx->attn_cnt;
-  no_capture(ctx, "attention counter growth");
+// A zeroed uint32 buffer of at least n entries (grown outside capture only).
+static uint32_t *zeroed_counters(mdma_ctx *ctx, uint32_t *&buf, uint64_t &cap_, uint64_t n, const char *what) {
+  if (n <= cap_) return buf;
+  no_capture(ctx, what);
   const uint64_t cap = n < 4096 ? 4096 : n + n / 4;
-  hip_check(hipStreamSynchronize(ctx->stream), "attention counter grow sync");
-  if (ctx->attn_cnt) hip_check(hipFree(ctx->attn_cnt), "attention counter free");
-  ctx->attn_cnt = nullptr;
-  ctx->attn_cnt_cap = 0;
+  hip_check(hipStreamSynchronize(ctx->stream), "counter grow sync");
+  if (buf) hip_check(hipFree(buf), "counter free");
+  buf = nullptr;
+  cap_ = 0;
   void *p = nullptr;
-  hip_check(hipMalloc(&p, cap * 4), "attention counter alloc");
-  hip_check(hipMemset(p, 0, cap * 4), "attention counter clear");
-  ctx->attn_cnt = static_cast<uint32_t *>(p);
-  ctx->attn_cnt_cap = cap;
-  return ctx->attn_cnt;
+  hip_check(hipMalloc(&p, cap * 4), "counter alloc");
+  hip_check(hipMemset(p, 0, cap * 4), "counter clear");
+  buf = static_cast<uint32_t *>(p);
+  cap_ = cap;
+  return buf;
+}
+
+uint32_t *attn_counters(mdma_ctx *ctx, uint64_t n) {
+  return zeroed_counters(ctx, ctx->attn_cnt, ctx->attn_cnt_cap, n, "attention counter growth");
+}
+
+uint32_t *gemm_counters(mdma_ctx *ctx, uint64_t n) {
+  if (ctx->capturing && n > ctx->gemm_cnt_cap) return nullptr;
+  return zeroed_counters(ctx, ctx->gemm_cnt, ctx->gemm_cnt_cap, n, "GEMM counter growth");
 }
 
 void q8_invalidate_range(mdma_ctx *ctx, const void *p, uint64_t bytes) {
@@ -322,6 +332,7 @@ void mdma_gfx950_destroy(mdma_ctx *ctx) {
   if (ctx->q8) (void)hipFree(ctx->q8);
   if (ctx->argmax_part) (void)hipFree(ctx->argmax_part);
   if (ctx->attn_cnt) (void)hipFree(ctx->attn_cnt);
+  if (ctx->gemm_cnt) (void)hipFree(ctx->gemm_cnt);
   if (ctx->rope_tab) (void)hipFree(ctx->rope_tab);
   if (ctx->host_ids) (void)hipHostFree(ctx->host_ids);
   (void)hipStreamDestroy(ctx->stream);

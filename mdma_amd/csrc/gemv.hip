@@ -872,16 +872,30 @@ void launch_gemv_f32_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up
 static bool try_gemm_i8(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t T) {
   if (T < GEMM_MIN_TOKENS) return false;
   for (int i = 0; i < n_jobs; i++)
-    if (!gemm_i8_supported(jobs[i].dtype, jobs[i].layout, jobs[i].n_in) || jobs[i].n_in != jobs[0].n_in)
+    if (!gemm_i8_supported(jobs[i].dtype, jobs[i].layout, jobs[i].n_in, jobs[i].n_out) ||
+        jobs[i].n_in != jobs[0].n_in)
       return false;
   const uint64_t n_in = jobs[0].n_in, n = T * n_in;
-  const uint64_t qb = (n + 255) / 256 * 256, db = (n / 32 * 4 + 255) / 256 * 256, sb = n / 16 * 4;
-  char *s = scratch(ctx, qb + db + sb);
+  const uint64_t qb = (n + 255) / 256 * 256, db = (n / 32 * 4 + 255) / 256 * 256,
+                 sb = (n / 16 * 4 + 255) / 256 * 256;
+  // Split-K partials (the jobs run one after another and share them).
+  uint64_t pd = 0, nc = 0;
+  for (int i = 0; i < n_jobs; i++) {
+    uint64_t p, c;
+    gemm_i8_split_need(ctx, jobs[i], T, &p, &c);
+    pd = p > pd ? p : pd;
+    nc = c > nc ? c : nc;
+  }
+  // Under stream capture the scratch cannot grow: past its size, unsplit.
+  if (ctx->capturing && qb + db + sb + pd * 8 > ctx->scratch_cap) pd = 0;
+  char *s = scratch(ctx, qb + db + sb + pd * 8);
   int8_t *qx = reinterpret_cast<int8_t *>(s);
   float *dx = reinterpret_cast<float *>(s + qb);
   int32_t *s16 = reinterpret_cast<int32_t *>(s + qb + db);
+  double *part = pd ? reinterpret_cast<double *>(s + qb + db + sb) : nullptr;
+  uint32_t *cnt = pd && nc ? gemm_counters(ctx, nc) : nullptr;
   launch_quantize_act(ctx, x, n, 32, qx, dx, s16);
-  for (int i = 0; i < n_jobs; i++) launch_gemm_i8(ctx, jobs[i], qx, dx, s16, T, jobs[i].y);
+  for (int i = 0; i < n_jobs; i++) launch_gemm_i8(ctx, jobs[i], qx, dx, s16, T, jobs[i].y, part, pd, cnt, nc);
   return true;
 }
 

@@ -94,6 +94,8 @@ struct mdma_ctx {
   uint64_t argmax_part_cap = 0;  // chunks
   uint32_t *attn_cnt = nullptr;
   uint64_t attn_cnt_cap = 0;
+  uint32_t *gemm_cnt = nullptr;  // split-K GEMM arrival counters (zero between launches)
+  uint64_t gemm_cnt_cap = 0;
 };
 
 struct mdma_graph {
@@ -114,6 +116,9 @@ char *argmax_parts(mdma_ctx *ctx, uint64_t chunks);
 // At least n zeroed arrival counters for split attention; each launch leaves
 // the counters it used at zero.
 uint32_t *attn_counters(mdma_ctx *ctx, uint64_t n);
+// Split-K GEMM arrival counters, zeroed at allocation (each launch leaves them
+// zero); nullptr when n exceeds what is allocated during stream capture.
+uint32_t *gemm_counters(mdma_ctx *ctx, uint64_t n);
 // Forget the cached int8 activations: every entry point that writes device
 // memory calls this (a qmatmul only when its output overlaps the cached x).
 inline void q8_invalidate(mdma_ctx *ctx) { ctx->q8_valid = false; }
@@ -176,12 +181,17 @@ void q8_mark(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in);
 bool q8_holds(mdma_ctx *ctx, const float *x, uint64_t n);
 void quantize_into_scratch(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in, int8_t **qx, float **dx,
                            int32_t **s16);
-// Prefill int8 MFMA GEMM (gemm_i8.hip) over prepared Q8_0 / Q4_K weights:
-// whether it covers (dtype, layout, n_in), and the launch for M tokens with
-// activations quantized per 32 (qx [M, K], sx [M, K/32], s16 [M, K/16]).
-bool gemm_i8_supported(int32_t dtype, int layout, uint64_t n_in);
+// Prefill int8 MFMA GEMM (gemm_i8.hip) over prepared Q8_0 / Q4_K / Q6_K
+// weights: whether it covers (dtype, layout, n_in, n_out); the split-K
+// partial storage (doubles) and counters a launch for M tokens asks for
+// (zero when it runs unsplit); and the launch with activations quantized per
+// 32 (qx [M, K], sx [M, K/32], s16 [M, K/16]). With part or cnt null, or
+// smaller than asked, the launch runs unsplit.
+bool gemm_i8_supported(int32_t dtype, int layout, uint64_t n_in, uint64_t n_out);
+void gemm_i8_split_need(const mdma_ctx *ctx, const GemvJob &w, uint64_t M, uint64_t *part_doubles,
+                        uint64_t *counters);
 void launch_gemm_i8(mdma_ctx *ctx, const GemvJob &w, const int8_t *qx, const float *sx, const int32_t *s16,
-                    uint64_t M, float *y);
+                    uint64_t M, float *y, double *part, uint64_t part_doubles, uint32_t *cnt, uint64_t counters);
 // Token count from which the int8 mode runs the MFMA GEMM instead of the GEMV.
 constexpr uint64_t GEMM_MIN_TOKENS = 16;
 void launch_quantize_act(mdma_ctx *ctx, const float *x, uint64_t n, uint64_t group, int8_t *q,
