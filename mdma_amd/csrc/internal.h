@@ -234,6 +234,16 @@ void launch_attn(mdma_ctx *ctx, const float *q, const uint16_t *k, const uint16_
 // group of at most 8 query heads per KV head, group outputs whole 256s).
 bool launch_attn_q8(mdma_ctx *ctx, const float *q, const uint16_t *k, const uint16_t *v, float *o, uint64_t n_q,
                     uint64_t kv_len, uint64_t hd, uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride = 0);
+// Decode attention with launch_rope_kv_write folded in: q, k, v are the
+// unrotated projections of n_q queries, each the single new token of its
+// sequence (seq_stride apart in kc / vc; or one query over one sequence,
+// seq_stride 0), all at rope position pos = kv_len - 1. The rotated key and
+// the value are written to the caches at that position, with the values
+// launch_rope_kv_write writes. int8_out: as launch_attn_q8. False, launching
+// nothing, when the shape has no such variant.
+bool launch_attn_rope(mdma_ctx *ctx, const float *q, const float *k, const float *v, const float *tab, uint32_t pos,
+                      uint16_t *kc, uint16_t *vc, float *o, uint64_t n_q, uint64_t kv_len, uint64_t hd,
+                      uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride, bool int8_out);
 void launch_argmax_rows(mdma_ctx *ctx, const float *x, uint64_t rows, uint64_t n, uint32_t *idx,
                         uint32_t *flag);
 

@@ -387,6 +387,17 @@ void run_layers(mdma_session *s, uint64_t T, uint32_t pos, uint64_t seq, bool ba
                                       c.n_kv_heads, stride);
     if (!fresh) launch_attn(ctx, fp(s->q), kc, vc, fp(s->attn_out), n_q, kv_len, hd, c.n_heads, c.n_kv_heads, stride);
   };
+  // One new token per sequence (a decode step): RoPE, the K/V cache write
+  // and attention in one launch.
+  auto decode_attend = [&](uint16_t *kc, uint16_t *vc, uint64_t stride) {
+    q8_invalidate(ctx);
+    const bool q8 = fuse_q8;
+    if (!launch_attn_rope(ctx, fp(s->q), fp(s->k), fp(s->v), tab, (uint32_t)pos, kc, vc, fp(s->attn_out), T, pos + 1,
+                          hd, c.n_heads, c.n_kv_heads, stride, q8))
+      return false;
+    fresh = q8;
+    return true;
+  };
   for (uint64_t i = 0; i < c.n_layers; i++) {
     const Layer &L = m->layers[i];
     if (i == 0) {
@@ -399,7 +410,10 @@ void run_layers(mdma_session *s, uint64_t T, uint32_t pos, uint64_t seq, bool ba
     gemv(ctx, qkv, 3, fp(s->normed), T, fresh);
     // KvCache::rope_write (src/kv_cache.rs:212-244): rotate q, store rotated k and v.
     uint16_t *kb = reinterpret_cast<uint16_t *>(s->kc[i]->ptr), *vb = reinterpret_cast<uint16_t *>(s->vc[i]->ptr);
-    if (batched) {
+    if ((batched || T == 1) && decode_attend(batched ? kb : kb + seq * cache_stride,
+                                             batched ? vb : vb + seq * cache_stride, batched ? cache_stride : 0)) {
+      // RoPE, the cache write and attention in one launch.
+    } else if (batched) {
       launch_rope_kv_write(ctx, fp(s->q), c.n_heads, fp(s->k), fp(s->v), c.n_kv_heads, hd, T, tab, pos,
                            kb + pos * kvw, vb + pos * kvw, cache_stride, 0);
       attend(kb, vb, T, pos + 1, cache_stride);

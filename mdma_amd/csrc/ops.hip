@@ -414,6 +414,14 @@ struct AttnQ8 {
   int32_t *s16;
 };
 
+// Decode with the query's RoPE and the new token's cache write folded in:
+// q, k, v are the projections before rotation ([n_q, heads, hd] f32); every
+// query's new key sits at its last visible position, rope position pos.
+struct AttnRope {
+  const float *k, *v, *tab;
+  uint32_t pos;
+};
+
 template <int CTRL, int ROWS>
 __device__ __forceinline__ float dpp_max(float v) {
   const float o = __builtin_bit_cast(
@@ -450,10 +458,17 @@ struct AttnTile {
   uint32_t v[16][C];  // V dim pairs of this wave's 16 keys
 };
 
-template <int C>
-__device__ __forceinline__ void attn_load(AttnTile<C> &t, const uint16_t *__restrict__ K,
-                                          const uint16_t *__restrict__ V, uint32_t tile, uint32_t visible,
-                                          uint32_t kv_row, uint32_t hd, uint32_t lane, uint32_t wave) {
+// The new key (ROPE: position visible - 1) is not taken from the cache: it is
+// rotated from kn / taken from vn (this query's head rows), rounded to f16
+// exactly as the cache stores it, and written to the cache by the lanes that
+// hold it (rope_kv_kernel's values). Every lane first issues its cache loads
+// (the new key's row is in the cache's bounds; its stale content is
+// replaced), so the new key's own loads add no round trip.
+template <int C, bool ROPE>
+__device__ __forceinline__ void attn_load(AttnTile<C> &t, uint16_t *__restrict__ K, uint16_t *__restrict__ V,
+                                          uint32_t tile, uint32_t visible, uint32_t kv_row, uint32_t hd,
+                                          uint32_t lane, uint32_t wave, const float *kn, const float *vn,
+                                          const float2 *cs) {
   const uint32_t jk = tile * ATT_TILE + wave * 16 + (lane >> 2), l4 = lane & 3;
 #pragma unroll
   for (int m = 0; m < 4 * C; m++) {
@@ -470,15 +485,49 @@ __device__ __forceinline__ void attn_load(AttnTile<C> &t, const uint16_t *__rest
       t.v[r][c] = jv < visible && d < hd ? *reinterpret_cast<const uint32_t *>(V + (size_t)jv * kv_row + d) : 0u;
     }
   }
+  if (!ROPE) return;
+  const uint32_t jn = visible - 1;  // the new key
+  if (jk == jn) {
+#pragma unroll
+    for (int m = 0; m < 4 * C; m++) {
+      const uint32_t d0 = 8 * l4 + 32 * m;
+      if (d0 >= hd) continue;
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        float x0 = kn[d0 + 2 * e], x1 = kn[d0 + 2 * e + 1];
+        const float2 c2 = cs[d0 / 2 + e];
+        rot(x0, x1, c2.x, c2.y);
+        w[e] = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
+      }
+      t.k[m] = make_uint4(w[0], w[1], w[2], w[3]);
+      *reinterpret_cast<uint4 *>(K + (size_t)jk * kv_row + d0) = t.k[m];
+    }
+  }
+  const uint32_t r0 = tile * ATT_TILE + wave * 16;
+  if (jn >= r0 && jn < r0 + 16) {  // this wave holds the new value row
+    const uint32_t rn = jn - r0;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      if (r != (int)rn) continue;
+#pragma unroll
+      for (int c = 0; c < C; c++) {
+        const uint32_t d = 2 * lane + 128 * c;
+        if (d >= hd) continue;
+        t.v[r][c] = (uint32_t)f2h(vn[d]) | ((uint32_t)f2h(vn[d + 1]) << 16);
+        *reinterpret_cast<uint32_t *>(V + (size_t)jn * kv_row + d) = t.v[r][c];
+      }
+    }
+  }
 }
 
-template <int G, int C, bool QUANT>
-__global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict__ q, const uint16_t *__restrict__ K,
-                                                         const uint16_t *__restrict__ V, float *__restrict__ o,
+template <int G, int C, bool QUANT, bool ROPE>
+__global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict__ q, uint16_t *__restrict__ K,
+                                                         uint16_t *__restrict__ V, float *__restrict__ o,
                                                          float *__restrict__ part, uint32_t *__restrict__ cnt,
                                                          uint32_t prefix, uint32_t hd, uint32_t n_q_heads,
                                                          uint32_t n_kv_heads, float scale, uint64_t seq_stride,
-                                                         uint32_t tpw, AttnQ8 q8) {
+                                                         uint32_t tpw, AttnQ8 q8, AttnRope rp) {
   __shared__ float qs[G][128 * C];
   __shared__ float sc[G][ATT_TILE];
   __shared__ float mrun[G], lrun[G], alph[G];
@@ -498,10 +547,25 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
   // Ping-pong tile buffers: the loads for tile+1 go out before tile is
   // computed (clamped to the run's last tile, so every load is in bounds and
   // the wait counts are fixed).
+  const float *kn = ROPE ? rp.k + ((size_t)i * n_kv_heads + kvh) * hd : nullptr;
+  const float *vn = ROPE ? rp.v + ((size_t)i * n_kv_heads + kvh) * hd : nullptr;
+  const float2 *cs = ROPE ? reinterpret_cast<const float2 *>(rp.tab) + (size_t)rp.pos * (hd / 2) : nullptr;
   AttnTile<C> ta, tb;
-  attn_load<C>(ta, K, V, t0, visible, kv_row, hd, lane, wave);
+  attn_load<C, ROPE>(ta, K, V, t0, visible, kv_row, hd, lane, wave, kn, vn, cs);
   const float *qv = q + ((size_t)i * n_q_heads + qh0) * hd;
-  for (uint32_t t = tid; t < G * hd; t += 256) qs[t / hd][t % hd] = qv[t];
+  if (ROPE) {
+    // Interleaved pairs rotated as rope_kv_kernel rotates q.
+    for (uint32_t p = tid; p < G * hd / 2; p += 256) {
+      const uint32_t h = p / (hd / 2), e = p % (hd / 2);
+      float x0 = qv[h * hd + 2 * e], x1 = qv[h * hd + 2 * e + 1];
+      const float2 c2 = cs[e];
+      rot(x0, x1, c2.x, c2.y);
+      qs[h][2 * e] = x0;
+      qs[h][2 * e + 1] = x1;
+    }
+  } else {
+    for (uint32_t t = tid; t < G * hd; t += 256) qs[t / hd][t % hd] = qv[t];
+  }
   if (tid < G) mrun[tid] = -INFINITY, lrun[tid] = 0.f;
   float acc[G][C][2];
 #pragma unroll
@@ -572,10 +636,10 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
     process(ta, t0);
   } else {
     for (uint32_t tile = t0; tile < t1; tile += 2) {
-      attn_load<C>(tb, K, V, min(tile + 1, t1 - 1), visible, kv_row, hd, lane, wave);
+      attn_load<C, ROPE>(tb, K, V, min(tile + 1, t1 - 1), visible, kv_row, hd, lane, wave, kn, vn, cs);
       process(ta, tile);
       if (tile + 1 >= t1) break;
-      attn_load<C>(ta, K, V, min(tile + 2, t1 - 1), visible, kv_row, hd, lane, wave);
+      attn_load<C, ROPE>(ta, K, V, min(tile + 2, t1 - 1), visible, kv_row, hd, lane, wave, kn, vn, cs);
       process(tb, tile + 1);
     }
   }
@@ -928,9 +992,13 @@ void launch_rope_kv_write(mdma_ctx *ctx, float *q, uint64_t q_heads, const float
 }
 
 namespace {
-bool attn_impl(mdma_ctx *ctx, const float *q, const uint16_t *k, const uint16_t *v, float *o, uint64_t n_q,
+// rope: RoPE and the new key's cache write folded in (decode only); the
+// cache is written only then. False, launching nothing, when q8 or rope is
+// asked for a shape without that variant.
+bool attn_impl(mdma_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t *vc, float *o, uint64_t n_q,
                uint64_t kv_len, uint64_t hd, uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride,
-               const AttnQ8 *q8) {
+               const AttnQ8 *q8, const AttnRope *rope = nullptr) {
+  uint16_t *k = const_cast<uint16_t *>(kc), *v = const_cast<uint16_t *>(vc);
   const float scale = 1.0f / sqrtf((float)hd);
   const uint32_t prefix = (uint32_t)(seq_stride ? kv_len - 1 : kv_len - n_q);
   const uint64_t G = n_kv_heads ? n_q_heads / n_kv_heads : 0, C = (hd + 127) / 128;
@@ -948,21 +1016,23 @@ bool attn_impl(mdma_ctx *ctx, const float *q, const uint16_t *k, const uint16_t 
   const bool split_ok = hd % 8 == 0 && hd <= 256 && (G == 1 || G == 2 || G == 4 || G == 8) && G * C <= 8 &&
                         n_splits < 65536 && n_q < 65536 && part_bytes <= (256ull << 20);
   if (q8 && !(split_ok && (G * hd) % 256 == 0)) return false;
+  if (rope && !(split_ok && n_q && kv_len && hd % 8 == 0 && (seq_stride || n_q == 1))) return false;
   if (split_ok && n_q && kv_len) {
     float *part = part_bytes ? reinterpret_cast<float *>(scratch(ctx, part_bytes)) : nullptr;
     uint32_t *cnt = part_bytes ? attn_counters(ctx, n_q * n_kv_heads) : nullptr;
     const AttnQ8 a8 = q8 ? *q8 : AttnQ8{nullptr, nullptr, nullptr};
+    const AttnRope ar = rope ? *rope : AttnRope{nullptr, nullptr, nullptr, 0};
     const dim3 grid((uint32_t)n_kv_heads, (uint32_t)n_splits, (uint32_t)n_q);
-#define MDMA_ATT(GG, CC)                                                                                       \
-  do {                                                                                                         \
-    if (q8)                                                                                                    \
-      attn_split_kernel<GG, CC, true><<<grid, dim3(256), 0, ctx->stream>>>(                                    \
-          q, k, v, o, part, cnt, prefix, (uint32_t)hd, (uint32_t)n_q_heads, (uint32_t)n_kv_heads, scale,      \
-          seq_stride, (uint32_t)tpw, a8);                                                                      \
-    else                                                                                                       \
-      attn_split_kernel<GG, CC, false><<<grid, dim3(256), 0, ctx->stream>>>(                                   \
-          q, k, v, o, part, cnt, prefix, (uint32_t)hd, (uint32_t)n_q_heads, (uint32_t)n_kv_heads, scale,      \
-          seq_stride, (uint32_t)tpw, a8);                                                                      \
+#define MDMA_ATT_GO(GG, CC, QQ, RR)                                                                            \
+  attn_split_kernel<GG, CC, QQ, RR><<<grid, dim3(256), 0, ctx->stream>>>(                                      \
+      q, k, v, o, part, cnt, prefix, (uint32_t)hd, (uint32_t)n_q_heads, (uint32_t)n_kv_heads, scale, seq_stride, \
+      (uint32_t)tpw, a8, ar)
+#define MDMA_ATT(GG, CC)                                \
+  do {                                                  \
+    if (q8 && rope) MDMA_ATT_GO(GG, CC, true, true);    \
+    else if (q8) MDMA_ATT_GO(GG, CC, true, false);      \
+    else if (rope) MDMA_ATT_GO(GG, CC, false, true);    \
+    else MDMA_ATT_GO(GG, CC, false, false);             \
   } while (0)
     if (C == 1) {
       if (G == 1) MDMA_ATT(1, 1);
@@ -975,6 +1045,7 @@ bool attn_impl(mdma_ctx *ctx, const float *q, const uint16_t *k, const uint16_t 
       else MDMA_ATT(4, 2);
     }
 #undef MDMA_ATT
+#undef MDMA_ATT_GO
     hip_check(hipGetLastError(), "attn launch");
     return true;
   }
@@ -997,6 +1068,22 @@ bool launch_attn_q8(mdma_ctx *ctx, const float *q, const uint16_t *k, const uint
   AttnQ8 a8;
   q8_slots(ctx, n_q, n_in, &a8.q, &a8.d, &a8.s16);
   if (!attn_impl(ctx, q, k, v, o, n_q, kv_len, hd, n_q_heads, n_kv_heads, seq_stride, &a8)) return false;
+  q8_mark(ctx, o, n_q, n_in);
+  return true;
+}
+
+bool launch_attn_rope(mdma_ctx *ctx, const float *q, const float *k, const float *v, const float *tab, uint32_t pos,
+                      uint16_t *kc, uint16_t *vc, float *o, uint64_t n_q, uint64_t kv_len, uint64_t hd,
+                      uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride, bool int8_out) {
+  if (!n_q || !kv_len || pos != kv_len - 1) return false;
+  const AttnRope rp{k, v, tab, pos};
+  if (!int8_out)
+    return attn_impl(ctx, q, kc, vc, o, n_q, kv_len, hd, n_q_heads, n_kv_heads, seq_stride, nullptr, &rp);
+  const uint64_t n_in = n_q_heads * hd;
+  if (n_in % 256) return false;
+  AttnQ8 a8;
+  q8_slots(ctx, n_q, n_in, &a8.q, &a8.d, &a8.s16);
+  if (!attn_impl(ctx, q, kc, vc, o, n_q, kv_len, hd, n_q_heads, n_kv_heads, seq_stride, &a8, &rp)) return false;
   q8_mark(ctx, o, n_q, n_in);
   return true;
 }

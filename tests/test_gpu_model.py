@@ -86,6 +86,39 @@ def test_batched_decode_equals_single_sequences(backend, tiny):
     m.close()
 
 
+# Grouped-query geometry (4 query heads per KV head, head_dim 64) with the
+# Q4_K_M type mix: the decode step's fused RoPE + cache write + attention runs
+# the G = 4 kernel, as at Llama-3-8B.
+GQA_SMALL = dict(n_layers=2, n_embd=512, n_heads=8, n_kv_heads=2, n_ff=1024, vocab=2048, n_ctx=128,
+                 rms_eps=1e-5, rope_theta=500000.0)
+
+
+@pytest.fixture(scope="module")
+def gqa(tmp_path_factory):
+    p = str(tmp_path_factory.mktemp("gguf") / "gqa.gguf")
+    llama_synth.write(p, GQA_SMALL, llama_synth.Q4_K_M, 3)
+    return p
+
+
+def test_gqa_q4km_greedy_and_batched_decode_match_oracle(backend, gqa):
+    backend.set_act_mode(ACT_F32)
+    r = gguf.Reader(gqa)
+    prompts = np.stack([synth.tokens(N_PROMPT, 2048, 2000 + b) for b in range(3)])
+    m = Model(backend, gqa)
+    s = m.session(N_PROMPT + 24, 1, N_PROMPT)
+    got, _ = s.generate(prompts[:1], 24)
+    want, _ = ffi.llama_generate(r, prompts[0], 24, kv_f16=True)
+    assert np.array_equal(got[0], want), (got[0].tolist(), want.tolist())
+    s.close()
+    s = m.session(N_PROMPT + 24, 3, N_PROMPT)
+    got, _ = s.generate(prompts, 24)
+    for b in range(3):
+        want, _ = ffi.llama_generate(r, prompts[b], 24, kv_f16=True)
+        assert np.array_equal(got[b], want), b
+    s.close()
+    m.close()
+
+
 def test_int8_mode_decodes(backend, tiny):
     backend.set_act_mode(ACT_I8)
     try:
