@@ -353,6 +353,56 @@ __device__ typename F::XI prologue_xi(const float *__restrict__ x, uint32_t u, b
   return F::make_xi(q, sums, amax / 127.0f);
 }
 
+// The same int8 activations, quantized once per workgroup: with one-wave
+// teams every wave of a workgroup needs all of x, so its 256 threads
+// quantize the (at most 64) units together into LDS, four threads per unit
+// (16 columns each, a 256-column group on 16 lanes of one wave), and every
+// lane then reads its own unit u back. The same arithmetic, bit for bit.
+// Called by all threads of the workgroup (it has a barrier).
+template <class F>
+__device__ typename F::XI prologue_xi_wg(const float *__restrict__ x, uint32_t U, uint32_t u, uint4 (*lq)[4],
+                                         int (*ls)[4], float *ld) {
+  const uint32_t t = threadIdx.x, qu = t >> 2, c = t & 3;
+  const bool live = qu < U;
+  const uint32_t col = F::chunk_col(live ? qu : 0, c);
+  float v[16];
+#pragma unroll
+  for (int k = 0; k < 16; k += 4) {
+    const float4 xv = live ? *reinterpret_cast<const float4 *>(x + col + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+    v[k] = xv.x, v[k + 1] = xv.y, v[k + 2] = xv.z, v[k + 3] = xv.w;
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int k = 0; k < 16; k++) amax = fmaxf(amax, fabsf(v[k]));
+  // Max over the quad (one unit), then over the 16-lane row (four units).
+  amax = fmaxf(amax, __builtin_bit_cast(float, quad_perm_u32<0xB1>(__builtin_bit_cast(uint32_t, amax))));
+  amax = fmaxf(amax, __builtin_bit_cast(float, quad_perm_u32<0x4E>(__builtin_bit_cast(uint32_t, amax))));
+  amax = fmaxf(amax, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, amax), 0x124, 0xF,
+                                                                          0xF, false)));  // row_ror:4
+  amax = fmaxf(amax, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, amax), 0x128, 0xF,
+                                                                          0xF, false)));  // row_ror:8
+  const float inv = amax == 0.f ? 0.f : 127.0f / amax;
+  uint32_t w4[4] = {0u, 0u, 0u, 0u};
+  int sm = 0;
+#pragma unroll
+  for (int k = 0; k < 16; k++) {
+    float r = roundf(v[k] * inv);
+    r = fminf(fmaxf(r, -127.f), 127.f);
+    const int qi = (int)r;
+    sm += qi;
+    w4[k >> 2] |= (uint32_t)(qi & 0xff) << (8 * (k & 3));
+  }
+  if (live) {
+    lq[qu][c] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+    ls[qu][c] = sm;
+    if ((t & 15) == 0) ld[qu >> 2] = amax / 127.0f;
+  }
+  lds_barrier();  // LDS only: the weight loads already issued stay in flight
+  const uint4 q[4] = {lq[u][0], lq[u][1], lq[u][2], lq[u][3]};
+  const int sums[4] = {ls[u][0], ls[u][1], ls[u][2], ls[u][3]};
+  return F::make_xi(q, sums, ld[u >> 2]);
+}
+
 // ------------------------------------------------------------- kernel ----
 
 struct TeamJob {
@@ -382,8 +432,10 @@ constexpr int nbuf() {
 // PRO: one token whose int8 activations the kernel quantizes from f32 x
 // itself instead of reading the quantized-x buffers (a separate
 // instantiation: the prologue's registers would otherwise lower every
-// launch's occupancy).
-template <class F, bool F32, int R, int ITERS, int TW, int PL, int TT, bool GATED, bool PRO = false>
+// launch's occupancy): 1 = each wave its own units (multi-wave teams,
+// whose waves hold different units), 2 = once per workgroup in LDS
+// (one-wave teams, whose waves all hold every unit).
+template <class F, bool F32, int R, int ITERS, int TW, int PL, int TT, bool GATED, int PRO = 0>
 __global__ __launch_bounds__(WG) void gemv_team(TeamSet ts, const float *__restrict__ xf,
                                                 const int8_t *__restrict__ qx, const float *__restrict__ dx,
                                                 const int32_t *__restrict__ s16, uint32_t T,
@@ -517,7 +569,14 @@ __global__ __launch_bounds__(WG) void gemv_team(TeamSet ts, const float *__restr
   };
   // Activations of the lane's units, loaded once. The first rows' weights
   // go out before them: the weights come from HBM, the activations from L2.
-  if constexpr (PRO) {
+  if constexpr (PRO == 2) {
+    static_assert(TW == 1 && PL == 1 && TT == 1, "workgroup prologue: one-wave teams, one unit per lane");
+    __shared__ uint4 pq[64][4];
+    __shared__ int ps[64][4];
+    __shared__ float pd[16];
+    first_loads();
+    xi[0][0] = prologue_xi_wg<F>(xf, U, uid[0], pq, ps, pd);
+  } else if constexpr (PRO == 1) {
     // The weights go out first, then each wave quantizes its lanes' x.
     first_loads();
 #pragma unroll
@@ -615,10 +674,10 @@ void launch_iters(mdma_ctx *ctx, TeamSet ts, int tw, int pl, const float *xf, co
 #define MDMA_TEAM_LAUNCH(TW_, PL_)                             \
   do {                                                         \
     if constexpr (PRO_OK) {                                    \
-      if (ts.pro) MDMA_TEAM_GO(TW_, PL_, true);                \
-      else MDMA_TEAM_GO(TW_, PL_, false);                      \
+      if (ts.pro) MDMA_TEAM_GO(TW_, PL_, TW_ == 1 ? 2 : 1);    \
+      else MDMA_TEAM_GO(TW_, PL_, 0);                          \
     } else {                                                   \
-      MDMA_TEAM_GO(TW_, PL_, false);                           \
+      MDMA_TEAM_GO(TW_, PL_, 0);                               \
     }                                                          \
   } while (0)
   if (tw == 1) MDMA_TEAM_LAUNCH(1, 1);

@@ -64,14 +64,10 @@ bool launch_gemv_i8_x(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, bool gated
   if (!team_layout_ok(jobs, gated ? 2 : n_jobs)) return false;
   const int32_t dt = jobs[0].dtype;
   if ((dt != DT_Q4_K && dt != DT_Q6_K) || jobs[0].n_in % 256) return false;
-  // Every wave reads its units' f32 x (4 bytes per column instead of ~1.3):
-  // a win where a wave's share of x is small against its rows -- teams of
-  // several waves (n_in > 4096) or very tall weights (the output head).
-  // For one-wave teams of short rows the shared lines of x become an L2
-  // hot spot and quantizing once beforehand is faster.
-  uint64_t rows = 0;
-  for (int i = 0; i < (gated ? 1 : n_jobs); i++) rows += jobs[i].n_out;
-  if (jobs[0].n_in <= 4096 && rows < 65536) return false;
+  // Multi-wave teams (n_in > 4096) quantize each wave's own units; one-wave
+  // teams quantize x once per workgroup in LDS (every wave of it needs all
+  // of x), which keeps the f32 reads of x off the L2 hot spot that one read
+  // per wave makes of them.
   launch_gemv_team(ctx, MDMA_ACT_I8, jobs, n_jobs, gated, x, 1, ygated, true);
   return true;
 }

@@ -408,7 +408,7 @@ def test_attention_int8_activations_bit_exact(backend, n_q, kv_len):
 
 
 @pytest.mark.parametrize("dtype", [Q4K, Q6K])
-@pytest.mark.parametrize("k", [8192, 14336])
+@pytest.mark.parametrize("k", [768, 2048, 4096, 8192, 14336])
 def test_one_token_in_kernel_quantization_bit_exact(backend, dtype, k):
     # One int8 token: the GEMV quantizes x itself; the result must be the
     # bits of the GEMV over separately quantized x (x cached by rmsnorm).
@@ -431,6 +431,33 @@ def test_one_token_in_kernel_quantization_bit_exact(backend, dtype, k):
         assert np.array_equal(backend.download_f32(y2), backend.download_f32(y3))
         cpu, exact = oracle_i8(dtype, synth.weight(dtype, rows, k, 41), rows, k, x)
         assert_parity(backend.download_f32(y1), cpu, exact, 1e-3, atol=1e-5)
+    finally:
+        backend.set_act_mode(backend_mod.ACT_F32)
+
+
+def test_fused_calls_in_kernel_quantization_bit_exact(backend):
+    # qmatmul_qkv and ffn_gate_up of one f32 token quantize x inside the
+    # kernel (once per workgroup for rows of 4096): the bits of the same
+    # calls over the cached int8 form of the same values.
+    k = 4096
+    raws = {"q": (Q6K, 64), "k": (Q6K, 32), "v": (Q6K, 32), "gate": (Q4K, 96), "up": (Q4K, 96)}
+    ws = {n: backend.upload_weight(synth.weight(dt, r, k, 60 + i), dt, (r, k)) for i, (n, (dt, r)) in enumerate(raws.items())}
+    x = synth.normal_f32(k, 61)
+    xb = backend.f32_buf(x)
+    yn = backend.alloc(k * 4)
+    backend.set_act_mode(backend_mod.ACT_I8)
+    try:
+        backend.rmsnorm(backend.f32_buf(np.ones(k, np.float32)), xb, yn, 1e-5)
+        yv = backend.f32_buf(backend.download_f32(yn))  # same values, not cached
+        outs = {}
+        for name, src in (("cached", yn), ("in_kernel", yv)):
+            o = [backend.alloc(raws[n][1] * 4) for n in ("q", "k", "v")]
+            backend.qmatmul_qkv(ws["q"], ws["k"], ws["v"], src, *o)
+            g, u, a = backend.alloc(96 * 4), backend.alloc(96 * 4), backend.alloc(96 * 4)
+            backend.ffn_gate_up(ws["gate"], ws["up"], src, g, u, a)
+            outs[name] = [backend.download_f32(b) for b in o + [a]]
+        for a_, b_ in zip(outs["cached"], outs["in_kernel"]):
+            assert np.array_equal(a_, b_)
     finally:
         backend.set_act_mode(backend_mod.ACT_F32)
 
