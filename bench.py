@@ -4,8 +4,12 @@
 Workload (the Q4_K decode-GEMV benchmark configuration): one step is one pass over a Llama-3-8B layer's
 seven Q4_K matrix-vector products at batch 1 (q and o 4096x4096, k and v
 1024x4096, gate and up 14336x4096, down 4096x14336), issued the way the decode
-path issues them: fused QKV, o, fused gate/up + SiLU, down -- four launches,
-each reading its own input buffer. Weights are synthetic (f16 d, dmin = |N(0,1)|*1e-3,
+path issues them: fused QKV, o, fused gate/up + SiLU, down -- four launches.
+The three 4096-wide launches read one input whose int8 form was written by the
+rmsnorm that produced it (the decode path fuses the quantization into the
+producers of these inputs: rmsnorm and attention), made once before the timed
+region; the down projection reads an f32 input and quantizes it in its own
+prologue, as in the decode path. Weights are synthetic (f16 d, dmin = |N(0,1)|*1e-3,
 six-bit scales and mins uniform in [0,63], nibbles uniform in [0,15]) and rotate over >= 1 GiB of distinct device copies so the 256 MB
 Infinity Cache cannot serve them. Each step is one replay of a captured HIP
 graph; the timed region is bracketed by stream synchronisation and HIP events
@@ -67,8 +71,11 @@ def x_bytes(n_in, mode):
 
 
 def launch_bytes(launch, mode):
-    _, names, n_in, rows = launch
-    return sum(w_bytes(n) for n in names) + x_bytes(n_in, mode) + rows * 4
+    """Weight bytes + input bytes as the launch reads them + f32 outputs. In
+    the int8 mode the down projection reads its f32 input (quantized in the
+    kernel); the others read an int8 form."""
+    name, names, n_in, rows = launch
+    return sum(w_bytes(n) for n in names) + x_bytes(n_in, "f32" if name == "down" else mode) + rows * 4
 
 
 class HipEvents:
@@ -105,18 +112,29 @@ class Workload:
         self.raws = {n: synth.weight(Q4K, r, c, SEED + i) for i, (n, (r, c)) in enumerate(SHAPES.items())}
         self.layers = [{n: be.upload_weight(self.raws[n], Q4K, SHAPES[n]) for n in SHAPES}
                        for _ in range(self.copies)]
-        self.x = {name: be.f32_buf(synth.normal_f32(n_in, SEED + 100 + i))
-                  for i, (name, _, n_in, _) in enumerate(LAUNCHES)}
+        # The 4096-wide input is an rmsnorm output (prepare() writes it and,
+        # in the int8 mode, its int8 form); x_raw is the rmsnorm's input.
+        self.x_raw = be.f32_buf(synth.normal_f32(4096, SEED + 100))
+        self.ones = be.f32_buf(np.ones(4096, np.float32))
+        self.x = {"x4k": be.alloc(4096 * 4), "down": be.f32_buf(synth.normal_f32(14336, SEED + 103))}
         self.y = {n: be.alloc(SHAPES[n][0] * 4) for n in SHAPES}
         self.act = be.alloc(14336 * 4)
 
+    def prepare(self, be):
+        """Write the 4096-wide input (and its int8 form, in the int8 mode)
+        the way the decode path does: by a fused rmsnorm. Every graph replay
+        drops the library's record of it, so this precedes each capture and
+        each run of eager launches."""
+        be.rmsnorm(self.ones, self.x_raw, self.x["x4k"], 1e-5)
+
     def launch(self, be, L, which):
+        x = self.x["x4k"]
         if which == "qkv":
-            be.qmatmul_qkv(L["q"], L["k"], L["v"], self.x["qkv"], self.y["q"], self.y["k"], self.y["v"])
+            be.qmatmul_qkv(L["q"], L["k"], L["v"], x, self.y["q"], self.y["k"], self.y["v"])
         elif which == "o":
-            be.qmatmul(L["o"], self.x["o"], self.y["o"])
+            be.qmatmul(L["o"], x, self.y["o"])
         elif which == "gate_up":
-            be.ffn_gate_up(L["gate"], L["up"], self.x["gate_up"], self.y["gate"], self.y["up"], self.act)
+            be.ffn_gate_up(L["gate"], L["up"], x, self.y["gate"], self.y["up"], self.act)
         else:
             be.qmatmul(L["down"], self.x["down"], self.y["down"])
 
@@ -141,8 +159,8 @@ def time_graphs(be, ev, graphs, steps, warmup):
 
 def per_launch(be, ev, wl, mode, reps):
     """Per launch kind, over every distinct weight copy, each launch as the
-    step issues it (in the int8 mode every one-token GEMV quantizes its f32
-    x in its own prologue, so the times include that quantization):
+    step issues it (in the int8 mode the down projection quantizes its f32 x
+    in its own prologue, so its time includes that quantization):
       - us_kernel: kernel duration from the dispatch's own start/end
         timestamps (hipExtLaunchKernel events, the figure a profiler's
         kernel trace reports), averaged over reps * copies eager launches;
@@ -153,11 +171,13 @@ def per_launch(be, ev, wl, mode, reps):
     starts, stops = [ev.event() for _ in range(n)], [ev.event() for _ in range(n)]
     for launch in LAUNCHES:
         name = launch[0]
+        wl.prepare(be)
         g = be.capture(lambda: [wl.launch(be, L, name) for L in wl.layers])
         ms = time_graphs(be, ev, [g], reps, 2)
         g.close()
         us_graph = ms * 1e3 / n
-        for L in wl.layers:  # warm: activations quantized, code loaded
+        wl.prepare(be)
+        for L in wl.layers:  # warm: code loaded
             wl.launch(be, L, name)
         be.join_execution()
         i = 0
@@ -177,29 +197,25 @@ def per_launch(be, ev, wl, mode, reps):
     return out
 
 
-def gate_up_cached_x(be, ev, wl, reps):
-    """The fused gate/up GEMV as the decode path runs it: x's int8 form was
-    written by the rmsnorm that produced x (fused), so the kernel reads the
-    int8 activations instead of quantizing. Kernel-only us per launch."""
-    k = SHAPES["gate"][1]
-    xn, ones = be.alloc(k * 4), be.f32_buf(np.ones(k, np.float32))
-    be.rmsnorm(ones, wl.x["gate_up"], xn, 1e-5)
+def gate_up_x_in_kernel(be, ev, wl, reps):
+    """The fused gate/up GEMV given an f32 x with no int8 form (a caller
+    outside the decode path): the kernel quantizes x in its own prologue.
+    Kernel-only us per launch."""
+    x = wl.x_raw
     n = reps * len(wl.layers)
     starts, stops = [ev.event() for _ in range(n)], [ev.event() for _ in range(n)]
     for L in wl.layers:
-        be.ffn_gate_up(L["gate"], L["up"], xn, wl.y["gate"], wl.y["up"], wl.act)
+        be.ffn_gate_up(L["gate"], L["up"], x, wl.y["gate"], wl.y["up"], wl.act)
     i = 0
     for _ in range(reps):
         for L in wl.layers:
             be.time_next_gemv(starts[i].value, stops[i].value)
-            be.ffn_gate_up(L["gate"], L["up"], xn, wl.y["gate"], wl.y["up"], wl.act)
+            be.ffn_gate_up(L["gate"], L["up"], x, wl.y["gate"], wl.y["up"], wl.act)
             i += 1
     be.join_execution()
     us = sum(ev.elapsed_ms(starts[j], stops[j]) for j in range(n)) * 1e3 / n
     for e in starts + stops:
         ev.destroy(e)
-    xn.close()
-    ones.close()
     return us
 
 
@@ -415,6 +431,7 @@ def main():
     results = {}
     for mode, code in (("i8", ACT_I8), ("f32", ACT_F32)):
         be.set_act_mode(code)
+        wl.prepare(be)
         graphs = [be.capture(lambda L=L: wl.step(be, L)) for L in wl.layers]
         ms = time_graphs(be, ev, graphs, args.steps, args.warmup)
         for g in graphs:
@@ -430,16 +447,17 @@ def main():
     main_mode = results["i8"]
     dom = main_mode["per_launch"]["gate_up"]
     be.set_act_mode(ACT_I8)
-    us_dec = gate_up_cached_x(be, ev, wl, args.reps)
+    us_xk = gate_up_x_in_kernel(be, ev, wl, args.reps)
+    b_xk = dom["bytes_per_launch"] + 3 * 4096  # x read as f32, not int8
     roof = {"bound": "hbm", "achieved": dom["GBps_kernel"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(dom["GBps_kernel"] / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_GATE_UP,
-            "kernel": "gemv_team<Q4G, int8, gated, x quantized in the kernel> (fused ffn gate/up + SiLU, "
-                      "2 x 14336x4096 Q4_K)",
+            "kernel": "gemv_team<Q4G, int8, gated, x staged in LDS> (fused ffn gate/up + SiLU, 2 x 14336x4096 Q4_K, "
+                      "x's int8 form from the fused rmsnorm)",
             "bytes_per_launch": dom["bytes_per_launch"], "us_per_launch": dom["us_kernel"],
-            "decode_variant": {"kernel": "gemv_team<Q4G, int8, gated> reading x's int8 form from the fused rmsnorm",
-                               "us_per_launch": round(us_dec, 3),
-                               "achieved": round(dom["bytes_per_launch"] / us_dec / 1e3, 1),
-                               "frac": round(dom["bytes_per_launch"] / us_dec / 1e3 / HBM_PEAK_GBS, 4)}}
+            "x_quantized_in_kernel": {"kernel": "gemv_team<Q4G, int8, gated, x-quant> (f32 x quantized in the prologue)",
+                                      "us_per_launch": round(us_xk, 3),
+                                      "achieved": round(b_xk / us_xk / 1e3, 1),
+                                      "frac": round(b_xk / us_xk / 1e3 / HBM_PEAK_GBS, 4)}}
     for L in wl.layers:  # free the rotated layer copies before the 8B model loads
         for w in L.values():
             w.buf.close()
@@ -452,7 +470,8 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(main_mode["ms_per_step"], 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "i8", "data": "synthetic",
         "config": {"workload": "Q4_K decode GEMV, one Llama-3-8B layer (fused qkv, o, fused gate/up+SiLU, down), "
-                               "batch 1, int8 activations", "global_batch": 1, "seq_len": 1, "parallelism": "none",
+                               "batch 1, int8 activations (qkv/o/gate_up read x's int8 form from its producer; "
+                               "down quantizes its f32 x in the kernel)", "global_batch": 1, "seq_len": 1, "parallelism": "none",
                    "weight_copies": wl.copies, "rotated_bytes": wl.copies * wl.layer_bytes, "seed": SEED},
         "pct_of_hbm_peak": round(100 * main_mode["GBps"] / HBM_PEAK_GBS, 2),
         "roofline": roof,

@@ -312,10 +312,10 @@ struct Q8G {
 // ----------------------------------------------------------- prologue ----
 // The int8 activations of unit u quantized from f32 x inside the GEMV, per
 // 256 columns (the four units of a quad): the arithmetic of
-// quantize_act_kernel, bit for bit.
+// quantize_act_kernel, bit for bit. Split into the loads of x and the
+// quantization, so the first weight loads can be issued between them.
 template <class F>
-__device__ typename F::XI prologue_xi(const float *__restrict__ x, uint32_t u, bool ok) {
-  float v[4][16];
+__device__ void prologue_load(const float *__restrict__ x, uint32_t u, bool ok, float (&v)[4][16]) {
 #pragma unroll
   for (int c = 0; c < 4; c++) {
     const uint32_t col = F::chunk_col(u, c);
@@ -325,6 +325,9 @@ __device__ typename F::XI prologue_xi(const float *__restrict__ x, uint32_t u, b
       v[c][k] = xv.x, v[c][k + 1] = xv.y, v[c][k + 2] = xv.z, v[c][k + 3] = xv.w;
     }
   }
+}
+template <class F>
+__device__ typename F::XI prologue_quant(const float (&v)[4][16]) {
   float amax = 0.f;
 #pragma unroll
   for (int c = 0; c < 4; c++)
@@ -358,19 +361,23 @@ __device__ typename F::XI prologue_xi(const float *__restrict__ x, uint32_t u, b
 // quantize the (at most 64) units together into LDS, four threads per unit
 // (16 columns each, a 256-column group on 16 lanes of one wave), and every
 // lane then reads its own unit u back. The same arithmetic, bit for bit.
-// Called by all threads of the workgroup (it has a barrier).
 template <class F>
-__device__ typename F::XI prologue_xi_wg(const float *__restrict__ x, uint32_t U, uint32_t u, uint4 (*lq)[4],
-                                         int (*ls)[4], float *ld) {
+__device__ void prologue_wg_load(const float *__restrict__ x, uint32_t U, float (&v)[16]) {
   const uint32_t t = threadIdx.x, qu = t >> 2, c = t & 3;
   const bool live = qu < U;
   const uint32_t col = F::chunk_col(live ? qu : 0, c);
-  float v[16];
 #pragma unroll
   for (int k = 0; k < 16; k += 4) {
     const float4 xv = live ? *reinterpret_cast<const float4 *>(x + col + k) : make_float4(0.f, 0.f, 0.f, 0.f);
     v[k] = xv.x, v[k + 1] = xv.y, v[k + 2] = xv.z, v[k + 3] = xv.w;
   }
+}
+// Called by all threads of the workgroup (it has a barrier).
+template <class F>
+__device__ typename F::XI prologue_wg_quant(const float (&v)[16], uint32_t U, uint32_t u, uint4 (*lq)[4],
+                                            int (*ls)[4], float *ld) {
+  const uint32_t t = threadIdx.x, qu = t >> 2, c = t & 3;
+  const bool live = qu < U;
   float amax = 0.f;
 #pragma unroll
   for (int k = 0; k < 16; k++) amax = fmaxf(amax, fabsf(v[k]));
@@ -429,12 +436,14 @@ constexpr int nbuf() {
 #endif
 }
 
-// PRO: one token whose int8 activations the kernel quantizes from f32 x
-// itself instead of reading the quantized-x buffers (a separate
+// PRO: how a one-token int8 launch gets its activations (each a separate
 // instantiation: the prologue's registers would otherwise lower every
-// launch's occupancy): 1 = each wave its own units (multi-wave teams,
-// whose waves hold different units), 2 = once per workgroup in LDS
-// (one-wave teams, whose waves all hold every unit).
+// launch's occupancy). 0 = every lane loads its units of the quantized-x
+// buffers. The kernel quantizes f32 x itself: 1 = each wave its own units
+// (multi-wave teams, whose waves hold different units), 2 = once per
+// workgroup in LDS (one-wave teams, whose waves all hold every unit).
+// 3 = the quantized-x buffers staged once per workgroup in LDS (one-wave
+// teams of the fused gate/up).
 template <class F, bool F32, int R, int ITERS, int TW, int PL, int TT, bool GATED, int PRO = 0>
 __global__ __launch_bounds__(WG) void gemv_team(TeamSet ts, const float *__restrict__ xf,
                                                 const int8_t *__restrict__ qx, const float *__restrict__ dx,
@@ -452,18 +461,18 @@ __global__ __launch_bounds__(WG) void gemv_team(TeamSet ts, const float *__restr
   __shared__ double red[TW > 1 ? TPW : 1][TW > 1 ? TW : 1][TW > 1 ? ITERS * NR * TT : 1];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int tw = wave % TW, slot = wave / TW;
-  // Team -> job (scalar, so every job field stays in SGPRs).
+  // Team -> job, branch-free: every field is read up front, so the
+  // kernel-argument loads form one batch before the first weight load, and
+  // every job field stays in SGPRs.
   uint32_t team = blockIdx.x * TPW + slot;
-  int ji = 0;
-  if (ts.n > 1 && team >= ts.j[0].teams) {
-    team -= ts.j[0].teams;
-    ji = 1;
-    if (ts.n > 2 && team >= ts.j[1].teams) {
-      team -= ts.j[1].teams;
-      ji = 2;
-    }
-  }
-  const TeamJob J = ji == 0 ? ts.j[0] : (ji == 1 ? ts.j[1] : ts.j[2]);
+  const uint32_t t0 = ts.j[0].teams, t1 = ts.j[1].teams;
+  const bool in1 = ts.n > 1 && team >= t0, in2 = ts.n > 2 && team >= t0 + t1;
+  team -= in2 ? t0 + t1 : (in1 ? t0 : 0u);
+  TeamJob J;
+  J.w = in2 ? ts.j[2].w : (in1 ? ts.j[1].w : ts.j[0].w);
+  J.y = in2 ? ts.j[2].y : (in1 ? ts.j[1].y : ts.j[0].y);
+  J.n_out = in2 ? ts.j[2].n_out : (in1 ? ts.j[1].n_out : ts.j[0].n_out);
+  J.teams = in2 ? ts.j[2].teams : (in1 ? t1 : t0);
   // A team past its job's end (the grid's last workgroup) runs the loop for
   // the barriers of its workgroup but stores nothing.
   const bool team_live = team < J.teams;
@@ -567,20 +576,45 @@ __global__ __launch_bounds__(WG) void gemv_team(TeamSet ts, const float *__restr
 #pragma unroll
     for (int it = 0; it < NBUF - 1 && it < ITERS; it++) load(buf[it], r_begin + it * R);
   };
-  // Activations of the lane's units, loaded once. The first rows' weights
-  // go out before them: the weights come from HBM, the activations from L2.
+  // Activations of the lane's units, loaded once. With an int8 x already
+  // in memory the first rows' weights go out before it (the weights come
+  // from HBM, x from L2); x that the kernel quantizes or stages through LDS
+  // goes out first, so the waits for it let the weight loads stay in flight
+  // (loads complete in order).
   if constexpr (PRO == 2) {
     static_assert(TW == 1 && PL == 1 && TT == 1, "workgroup prologue: one-wave teams, one unit per lane");
     __shared__ uint4 pq[64][4];
     __shared__ int ps[64][4];
     __shared__ float pd[16];
+    float v[16];
+    prologue_wg_load<F>(xf, U, v);
     first_loads();
-    xi[0][0] = prologue_xi_wg<F>(xf, U, uid[0], pq, ps, pd);
+    xi[0][0] = prologue_wg_quant<F>(v, U, uid[0], pq, ps, pd);
+  } else if constexpr (PRO == 3) {
+    // int8 x staged once per workgroup in LDS (one-wave teams: every wave
+    // of the workgroup reads all of it): one load per thread instead of
+    // six per lane.
+    static_assert(TW == 1 && PL == 1 && TT == 1, "workgroup x staging: one-wave teams, one unit per lane");
+    __shared__ uint4 sq[WG];
+    __shared__ int32_t ss[WG];
+    __shared__ float sd[WG / 16];
+    const uint32_t t = threadIdx.x;
+    const bool lq = t < n_in / 16, ld = t < n_in / 256;  // n_in <= 64 * 64 (one-wave teams)
+    const uint4 vq = lq ? ldx16(qx + 16 * (size_t)t) : make_uint4(0, 0, 0, 0);
+    const int32_t vs = lq ? s16[t] : 0;
+    const float vd = ld ? dx[t] : 0.f;
+    first_loads();
+    if (lq) sq[t] = vq, ss[t] = vs;
+    if (ld) sd[t] = vd;
+    lds_barrier();
+    xi[0][0] = F::loadxi(reinterpret_cast<const int8_t *>(sq), sd, ss, uid[0]);
   } else if constexpr (PRO == 1) {
-    // The weights go out first, then each wave quantizes its lanes' x.
+    float v[PL][4][16];
+#pragma unroll
+    for (int p = 0; p < PL; p++) prologue_load<F>(xf, uid[p], uok[p], v[p]);
     first_loads();
 #pragma unroll
-    for (int p = 0; p < PL; p++) xi[p][0] = prologue_xi<F>(xf, uid[p], uok[p]);
+    for (int p = 0; p < PL; p++) xi[p][0] = prologue_quant<F>(v[p]);
   } else if constexpr (!F32) {
     first_loads();
 #pragma unroll
@@ -662,6 +696,7 @@ void launch_iters(mdma_ctx *ctx, TeamSet ts, int tw, int pl, const float *xf, co
   hipEvent_t t0 = ctx->time_start, t1 = ctx->time_stop;
   ctx->time_start = ctx->time_stop = nullptr;
   constexpr bool PRO_OK = !F32 && TT == 1 && !std::is_same<F, Q8G>::value;
+  constexpr bool STAGE_OK = !F32 && TT == 1 && GATED;
 #define MDMA_TEAM_GO(TW_, PL_, PRO_)                                                                              \
   do {                                                                                                            \
     if (t0 || t1)                                                                                                 \
@@ -671,14 +706,16 @@ void launch_iters(mdma_ctx *ctx, TeamSet ts, int tw, int pl, const float *xf, co
       gemv_team<F, F32, R, ITERS, TW_, PL_, TT, GATED, PRO_><<<grid, block, 0, ctx->stream>>>(ts, xf, qx, dx,   \
                                                                                               s16, T, yg);      \
   } while (0)
-#define MDMA_TEAM_LAUNCH(TW_, PL_)                             \
-  do {                                                         \
-    if constexpr (PRO_OK) {                                    \
-      if (ts.pro) MDMA_TEAM_GO(TW_, PL_, TW_ == 1 ? 2 : 1);    \
-      else MDMA_TEAM_GO(TW_, PL_, 0);                          \
-    } else {                                                   \
-      MDMA_TEAM_GO(TW_, PL_, 0);                               \
-    }                                                          \
+#define MDMA_TEAM_LAUNCH(TW_, PL_)                                      \
+  do {                                                                  \
+    if constexpr (PRO_OK) {                                             \
+      if (ts.pro) {                                                     \
+        MDMA_TEAM_GO(TW_, PL_, TW_ == 1 ? 2 : 1);                       \
+        break;                                                          \
+      }                                                                 \
+    }                                                                   \
+    if constexpr (STAGE_OK && TW_ == 1 && PL_ == 1) MDMA_TEAM_GO(TW_, PL_, 3); \
+    else MDMA_TEAM_GO(TW_, PL_, 0);                                     \
   } while (0)
   if (tw == 1) MDMA_TEAM_LAUNCH(1, 1);
   else if (tw == 2) MDMA_TEAM_LAUNCH(2, 1);
@@ -708,6 +745,11 @@ void launch_fmt(mdma_ctx *ctx, TeamSet ts, const float *xf, const int8_t *qx, co
   const uint64_t groups = ((rows + want - 1) / want + R - 1) / R;
   if constexpr (TT > 1) {
     launch_iters<F, F32, R, 4, TT, GATED>(ctx, ts, tw, pl, xf, qx, dx, s16, T, yg);
+  } else if (GATED && !F32 && !ts.pro && tw == 1) {
+    // The fused gate/up reading a quantized x: one row of gate and up per
+    // wave (the most waves, each with all its loads issued at once), x
+    // staged through LDS once per workgroup.
+    launch_iters<F, F32, R, 1, TT, GATED>(ctx, ts, tw, pl, xf, qx, dx, s16, T, yg);
   } else {
     if (groups <= 1) launch_iters<F, F32, R, 1, TT, GATED>(ctx, ts, tw, pl, xf, qx, dx, s16, T, yg);
     else if (groups <= 2) launch_iters<F, F32, R, 2, TT, GATED>(ctx, ts, tw, pl, xf, qx, dx, s16, T, yg);
