@@ -239,19 +239,21 @@ static uint32_t *zeroed_counters(mdma_ctx *ctx, uint32_t *&buf, uint64_t &cap_, 
   cap_ = 0;
   void *p = nullptr;
   hip_check(hipMalloc(&p, cap * 4), "counter alloc");
-  hip_check(hipMemset(p, 0, cap * 4), "counter clear");
+  // On the context's stream (non-blocking: it does not wait for work on the
+  // null stream), so the launches that use the counters follow the clear.
+  hip_check(hipMemsetAsync(p, 0, cap * 4, ctx->stream), "counter clear");
   buf = static_cast<uint32_t *>(p);
   cap_ = cap;
   return buf;
 }
 
 uint32_t *attn_counters(mdma_ctx *ctx, uint64_t n) {
-  return zeroed_counters(ctx, ctx->attn_cnt, ctx->attn_cnt_cap, n, "attention counter growth");
+  return zeroed_counters(ctx, ctx->attn_cnt, ctx->attn_cnt_cap, n * CNT_STRIDE, "attention counter growth");
 }
 
 uint32_t *gemm_counters(mdma_ctx *ctx, uint64_t n) {
-  if (ctx->capturing && n > ctx->gemm_cnt_cap) return nullptr;
-  return zeroed_counters(ctx, ctx->gemm_cnt, ctx->gemm_cnt_cap, n, "GEMM counter growth");
+  if (ctx->capturing && n * CNT_STRIDE > ctx->gemm_cnt_cap) return nullptr;
+  return zeroed_counters(ctx, ctx->gemm_cnt, ctx->gemm_cnt_cap, n * CNT_STRIDE, "GEMM counter growth");
 }
 
 void q8_invalidate_range(mdma_ctx *ctx, const void *p, uint64_t bytes) {

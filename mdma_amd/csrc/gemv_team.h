@@ -696,7 +696,7 @@ void launch_iters(mdma_ctx *ctx, TeamSet ts, int tw, int pl, const float *xf, co
   hipEvent_t t0 = ctx->time_start, t1 = ctx->time_stop;
   ctx->time_start = ctx->time_stop = nullptr;
   constexpr bool PRO_OK = !F32 && TT == 1 && !std::is_same<F, Q8G>::value;
-  constexpr bool STAGE_OK = !F32 && TT == 1 && GATED;
+  constexpr bool STAGE_OK = !F32 && TT == 1 && GATED && ITERS == 1;
 #define MDMA_TEAM_GO(TW_, PL_, PRO_)                                                                              \
   do {                                                                                                            \
     if (t0 || t1)                                                                                                 \

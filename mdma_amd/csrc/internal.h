@@ -113,11 +113,17 @@ char *q8_buffer(mdma_ctx *ctx, uint64_t bytes);
 // Device space for `chunks` partial results of the two-pass argmax (grown
 // like scratch).
 char *argmax_parts(mdma_ctx *ctx, uint64_t chunks);
-// At least n zeroed arrival counters for split attention; each launch leaves
-// the counters it used at zero.
+// Arrival counters that workgroups of one launch update concurrently sit one
+// per CNT_STRIDE entries (256 bytes): device-scope atomics on one cache line
+// are served one at a time, so counters sharing a line would serialize the
+// arrivals of unrelated workgroups.
+constexpr uint32_t CNT_STRIDE = 64;
+// Zeroed arrival counters for split attention, n counters at CNT_STRIDE
+// apart; each launch leaves the counters it used at zero.
 uint32_t *attn_counters(mdma_ctx *ctx, uint64_t n);
-// Split-K GEMM arrival counters, zeroed at allocation (each launch leaves them
-// zero); nullptr when n exceeds what is allocated during stream capture.
+// Split-K GEMM arrival counters (n at CNT_STRIDE apart), zeroed at allocation
+// (each launch leaves them zero); nullptr when n exceeds what is allocated
+// during stream capture.
 uint32_t *gemm_counters(mdma_ctx *ctx, uint64_t n);
 // Forget the cached int8 activations: every entry point that writes device
 // memory calls this (a qmatmul only when its output overlaps the cached x).

@@ -690,7 +690,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (tid == 0) {
-      uint32_t *c = cnt + (size_t)i * n_kv_heads + kvh;
+      uint32_t *c = cnt + ((size_t)i * n_kv_heads + kvh) * CNT_STRIDE;
       const uint32_t prev = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       last = prev == live - 1;
       // every run of this (query, KV head) has arrived: ready for the next call
