@@ -25,7 +25,9 @@
 //            against m repeated in every byte;
 //      Q6_K  d*sum(sc*isum) with q - 32 fed as signed bytes;
 //      Q8_0  sum(d*isum) per 32-column block;
-//    then times the token's per-256 activation scale, accumulated in f64.
+//    then times the token's per-256 activation scale, accumulated in f32
+//    (a handful of registers per result instead of twice that: the kernel's
+//    speed is set by how many waves its registers let a SIMD hold).
 //  - TW waves split a tile's columns in fixed chunks whose sums meet in LDS
 //    (wave 0 adds them in a fixed order and stores, so results do not
 //    depend on TW or on what else shares the launch).
@@ -104,7 +106,7 @@ struct BQ4 {
       x.hi[p] = xr(col + 32);
     }
   }
-  __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, double *c) {
+  __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, float *c) {
     const uint32_t n = l & 15, g = l >> 4;
     const uint4 h = *reinterpret_cast<const uint4 *>(lds + 16 * RS + 16 * n);
     constexpr uint64_t M4 = 0x0F0F0F0F0F0F0F0Full, ONES = 0x0101010101010101ull;
@@ -123,9 +125,9 @@ struct BQ4 {
       dm = mma(x.lo[p], (uint64_t)ma * ONES, dm);
       dm = mma(x.hi[p], (uint64_t)mb * ONES, dm);
     }
-    const double d = (double)h2f(h.x), dmin = (double)h2f(h.x >> 16);
+    const float d = h2f(h.x), dmin = h2f(h.x >> 16);
 #pragma unroll
-    for (int j = 0; j < 4; j++) c[j] = d * (double)ai[j] - dmin * (double)dm[j];
+    for (int j = 0; j < 4; j++) c[j] = d * (float)ai[j] - dmin * (float)dm[j];
   }
 };
 
@@ -187,7 +189,7 @@ struct BQ6 {
 #pragma unroll
       for (int r = 0; r < 4; r++) x.q[v][r] = xr(col(4 * b + 2 * v + (g >> 1), r) + 8 * (g & 1));
   }
-  __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, double *c) {
+  __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, float *c) {
     const uint32_t n = l & 15, g = l >> 4;
     const uint4 sc4 = *reinterpret_cast<const uint4 *>(lds + 16 * RS + 16 * n);
     const uint32_t scw[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
@@ -214,9 +216,9 @@ struct BQ6 {
         for (int j = 0; j < 4; j++) ai[j] += __mul24(s0, d0[j]) + __mul24(s1, d1[j]);
       }
     }
-    const double d = (double)*reinterpret_cast<const float *>(lds + 16 * RS + 256 + 4 * n);
+    const float d = *reinterpret_cast<const float *>(lds + 16 * RS + 256 + 4 * n);
 #pragma unroll
-    for (int j = 0; j < 4; j++) c[j] = d * (double)ai[j];
+    for (int j = 0; j < 4; j++) c[j] = d * (float)ai[j];
   }
 };
 
@@ -257,20 +259,20 @@ struct BQ8 {
 #pragma unroll
     for (int i = 0; i < 8; i++) x.q[i] = xr(256 * b + 32 * i + 8 * g);
   }
-  __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, double *c) {
+  __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, float *c) {
     const uint32_t n = l & 15, g = l >> 4;
     const uint4 d4 = *reinterpret_cast<const uint4 *>(lds + 16 * RS + 16 * n);
     const uint32_t dw[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
-    for (int j = 0; j < 4; j++) c[j] = 0.0;
+    for (int j = 0; j < 4; j++) c[j] = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const uint64_t w = *reinterpret_cast<const uint64_t *>(lds + n * RS + 32 * i + 8 * g);
       const v4i z = {};
       const v4i dq = mma(x.q[i], w, z);
-      const double d = (double)h2f(dw[i >> 1] >> (16 * (i & 1)));
+      const float d = h2f(dw[i >> 1] >> (16 * (i & 1)));
 #pragma unroll
-      for (int j = 0; j < 4; j++) c[j] = fma(d, (double)dq[j], c[j]);
+      for (int j = 0; j < 4; j++) c[j] = fmaf(d, (float)dq[j], c[j]);
     }
   }
 };
@@ -298,7 +300,7 @@ __global__ __launch_bounds__(64 * TW) void gemv_batch(BatchSet bs, const int8_t 
                                                       const float *__restrict__ dx, uint32_t T,
                                                       float *__restrict__ ygated) {
   constexpr int NR = GATED ? 2 : 1;
-  __shared__ double red[TW > 1 ? NCHMAX : 1][NR][4][64];
+  __shared__ float red[TW > 1 ? NCHMAX : 1][NR][4][64];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   uint32_t tile = blockIdx.x;
   int ji = 0;
@@ -330,7 +332,7 @@ __global__ __launch_bounds__(64 * TW) void gemv_batch(BatchSet bs, const int8_t 
   uint32_t tj[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; j++) tj[j] = 4 * (lane >> 4) + j;
-  double acc[NR][NJ], tot[NR][NJ];
+  float acc[NR][NJ], tot[NR][NJ];
   // A block's loads in flight: the weights (to be staged) and the lane's x.
   struct Slot {
     typename F::Raw w[NR];
@@ -354,10 +356,10 @@ __global__ __launch_bounds__(64 * TW) void gemv_batch(BatchSet bs, const int8_t 
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
     for (int r = 0; r < NR; r++) {
-      double c[NJ];
+      float c[NJ];
       F::compute(stage[wave][r], sl.x, lane, c);
 #pragma unroll
-      for (int j = 0; j < NJ; j++) acc[r][j] = fma((double)sl.s[j], c[j], acc[r][j]);
+      for (int j = 0; j < NJ; j++) acc[r][j] = fmaf(sl.s[j], c[j], acc[r][j]);
     }
   };
   // The wave's chunks and their blocks.
@@ -384,25 +386,20 @@ __global__ __launch_bounds__(64 * TW) void gemv_batch(BatchSet bs, const int8_t 
   for (int r = 0; r < NR; r++)
 #pragma unroll
     for (int j = 0; j < NJ; j++) acc[r][j] = tot[r][j] = 0.0;
-  // Three slots in rotation: blocks b+1 and b+2 are in flight while block
-  // b is computed (loads clamped to the wave's last block: in bounds, fixed
-  // wait counts).
+  // Two slots in rotation: block b+1 is in flight while block b is computed
+  // (loads clamped to the wave's last block: in bounds, fixed wait counts).
+  // A third slot costs registers that would otherwise hold another wave.
   if (b0 < b1) {
-    Slot s0, s1, s2;
+    Slot s0, s1;
     fill(s0, b0);
-    fill(s1, min(b0 + 1, b1 - 1));
-    for (uint32_t b = b0; b < b1; b += 3) {
-      fill(s2, min(b + 2, b1 - 1));
+    for (uint32_t b = b0; b < b1; b += 2) {
+      fill(s1, min(b + 1, b1 - 1));
       use(s0);
       chunk_done(b);
       if (b + 1 >= b1) break;
-      fill(s0, min(b + 3, b1 - 1));
+      fill(s0, min(b + 2, b1 - 1));
       use(s1);
       chunk_done(b + 1);
-      if (b + 2 >= b1) break;
-      fill(s1, min(b + 4, b1 - 1));
-      use(s2);
-      chunk_done(b + 2);
     }
   }
   if constexpr (TW > 1) {
@@ -451,15 +448,15 @@ void launch_tw(mdma_ctx *ctx, const BatchSet &bs, uint32_t tiles, bool gated, co
 template <class F>
 void launch_fmt(mdma_ctx *ctx, const BatchSet &bs, uint32_t tiles, bool gated, const int8_t *qx, const float *dx,
                 uint32_t T, float *yg) {
-  // Waves per tile: enough for about 8 waves per CU, at most one per chunk.
+  // Waves per tile: enough for about 8 waves per CU, at most one per chunk
+  // and at most 4 (longer chains per wave beat more, shorter ones here).
   const uint32_t nb = bs.n_in / 256, nch = nb < NCHMAX ? nb : NCHMAX;
   uint32_t tw = 1;
-  while (tw < 8 && 2 * tw <= nch && (uint64_t)tiles * tw < (uint64_t)ctx->cu_count * 8) tw *= 2;
+  while (tw < 4 && 2 * tw <= nch && (uint64_t)tiles * tw < (uint64_t)ctx->cu_count * 8) tw *= 2;
   switch (tw) {
     case 1: launch_tw<F, 1>(ctx, bs, tiles, gated, qx, dx, T, yg); break;
     case 2: launch_tw<F, 2>(ctx, bs, tiles, gated, qx, dx, T, yg); break;
-    case 4: launch_tw<F, 4>(ctx, bs, tiles, gated, qx, dx, T, yg); break;
-    default: launch_tw<F, 8>(ctx, bs, tiles, gated, qx, dx, T, yg); break;
+    default: launch_tw<F, 4>(ctx, bs, tiles, gated, qx, dx, T, yg); break;
   }
 }
 
