@@ -630,16 +630,13 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const float *__restri
   int qi[4], sum = 0;
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    float r = roundf(v[k] * inv);
-    r = fminf(fmaxf(r, -127.f), 127.f);
-    qi[k] = (int)r;
+    qi[k] = q8_round(v[k] * inv);
     sum += qi[k];
   }
   sum += __shfl_xor(sum, 1, 64);  // 16 values = 4 lanes
   sum += __shfl_xor(sum, 2, 64);
   if (!live) return;
-  *reinterpret_cast<uint32_t *>(q + base) = (uint32_t)(qi[0] & 0xff) | ((uint32_t)(qi[1] & 0xff) << 8) |
-                                            ((uint32_t)(qi[2] & 0xff) << 16) | ((uint32_t)(qi[3] & 0xff) << 24);
+  *reinterpret_cast<uint32_t *>(q + base) = pack4_i8(qi[0], qi[1], qi[2], qi[3]);
   const int lane = threadIdx.x & 63;
   if ((lane & 3) == 0) s16[base / 16] = sum;
   if ((lane & (LPG - 1)) == 0) d[base / G] = amax / 127.0f;

@@ -340,15 +340,14 @@ __device__ typename F::XI prologue_quant(const float (&v)[4][16]) {
   int sums[4];
 #pragma unroll
   for (int c = 0; c < 4; c++) {
-    uint32_t w4[4] = {0u, 0u, 0u, 0u};
+    uint32_t w4[4];
     int sm = 0;
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
-      float r = roundf(v[c][k] * inv);
-      r = fminf(fmaxf(r, -127.f), 127.f);
-      const int qi = (int)r;
-      sm += qi;
-      w4[k >> 2] |= (uint32_t)(qi & 0xff) << (8 * (k & 3));
+    for (int k = 0; k < 16; k += 4) {
+      const int q0 = q8_round(v[c][k] * inv), q1 = q8_round(v[c][k + 1] * inv);
+      const int q2 = q8_round(v[c][k + 2] * inv), q3 = q8_round(v[c][k + 3] * inv);
+      sm += (q0 + q1) + (q2 + q3);
+      w4[k >> 2] = pack4_i8(q0, q1, q2, q3);
     }
     q[c] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
     sums[c] = sm;
@@ -389,15 +388,14 @@ __device__ typename F::XI prologue_wg_quant(const float (&v)[16], uint32_t U, ui
   amax = fmaxf(amax, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, amax), 0x128, 0xF,
                                                                           0xF, false)));  // row_ror:8
   const float inv = amax == 0.f ? 0.f : 127.0f / amax;
-  uint32_t w4[4] = {0u, 0u, 0u, 0u};
+  uint32_t w4[4];
   int sm = 0;
 #pragma unroll
-  for (int k = 0; k < 16; k++) {
-    float r = roundf(v[k] * inv);
-    r = fminf(fmaxf(r, -127.f), 127.f);
-    const int qi = (int)r;
-    sm += qi;
-    w4[k >> 2] |= (uint32_t)(qi & 0xff) << (8 * (k & 3));
+  for (int k = 0; k < 16; k += 4) {
+    const int q0 = q8_round(v[k] * inv), q1 = q8_round(v[k + 1] * inv);
+    const int q2 = q8_round(v[k + 2] * inv), q3 = q8_round(v[k + 3] * inv);
+    sm += (q0 + q1) + (q2 + q3);
+    w4[k >> 2] = pack4_i8(q0, q1, q2, q3);
   }
   if (live) {
     lq[qu][c] = make_uint4(w4[0], w4[1], w4[2], w4[3]);

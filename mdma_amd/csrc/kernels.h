@@ -34,6 +34,25 @@ __device__ __forceinline__ uint32_t ldu16(const uint8_t *p) {
 // 2-byte aligned inside a row).
 __device__ __forceinline__ uint32_t ld2x16(const uint8_t *p) { return ldu16(p) | (ldu16(p + 2) << 16); }
 
+// The int8 of an activation already scaled by 127/amax: round half away from
+// zero, clamped to [-127, 127] (a NaN gives -127, as fminf(fmaxf(NaN, -127),
+// 127) does). trunc(r + copysign(0.5 - 2^-25, r)) equals roundf(r) for every
+// float |r| < 2^22: a tie k + 0.5 sums to k + 1 - 2^-25, which rounds to
+// k + 1; below a tie the sum stays more than half an ulp under k + 1; above
+// it the sum is at least k + 1. (Adding 0.5 itself fails at 0.5 - 2^-25,
+// whose sum rounds up to 1.) Five instructions instead of roundf's seven
+// plus the clamp.
+__device__ __forceinline__ int q8_round(float r) {
+  const float t = r + __builtin_copysignf(0x1.fffffep-2f, r);
+  return (int)fminf(fmaxf(t, -127.f), 127.f);
+}
+// Bytes 0 of four ints packed into one dword (q0 lowest).
+__device__ __forceinline__ uint32_t pack4_i8(int q0, int q1, int q2, int q3) {
+  const uint32_t lo = __builtin_amdgcn_perm((uint32_t)q1, (uint32_t)q0, 0x0c0c0400u);
+  const uint32_t hi = __builtin_amdgcn_perm((uint32_t)q3, (uint32_t)q2, 0x04000c0cu);
+  return lo | hi;
+}
+
 // Wave-wide sum through DPP lane moves (no LDS round trips): xor 1, xor 2,
 // half-row mirror, row mirror (16-lane sums in every lane), then row
 // broadcasts 15 and 31. The total is valid in lane 63 only.

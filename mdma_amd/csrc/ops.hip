@@ -212,15 +212,12 @@ __global__ __launch_bounds__(1024) void rmsnorm_row_kernel(const float *__restri
       int qi[4], sm = 0;
 #pragma unroll
       for (int k = 0; k < 4; k++) {
-        float rr = roundf(r[k] * inv);
-        rr = fminf(fmaxf(rr, -127.f), 127.f);
-        qi[k] = (int)rr;
+        qi[k] = q8_round(r[k] * inv);
         sm += qi[k];
       }
       sm += __shfl_xor(sm, 1, 64);
       sm += __shfl_xor(sm, 2, 64);
-      *reinterpret_cast<uint32_t *>(q + base + i) = (uint32_t)(qi[0] & 0xff) | ((uint32_t)(qi[1] & 0xff) << 8) |
-                                                    ((uint32_t)(qi[2] & 0xff) << 16) | ((uint32_t)(qi[3] & 0xff) << 24);
+      *reinterpret_cast<uint32_t *>(q + base + i) = pack4_i8(qi[0], qi[1], qi[2], qi[3]);
       if ((lane & 3) == 0) qs16[(base + i) / 16] = sm;
       if (lane == 0) qd[(base + i) / 256] = amax / 127.0f;
     }
@@ -759,9 +756,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
       __syncthreads();
       amax = fmaxf(fmaxf(gmax[0], gmax[1]), fmaxf(gmax[2], gmax[3]));
       const float inv = amax == 0.f ? 0.f : 127.0f / amax;
-      float r = roundf(out[k] * inv);
-      r = fminf(fmaxf(r, -127.f), 127.f);
-      const int qi = (int)r;
+      const int qi = q8_round(out[k] * inv);
       int sm = qi;
 #pragma unroll
       for (int off = 8; off >= 1; off >>= 1) sm += __shfl_xor(sm, off, 64);
