@@ -441,9 +441,18 @@ constexpr int nbuf() {
 // (multi-wave teams, whose waves hold different units), 2 = once per
 // workgroup in LDS (one-wave teams, whose waves all hold every unit).
 // 3 = the quantized-x buffers staged once per workgroup in LDS (one-wave
-// teams of the fused gate/up).
+// teams of the fused gate/up). 4 = f32 x quantized once per workgroup of
+// MDMA_PRO4_TEAMS multi-wave teams into LDS (rows of up to 16384 columns):
+// each team needs all of x, so sharing it divides the f32 reads of x and the
+// quantization work by the teams per workgroup.
+// Teams of a multi-wave workgroup quantizing x once for all of them (PRO 4).
+#ifndef MDMA_PRO4_TEAMS
+#define MDMA_PRO4_TEAMS 2
+#endif
+constexpr int team_wg(int pro, int tw) { return pro == 4 ? 64 * tw * MDMA_PRO4_TEAMS : WG; }
+
 template <class F, bool F32, int R, int ITERS, int TW, int PL, int TT, bool GATED, int PRO = 0>
-__global__ __launch_bounds__(WG) void gemv_team(TeamSet ts, const float *__restrict__ xf,
+__global__ __launch_bounds__(team_wg(PRO, TW)) void gemv_team(TeamSet ts, const float *__restrict__ xf,
                                                 const int8_t *__restrict__ qx, const float *__restrict__ dx,
                                                 const int32_t *__restrict__ s16, uint32_t T,
                                                 float *__restrict__ ygated) {
@@ -451,7 +460,7 @@ __global__ __launch_bounds__(WG) void gemv_team(TeamSet ts, const float *__restr
   // in the f32 mode; lane and wave partials are added in f64, so outputs
   // that cancel (|y| << sum |w*x|) keep their relative accuracy.
   using Acc = typename std::conditional<F32, double, float>::type;
-  constexpr int TPW = WG / 64 / TW;  // teams per workgroup
+  constexpr int TPW = team_wg(PRO, TW) / 64 / TW;  // teams per workgroup
   constexpr int NR = GATED ? 2 * R : R;
   constexpr int NBUF = nbuf<F32, TW>();
   // Multi-wave teams: each wave's per-row totals for the whole run, added
@@ -606,6 +615,57 @@ __global__ __launch_bounds__(WG) void gemv_team(TeamSet ts, const float *__restr
     if (ld) sd[t] = vd;
     lds_barrier();
     xi[0][0] = F::loadxi(reinterpret_cast<const int8_t *>(sq), sd, ss, uid[0]);
+  } else if constexpr (PRO == 4) {
+    static_assert(TW > 1 && PL == 1 && TT == 1, "workgroup-shared quantization: multi-wave teams, one unit per lane");
+    constexpr int NT = team_wg(4, TW);
+    constexpr int NP = (16384 / 16 + NT - 1) / NT;  // passes of 16-column chunks
+    __shared__ uint4 xq4[16384 / 16];
+    __shared__ int32_t xs4[16384 / 16];
+    __shared__ float xd4[16384 / 256];
+    // Chunk c = 16 columns; the 16 chunks of a 256-group sit on one DPP row
+    // of 16 lanes (NT is a multiple of 64).
+    const uint32_t nch = n_in / 16;
+    float v[NP][16];
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+      const uint32_t c = threadIdx.x + NT * p;
+#pragma unroll
+      for (int k = 0; k < 16; k += 4) {
+        const float4 xv = c < nch ? *reinterpret_cast<const float4 *>(xf + 16 * c + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        v[p][k] = xv.x, v[p][k + 1] = xv.y, v[p][k + 2] = xv.z, v[p][k + 3] = xv.w;
+      }
+    }
+    first_loads();
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+      const uint32_t c = threadIdx.x + NT * p;
+      float amax = 0.f;
+#pragma unroll
+      for (int k = 0; k < 16; k++) amax = fmaxf(amax, fabsf(v[p][k]));
+      amax = fmaxf(amax, __builtin_bit_cast(float, quad_perm_u32<0xB1>(__builtin_bit_cast(uint32_t, amax))));
+      amax = fmaxf(amax, __builtin_bit_cast(float, quad_perm_u32<0x4E>(__builtin_bit_cast(uint32_t, amax))));
+      amax = fmaxf(amax, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, amax), 0x124, 0xF,
+                                                                              0xF, false)));  // row_ror:4
+      amax = fmaxf(amax, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, amax), 0x128, 0xF,
+                                                                              0xF, false)));  // row_ror:8
+      const float inv = amax == 0.f ? 0.f : 127.0f / amax;
+      uint32_t w4[4];
+      int sm = 0;
+#pragma unroll
+      for (int k = 0; k < 16; k += 4) {
+        const int q0 = q8_round(v[p][k] * inv), q1 = q8_round(v[p][k + 1] * inv);
+        const int q2 = q8_round(v[p][k + 2] * inv), q3 = q8_round(v[p][k + 3] * inv);
+        sm += (q0 + q1) + (q2 + q3);
+        w4[k >> 2] = pack4_i8(q0, q1, q2, q3);
+      }
+      if (c < nch) {
+        xq4[c] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        xs4[c] = sm;
+        if ((c & 15) == 0) xd4[c >> 4] = amax / 127.0f;
+      }
+    }
+    lds_barrier();  // LDS only: the weight loads already issued stay in flight
+    xi[0][0] = F::loadxi(reinterpret_cast<const int8_t *>(xq4), xd4, xs4, uid[0]);
   } else if constexpr (PRO == 1) {
     float v[PL][4][16];
 #pragma unroll
@@ -687,13 +747,14 @@ void launch_iters(mdma_ctx *ctx, TeamSet ts, int tw, int pl, const float *xf, co
     ts.j[i].teams = (ts.j[i].n_out + ts.rpt - 1) / ts.rpt;
     teams += ts.j[i].teams;
   }
-  const int tpw = WG / 64 / tw;
-  const dim3 grid((uint32_t)((teams + tpw - 1) / tpw)), block(WG);
+  constexpr bool PRO_OK = !F32 && TT == 1 && !std::is_same<F, Q8G>::value;
+  const bool pro4 = PRO_OK && ts.pro && tw > 1 && pl == 1;
+  const int wg = pro4 ? 64 * tw * MDMA_PRO4_TEAMS : WG, tpw = wg / 64 / tw;
+  const dim3 grid((uint32_t)((teams + tpw - 1) / tpw)), block(wg);
   // With timing events set, the dispatch itself timestamps them (kernel-only
   // duration, as a profiler measures it); they apply to one launch.
   hipEvent_t t0 = ctx->time_start, t1 = ctx->time_stop;
   ctx->time_start = ctx->time_stop = nullptr;
-  constexpr bool PRO_OK = !F32 && TT == 1 && !std::is_same<F, Q8G>::value;
   constexpr bool STAGE_OK = !F32 && TT == 1 && GATED && ITERS == 1;
 #define MDMA_TEAM_GO(TW_, PL_, PRO_)                                                                              \
   do {                                                                                                            \
@@ -708,7 +769,8 @@ void launch_iters(mdma_ctx *ctx, TeamSet ts, int tw, int pl, const float *xf, co
   do {                                                                  \
     if constexpr (PRO_OK) {                                             \
       if (ts.pro) {                                                     \
-        MDMA_TEAM_GO(TW_, PL_, TW_ == 1 ? 2 : 1);                       \
+        if constexpr (TW_ > 1 && PL_ == 1) MDMA_TEAM_GO(TW_, PL_, 4);   \
+        else MDMA_TEAM_GO(TW_, PL_, TW_ == 1 ? 2 : 1);                  \
         break;                                                          \
       }                                                                 \
     }                                                                   \
@@ -743,6 +805,16 @@ void launch_fmt(mdma_ctx *ctx, TeamSet ts, const float *xf, const int8_t *qx, co
   const uint64_t groups = ((rows + want - 1) / want + R - 1) / R;
   if constexpr (TT > 1) {
     launch_iters<F, F32, R, 4, TT, GATED>(ctx, ts, tw, pl, xf, qx, dx, s16, T, yg);
+  } else if (!F32 && !std::is_same<F, Q8G>::value && ts.pro && tw > 1 && pl == 1) {
+    // x quantized once per workgroup of MDMA_PRO4_TEAMS teams: about one
+    // workgroup per CU.
+    const uint64_t per = (uint64_t)ctx->cu_count * MDMA_PRO4_TEAMS;
+    const uint64_t g4 = ((rows + per - 1) / per + R - 1) / R;
+    if (g4 <= 1) launch_iters<F, F32, R, 1, TT, GATED>(ctx, ts, tw, pl, xf, qx, dx, s16, T, yg);
+    else if (g4 <= 2) launch_iters<F, F32, R, 2, TT, GATED>(ctx, ts, tw, pl, xf, qx, dx, s16, T, yg);
+    else if (g4 <= 4) launch_iters<F, F32, R, 4, TT, GATED>(ctx, ts, tw, pl, xf, qx, dx, s16, T, yg);
+    else if (g4 <= 8) launch_iters<F, F32, R, 8, TT, GATED>(ctx, ts, tw, pl, xf, qx, dx, s16, T, yg);
+    else launch_iters<F, F32, R, 16, TT, GATED>(ctx, ts, tw, pl, xf, qx, dx, s16, T, yg);
   } else if (GATED && !F32 && !ts.pro && tw == 1) {
     // The fused gate/up reading a quantized x: one row of gate and up per
     // wave (the most waves, each with all its loads issued at once), x
