@@ -441,7 +441,7 @@ constexpr int nbuf() {
 // (multi-wave teams, whose waves hold different units), 2 = once per
 // workgroup in LDS (one-wave teams, whose waves all hold every unit).
 // 3 = the quantized-x buffers staged once per workgroup in LDS (one-wave
-// teams of the fused gate/up). 4 = f32 x quantized once per workgroup of
+// teams of the fused gate/up and of Q4_K). 4 = f32 x quantized once per workgroup of
 // MDMA_PRO4_TEAMS multi-wave teams into LDS (rows of up to 16384 columns):
 // each team needs all of x, so sharing it divides the f32 reads of x and the
 // quantization work by the teams per workgroup.
@@ -755,7 +755,9 @@ void launch_iters(mdma_ctx *ctx, TeamSet ts, int tw, int pl, const float *xf, co
   // duration, as a profiler measures it); they apply to one launch.
   hipEvent_t t0 = ctx->time_start, t1 = ctx->time_stop;
   ctx->time_start = ctx->time_stop = nullptr;
-  constexpr bool STAGE_OK = !F32 && TT == 1 && GATED && ITERS == 1;
+  // Staging x through LDS pays for the fused gate/up and for Q4_K rows; the
+  // Q6_K one-wave launches measured faster with per-lane loads.
+  constexpr bool STAGE_OK = !F32 && TT == 1 && ITERS == 1 && (GATED || std::is_same<F, Q4G>::value);
 #define MDMA_TEAM_GO(TW_, PL_, PRO_)                                                                              \
   do {                                                                                                            \
     if (t0 || t1)                                                                                                 \
