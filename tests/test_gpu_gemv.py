@@ -408,11 +408,14 @@ def test_attention_int8_activations_bit_exact(backend, n_q, kv_len):
 
 
 @pytest.mark.parametrize("dtype", [Q4K, Q6K])
-@pytest.mark.parametrize("k", [768, 2048, 4096, 8192, 14336])
-def test_one_token_in_kernel_quantization_bit_exact(backend, dtype, k):
+@pytest.mark.parametrize("k,rows", [(768, 48), (2048, 48), (4096, 48), (8192, 48), (14336, 48), (8192, 50),
+                                    (14336, 50), (14336, 4096)])
+def test_one_token_in_kernel_quantization_bit_exact(backend, dtype, k, rows):
     # One int8 token: the GEMV quantizes x itself; the result must be the
     # bits of the GEMV over separately quantized x (x cached by rmsnorm).
-    rows = 48
+    # Rows of more than 4096 columns run two multi-wave teams per workgroup
+    # sharing one quantization of x; 50 rows leave the last workgroup with a
+    # team past the end, 4096 rows are the down projection's shape.
     w = backend.upload_weight(synth.weight(dtype, rows, k, 41), dtype, (rows, k))
     x = synth.normal_f32(k, 42) * 3
     x[:256] = 0  # an all-zero group
