@@ -34,6 +34,7 @@ of the same step).
 """
 import argparse
 import ctypes as C
+import hashlib
 import json
 import os
 import sys
@@ -347,7 +348,8 @@ def e2e_decode(be, n_prompt=512, n_gen=256, batches=(1, 8), path="/tmp/mdma_benc
                             "decode_tok_s": round(B * len(dec) / dec.sum(), 1),
                             "decode_ms_per_step_p50": round(float(np.median(dec)) * 1e3, 3),
                             "decode_ms_per_step_p90": round(float(np.percentile(dec, 90)) * 1e3, 3),
-                            "weight_stream_GBps": round(out["weight_bytes"] / float(np.median(dec)) / 1e9, 1)}
+                            "weight_stream_GBps": round(out["weight_bytes"] / float(np.median(dec)) / 1e9, 1),
+                            "tokens_sha1": hashlib.sha1(np.ascontiguousarray(toks).tobytes()).hexdigest()[:16]}
         print(f"[bench] e2e batch {B}: {out[f'batch{B}']}", file=sys.stderr, flush=True)
         s.close()
     m.close()

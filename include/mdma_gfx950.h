@@ -117,6 +117,12 @@ int mdma_gfx950_set_buffer_budget(mdma_ctx *ctx, uint64_t weights, uint64_t kv, 
 int mdma_gfx950_buffer_usage(mdma_ctx *ctx, int pool, uint64_t *used, uint64_t *limit);
 /* Extra: select the decode GEMV activation mode (default MDMA_ACT_F32). */
 int mdma_gfx950_set_act_mode(mdma_ctx *ctx, int mode);
+/* Extra: in the int8 mode's one-token decode, fuse each layer's attention
+ * RMSNorm into the GEMVs around it (the down projection stores the residual
+ * stream and sums of squares, the QKV GEMV normalizes in its prologue).
+ * Default on; off runs the separate norm kernel (for A/B measurement and
+ * the parity test of the fused path). */
+int mdma_gfx950_set_norm_fusion(mdma_ctx *ctx, int on);
 /* Extra: the HIP stream (hipStream_t) every launch of this context uses. */
 void *mdma_gfx950_stream(mdma_ctx *ctx);
 

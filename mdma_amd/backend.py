@@ -70,7 +70,8 @@ _SIGS = {
     "device_label": [_P, C.c_char_p, C.c_size_t], "total_device_bytes": [_P],
     "available_device_bytes": [_P, _P], "supports_weight_dtype": [_P, _I32], "max_head_dim": [_P],
     "kv_elem_bytes": [_P], "join_execution": [_P], "set_buffer_budget": [_P, _U64, _U64, _U64],
-    "buffer_usage": [_P, C.c_int, _P, _P], "set_act_mode": [_P, C.c_int], "stream": [_P],
+    "buffer_usage": [_P, C.c_int, _P, _P], "set_act_mode": [_P, C.c_int],
+    "set_norm_fusion": [_P, C.c_int], "stream": [_P],
     "alloc": [_P, _U64, C.c_int, _P], "free": [_P], "buf_len": [_P], "buf_view": [_P, _U64, _U64, _P],
     "upload": [_P, _P, _U64, _P, _U64], "download": [_P, _P, _U64, _P, _U64],
     "copy": [_P, _P, _U64, _P, _U64, _U64], "upload_weight": [_P, _P, _U64, C.c_int, _I32, _U64, _U64, _P],
@@ -249,6 +250,9 @@ class Gfx950Backend:
 
     def set_act_mode(self, mode: int):
         _check(lib().mdma_gfx950_set_act_mode(self.ctx, mode))
+
+    def set_norm_fusion(self, on: bool):
+        _check(lib().mdma_gfx950_set_norm_fusion(self.ctx, int(bool(on))))
 
     def stream(self) -> int:
         return int(lib().mdma_gfx950_stream(self.ctx) or 0)

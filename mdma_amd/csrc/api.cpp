@@ -228,6 +228,21 @@ char *argmax_parts(mdma_ctx *ctx, uint64_t chunks) {
   return ctx->argmax_part;
 }
 
+double *ssq_parts(mdma_ctx *ctx, uint64_t n) {
+  if (n <= ctx->ssq_cap) return ctx->ssq;
+  no_capture(ctx, "norm partials growth");
+  const uint64_t cap = n < 4096 ? 4096 : n + n / 4;
+  hip_check(hipStreamSynchronize(ctx->stream), "norm partials grow sync");
+  if (ctx->ssq) hip_check(hipFree(ctx->ssq), "norm partials free");
+  ctx->ssq = nullptr;
+  ctx->ssq_cap = 0;
+  void *p = nullptr;
+  hip_check(hipMalloc(&p, cap * 8), "norm partials alloc");
+  ctx->ssq = static_cast<double *>(p);
+  ctx->ssq_cap = cap;
+  return ctx->ssq;
+}
+
 // A zeroed uint32 buffer of at least n entries (grown outside capture only).
 static uint32_t *zeroed_counters(mdma_ctx *ctx, uint32_t *&buf, uint64_t &cap_, uint64_t n, const char *what) {
   if (n <= cap_) return buf;
@@ -335,6 +350,7 @@ void mdma_gfx950_destroy(mdma_ctx *ctx) {
   if (ctx->argmax_part) (void)hipFree(ctx->argmax_part);
   if (ctx->attn_cnt) (void)hipFree(ctx->attn_cnt);
   if (ctx->gemm_cnt) (void)hipFree(ctx->gemm_cnt);
+  if (ctx->ssq) (void)hipFree(ctx->ssq);
   if (ctx->rope_tab) (void)hipFree(ctx->rope_tab);
   if (ctx->host_ids) (void)hipHostFree(ctx->host_ids);
   (void)hipStreamDestroy(ctx->stream);
@@ -408,6 +424,14 @@ int mdma_gfx950_set_act_mode(mdma_ctx *ctx, int mode) {
     if (mode != MDMA_ACT_F32 && mode != MDMA_ACT_I8) shape_fail("set_act_mode: unknown mode");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
     ctx->act_mode = mode;
+  });
+}
+
+int mdma_gfx950_set_norm_fusion(mdma_ctx *ctx, int on) {
+  return guarded([&] {
+    need(ctx, "set_norm_fusion");
+    std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    ctx->norm_fusion = on != 0;
   });
 }
 

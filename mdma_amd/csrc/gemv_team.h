@@ -420,6 +420,17 @@ struct TeamSet {
   int n;
   uint32_t n_in, rpt;  // shared row length; rows per team (a multiple of R)
   bool pro;            // one token, int8: x (f32) quantized in the prologue
+  // One token, the residual stream of a Llama layer: with res set, a plain
+  // launch stores y = res + W x and each workgroup the sum of squares of its
+  // rows of y (f32 squares added in f64) in ssq[workgroup].
+  const float *res;
+  double *ssq;
+  // One token, PRO 5: x = rmsnorm(nsum) * nw, the sum of squares of nsum
+  // being the n_part partials npart that its producer stored.
+  const float *nsum, *nw;
+  const double *npart;
+  uint32_t n_part;
+  float eps;
 };
 
 // Row groups in flight per wave (loads issued NBUF-1 groups ahead): three
@@ -441,7 +452,10 @@ constexpr int nbuf() {
 // (multi-wave teams, whose waves hold different units), 2 = once per
 // workgroup in LDS (one-wave teams, whose waves all hold every unit).
 // 3 = the quantized-x buffers staged once per workgroup in LDS (one-wave
-// teams of the fused gate/up and of Q4_K). 4 = f32 x quantized once per workgroup of
+// teams of the fused gate/up and of Q4_K). 5 = x computed as the rmsnorm of
+// the residual stream (TeamSet::nsum) and quantized once per workgroup in
+// LDS (one-wave teams; the norm fused into the GEMV that reads it).
+// 4 = f32 x quantized once per workgroup of
 // MDMA_PRO4_TEAMS multi-wave teams into LDS (rows of up to 16384 columns):
 // each team needs all of x, so sharing it divides the f32 reads of x and the
 // quantization work by the teams per workgroup.
@@ -511,6 +525,7 @@ __global__ __launch_bounds__(team_wg(PRO, TW)) void gemv_team(TeamSet ts, const 
       for (int p = 0; p < PL; p++) w[p][r] = F::load(rp, uid[p], U);
     }
   };
+  double ssq_lane = 0.0;  // residual mode: this lane's stored rows' squares
   auto consume = [&](const typename F::W(&w)[PL][NR], int it) {
     const uint32_t r0 = r_begin + it * R;
     Acc s[NR][TT];
@@ -572,7 +587,12 @@ __global__ __launch_bounds__(team_wg(PRO, TW)) void gemv_team(TeamSet ts, const 
             const float g = (float)tot[r][t], up = (float)tot[R + r][t];
             ygated[(size_t)t * n_out + row] = g / (1.0f + expf(-g)) * up;
           } else {
-            J.y[(size_t)t * n_out + row] = (float)tot[r][t];
+            float yv = (float)tot[r][t];
+            if (ts.res) {  // uniform; one token
+              yv = ts.res[row] + yv;
+              ssq_lane += (double)(yv * yv);
+            }
+            J.y[(size_t)t * n_out + row] = yv;
           }
         }
       }
@@ -596,6 +616,37 @@ __global__ __launch_bounds__(team_wg(PRO, TW)) void gemv_team(TeamSet ts, const 
     float v[16];
     prologue_wg_load<F>(xf, U, v);
     first_loads();
+    xi[0][0] = prologue_wg_quant<F>(v, U, uid[0], pq, ps, pd);
+  } else if constexpr (PRO == 5) {
+    // x = rmsnorm(nsum) * nw (the arithmetic of rmsnorm_row_kernel: f32
+    // squares added in f64, mean in f32, scale 1/sqrtf(mean + eps), x =
+    // (v * scale) * w), then quantized once per workgroup into LDS as PRO 2
+    // does. The sum of squares comes from the producer's per-workgroup f64
+    // partials: another order of the f64 additions moves the total by a
+    // few f64 ulps, far below the f32 rounding of the mean.
+    static_assert(TW == 1 && PL == 1 && TT == 1, "normalizing prologue: one-wave teams, one unit per lane");
+    __shared__ uint4 pq[64][4];
+    __shared__ int ps[64][4];
+    __shared__ float pd[16];
+    __shared__ double ptot[WG / 64];
+    float v[16], wn[16];
+    prologue_wg_load<F>(ts.nsum, U, v);
+    prologue_wg_load<F>(ts.nw, U, wn);
+    double pt = threadIdx.x < ts.n_part ? ts.npart[threadIdx.x] : 0.0;  // n_part <= WG
+    first_loads();
+    pt = wave_total63(pt);
+    if (lane == 63) ptot[wave] = pt;
+    lds_barrier();
+    double tot = 0.0;
+#pragma unroll
+    for (int k = 0; k < WG / 64; k++) tot += ptot[k];
+    const float mean_sq = (float)tot / (float)n_in;
+    const float scale = 1.0f / sqrtf(mean_sq + ts.eps);
+    {
+#pragma clang fp contract(off)
+#pragma unroll
+      for (int k = 0; k < 16; k++) v[k] = (v[k] * scale) * wn[k];
+    }
     xi[0][0] = prologue_wg_quant<F>(v, U, uid[0], pq, ps, pd);
   } else if constexpr (PRO == 3) {
     // int8 x staged once per workgroup in LDS (one-wave teams: every wave
@@ -719,8 +770,28 @@ __global__ __launch_bounds__(team_wg(PRO, TW)) void gemv_team(TeamSet ts, const 
           const float gf = (float)g, uf = (float)u;
           ygated[(size_t)t * n_out + row] = gf / (1.0f + expf(-gf)) * uf;
         } else {
-          J.y[(size_t)t * n_out + row] = (float)g;
+          float yv = (float)g;
+          if (ts.res) {  // uniform; one token
+            yv = ts.res[row] + yv;
+            ssq_lane += (double)(yv * yv);
+          }
+          J.y[(size_t)t * n_out + row] = yv;
         }
+      }
+    }
+  }
+  if constexpr (!GATED) {
+    if (ts.res) {
+      // The workgroup's sum of squares: each wave's lanes, then the waves in
+      // order (f32 squares added in f64, as the separate rmsnorm adds them).
+      __shared__ double ssq_w[team_wg(PRO, TW) / 64];
+      const double v = wave_total63(ssq_lane);
+      if (lane == 63) ssq_w[wave] = v;
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        double tsum = 0.0;
+        for (int k = 0; k < team_wg(PRO, TW) / 64; k++) tsum += ssq_w[k];
+        ts.ssq[blockIdx.x] = tsum;
       }
     }
   }
@@ -751,6 +822,7 @@ void launch_iters(mdma_ctx *ctx, TeamSet ts, int tw, int pl, const float *xf, co
   const bool pro4 = PRO_OK && ts.pro && tw > 1 && pl == 1;
   const int wg = pro4 ? 64 * tw * MDMA_PRO4_TEAMS : WG, tpw = wg / 64 / tw;
   const dim3 grid((uint32_t)((teams + tpw - 1) / tpw)), block(wg);
+  ctx->team_grid = grid.x;
   // With timing events set, the dispatch itself timestamps them (kernel-only
   // duration, as a profiler measures it); they apply to one launch.
   hipEvent_t t0 = ctx->time_start, t1 = ctx->time_stop;
@@ -758,6 +830,7 @@ void launch_iters(mdma_ctx *ctx, TeamSet ts, int tw, int pl, const float *xf, co
   // Staging x through LDS pays for the fused gate/up and for Q4_K rows; the
   // Q6_K one-wave launches measured faster with per-lane loads.
   constexpr bool STAGE_OK = !F32 && TT == 1 && ITERS == 1 && (GATED || std::is_same<F, Q4G>::value);
+  constexpr bool NORM_OK = !F32 && TT == 1 && !GATED && !std::is_same<F, Q8G>::value;
 #define MDMA_TEAM_GO(TW_, PL_, PRO_)                                                                              \
   do {                                                                                                            \
     if (t0 || t1)                                                                                                 \
@@ -776,6 +849,13 @@ void launch_iters(mdma_ctx *ctx, TeamSet ts, int tw, int pl, const float *xf, co
         break;                                                          \
       }                                                                 \
     }                                                                   \
+    if constexpr (NORM_OK && TW_ == 1 && PL_ == 1) {                    \
+      if (ts.nsum) {                                                    \
+        MDMA_TEAM_GO(TW_, PL_, 5);                                      \
+        break;                                                          \
+      }                                                                 \
+    }                                                                   \
+    if (ts.nsum) fail(MDMA_ERR_BACKEND, "normalizing GEMV: no variant for this shape"); \
     if constexpr (STAGE_OK && TW_ == 1 && PL_ == 1) MDMA_TEAM_GO(TW_, PL_, 3); \
     else MDMA_TEAM_GO(TW_, PL_, 0);                                     \
   } while (0)

@@ -72,6 +72,37 @@ bool launch_gemv_i8_x(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, bool gated
   return true;
 }
 
+uint32_t launch_gemv_i8_residual(mdma_ctx *ctx, const GemvJob &job, const float *x, const float *res) {
+  if (!team_layout_ok(&job, 1) || job.n_in % 256 || !job.y) return 0;
+  const int32_t dt = job.dtype;
+  // x quantized in the kernel's prologue unless its int8 form is cached
+  // (Q8_0 has no in-kernel form: its x is quantized separately).
+  const bool pro = dt != DT_Q8_0 && !q8_holds(ctx, x, job.n_in);
+  TeamNorm nm;
+  nm.res = res;
+  nm.ssq = ssq_parts(ctx, 65536);
+  ctx->team_grid = 0;
+  launch_gemv_team(ctx, MDMA_ACT_I8, &job, 1, false, x, 1, nullptr, pro, &nm);
+  if (ctx->team_grid > 65536) fail(MDMA_ERR_BACKEND, "residual GEMV: more workgroups than norm partials");
+  return ctx->team_grid;
+}
+
+bool launch_gemv_i8_normed(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *nsum, const float *nw,
+                           uint32_t n_part, float eps) {
+  if (!team_layout_ok(jobs, n_jobs) || !n_part || n_part > 256) return false;
+  const uint64_t n_in = jobs[0].n_in;
+  // One-wave teams of Q4_K / Q6_K rows (64-column units), whole 256-groups.
+  if ((jobs[0].dtype != DT_Q4_K && jobs[0].dtype != DT_Q6_K) || n_in % 256 || n_in / 64 > 64) return false;
+  TeamNorm nm;
+  nm.nsum = nsum;
+  nm.nw = nw;
+  nm.npart = ssq_parts(ctx, n_part);
+  nm.n_part = n_part;
+  nm.eps = eps;
+  launch_gemv_team(ctx, MDMA_ACT_I8, jobs, n_jobs, false, nsum, 1, nullptr, false, &nm);
+  return true;
+}
+
 bool team_layout_ok(const GemvJob *jobs, int n_jobs) {
   for (int i = 0; i < n_jobs; i++)
     if (jobs[i].layout != MDMA_LAYOUT_GFX950 || jobs[i].dtype != jobs[0].dtype || jobs[i].n_in != jobs[0].n_in)
@@ -82,18 +113,27 @@ bool team_layout_ok(const GemvJob *jobs, int n_jobs) {
 }
 
 void launch_gemv_team(mdma_ctx *ctx, int mode, const GemvJob *jobs, int n_jobs, bool gated, const float *x,
-                      uint64_t T, float *ygated, bool pro) {
+                      uint64_t T, float *ygated, bool pro, const TeamNorm *nm) {
   const uint64_t n_in = jobs[0].n_in;
   int8_t *qx = nullptr;
   float *dx = nullptr;
   int32_t *s16 = nullptr;
   const bool f32 = mode != MDMA_ACT_I8;
   const int32_t dt = jobs[0].dtype;
-  if (!f32 && !pro) quantize_into_scratch(ctx, x, T, n_in, &qx, &dx, &s16);
+  if (!f32 && !pro && !(nm && nm->nsum)) quantize_into_scratch(ctx, x, T, n_in, &qx, &dx, &s16);
   for (uint64_t t0 = 0; t0 < T; t0 += 8) {
     const uint32_t tn = (uint32_t)(T - t0 < 8 ? T - t0 : 8);
     TeamSet ts{};
     ts.pro = pro;
+    if (nm) {  // one token only (the callers check)
+      ts.res = nm->res;
+      ts.ssq = nm->ssq;
+      ts.nsum = nm->nsum;
+      ts.nw = nm->nw;
+      ts.npart = nm->npart;
+      ts.n_part = nm->n_part;
+      ts.eps = nm->eps;
+    }
     ts.n = gated ? 1 : n_jobs;  // gated: teams cover the gate rows and also read up
     ts.n_in = (uint32_t)n_in;
     for (int i = 0; i < (gated ? 2 : n_jobs); i++) {

@@ -68,6 +68,7 @@ struct mdma_ctx {
   std::recursive_mutex lock;
   mdma::Pool pools[3];
   int act_mode = MDMA_ACT_F32;
+  bool norm_fusion = true;  // one-token int8 decode: attention rmsnorm fused into the GEMVs around it
   std::string label;
   uint64_t total_bytes = 0;
   int cu_count = 0;
@@ -96,6 +97,9 @@ struct mdma_ctx {
   uint64_t attn_cnt_cap = 0;
   uint32_t *gemm_cnt = nullptr;  // split-K GEMM arrival counters (zero between launches)
   uint64_t gemm_cnt_cap = 0;
+  double *ssq = nullptr;  // per-workgroup sums of squares of a residual-stream GEMV (norm fusion)
+  uint64_t ssq_cap = 0;
+  uint32_t team_grid = 0;  // workgroups of the last row-team launch
 };
 
 struct mdma_graph {
@@ -174,8 +178,33 @@ bool gemv_batch_ok(const GemvJob *jobs, int n_jobs, uint64_t T);
 void launch_gemv_batch(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, bool gated, const float *x, uint64_t T,
                        float *ygated);
 // pro: one token in the int8 mode, x quantized by the GEMV's prologue.
+// The rmsnorm of a Llama layer's residual stream fused into the GEMVs on
+// either side of it (one token, int8 mode): res/ssq for the GEMV that
+// produces the stream (it stores y = res + W x and per-workgroup sums of
+// squares of y), nsum/nw/npart/n_part/eps for the GEMV that reads the norm
+// (its x = rmsnorm(nsum) * nw, quantized in its prologue).
+struct TeamNorm {
+  const float *res = nullptr;
+  double *ssq = nullptr;
+  const float *nsum = nullptr, *nw = nullptr;
+  const double *npart = nullptr;
+  uint32_t n_part = 0;
+  float eps = 0.f;
+};
 void launch_gemv_team(mdma_ctx *ctx, int mode, const GemvJob *jobs, int n_jobs, bool gated, const float *x,
-                      uint64_t T, float *ygated, bool pro = false);
+                      uint64_t T, float *ygated, bool pro = false, const TeamNorm *nm = nullptr);
+// Space for n per-workgroup sums of squares (grown outside capture).
+double *ssq_parts(mdma_ctx *ctx, uint64_t n);
+// One token, int8 mode: y = res + W x for one prepared weight, leaving the
+// workgroups' sums of squares of y in ssq_parts; returns how many (0: not
+// done, nothing launched).
+uint32_t launch_gemv_i8_residual(mdma_ctx *ctx, const GemvJob &job, const float *x, const float *res);
+// One token, int8 mode: the jobs (one-wave rows, whole 256-column groups)
+// over x = rmsnorm(nsum) * nw, the sum of squares of nsum being the n_part
+// partials in ssq_parts; false (nothing launched) when the shape does not
+// allow it.
+bool launch_gemv_i8_normed(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *nsum, const float *nw,
+                           uint32_t n_part, float eps);
 // The int8 activations of x [T, n_in] (per-256 f32 scales, per-16 sums) in
 // the context's activation buffer, quantized now unless it already holds
 // exactly this x.

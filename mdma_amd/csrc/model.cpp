@@ -398,16 +398,28 @@ void run_layers(mdma_session *s, uint64_t T, uint32_t pos, uint64_t seq, bool ba
     fresh = q8;
     return true;
   };
+  // One token per step (decode of one sequence): the attention rmsnorm of
+  // layers after the first is fused into the GEMVs around it. The previous
+  // layer's down projection stores the residual stream x + W act and
+  // per-workgroup sums of squares; the QKV GEMV normalizes x in its prologue.
+  // n_part > 0: x already holds the residual stream and the partials wait.
+  const bool fuse_norm = ctx->norm_fusion && fuse_q8 && T == 1 && !batched;
+  uint32_t n_part = 0;
   for (uint64_t i = 0; i < c.n_layers; i++) {
     const Layer &L = m->layers[i];
+    GemvJob qkv[3] = {L.wq.job(fp(s->q)), L.wk.job(fp(s->k)), L.wv.job(fp(s->v))};
+    bool qkv_done = false;
     if (i == 0) {
       fresh = norm(L.attn_norm, fp(x), nullptr, nullptr);
+    } else if (n_part) {
+      q8_invalidate(ctx);
+      qkv_done = launch_gemv_i8_normed(ctx, qkv, 3, fp(x), fp(L.attn_norm), n_part, c.rms_eps);
+      if (!qkv_done) fresh = norm(L.attn_norm, fp(x), nullptr, nullptr);
     } else {
       fresh = norm(L.attn_norm, fp(x), fp(s->proj), fp(x_alt));
       std::swap(x, x_alt);
     }
-    GemvJob qkv[3] = {L.wq.job(fp(s->q)), L.wk.job(fp(s->k)), L.wv.job(fp(s->v))};
-    gemv(ctx, qkv, 3, fp(s->normed), T, fresh);
+    if (!qkv_done) gemv(ctx, qkv, 3, fp(s->normed), T, fresh);
     // KvCache::rope_write (src/kv_cache.rs:212-244): rotate q, store rotated k and v.
     uint16_t *kb = reinterpret_cast<uint16_t *>(s->kc[i]->ptr), *vb = reinterpret_cast<uint16_t *>(s->vc[i]->ptr);
     if ((batched || T == 1) && decode_attend(batched ? kb : kb + seq * cache_stride,
@@ -428,13 +440,26 @@ void run_layers(mdma_session *s, uint64_t T, uint32_t pos, uint64_t seq, bool ba
     fresh = norm(L.ffn_norm, fp(x), fp(s->proj), fp(x_alt));
     std::swap(x, x_alt);
     gemv_gated(ctx, L.gate.job(fp(s->gate)), L.up.job(fp(s->up)), fp(s->normed), T, fp(s->act), fresh);
-    GemvJob dn = L.down.job(fp(s->proj));
-    gemv(ctx, &dn, 1, fp(s->act), T);
+    n_part = 0;
+    if (fuse_norm) {
+      // y = x + W act into the other residual buffer (the new stream).
+      q8_invalidate(ctx);
+      n_part = launch_gemv_i8_residual(ctx, L.down.job(fp(x_alt)), fp(s->act), fp(x));
+      if (n_part) std::swap(x, x_alt);
+    }
+    if (!n_part) {
+      GemvJob dn = L.down.job(fp(s->proj));
+      gemv(ctx, &dn, 1, fp(s->act), T);
+    }
   }
   // The head GEMV quantizes the final-normed rows itself when it needs
   // them (only the rows it reads, which may be a subset).
-  launch_rmsnorm(ctx, fp(m->output_norm), E, fp(x), fp(s->proj), fp(x_alt), fp(s->normed), T, c.rms_eps);
-  std::swap(x, x_alt);
+  if (n_part) {
+    launch_rmsnorm(ctx, fp(m->output_norm), E, fp(x), nullptr, nullptr, fp(s->normed), T, c.rms_eps);
+  } else {
+    launch_rmsnorm(ctx, fp(m->output_norm), E, fp(x), fp(s->proj), fp(x_alt), fp(s->normed), T, c.rms_eps);
+    std::swap(x, x_alt);
+  }
   // Keep s->x as the buffer holding the residual stream.
   if (x != s->x) std::swap(s->x, s->x_alt);
 }

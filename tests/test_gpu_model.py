@@ -119,6 +119,36 @@ def test_gqa_q4km_greedy_and_batched_decode_match_oracle(backend, gqa):
     m.close()
 
 
+def test_int8_decode_norm_fusion_matches_separate_norm(backend, gqa):
+    """One-token int8 decode fuses each later layer's attention RMSNorm into
+    the previous down projection (it stores x + W act and per-workgroup f64
+    sums of squares) and the QKV GEMV's prologue (it normalizes and quantizes
+    x in LDS). The logits must be those of the separate norm kernel: the same
+    f32 arithmetic, only the f64 additions of the squares in another order
+    (a few f64 ulps, far below the mean's f32 rounding)."""
+    backend.set_act_mode(ACT_I8)
+    p = synth.tokens(N_PROMPT, 2048, 2100)
+    runs = []
+    try:
+        m = Model(backend, gqa)
+        for fused in (True, False):
+            backend.set_norm_fusion(fused)
+            s = m.session(N_PROMPT + 16, 1, N_PROMPT)
+            logits = [s.prefill(p, 0)]
+            for k in range(12):
+                logits.append(s.forward(int(np.argmax(logits[-1])), N_PROMPT + k))
+            runs.append(np.stack(logits))
+            s.close()
+        m.close()
+    finally:
+        backend.set_norm_fusion(True)
+        backend.set_act_mode(ACT_F32)
+    fused, sep = runs
+    assert np.all(np.isfinite(fused))
+    np.testing.assert_allclose(fused, sep, rtol=1e-5, atol=1e-6)
+    assert np.array_equal(fused.argmax(axis=1), sep.argmax(axis=1))
+
+
 def test_int8_mode_decodes(backend, tiny):
     backend.set_act_mode(ACT_I8)
     try:
