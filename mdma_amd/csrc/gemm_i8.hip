@@ -47,10 +47,6 @@ __device__ __forceinline__ uint32_t q6_bytes(uint32_t a, uint32_t b, uint32_t h,
     default: return ((b >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u);
   }
 }
-__device__ __forceinline__ uint32_t q6_centred(uint32_t v) {
-  const uint32_t s = ~v & 0x20202020u;  // bytes below 32 become negative
-  return (v ^ 0x20202020u) | (s << 1) | (s << 2);
-}
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -206,8 +202,8 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
       const uint4 A = rw[0], B = rw[1], Q = rw[2];
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        const uint4 v = make_uint4(q6_centred(q6_bytes(A.x, B.x, Q.x, r)), q6_centred(q6_bytes(A.y, B.y, Q.y, r)),
-                                   q6_centred(q6_bytes(A.z, B.z, Q.z, r)), q6_centred(q6_bytes(A.w, B.w, Q.w, r)));
+        const uint4 v = make_uint4(q6_centre4(q6_bytes(A.x, B.x, Q.x, r)), q6_centre4(q6_bytes(A.y, B.y, Q.y, r)),
+                                   q6_centre4(q6_bytes(A.z, B.z, Q.z, r)), q6_centre4(q6_bytes(A.w, B.w, Q.w, r)));
         *reinterpret_cast<uint4 *>(&ws[r][row][16 * h]) = v;
       }
       if (tid < 128) {

@@ -49,7 +49,12 @@ constexpr uint32_t TROWS = 16;  // rows per tile
 // plane and the next block the other half.
 __device__ __forceinline__ uint64_t ldw8(const uint8_t *p) { return *reinterpret_cast<const uint64_t *>(p); }
 __device__ __forceinline__ uint32_t ldw4(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
-__device__ __forceinline__ uint32_t ldw2(const uint8_t *p) { return *reinterpret_cast<const uint16_t *>(p); }
+// A byte value (0..255) in all eight bytes: one byte permute (a multiply by
+// 0x01010101 is quarter rate).
+__device__ __forceinline__ uint64_t bytes8(int v) {
+  const uint64_t r = __builtin_amdgcn_perm(0u, (uint32_t)v, 0u);
+  return r | (r << 32);
+}
 __device__ __forceinline__ v4i mma(uint64_t x, uint64_t w, v4i c) {
   return __builtin_amdgcn_mfma_i32_16x16x32_i8((long)x, (long)w, c, 0, 0, 0);
 }
@@ -109,7 +114,7 @@ struct BQ4 {
   __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, float *c) {
     const uint32_t n = l & 15, g = l >> 4;
     const uint4 h = *reinterpret_cast<const uint4 *>(lds + 16 * RS + 16 * n);
-    constexpr uint64_t M4 = 0x0F0F0F0F0F0F0F0Full, ONES = 0x0101010101010101ull;
+    constexpr uint64_t M4 = 0x0F0F0F0F0F0F0F0Full;
     v4i ai = {}, dm = {};
 #pragma unroll
     for (int p = 0; p < 4; p++) {
@@ -122,8 +127,8 @@ struct BQ4 {
       // 24-bit multiplies (full rate): |isum| <= 15*127*32.
 #pragma unroll
       for (int j = 0; j < 4; j++) ai[j] += __mul24(sca, da[j]) + __mul24(scb, db[j]);
-      dm = mma(x.lo[p], (uint64_t)ma * ONES, dm);
-      dm = mma(x.hi[p], (uint64_t)mb * ONES, dm);
+      dm = mma(x.lo[p], bytes8(ma), dm);
+      dm = mma(x.hi[p], bytes8(mb), dm);
     }
     const float d = h2f(h.x), dmin = h2f(h.x >> 16);
 #pragma unroll
@@ -149,17 +154,13 @@ struct BQ6 {
       default: return ((b >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u);
     }
   }
-  // Bytes u6 (0..63) to the signed int8 u6 - 32.
-  __device__ static uint32_t centred(uint32_t v) {
-    const uint32_t s = ~v & 0x20202020u;
-    return (v ^ 0x20202020u) | (s << 1) | (s << 2);
-  }
   __device__ static uint32_t col(uint32_t u, int r) {
     return 256 * (u >> 2) + 128 * ((u >> 1) & 1) + 32 * r + 16 * (u & 1);
   }
   struct Raw {
     uint4 a, b, q, s;
-    uint32_t d;
+    uint32_t d;    // the f16 d of blocks 2(b/2) and 2(b/2)+1 (one aligned word)
+    uint32_t dsh;  // 16 * (b % 2): d's half
   };
   struct X {
     uint64_t q[2][4];  // [unit pair][quarter]
@@ -171,7 +172,12 @@ struct BQ6 {
     r.b = ld16(prow + 16 * (size_t)U + o);
     r.q = ld16(prow + 32 * (size_t)U + o);
     r.s = ld16(hrow + 48 * (size_t)U + 16 * (size_t)b);
-    r.d = ldw2(hrow + 52 * (size_t)U + 2 * (size_t)b);
+    // A 32-bit load: the f16 is taken out of it after the LDS round trip
+    // (a 16-bit load's value would be re-masked where the compiler chooses,
+    // possibly at the loop's latch, which then waits for the prefetch). The
+    // row's padding covers the word's second half for the last odd block.
+    r.d = ldw4(hrow + 52 * (size_t)U + 4 * (size_t)(b >> 1));
+    r.dsh = 16 * (b & 1);
   }
   __device__ static void lstore(const Raw &r, uint8_t *lds, uint32_t l) {
     uint8_t *p = lds + (l >> 2) * RS + 48 * (l & 3);
@@ -180,7 +186,8 @@ struct BQ6 {
     *reinterpret_cast<uint4 *>(p + 32) = r.q;
     if (l < 16) {
       *reinterpret_cast<uint4 *>(lds + 16 * RS + 16 * l) = r.s;
-      *reinterpret_cast<float *>(lds + 16 * RS + 256 + 4 * l) = h2f(r.d);
+      // d's word goes to LDS as loaded; its half is taken after the read back.
+      *reinterpret_cast<uint32_t *>(lds + 16 * RS + 256 + 4 * l) = r.d >> r.dsh;
     }
   }
   __device__ static void loadx(const XRow &xr, uint32_t b, uint32_t g, X &x) {
@@ -202,8 +209,8 @@ struct BQ6 {
       const uint64_t wq = *reinterpret_cast<const uint64_t *>(p + 32);
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        const uint32_t lo = centred(u6((uint32_t)wa, (uint32_t)wb, (uint32_t)wq, r));
-        const uint32_t hi = centred(u6((uint32_t)(wa >> 32), (uint32_t)(wb >> 32), (uint32_t)(wq >> 32), r));
+        const uint32_t lo = q6_centre4(u6((uint32_t)wa, (uint32_t)wb, (uint32_t)wq, r));
+        const uint32_t hi = q6_centre4(u6((uint32_t)(wa >> 32), (uint32_t)(wb >> 32), (uint32_t)(wq >> 32), r));
         const uint64_t wv = (uint64_t)lo | ((uint64_t)hi << 32);
         // Unit 2v: lanes g < 2; unit 2v+1: lanes g >= 2.
         const v4i z = {};
@@ -216,7 +223,7 @@ struct BQ6 {
         for (int j = 0; j < 4; j++) ai[j] += __mul24(s0, d0[j]) + __mul24(s1, d1[j]);
       }
     }
-    const float d = *reinterpret_cast<const float *>(lds + 16 * RS + 256 + 4 * n);
+    const float d = h2f((uint16_t)*reinterpret_cast<const uint32_t *>(lds + 16 * RS + 256 + 4 * n));
 #pragma unroll
     for (int j = 0; j < 4; j++) c[j] = d * (float)ai[j];
   }
@@ -295,7 +302,10 @@ struct BatchSet {
 // does not depend on TW (fused and separate calls, whatever their tile
 // counts, give identical bits).
 constexpr int NCHMAX = 8;
-template <class F, int TW, bool GATED>
+#ifndef MDMA_BATCH_NS
+#define MDMA_BATCH_NS 2
+#endif
+template <class F, int TW, bool GATED, int NS>
 __global__ __launch_bounds__(64 * TW) void gemv_batch(BatchSet bs, const int8_t *__restrict__ qx,
                                                       const float *__restrict__ dx, uint32_t T,
                                                       float *__restrict__ ygated) {
@@ -332,6 +342,12 @@ __global__ __launch_bounds__(64 * TW) void gemv_batch(BatchSet bs, const int8_t 
   uint32_t tj[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; j++) tj[j] = 4 * (lane >> 4) + j;
+  // Scale loads are unconditional (a token past T reads token T-1's scale;
+  // its results are never stored): a load under a branch leaves the
+  // compiler unsure how many loads are in flight, and it then waits for all.
+  uint32_t tj_c[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; j++) tj_c[j] = min(tj[j], T - 1);
   float acc[NR][NJ], tot[NR][NJ];
   // A block's loads in flight: the weights (to be staged) and the lane's x.
   struct Slot {
@@ -344,7 +360,7 @@ __global__ __launch_bounds__(64 * TW) void gemv_batch(BatchSet bs, const int8_t 
     for (int r = 0; r < NR; r++) F::gload(prow[r], hrow[r], U, b, lane, sl.w[r]);
     F::loadx(xr, b, g, sl.x);
 #pragma unroll
-    for (int j = 0; j < NJ; j++) sl.s[j] = tj[j] < T ? dx[(size_t)tj[j] * nb + b] : 0.f;
+    for (int j = 0; j < NJ; j++) sl.s[j] = dx[(size_t)tj_c[j] * nb + b];
   };
   // Stage the weights in the wave's LDS, read them back as operands. The
   // LDS-only waits order the stores before the reads (and the previous
@@ -386,20 +402,28 @@ __global__ __launch_bounds__(64 * TW) void gemv_batch(BatchSet bs, const int8_t 
   for (int r = 0; r < NR; r++)
 #pragma unroll
     for (int j = 0; j < NJ; j++) acc[r][j] = tot[r][j] = 0.0;
-  // Two slots in rotation: block b+1 is in flight while block b is computed
-  // (loads clamped to the wave's last block: in bounds, fixed wait counts).
-  // A third slot costs registers that would otherwise hold another wave.
+  // NS slots in rotation, each refilled right after its block is computed:
+  // while a block is computed the NS-1 blocks after it are in flight (loads
+  // clamped to the wave's last block: in bounds, fixed wait counts).
   if (b0 < b1) {
-    Slot s0, s1;
-    fill(s0, b0);
-    for (uint32_t b = b0; b < b1; b += 2) {
-      fill(s1, min(b + 1, b1 - 1));
-      use(s0);
-      chunk_done(b);
-      if (b + 1 >= b1) break;
-      fill(s0, min(b + 2, b1 - 1));
-      use(s1);
-      chunk_done(b + 1);
+    Slot sl[NS];
+#pragma unroll
+    for (int i = 0; i < NS; i++) {
+      fill(sl[i], min(b0 + i, b1 - 1));
+      __builtin_amdgcn_sched_barrier(0);  // slots issued in order (see below)
+    }
+    for (uint32_t b = b0; b < b1; b += NS) {
+#pragma unroll
+      for (int i = 0; i < NS; i++) {
+        use(sl[i]);
+        chunk_done(b + i);
+        if (b + i + 1 >= b1) break;
+        fill(sl[i], min(b + i + NS, b1 - 1));
+        // Keep the refill's loads here: sunk past the next block's compute
+        // they would be the newest in flight, and the in-order wait for the
+        // next block would then wait for them too.
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   }
   if constexpr (TW > 1) {
@@ -424,7 +448,7 @@ __global__ __launch_bounds__(64 * TW) void gemv_batch(BatchSet bs, const int8_t 
   }
 }
 
-template <class F, int TW>
+template <class F, int TW, int NS>
 void launch_tw(mdma_ctx *ctx, const BatchSet &bs, uint32_t tiles, bool gated, const int8_t *qx, const float *dx,
                uint32_t T, float *yg) {
   hipEvent_t t0 = ctx->time_start, t1 = ctx->time_stop;
@@ -432,15 +456,15 @@ void launch_tw(mdma_ctx *ctx, const BatchSet &bs, uint32_t tiles, bool gated, co
   const dim3 grid(tiles), block(64 * TW);
   if (gated) {
     if (t0 || t1)
-      hipExtLaunchKernelGGL(gemv_batch<F, TW, true>, grid, block, 0, ctx->stream, t0, t1, 0, bs, qx, dx, T, yg);
+      hipExtLaunchKernelGGL(gemv_batch<F, TW, true, NS>, grid, block, 0, ctx->stream, t0, t1, 0, bs, qx, dx, T, yg);
     else
-      gemv_batch<F, TW, true><<<grid, block, 0, ctx->stream>>>(bs, qx, dx, T, yg);
+      gemv_batch<F, TW, true, NS><<<grid, block, 0, ctx->stream>>>(bs, qx, dx, T, yg);
   } else {
     if (t0 || t1)
-      hipExtLaunchKernelGGL(gemv_batch<F, TW, false>, grid, block, 0, ctx->stream, t0, t1, 0, bs, qx, dx, T,
+      hipExtLaunchKernelGGL(gemv_batch<F, TW, false, NS>, grid, block, 0, ctx->stream, t0, t1, 0, bs, qx, dx, T,
                             yg);
     else
-      gemv_batch<F, TW, false><<<grid, block, 0, ctx->stream>>>(bs, qx, dx, T, yg);
+      gemv_batch<F, TW, false, NS><<<grid, block, 0, ctx->stream>>>(bs, qx, dx, T, yg);
   }
   hip_check(hipGetLastError(), "gemv batch launch");
 }
@@ -453,10 +477,12 @@ void launch_fmt(mdma_ctx *ctx, const BatchSet &bs, uint32_t tiles, bool gated, c
   const uint32_t nb = bs.n_in / 256, nch = nb < NCHMAX ? nb : NCHMAX;
   uint32_t tw = 1;
   while (tw < 4 && 2 * tw <= nch && (uint64_t)tiles * tw < (uint64_t)ctx->cu_count * 8) tw *= 2;
+  // Two slots per wave: three or four (all loads of a short run in flight)
+  // measured slower at every shape, the extra registers costing a wave.
   switch (tw) {
-    case 1: launch_tw<F, 1>(ctx, bs, tiles, gated, qx, dx, T, yg); break;
-    case 2: launch_tw<F, 2>(ctx, bs, tiles, gated, qx, dx, T, yg); break;
-    default: launch_tw<F, 4>(ctx, bs, tiles, gated, qx, dx, T, yg); break;
+    case 1: launch_tw<F, 1, MDMA_BATCH_NS>(ctx, bs, tiles, gated, qx, dx, T, yg); break;
+    case 2: launch_tw<F, 2, MDMA_BATCH_NS>(ctx, bs, tiles, gated, qx, dx, T, yg); break;
+    default: launch_tw<F, 4, MDMA_BATCH_NS>(ctx, bs, tiles, gated, qx, dx, T, yg); break;
   }
 }
 

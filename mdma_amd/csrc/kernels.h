@@ -34,6 +34,15 @@ __device__ __forceinline__ uint32_t ldu16(const uint8_t *p) {
 // 2-byte aligned inside a row).
 __device__ __forceinline__ uint32_t ld2x16(const uint8_t *p) { return ldu16(p) | (ldu16(p + 2) << 16); }
 
+// Four Q6_K values (bytes 0..63) as the signed int8 bytes v - 32. With bit 7
+// set first every byte is at least 0x80, so subtracting 0x20 per byte never
+// borrows from the next; clearing bit 7 again leaves (v - 32) mod 256. Three
+// full-rate operations (a sign-fill of bit 5 instead compiles to a
+// quarter-rate multiply by 6).
+__device__ __forceinline__ uint32_t q6_centre4(uint32_t v) {
+  return ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+}
+
 // The int8 of an activation already scaled by 127/amax: round half away from
 // zero, clamped to [-127, 127] (a NaN gives -127, as fminf(fmaxf(NaN, -127),
 // 127) does). trunc(r + copysign(0.5 - 2^-25, r)) equals roundf(r) for every
