@@ -485,6 +485,18 @@ __global__ __launch_bounds__(team_wg(PRO, TW)) void gemv_team(TeamSet ts, const 
   // Team -> job, branch-free: every field is read up front, so the
   // kernel-argument loads form one batch before the first weight load, and
   // every job field stays in SGPRs.
+  // Every kernel argument this variant reads, pinned in SGPRs before any
+  // other work: the scalar loads of the argument segment then go out
+  // together and are waited for once, instead of in a chain of round trips
+  // as each value's first use (some inside branches) comes up.
+  sgpr_ready(ts.n, ts.n_in, ts.rpt, ts.j[0].w, ts.j[0].y, ts.j[0].n_out, ts.j[0].teams, ts.j[1].w, ts.j[1].y,
+             ts.j[1].n_out, ts.j[1].teams, ts.j[2].w, ts.j[2].y, ts.j[2].n_out, ts.j[2].teams);
+  if constexpr (PRO == 1 || PRO == 2 || PRO == 4) sgpr_ready(xf);
+  else if constexpr (PRO == 5) sgpr_ready(ts.nsum, ts.nw, ts.npart, ts.n_part, ts.eps);
+  else if constexpr (!F32) sgpr_ready(qx, dx, s16);
+  else sgpr_ready(xf);
+  if constexpr (GATED) sgpr_ready(ygated);
+  else if constexpr (!F32 && TT == 1) sgpr_ready(ts.res, ts.ssq);
   uint32_t team = blockIdx.x * TPW + slot;
   const uint32_t t0 = ts.j[0].teams, t1 = ts.j[1].teams;
   const bool in1 = ts.n > 1 && team >= t0, in2 = ts.n > 2 && team >= t0 + t1;

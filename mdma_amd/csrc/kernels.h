@@ -9,6 +9,18 @@ namespace {
 
 // Workgroup barrier ordering LDS only: unlike __syncthreads it does not wait
 // for this wave's global loads, so a prefetch stays in flight across it.
+// Values made ready in SGPRs at this point (kernel arguments: their scalar
+// loads are issued here, together).
+template <class A>
+__device__ __forceinline__ int sgpr_ready1(const A &a) {
+  asm volatile("" ::"s"(a));
+  return 0;
+}
+template <class... A>
+__device__ __forceinline__ void sgpr_ready(const A &...a) {
+  const int order[] = {sgpr_ready1(a)...};  // in argument order
+  (void)order;
+}
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
