@@ -455,65 +455,31 @@ struct AttnTile {
   uint32_t v[16][C];  // V dim pairs of this wave's 16 keys
 };
 
-// The new key (ROPE: position visible - 1) is not taken from the cache: it is
-// rotated from kn / taken from vn (this query's head rows), rounded to f16
-// exactly as the cache stores it, and written to the cache by the lanes that
-// hold it (rope_kv_kernel's values). Every lane first issues its cache loads
-// (the new key's row is in the cache's bounds; its stale content is
-// replaced), so the new key's own loads add no round trip.
-template <int C, bool ROPE>
-__device__ __forceinline__ void attn_load(AttnTile<C> &t, uint16_t *__restrict__ K, uint16_t *__restrict__ V,
-                                          uint32_t tile, uint32_t visible, uint32_t kv_row, uint32_t hd,
-                                          uint32_t lane, uint32_t wave, const float *kn, const float *vn,
-                                          const float2 *cs) {
-  const uint32_t jk = tile * ATT_TILE + wave * 16 + (lane >> 2), l4 = lane & 3;
+// One tile's K slices and V pairs. Every load is unconditional, its row
+// clamped to visible - 1 and its dims to the head: a load under a branch
+// becomes a register copy after it, which waits for every load in flight.
+// The values of rows past visible and dims past hd are never used (their
+// scores are masked, their P.V terms zeroed, their dims not stored).
+template <int C>
+__device__ __forceinline__ void attn_load(AttnTile<C> &t, const uint16_t *__restrict__ K,
+                                          const uint16_t *__restrict__ V, uint32_t tile, uint32_t visible,
+                                          uint32_t kv_row, uint32_t hd, uint32_t lane, uint32_t wave) {
+  // 32-bit element offsets from the (uniform) cache bases, and V rows
+  // uniform per wave: addresses stay in SGPRs plus one VGPR offset.
+  const uint32_t jk = min(tile * ATT_TILE + wave * 16 + (lane >> 2), visible - 1), l4 = lane & 3;
 #pragma unroll
   for (int m = 0; m < 4 * C; m++) {
-    const uint32_t d0 = 8 * l4 + 32 * m;
-    t.k[m] = jk < visible && d0 < hd ? *reinterpret_cast<const uint4 *>(K + (size_t)jk * kv_row + d0)
-                                     : make_uint4(0, 0, 0, 0);
+    const uint32_t d0 = min(8 * l4 + 32 * m, hd - 8);
+    t.k[m] = *reinterpret_cast<const uint4 *>(K + (jk * kv_row + d0));
   }
 #pragma unroll
   for (int r = 0; r < 16; r++) {
-    const uint32_t jv = tile * ATT_TILE + wave * 16 + r;
+    const uint32_t jv = min(tile * ATT_TILE + wave * 16 + r, visible - 1);
+    const uint16_t *vrow = V + jv * kv_row;
 #pragma unroll
     for (int c = 0; c < C; c++) {
-      const uint32_t d = 2 * lane + 128 * c;
-      t.v[r][c] = jv < visible && d < hd ? *reinterpret_cast<const uint32_t *>(V + (size_t)jv * kv_row + d) : 0u;
-    }
-  }
-  if (!ROPE) return;
-  const uint32_t jn = visible - 1;  // the new key
-  if (jk == jn) {
-#pragma unroll
-    for (int m = 0; m < 4 * C; m++) {
-      const uint32_t d0 = 8 * l4 + 32 * m;
-      if (d0 >= hd) continue;
-      uint32_t w[4];
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        float x0 = kn[d0 + 2 * e], x1 = kn[d0 + 2 * e + 1];
-        const float2 c2 = cs[d0 / 2 + e];
-        rot(x0, x1, c2.x, c2.y);
-        w[e] = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
-      }
-      t.k[m] = make_uint4(w[0], w[1], w[2], w[3]);
-      *reinterpret_cast<uint4 *>(K + (size_t)jk * kv_row + d0) = t.k[m];
-    }
-  }
-  const uint32_t r0 = tile * ATT_TILE + wave * 16;
-  if (jn >= r0 && jn < r0 + 16) {  // this wave holds the new value row
-    const uint32_t rn = jn - r0;
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      if (r != (int)rn) continue;
-#pragma unroll
-      for (int c = 0; c < C; c++) {
-        const uint32_t d = 2 * lane + 128 * c;
-        if (d >= hd) continue;
-        t.v[r][c] = (uint32_t)f2h(vn[d]) | ((uint32_t)f2h(vn[d + 1]) << 16);
-        *reinterpret_cast<uint32_t *>(V + (size_t)jn * kv_row + d) = t.v[r][c];
-      }
+      const uint32_t d = min(2 * lane + 128 * c, hd - 2);
+      t.v[r][c] = *reinterpret_cast<const uint32_t *>(vrow + d);
     }
   }
 }
@@ -532,36 +498,77 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
   __shared__ float gmax[4];
   __shared__ float wml[G][ATT_MAX_RUNS][2];
   __shared__ uint32_t last;
+  __shared__ __attribute__((aligned(16))) uint32_t knew[ROPE ? 64 * C : 4];  // the new row's f16 pairs
+  __shared__ uint32_t vnew[ROPE ? 64 * C : 1];
+  // The arguments' scalar loads in one batch (one wait, not a chain).
+  sgpr_ready(q, K, V, o, part, cnt, prefix, hd, n_q_heads, n_kv_heads, scale, seq_stride, tpw);
+  if constexpr (QUANT) sgpr_ready(q8.q, q8.d, q8.s16);
+  if constexpr (ROPE) sgpr_ready(rp.k, rp.v, rp.tab, rp.pos);
   const uint32_t kvh = blockIdx.x, split = blockIdx.y, i = blockIdx.z, n_splits = gridDim.y;
   const uint32_t visible = seq_stride ? prefix + 1 : prefix + i + 1;
   const uint32_t tiles = (visible + ATT_TILE - 1) / ATT_TILE, t0 = split * tpw;
   if (t0 >= tiles) return;  // this query's keys end before the run
   const uint32_t t1 = min(t0 + tpw, tiles), live = (tiles + tpw - 1) / tpw;
   const uint32_t kv_row = n_kv_heads * hd, qh0 = kvh * G;
-  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l4 = lane & 3;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, l4 = lane & 3;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   K += (size_t)i * seq_stride + (size_t)kvh * hd;
   V += (size_t)i * seq_stride + (size_t)kvh * hd;
+  // Loads in the order they are needed: q's pairs (and with ROPE the new
+  // key's and value's pairs and their rotation), then the first tile. Every
+  // load is unconditional (indices clamped), so each wait below is for the
+  // loads it needs and not for the tile behind them.
+  const float *qv = q + ((size_t)i * n_q_heads + qh0) * hd;
+  constexpr int QP = (G * 64 * C + 255) / 256;  // q pairs per thread
+  const uint32_t hp = hd / 2, n_qp = G * hp;
+  float2 qx[QP], qcs[QP];
+#pragma unroll
+  for (int k = 0; k < QP; k++) {
+    const uint32_t p = min(tid + 256 * k, n_qp - 1), h = p / hp, e = p % hp;
+    qx[k] = *reinterpret_cast<const float2 *>(qv + h * hd + 2 * e);
+    if (ROPE) qcs[k] = reinterpret_cast<const float2 *>(rp.tab)[(size_t)rp.pos * hp + e];
+  }
+  // The new key (ROPE: position visible - 1) is not read from the cache: it
+  // is rotated from rp.k and rounded to f16 exactly as the cache stores it
+  // (rope_kv_kernel's values), kept in LDS with the new value, substituted
+  // where the scores and P.V meet that row, and written to the cache by the
+  // run that holds it.
+  const uint32_t jn = visible - 1, en = min(tid, hp - 1);
+  float2 kn2, vn2, cn2;
+  if (ROPE) {
+    kn2 = reinterpret_cast<const float2 *>(rp.k + ((size_t)i * n_kv_heads + kvh) * hd)[en];
+    vn2 = reinterpret_cast<const float2 *>(rp.v + ((size_t)i * n_kv_heads + kvh) * hd)[en];
+    cn2 = reinterpret_cast<const float2 *>(rp.tab)[(size_t)rp.pos * hp + en];
+  }
   // Ping-pong tile buffers: the loads for tile+1 go out before tile is
   // computed (clamped to the run's last tile, so every load is in bounds and
   // the wait counts are fixed).
-  const float *kn = ROPE ? rp.k + ((size_t)i * n_kv_heads + kvh) * hd : nullptr;
-  const float *vn = ROPE ? rp.v + ((size_t)i * n_kv_heads + kvh) * hd : nullptr;
-  const float2 *cs = ROPE ? reinterpret_cast<const float2 *>(rp.tab) + (size_t)rp.pos * (hd / 2) : nullptr;
   AttnTile<C> ta, tb;
-  attn_load<C, ROPE>(ta, K, V, t0, visible, kv_row, hd, lane, wave, kn, vn, cs);
-  const float *qv = q + ((size_t)i * n_q_heads + qh0) * hd;
-  if (ROPE) {
-    // Interleaved pairs rotated as rope_kv_kernel rotates q.
-    for (uint32_t p = tid; p < G * hd / 2; p += 256) {
-      const uint32_t h = p / (hd / 2), e = p % (hd / 2);
-      float x0 = qv[h * hd + 2 * e], x1 = qv[h * hd + 2 * e + 1];
-      const float2 c2 = cs[e];
-      rot(x0, x1, c2.x, c2.y);
+  __builtin_amdgcn_sched_barrier(0);  // q and the new row's loads go out first
+  attn_load<C>(ta, K, V, t0, visible, kv_row, hd, lane, wave);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int k = 0; k < QP; k++) {
+    const uint32_t p = tid + 256 * k;
+    if (p < n_qp) {
+      const uint32_t h = p / hp, e = p % hp;
+      float x0 = qx[k].x, x1 = qx[k].y;
+      if (ROPE) rot(x0, x1, qcs[k].x, qcs[k].y);  // interleaved pairs, as rope_kv_kernel rotates q
       qs[h][2 * e] = x0;
       qs[h][2 * e + 1] = x1;
     }
-  } else {
-    for (uint32_t t = tid; t < G * hd; t += 256) qs[t / hd][t % hd] = qv[t];
+  }
+  if (ROPE && tid < hp) {
+    float x0 = kn2.x, x1 = kn2.y;
+    rot(x0, x1, cn2.x, cn2.y);
+    const uint32_t kw = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
+    const uint32_t vw = (uint32_t)f2h(vn2.x) | ((uint32_t)f2h(vn2.y) << 16);
+    knew[tid] = kw;
+    vnew[tid] = vw;
+    if (jn / ATT_TILE >= t0 && jn / ATT_TILE < t1) {
+      *reinterpret_cast<uint32_t *>(K + (size_t)jn * kv_row + 2 * tid) = kw;
+      *reinterpret_cast<uint32_t *>(V + (size_t)jn * kv_row + 2 * tid) = vw;
+    }
   }
   if (tid < G) mrun[tid] = -INFINITY, lrun[tid] = 0.f;
   float acc[G][C][2];
@@ -571,6 +578,9 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
     for (int c = 0; c < C; c++) acc[h][c][0] = acc[h][c][1] = 0.f;
   lds_barrier();
   auto process = [&](const AttnTile<C> &cur, uint32_t tile) {
+    // The tile holding the new row takes its K and V from LDS.
+    const bool has_new = ROPE && tile == jn / ATT_TILE;
+    const bool key_new = has_new && tile * ATT_TILE + wave * 16 + (lane >> 2) == jn;
     float s[G];
 #pragma unroll
     for (int h = 0; h < G; h++) s[h] = 0.f;
@@ -578,7 +588,12 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
     for (int m = 0; m < 4 * C; m++) {
       const uint32_t d0 = 8 * l4 + 32 * m;
       if (d0 < hd) {
-        const uint32_t kk[4] = {cur.k[m].x, cur.k[m].y, cur.k[m].z, cur.k[m].w};
+        uint4 k4 = cur.k[m];
+        if (has_new) {
+          const uint4 nk = *reinterpret_cast<const uint4 *>(&knew[d0 / 2]);
+          if (key_new) k4 = nk;
+        }
+        const uint32_t kk[4] = {k4.x, k4.y, k4.z, k4.w};
 #pragma unroll
         for (int e = 0; e < 8; e++) {
           const float kf = h2f((uint16_t)(kk[e >> 1] >> (16 * (e & 1))));
@@ -617,13 +632,22 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
     }
 #pragma unroll
     for (int r = 0; r < 16; r++) {
+      // wave-uniform: row r of this wave past visible (its value may be
+      // anything, even NaN: zeroed, not weighted by 0), or the new row
+      const uint32_t jr = tile * ATT_TILE + wave * 16 + r;
+      uint32_t vr[C];
+#pragma unroll
+      for (int c = 0; c < C; c++) {
+        vr[c] = jr < visible ? cur.v[r][c] : 0u;
+        if (has_new && jr == jn && 2 * lane + 128 * c < hd) vr[c] = vnew[lane + 64 * c];
+      }
 #pragma unroll
       for (int h = 0; h < G; h++) {
         const float ph = sc[h][wave * 16 + r];
 #pragma unroll
         for (int c = 0; c < C; c++) {
-          acc[h][c][0] = fmaf(ph, h2f(cur.v[r][c] & 0xffffu), acc[h][c][0]);
-          acc[h][c][1] = fmaf(ph, h2f(cur.v[r][c] >> 16), acc[h][c][1]);
+          acc[h][c][0] = fmaf(ph, h2f(vr[c] & 0xffffu), acc[h][c][0]);
+          acc[h][c][1] = fmaf(ph, h2f(vr[c] >> 16), acc[h][c][1]);
         }
       }
     }
@@ -633,10 +657,10 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
     process(ta, t0);
   } else {
     for (uint32_t tile = t0; tile < t1; tile += 2) {
-      attn_load<C, ROPE>(tb, K, V, min(tile + 1, t1 - 1), visible, kv_row, hd, lane, wave, kn, vn, cs);
+      attn_load<C>(tb, K, V, min(tile + 1, t1 - 1), visible, kv_row, hd, lane, wave);
       process(ta, tile);
       if (tile + 1 >= t1) break;
-      attn_load<C, ROPE>(ta, K, V, min(tile + 2, t1 - 1), visible, kv_row, hd, lane, wave, kn, vn, cs);
+      attn_load<C>(ta, K, V, min(tile + 2, t1 - 1), visible, kv_row, hd, lane, wave);
       process(tb, tile + 1);
     }
   }
