@@ -722,22 +722,26 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
     // Merge weights w[h][s] = exp(m_s - M) / L with M = max m_s and
     // L = sum l_s exp(m_s - M); then out = sum_s w[h][s] * partial_s.
     // The partial vectors are loaded first, so both loads overlap.
+    // Every load unconditional (indices clamped; the terms of runs past
+    // live are not used), the (m, l) pairs first: one wait for all of them.
+    static_assert(G * ATT_MAX_RUNS <= 256, "one (m, l) pair per thread");
+    float ml[2] = {0.f, 0.f};
+    const uint32_t e_ml = min(tid, G * live - 1), h_ml = e_ml / live, s_ml = e_ml % live;
+    {
+      const float *pp = part + ((orow / hd + h_ml) * n_splits + s_ml) * (hd + 2) + hd;
+      ml[0] = load_dev(pp);
+      ml[1] = load_dev(pp + 1);
+    }
     float pv[NO][ATT_MAX_RUNS];
 #pragma unroll
     for (int k = 0; k < NO; k++) {
-      const uint32_t t = tid + 256 * k;
+      const uint32_t t = min(tid + 256 * k, G * hd - 1);
       const uint32_t h = t / hd, d = t % hd;
       const float *pb = part + (orow / hd + h) * n_splits * (hd + 2) + d;
 #pragma unroll
-      for (uint32_t s2 = 0; s2 < ATT_MAX_RUNS; s2++)
-        pv[k][s2] = t < G * hd && s2 < live ? load_dev(pb + s2 * (hd + 2)) : 0.f;
+      for (uint32_t s2 = 0; s2 < ATT_MAX_RUNS; s2++) pv[k][s2] = load_dev(pb + min(s2, live - 1) * (hd + 2));
     }
-    for (uint32_t e = tid; e < G * live; e += 256) {
-      const uint32_t h = e / live, s2 = e % live;
-      const float *pp = part + ((orow / hd + h) * n_splits + s2) * (hd + 2) + hd;
-      wml[h][s2][0] = load_dev(pp);
-      wml[h][s2][1] = load_dev(pp + 1);
-    }
+    if (tid < G * live) wml[h_ml][s_ml][0] = ml[0], wml[h_ml][s_ml][1] = ml[1];
     __syncthreads();
     if (tid < G) {
       float M = -INFINITY;
