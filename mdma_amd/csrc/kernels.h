@@ -7,8 +7,6 @@
 namespace mdma {
 namespace {
 
-// Workgroup barrier ordering LDS only: unlike __syncthreads it does not wait
-// for this wave's global loads, so a prefetch stays in flight across it.
 // Values made ready in SGPRs at this point (kernel arguments: their scalar
 // loads are issued here, together).
 template <class A>
@@ -21,6 +19,8 @@ __device__ __forceinline__ void sgpr_ready(const A &...a) {
   const int order[] = {sgpr_ready1(a)...};  // in argument order
   (void)order;
 }
+// Workgroup barrier ordering LDS only: unlike __syncthreads it does not wait
+// for this wave's global loads, so a prefetch stays in flight across it.
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
@@ -100,6 +100,28 @@ __device__ __forceinline__ V wave_total63(V v) {
   v = dpp_step<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
   v = dpp_step<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
   return v;
+}
+
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_max(float v) {
+  const float o = __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, -INFINITY), __builtin_bit_cast(int, v), CTRL, ROWS,
+                                         0xF, false));
+  return fmaxf(v, o);
+}
+// Max / sum over the 64 lanes, the result in every lane.
+__device__ __forceinline__ float wave_max_all(float v) {
+  v = dpp_max<0xB1, 0xF>(v);
+  v = dpp_max<0x4E, 0xF>(v);
+  v = dpp_max<0x141, 0xF>(v);
+  v = dpp_max<0x140, 0xF>(v);
+  v = dpp_max<0x142, 0xA>(v);
+  v = dpp_max<0x143, 0xC>(v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ __forceinline__ float wave_sum_all(float v) {
+  v = wave_total63(v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 // Six-bit (scale, min) of Q4_K sub-blocks 2p and 2p+1 from the header's

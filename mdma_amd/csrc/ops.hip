@@ -184,9 +184,10 @@ __global__ __launch_bounds__(1024) void rmsnorm_row_kernel(const float *__restri
       ss += (double)sq;
     }
   }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-  if (lane == 0) sh[wave] = ss;
+  // Wave sums through DPP lane moves (no LDS round trips), then the waves'
+  // in order.
+  ss = wave_total63(ss);
+  if (lane == 63) sh[wave] = ss;
   __syncthreads();
   double tot = 0.0;
   for (int k = 0; k < 16; k++) tot += sh[k];
@@ -205,9 +206,8 @@ __global__ __launch_bounds__(1024) void rmsnorm_row_kernel(const float *__restri
     }
     *reinterpret_cast<float4 *>(y + base + i) = make_float4(r[0], r[1], r[2], r[3]);
     if (QUANT) {
-      float amax = fmaxf(fmaxf(fabsf(r[0]), fabsf(r[1])), fmaxf(fabsf(r[2]), fabsf(r[3])));
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+      // A wave's 4 x 64 values are one 256-group.
+      const float amax = wave_max_all(fmaxf(fmaxf(fabsf(r[0]), fabsf(r[1])), fmaxf(fabsf(r[2]), fabsf(r[3]))));
       const float inv = amax == 0.f ? 0.f : 127.0f / amax;
       int qi[4], sm = 0;
 #pragma unroll
@@ -215,8 +215,9 @@ __global__ __launch_bounds__(1024) void rmsnorm_row_kernel(const float *__restri
         qi[k] = q8_round(r[k] * inv);
         sm += qi[k];
       }
-      sm += __shfl_xor(sm, 1, 64);
-      sm += __shfl_xor(sm, 2, 64);
+      // sums of 16 columns: the quad of lanes, every lane of it
+      sm += (int)dpp_u32<0xB1, 0xF>((uint32_t)sm);
+      sm += (int)dpp_u32<0x4E, 0xF>((uint32_t)sm);
       *reinterpret_cast<uint32_t *>(q + base + i) = pack4_i8(qi[0], qi[1], qi[2], qi[3]);
       if ((lane & 3) == 0) qs16[(base + i) / 16] = sm;
       if (lane == 0) qd[(base + i) / 256] = amax / 127.0f;
@@ -419,28 +420,6 @@ struct AttnRope {
   uint32_t pos;
 };
 
-template <int CTRL, int ROWS>
-__device__ __forceinline__ float dpp_max(float v) {
-  const float o = __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, -INFINITY), __builtin_bit_cast(int, v), CTRL, ROWS,
-                                         0xF, false));
-  return fmaxf(v, o);
-}
-// Max / sum over the 64 lanes, the result in every lane.
-__device__ __forceinline__ float wave_max_all(float v) {
-  v = dpp_max<0xB1, 0xF>(v);
-  v = dpp_max<0x4E, 0xF>(v);
-  v = dpp_max<0x141, 0xF>(v);
-  v = dpp_max<0x140, 0xF>(v);
-  v = dpp_max<0x142, 0xA>(v);
-  v = dpp_max<0x143, 0xC>(v);
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-}
-__device__ __forceinline__ float wave_sum_all(float v) {
-  v = wave_total63(v);
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-}
-
 // Device-scope (all XCDs) coherent store and load of one float.
 __device__ __forceinline__ void store_dev(float *p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -495,7 +474,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
   __shared__ float sc[G][ATT_TILE];
   __shared__ float mrun[G], lrun[G], alph[G];
   __shared__ float red[4][G][128 * C];
-  __shared__ float gmax[4];
+  __shared__ float gmax[(G * 128 * C + 255) / 256][4];
   __shared__ float wml[G][ATT_MAX_RUNS][2];
   __shared__ uint32_t last;
   __shared__ __attribute__((aligned(16))) uint32_t knew[ROPE ? 64 * C : 4];  // the new row's f16 pairs
@@ -774,20 +753,27 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
     if (t < G * hd) o[orow + t] = out[k];
   }
   if (QUANT) {
-    // G*hd is whole groups of 256: output k of every thread is group k.
+    // G*hd is whole groups of 256: output k of every thread is group k. The
+    // waves' maxima of every group meet in LDS behind one barrier.
 #pragma unroll
     for (int k = 0; k < NO; k++) {
       if (256 * k >= G * hd) break;
-      float amax = wave_max_all(fabsf(out[k]));
-      __syncthreads();
-      if (lane == 0) gmax[wave] = amax;
-      __syncthreads();
-      amax = fmaxf(fmaxf(gmax[0], gmax[1]), fmaxf(gmax[2], gmax[3]));
+      const float wm = wave_max_all(fabsf(out[k]));
+      if (lane == 0) gmax[k][wave] = wm;
+    }
+    lds_barrier();
+#pragma unroll
+    for (int k = 0; k < NO; k++) {
+      if (256 * k >= G * hd) break;
+      const float amax = fmaxf(fmaxf(gmax[k][0], gmax[k][1]), fmaxf(gmax[k][2], gmax[k][3]));
       const float inv = amax == 0.f ? 0.f : 127.0f / amax;
       const int qi = q8_round(out[k] * inv);
+      // sum of 16 columns: quads, then half rows and rows (every lane)
       int sm = qi;
-#pragma unroll
-      for (int off = 8; off >= 1; off >>= 1) sm += __shfl_xor(sm, off, 64);
+      sm += (int)dpp_u32<0xB1, 0xF>((uint32_t)sm);
+      sm += (int)dpp_u32<0x4E, 0xF>((uint32_t)sm);
+      sm += (int)dpp_u32<0x141, 0xF>((uint32_t)sm);
+      sm += (int)dpp_u32<0x140, 0xF>((uint32_t)sm);
       const size_t e = orow + tid + 256 * k;
       q8.q[e] = (int8_t)qi;
       if ((lane & 15) == 0) q8.s16[e / 16] = sm;
