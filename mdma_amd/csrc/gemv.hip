@@ -623,9 +623,17 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const float *__restri
     const float4 t = *reinterpret_cast<const float4 *>(x + base);
     v[0] = t.x, v[1] = t.y, v[2] = t.z, v[3] = t.w;
   }
+  static_assert(LPG == 8 || LPG == 64, "groups of 32 or 256");
+  // Group maxima and 16-column sums through DPP lane moves (every lane of
+  // the group gets the result).
   float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-#pragma unroll
-  for (int o = LPG / 2; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  if constexpr (LPG == 64) {
+    amax = wave_max_all(amax);
+  } else {
+    amax = dpp_max<0xB1, 0xF>(amax);
+    amax = dpp_max<0x4E, 0xF>(amax);
+    amax = dpp_max<0x141, 0xF>(amax);  // half-row mirror: 8 lanes
+  }
   const float inv = amax == 0.f ? 0.f : 127.0f / amax;
   int qi[4], sum = 0;
 #pragma unroll
@@ -633,8 +641,8 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const float *__restri
     qi[k] = q8_round(v[k] * inv);
     sum += qi[k];
   }
-  sum += __shfl_xor(sum, 1, 64);  // 16 values = 4 lanes
-  sum += __shfl_xor(sum, 2, 64);
+  sum += (int)dpp_u32<0xB1, 0xF>((uint32_t)sum);  // 16 values = 4 lanes
+  sum += (int)dpp_u32<0x4E, 0xF>((uint32_t)sum);
   if (!live) return;
   *reinterpret_cast<uint32_t *>(q + base) = pack4_i8(qi[0], qi[1], qi[2], qi[3]);
   const int lane = threadIdx.x & 63;
