@@ -820,6 +820,9 @@ __global__ __launch_bounds__(team_wg(PRO, TW)) void gemv_team(TeamSet ts, const 
 #ifndef MDMA_TEAM_WAVES_PER_CU
 #define MDMA_TEAM_WAVES_PER_CU 12
 #endif
+#ifndef MDMA_NORM_WAVES_PER_CU
+#define MDMA_NORM_WAVES_PER_CU 3
+#endif
 
 template <class F, bool F32, int R, int ITERS, int TT, bool GATED>
 void launch_iters(mdma_ctx *ctx, TeamSet ts, int tw, int pl, const float *xf, const int8_t *qx, const float *dx,
@@ -895,7 +898,10 @@ void launch_fmt(mdma_ctx *ctx, TeamSet ts, const float *xf, const int8_t *qx, co
   // CU, rounded up to a power of two (at most 16; batched: 4).
   uint64_t rows = 0;
   for (int i = 0; i < ts.n; i++) rows += ts.j[i].n_out;
-  const uint64_t want = (uint64_t)ctx->cu_count * MDMA_TEAM_WAVES_PER_CU / tw;
+  // A normalizing prologue reads 32 KB of f32 per workgroup: fewer, longer
+  // teams read it fewer times (at Llama-3-8B's QKV, 3 waves per CU: four
+  // row groups per team, measured best against 1, 2, 6 and 12).
+  const uint64_t want = (uint64_t)ctx->cu_count * (ts.nsum ? MDMA_NORM_WAVES_PER_CU : MDMA_TEAM_WAVES_PER_CU) / tw;
   const uint64_t groups = ((rows + want - 1) / want + R - 1) / R;
   if constexpr (TT > 1) {
     launch_iters<F, F32, R, 4, TT, GATED>(ctx, ts, tw, pl, xf, qx, dx, s16, T, yg);
