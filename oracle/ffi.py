@@ -41,6 +41,8 @@ def lib():
             "orc_quantize_act": (C.c_int, [_P, _Z, _Z, _P, _P, _P]),
             "orc_block_dot_i32": (C.c_int, [C.c_int, _P, _Z, _Z, _Z, _P, _Z, _P]),
             "orc_llama_generate": (C.c_int, [_P, _P, _Z, _Z, _P, _P]),
+            "orc_llama_run": (C.c_int, [_P, _P, _Z, _Z, _P, _P, _P]),
+            "orc_i8_group": (_Z, [C.c_int, _Z, _Z, _Z]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -209,11 +211,16 @@ class _M(C.Structure):
     _fields_ = [(n, _Z) for n in ("n_layers", "n_embd", "n_ff", "n_heads", "n_kv_heads", "head_dim",
                                   "n_ctx", "vocab")] + \
                [("rope_theta", C.c_float), ("rms_eps", C.c_float), ("token_embd", _W), ("output", _W),
-                ("output_norm", _P), ("layers", _P), ("kv_f16", C.c_int), ("n_threads", C.c_int)]
+                ("output_norm", _P), ("layers", _P), ("kv_f16", C.c_int), ("n_threads", C.c_int),
+                ("act_i8", C.c_int)]
 
 
-def llama_generate(gguf_reader, prompt, n_gen: int, kv_f16: bool = True, threads: int = 0):
-    """Greedy tokens (and final logits) of the oracle Llama on a GGUF model."""
+def i8_group(dtype: int, n_out: int, n_in: int, T: int) -> int:
+    """Activation group (32, 256, or 0 for f32) of the int8 mode's GEMV."""
+    return int(lib().orc_i8_group(dtype, n_out, n_in, T))
+
+
+def _model(gguf_reader, kv_f16: bool, threads: int, act_i8: bool):
     g = gguf_reader
     md = g.metadata
     arch = md["general.architecture"]
@@ -237,6 +244,7 @@ def llama_generate(gguf_reader, prompt, n_gen: int, kv_f16: bool = True, threads
                        W(p + "attn_output.weight"), W(p + "ffn_gate.weight"), W(p + "ffn_up.weight"),
                        W(p + "ffn_down.weight"), arr(p + "attn_norm.weight").ctypes.data,
                        arr(p + "ffn_norm.weight").ctypes.data)
+    keep.append(layers)
     n_embd, n_heads = md[f"{arch}.embedding_length"], md[f"{arch}.attention.head_count"]
     te = g.tensors["token_embd.weight"]
     m = _M(n_layers, n_embd, md[f"{arch}.feed_forward_length"], n_heads,
@@ -244,10 +252,31 @@ def llama_generate(gguf_reader, prompt, n_gen: int, kv_f16: bool = True, threads
            md[f"{arch}.context_length"], te.shape[0], float(md.get(f"{arch}.rope.freq_base", 10000.0)),
            float(md[f"{arch}.attention.layer_norm_rms_epsilon"]), W("token_embd.weight"), W("output.weight"),
            arr("output_norm.weight").ctypes.data, C.cast(layers, C.c_void_p), int(kv_f16),
-           threads or os.cpu_count() or 1)
+           threads or os.cpu_count() or 1, int(act_i8))
+    return m, keep, te.shape[0]
+
+
+def llama_generate(gguf_reader, prompt, n_gen: int, kv_f16: bool = True, threads: int = 0, act_i8: bool = False):
+    """Greedy tokens (and final logits) of the oracle Llama on a GGUF model."""
+    toks, logits = llama_run(gguf_reader, prompt, n_gen, kv_f16=kv_f16, threads=threads, act_i8=act_i8)
+    return toks, logits[-1]
+
+
+def llama_run(gguf_reader, prompt, n_gen: int, forced=None, kv_f16: bool = True, threads: int = 0,
+              act_i8: bool = False):
+    """(greedy token of every step [n_gen], logits of every step [n_gen, vocab]).
+    forced: tokens fed to steps 1..n_gen-1 instead of the greedy ones
+    (teacher forcing). act_i8: the int8 activation mode, x requantized
+    before every GEMV the device quantizes for (i8_group)."""
+    m, keep, vocab = _model(gguf_reader, kv_f16, threads, act_i8)
     prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
     out = np.zeros(n_gen, dtype=np.uint32)
-    logits = np.zeros(te.shape[0], dtype=np.float32)
-    _chk("llama_generate", lib().orc_llama_generate(C.byref(m), _p(prompt), prompt.size, n_gen, _p(out),
-                                                    _p(logits)))
+    logits = np.zeros((n_gen, vocab), dtype=np.float32)
+    fp = None
+    if forced is not None:
+        forced = np.ascontiguousarray(forced, dtype=np.uint32)
+        assert forced.size >= n_gen - 1
+        fp = _p(forced)
+    _chk("llama_run", lib().orc_llama_run(C.byref(m), _p(prompt), prompt.size, n_gen, fp, _p(out), _p(logits)))
+    del keep
     return out, logits

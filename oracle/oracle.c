@@ -584,10 +584,44 @@ typedef struct {
     float *x, *x_alt, *normed, *q, *k, *v, *attn_out, *proj, *gate, *up, *act;
 } orc_ws;
 
+/* Activation group of the device's int8 mode for one GEMV of T tokens: 32
+ * where it runs the prefill GEMM (T >= 16 on Q8_0 rows of whole 128-column
+ * tiles or Q4_K / Q6_K rows of whole 256-column blocks, weights below 4 GiB),
+ * 256 where it runs a decode GEMV (quantized weights, whole 256-column
+ * groups), 0 where it keeps f32 activations (float weights, other widths). */
+size_t orc_i8_group(int dtype, size_t n_out, size_t n_in, size_t T) {
+    int quant = dtype == ORC_Q8_0 || dtype == ORC_Q4_K || dtype == ORC_Q6_K;
+    if (!quant)
+        return 0;
+    size_t bs = orc_block_size(dtype), ts = orc_type_size(dtype);
+    size_t row = (n_in / bs * ts + 15) / 16 * 16; /* prepared row bytes */
+    int gemm_w = dtype == ORC_Q8_0 ? n_in % 128 == 0 : n_in % 256 == 0;
+    if (T >= 16 && gemm_w && (unsigned long long)n_out * row < (1ull << 32))
+        return 32;
+    return n_in % 256 == 0 ? 256 : 0;
+}
+
+/* "Requantize, then CPU qmatmul" (src/backend/rocm/decode/tests.rs:68-77):
+ * in the int8 mode every token row of x is quantized per group and the CPU
+ * qmatmul runs on the dequantized values q*d. */
 static int qm(const orc_model *m, const orc_weight *w, const float *x, size_t T, float *y) {
     size_t row_bytes = orc_type_size(w->dtype) * (w->n_in / orc_block_size(w->dtype));
-    return orc_qmatmul(w->dtype, w->data, row_bytes * w->n_out, w->n_out, w->n_in, x, T * w->n_in,
-                       y, T * w->n_out, m->n_threads);
+    size_t g = m->act_i8 ? orc_i8_group(w->dtype, w->n_out, w->n_in, T) : 0;
+    if (!g)
+        return orc_qmatmul(w->dtype, w->data, row_bytes * w->n_out, w->n_out, w->n_in, x,
+                           T * w->n_in, y, T * w->n_out, m->n_threads);
+    size_t n = T * w->n_in;
+    int8_t *q = (int8_t *)malloc(n);
+    float *d = (float *)malloc(n / g * sizeof(float)), *xh = (float *)malloc(n * sizeof(float));
+    orc_quantize_act(x, n, g, q, d, NULL);
+    for (size_t i = 0; i < n; i++)
+        xh[i] = (float)q[i] * d[i / g];
+    int st = orc_qmatmul(w->dtype, w->data, row_bytes * w->n_out, w->n_out, w->n_in, xh, n, y,
+                         T * w->n_out, m->n_threads);
+    free(q);
+    free(d);
+    free(xh);
+    return st;
 }
 
 static void swap(float **a, float **b) {
@@ -657,9 +691,13 @@ static int nonfinite(const float *v, size_t n) {
 
 /* Model::prefill (src/model.rs:398-468), then the greedy loop of
  * inference::sample (src/inference.rs:102-124) without EOS: n_gen tokens,
- * n_gen - 1 Model::forward calls (src/model.rs:326-387). */
-int orc_llama_generate(const orc_model *m, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
-                       uint32_t *out_tokens, float *last_logits) {
+ * n_gen - 1 Model::forward calls (src/model.rs:326-387). With `forced`
+ * non-null, step i + 1 is fed forced[i] instead of the greedy token of step
+ * i (teacher forcing: every step's logits are then those of one fixed token
+ * sequence); out_tokens still receives each step's greedy token.
+ * step_logits (nullable) receives the logits of every step, [n_gen][vocab]. */
+int orc_llama_run(const orc_model *m, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
+                  const uint32_t *forced, uint32_t *out_tokens, float *step_logits) {
     if (!n_prompt || !n_gen || n_prompt + n_gen > m->n_ctx)
         return 1; /* ContextLimit */
     size_t E = m->n_embd, kvw = m->n_kv_heads * m->head_dim, qw = m->n_heads * m->head_dim;
@@ -668,8 +706,8 @@ int orc_llama_generate(const orc_model *m, const uint32_t *prompt, size_t n_prom
     float **kc = (float **)calloc(m->n_layers, sizeof(float *));
     float **vc = (float **)calloc(m->n_layers, sizeof(float *));
     for (size_t i = 0; i < m->n_layers; i++) {
-        kc[i] = (float *)calloc(m->n_ctx * kvw, sizeof(float));
-        vc[i] = (float *)calloc(m->n_ctx * kvw, sizeof(float));
+        kc[i] = (float *)calloc((n_prompt + n_gen) * kvw, sizeof(float));
+        vc[i] = (float *)calloc((n_prompt + n_gen) * kvw, sizeof(float));
     }
     ws.x = (float *)calloc(T * E, 4);
     ws.x_alt = (float *)calloc(T * E, 4);
@@ -691,16 +729,21 @@ int orc_llama_generate(const orc_model *m, const uint32_t *prompt, size_t n_prom
             st = 10; /* Backend("empty or nonfinite logits") */
             break;
         }
+        if (step_logits)
+            memcpy(step_logits + i * m->vocab, logits, m->vocab * 4);
         uint32_t tok = orc_greedy(logits, m->vocab);
         out_tokens[i] = tok;
         if (i + 1 < n_gen) {
-            st = run(m, &ws, kc, vc, &tok, 1, (uint32_t)(n_prompt + i));
+            uint32_t feed = forced ? forced[i] : tok;
+            if (feed >= m->vocab) {
+                st = 2;
+                break;
+            }
+            st = run(m, &ws, kc, vc, &feed, 1, (uint32_t)(n_prompt + i));
             if (!st)
                 st = qm(m, &m->output, ws.normed, 1, logits);
         }
     }
-    if (last_logits && !st)
-        memcpy(last_logits, logits, m->vocab * 4);
     for (size_t i = 0; i < m->n_layers; i++) {
         free(kc[i]);
         free(vc[i]);
@@ -719,5 +762,17 @@ int orc_llama_generate(const orc_model *m, const uint32_t *prompt, size_t n_prom
     free(ws.up);
     free(ws.act);
     free(logits);
+    return st;
+}
+
+int orc_llama_generate(const orc_model *m, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
+                       uint32_t *out_tokens, float *last_logits) {
+    float *all = last_logits ? (float *)malloc(n_gen * m->vocab * 4) : NULL;
+    if (last_logits && !all)
+        return 8;
+    int st = orc_llama_run(m, prompt, n_prompt, n_gen, NULL, out_tokens, all);
+    if (!st && last_logits)
+        memcpy(last_logits, all + (n_gen - 1) * m->vocab, m->vocab * 4);
+    free(all);
     return st;
 }

@@ -74,8 +74,12 @@ typedef struct {
     const orc_layer *layers;
     int kv_f16; /* round K/V through f16 on store, as an f16 KV cache does */
     int n_threads;
+    int act_i8; /* int8 activation mode: x requantized before each GEMV (orc_i8_group) */
 } orc_model;
 
+size_t orc_i8_group(int dtype, size_t n_out, size_t n_in, size_t T);
+int orc_llama_run(const orc_model *m, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
+                  const uint32_t *forced, uint32_t *out_tokens, float *step_logits);
 int orc_llama_generate(const orc_model *m, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
                        uint32_t *out_tokens, float *last_logits);
 

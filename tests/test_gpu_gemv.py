@@ -10,6 +10,7 @@ oversize with a canary tail that must survive (decode/tests.rs:98,123-126).
 import numpy as np
 import pytest
 
+import npq
 from conftest import assert_parity, f32_exact
 from mdma_amd import synth
 from mdma_amd import backend as backend_mod
@@ -63,9 +64,9 @@ def run_qmatmul(be, dtype, raw, rows, k, x, mode="default", layout=0):
 
 
 def oracle_f32(dtype, raw, rows, k, x):
+    """(CPU oracle output, f64 dot of the exact block values) [T, rows]."""
     cpu = ffi.qmatmul(dtype, raw, rows, k, x)
-    W = ffi.dequantize_row(dtype, raw, rows * k).reshape(rows, k)
-    return cpu, f32_exact(W, x)
+    return cpu, f32_exact(npq.dequantize(dtype, raw, rows, k), x)
 
 
 KS = {Q4K: (256, 512, 768), Q6K: (256, 512, 768), Q8: (32, 288, 768), F32: (3, 288), F16: (64, 288)}
@@ -138,8 +139,8 @@ def test_q6k_f32_mode_config3_shapes(backend, shape, T):
     exact = np.empty_like(cpu, dtype=np.float64)
     for r0 in range(0, rows, 8192):
         r1 = min(rows, r0 + 8192)
-        W = ffi.dequantize_row(Q6K, raw[r0 * (k // 256) * 210:r1 * (k // 256) * 210], (r1 - r0) * k)
-        exact[:, r0:r1] = f32_exact(W.reshape(r1 - r0, k), x)
+        W = npq.dequantize(Q6K, raw[r0 * (k // 256) * 210:r1 * (k // 256) * 210], r1 - r0, k)
+        exact[:, r0:r1] = f32_exact(W, x)
     assert_parity(got, cpu, exact, 1e-5, what=f"Q6_K {shape} T={T}")
 
 
@@ -164,7 +165,7 @@ def test_i8_mode_reference_shapes(backend, dtype):
 
 
 @pytest.mark.parametrize("dtype", [Q4K, Q6K, Q8])
-@pytest.mark.parametrize("shape", [(4096, 4096), (14336, 4096), (4096, 14336)])
+@pytest.mark.parametrize("shape", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)])
 def test_i8_mode_llama3_8b_shapes(backend, dtype, shape):
     rows, k = shape
     raw = synth.weight(dtype, rows, k, 11)
@@ -463,6 +464,111 @@ def test_fused_calls_in_kernel_quantization_bit_exact(backend):
             assert np.array_equal(a_, b_)
     finally:
         backend.set_act_mode(backend_mod.ACT_F32)
+
+
+def sampled_rows(dtype, raw, rows, k, picks):
+    """(row indices, raw bytes of those rows): weight rows are contiguous, so
+    a run of rows is a weight of its own for the oracle."""
+    rb = len(raw) // rows
+    idx = np.concatenate([np.arange(r0, min(rows, r0 + n)) for r0, n in picks])
+    return idx, np.concatenate([raw[r * rb:(r + 1) * rb] for r in idx])
+
+
+def gate_up_oracle(dtype, g_raw, u_raw, rows, k, xq):
+    """CPU gate and up GEMVs on the (requantized) input, then CPU silu_mul
+    (Backend::ffn_gate_up's default, src/backend.rs:472-489); exact = the
+    f64 chain on the oracle's dequantized weights."""
+    cg, eg = oracle_f32(dtype, g_raw, rows, k, xq)
+    cu, eu = oracle_f32(dtype, u_raw, rows, k, xq)
+    cpu = ffi.silu_mul(cg.reshape(-1), cu.reshape(-1))
+    return cpu, (eg / (1 + np.exp(-eg)) * eu).reshape(-1)
+
+
+@pytest.mark.parametrize("dtype", [Q4K, Q6K])
+@pytest.mark.parametrize("variant", ["x_lds", "x_quant"])
+def test_one_token_gate_up_i8_matches_oracle(backend, dtype, variant):
+    """The decode path's dominant kernel: the fused gate/up + SiLU of one
+    token in the int8 mode at Llama-3-8B's 14336x4096, in both forms the
+    decode path runs. x_lds: x is an rmsnorm output whose int8 form the
+    rmsnorm left in the activation cache; the kernel stages it once per
+    workgroup in LDS. x_quant: x is a plain f32 buffer; the kernel quantizes
+    it in its own prologue. Oracle: requantize x per 256, CPU gate and up,
+    CPU silu_mul (src/backend/rocm/decode/tests.rs:68-130), 1e-3 relative."""
+    rows, k = 14336, 4096
+    g_raw, u_raw = synth.weight(dtype, rows, k, 71), synth.weight(dtype, rows, k, 72)
+    g = backend.upload_weight(g_raw, dtype, (rows, k))
+    u = backend.upload_weight(u_raw, dtype, (rows, k))
+    x_h = synth.normal_f32(k, 73) * 2
+    x_h[256:512] = 0  # an all-zero group
+    gs, us = backend.alloc(rows * 4), backend.alloc(rows * 4)
+    y = backend.f32_buf(np.full(rows + 8, CANARY, np.float32))
+    backend.set_act_mode(backend_mod.ACT_I8)
+    try:
+        if variant == "x_lds":
+            xb = backend.alloc(k * 4)
+            backend.rmsnorm(backend.f32_buf(np.full(k, 0.5, np.float32)), backend.f32_buf(x_h), xb, 1e-5)
+            x_used = backend.download_f32(xb)
+        else:
+            xb = backend.f32_buf(x_h)
+            x_used = x_h
+        backend.ffn_gate_up(g, u, xb, gs, us, y)
+        got = backend.download_f32(y)
+    finally:
+        backend.set_act_mode(backend_mod.ACT_F32)
+    assert np.all(got[rows:] == CANARY), "wrote past the output"
+    q, d, _ = ffi.quantize_act(x_used, 256)
+    cpu, exact = gate_up_oracle(dtype, g_raw, u_raw, rows, k, ffi.dequantize_act(q, d, 256))
+    rate = assert_parity(got[:rows], cpu, exact, 1e-3, atol=1e-5, what=f"gate/up i8 {dtype} {variant}")
+    print(f"gate/up i8 dtype={dtype} {variant}: plain 1e-3/1e-5 pass rate {rate:.5f}")
+
+
+HEAD = (128256, 4096)
+HEAD_PICKS = ((0, 2048), (64128 - 1000, 2000), (128256 - 2048, 2048))
+
+
+@pytest.mark.parametrize("mode,T", [("i8", 1), ("i8", 4), ("i8", 8), ("f32", 4), ("f32", 8)])
+@pytest.mark.parametrize("cached", [False, True])
+def test_q6k_head_matches_oracle(backend, mode, T, cached):
+    """The Q6_K output head at its full 128256x4096 shape, batch 1 (int8:
+    the ITERS16 run of the one-token kernels), 4 and 8 (the decode-batching
+    case), in both activation modes. x either comes from an rmsnorm (in the
+    int8 mode its int8 form is cached) or is a plain f32 buffer. The oracle
+    checks 6096 output rows at the start, middle and end of the vocabulary
+    (weight rows are contiguous, so a run of rows is its own weight)."""
+    if mode == "f32" and cached:
+        pytest.skip("the f32 mode has no int8 cache")
+    rows, k = HEAD
+    raw = synth.weight(Q6K, rows, k, 81)
+    w = backend.upload_weight(raw, Q6K, HEAD)
+    x_h = synth.normal_f32(T * k, 82 + T)
+    yb = backend.f32_buf(np.full(T * rows + 8, CANARY, np.float32))
+    backend.set_act_mode(backend_mod.ACT_I8 if mode == "i8" else backend_mod.ACT_F32)
+    try:
+        if cached:
+            xb = backend.alloc(T * k * 4)
+            backend.rmsnorm(backend.f32_buf(np.full(k, 0.7, np.float32)), backend.f32_buf(x_h), xb, 1e-5)
+            x_used = backend.download_f32(xb)
+        else:
+            xb = backend.f32_buf(x_h)
+            x_used = x_h
+        backend.qmatmul(w, xb, yb)
+        got = backend.download_f32(yb)
+    finally:
+        backend.set_act_mode(backend_mod.ACT_F32)
+    assert np.all(got[T * rows:] == CANARY), "wrote past the output"
+    got = got[:T * rows].reshape(T, rows)
+    idx, sub = sampled_rows(Q6K, raw, rows, k, HEAD_PICKS)
+    if mode == "i8":
+        xq = np.concatenate([ffi.dequantize_act(*ffi.quantize_act(x_used[t * k:(t + 1) * k], 256)[:2], 256)
+                             for t in range(T)])
+    else:
+        xq = x_used
+    cpu, exact = oracle_f32(Q6K, sub, idx.size, k, xq)
+    rtol = 1e-3 if mode == "i8" else 1e-5
+    rate = assert_parity(got[:, idx], cpu, exact, rtol, atol=1e-5 if mode == "i8" else 1e-6,
+                         what=f"head {mode} T={T} cached={cached}")
+    print(f"Q6_K head {mode} T={T} cached={cached}: plain pass rate {rate:.5f}")
+    w.buf.close()
 
 
 # ---------------------------------------------------------- shape rules ----

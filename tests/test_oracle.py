@@ -379,3 +379,31 @@ def test_block_dot_extremes_fit_int32():
     raw[0, 2:] = np.int8(-127).view(np.uint8)
     qx = np.full(32, -128, np.int8)
     assert ffi.block_dot_i32(Q8, raw.reshape(-1), 1, 32, qx, 1)[0, 0, 0] == 127 * 128 * 32
+
+
+# ------------------------------------------------- independent decoders ----
+
+@pytest.mark.parametrize("dtype", [Q8, Q4K, Q6K])
+def test_oracle_decoders_equal_independent_numpy_statement(dtype):
+    """tests/npq.py states the block formats independently, in exact f64.
+    The oracle's f32 values must be those exact values rounded once to f32
+    (Q6_K and Q8_0 values are exact in f32; Q4_K's (d*sc)*q - dmin*m rounds
+    once, in the subtraction)."""
+    import npq
+    rows, k = 64, 512 if dtype != Q8 else 288
+    raw = synth.weight(dtype, rows, k, 123)
+    got = ffi.dequantize_row(dtype, raw, rows * k)
+    want = npq.dequantize(dtype, raw, rows, k).astype(np.float32).reshape(-1)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # All-byte-value blocks (every scale/min/high-bit pattern).
+    nb = 300
+    tsz = {Q8: 34, Q4K: 144, Q6K: 210}[dtype]
+    rb = ((np.arange(nb * tsz, dtype=np.uint32) * 73 + 19) & 255).astype(np.uint8).reshape(nb, tsz)
+    off = {Q8: 0, Q4K: 0, Q6K: 208}[dtype]
+    rb[:, off:off + 2] = np.frombuffer(np.float16(0.0123).tobytes(), np.uint8)
+    if dtype == Q4K:
+        rb[:, 2:4] = np.frombuffer(np.float16(0.0071).tobytes(), np.uint8)
+    bs = {Q8: 32, Q4K: 256, Q6K: 256}[dtype]
+    got = ffi.dequantize_row(dtype, rb.reshape(-1), nb * bs)
+    want = npq.dequantize(dtype, rb.reshape(-1), 1, nb * bs).astype(np.float32).reshape(-1)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
