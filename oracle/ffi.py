@@ -252,7 +252,7 @@ def _model(gguf_reader, kv_f16: bool, threads: int, act_i8: bool):
            md[f"{arch}.context_length"], te.shape[0], float(md.get(f"{arch}.rope.freq_base", 10000.0)),
            float(md[f"{arch}.attention.layer_norm_rms_epsilon"]), W("token_embd.weight"), W("output.weight"),
            arr("output_norm.weight").ctypes.data, C.cast(layers, C.c_void_p), int(kv_f16),
-           threads or os.cpu_count() or 1, int(act_i8))
+           threads or os.cpu_count() or 1, 31 if act_i8 is True else int(act_i8))
     return m, keep, te.shape[0]
 
 
@@ -267,7 +267,8 @@ def llama_run(gguf_reader, prompt, n_gen: int, forced=None, kv_f16: bool = True,
     """(greedy token of every step [n_gen], logits of every step [n_gen, vocab]).
     forced: tokens fed to steps 1..n_gen-1 instead of the greedy ones
     (teacher forcing). act_i8: the int8 activation mode, x requantized
-    before every GEMV the device quantizes for (i8_group)."""
+    before every GEMV the device quantizes for (i8_group); an int selects
+    the GEMVs by bit (1 qkv, 2 o, 4 gate/up, 8 down, 16 head)."""
     m, keep, vocab = _model(gguf_reader, kv_f16, threads, act_i8)
     prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
     out = np.zeros(n_gen, dtype=np.uint32)

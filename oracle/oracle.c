@@ -604,9 +604,9 @@ size_t orc_i8_group(int dtype, size_t n_out, size_t n_in, size_t T) {
 /* "Requantize, then CPU qmatmul" (src/backend/rocm/decode/tests.rs:68-77):
  * in the int8 mode every token row of x is quantized per group and the CPU
  * qmatmul runs on the dequantized values q*d. */
-static int qm(const orc_model *m, const orc_weight *w, const float *x, size_t T, float *y) {
+static int qm_kind(const orc_model *m, int kind, const orc_weight *w, const float *x, size_t T, float *y) {
     size_t row_bytes = orc_type_size(w->dtype) * (w->n_in / orc_block_size(w->dtype));
-    size_t g = m->act_i8 ? orc_i8_group(w->dtype, w->n_out, w->n_in, T) : 0;
+    size_t g = (m->act_i8 & kind) ? orc_i8_group(w->dtype, w->n_out, w->n_in, T) : 0;
     if (!g)
         return orc_qmatmul(w->dtype, w->data, row_bytes * w->n_out, w->n_out, w->n_in, x,
                            T * w->n_in, y, T * w->n_out, m->n_threads);
@@ -622,6 +622,20 @@ static int qm(const orc_model *m, const orc_weight *w, const float *x, size_t T,
     free(d);
     free(xh);
     return st;
+}
+
+static int qm(const orc_model *m, const orc_weight *w, const float *x, size_t T, float *y) {
+    int kind = w == &m->output ? ORC_I8_HEAD : ORC_I8_QKV;
+    for (size_t i = 0; i < m->n_layers; i++) {
+        const orc_layer *L = &m->layers[i];
+        if (w == &L->wo)
+            kind = ORC_I8_O;
+        else if (w == &L->w_gate || w == &L->w_up)
+            kind = ORC_I8_GATE_UP;
+        else if (w == &L->w_down)
+            kind = ORC_I8_DOWN;
+    }
+    return qm_kind(m, kind, w, x, T, y);
 }
 
 static void swap(float **a, float **b) {

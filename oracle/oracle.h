@@ -74,8 +74,11 @@ typedef struct {
     const orc_layer *layers;
     int kv_f16; /* round K/V through f16 on store, as an f16 KV cache does */
     int n_threads;
-    int act_i8; /* int8 activation mode: x requantized before each GEMV (orc_i8_group) */
+    int act_i8; /* int8 activation mode: bits of the GEMVs whose x is requantized (orc_i8_group) */
 } orc_model;
+
+/* orc_model.act_i8 bits: which GEMVs of the int8 mode requantize x. */
+enum { ORC_I8_QKV = 1, ORC_I8_O = 2, ORC_I8_GATE_UP = 4, ORC_I8_DOWN = 8, ORC_I8_HEAD = 16, ORC_I8_ALL = 31 };
 
 size_t orc_i8_group(int dtype, size_t n_out, size_t n_in, size_t T);
 int orc_llama_run(const orc_model *m, const uint32_t *prompt, size_t n_prompt, size_t n_gen,

@@ -30,7 +30,7 @@ def f32_exact(W: np.ndarray, x: np.ndarray) -> np.ndarray:
 PARITY_LOG = []
 
 
-def assert_parity(got, cpu, exact, rtol, atol=1e-6, what=""):
+def assert_parity(got, cpu, exact, rtol, atol=1e-6, what="", correctly_rounded=False):
     """Per-element parity against the CPU oracle.
 
     The oracle sums each dot product sequentially in f32 (reference
@@ -46,6 +46,11 @@ def assert_parity(got, cpu, exact, rtol, atol=1e-6, what=""):
     with the same x -- the quantity the f32-mode kernels compute before their
     one rounding. Non-finite values fail. The plain pass rate (no slack term)
     is returned and logged for the session summary.
+
+    correctly_rounded: the f32-mode GEMVs form each dot product exactly (f64
+    products and sums) and round once, so every element must be at least as
+    close to exact as the CPU's sequential f32 sum, which no rounding of the
+    exact value can lose to: |gpu - exact| <= |cpu - exact| everywhere.
     """
     got = np.asarray(got, dtype=np.float64).reshape(-1)
     cpu = np.asarray(cpu, dtype=np.float64).reshape(-1)
@@ -58,7 +63,12 @@ def assert_parity(got, cpu, exact, rtol, atol=1e-6, what=""):
     assert bad.size == 0, (f"{what}: {bad.size}/{got.size} elements outside tolerance; first {bad[:5]}: "
                            f"gpu {got[bad[:5]]} cpu {cpu[bad[:5]]} exact {exact[bad[:5]]}")
     plain = float(np.mean(err <= atol + rtol * np.abs(cpu)))
-    gpu_closer = float(np.mean(np.abs(got - exact) <= np.abs(cpu - exact)))
+    closer = np.abs(got - exact) <= np.abs(cpu - exact)
+    gpu_closer = float(np.mean(closer))
+    if correctly_rounded:
+        far = np.nonzero(~closer)[0]
+        assert far.size == 0, (f"{what}: {far.size} elements farther from exact than the CPU; first {far[:5]}: "
+                               f"gpu {got[far[:5]]} cpu {cpu[far[:5]]} exact {exact[far[:5]]}")
     PARITY_LOG.append((what, got.size, rtol, atol, plain, gpu_closer))
     return plain
 

@@ -81,7 +81,7 @@ def test_f32_mode_reference_shapes_and_inputs(backend, dtype):
                 x = x_kind(kind, k)
                 got = run_qmatmul(backend, dtype, raw, rows, k, x, "f32")
                 cpu, exact = oracle_f32(dtype, raw, rows, k, x)
-                assert_parity(got, cpu, exact, 1e-5, what=f"dtype={dtype} rows={rows} k={k} x={kind}")
+                assert_parity(got, cpu, exact, 1e-5, what=f"dtype={dtype} rows={rows} k={k} x={kind}", correctly_rounded=True)
                 if kind == 2:
                     assert np.all(got == 0)
 
@@ -93,7 +93,7 @@ def test_f32_mode_float_weights(backend, dtype):
         x = synth.normal_f32(2 * k, 4)
         got = run_qmatmul(backend, dtype, raw, rows, k, x)
         cpu, exact = oracle_f32(dtype, raw, rows, k, x)
-        assert_parity(got, cpu, exact, 1e-5, what=f"dtype={dtype}")
+        assert_parity(got, cpu, exact, 1e-5, what=f"dtype={dtype}", correctly_rounded=True)
     # src/backend/test_support.rs:254-268 hand-computed batch.
     w = np.array([1.0, -2.0, 3.0, 4.0, 5.0, -6.0], np.float32).view(np.uint8)
     got = run_qmatmul(backend, F32, w, 2, 3, np.array([2.0, -1.0, 0.5, -1.0, 2.0, 1.0], np.float32))
@@ -108,10 +108,10 @@ def test_f32_mode_batched_tokens(backend, dtype, T):
     x = synth.normal_f32(T * k, 200 + T)
     got = run_qmatmul(backend, dtype, raw, rows, k, x, "f32")
     cpu, exact = oracle_f32(dtype, raw, rows, k, x)
-    assert_parity(got, cpu, exact, 1e-5, what=f"dtype={dtype} T={T}")
+    assert_parity(got, cpu, exact, 1e-5, what=f"dtype={dtype} T={T}", correctly_rounded=True)
     # The single-token call (the decode kernel) meets the same bar on token 0.
     one = run_qmatmul(backend, dtype, raw, rows, k, x[:k], "f32")
-    assert_parity(one[0], cpu[0], exact[0], 1e-5, what=f"dtype={dtype} T=1 of {T}")
+    assert_parity(one[0], cpu[0], exact[0], 1e-5, what=f"dtype={dtype} T=1 of {T}", correctly_rounded=True)
 
 
 SHAPES_8B = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]
@@ -124,7 +124,7 @@ def test_q4k_f32_mode_llama3_8b_shapes(backend, shape):
     x = synth.normal_f32(k, 2)
     got = run_qmatmul(backend, Q4K, raw, rows, k, x, "f32")
     cpu, exact = oracle_f32(Q4K, raw, rows, k, x)
-    rate = assert_parity(got, cpu, exact, 1e-5, what=f"Q4_K {shape}")
+    rate = assert_parity(got, cpu, exact, 1e-5, what=f"Q4_K {shape}", correctly_rounded=True)
     print(f"Q4_K {shape}: plain 1e-5/1e-6 pass rate vs sequential oracle {rate:.4f}")
 
 
@@ -141,7 +141,7 @@ def test_q6k_f32_mode_config3_shapes(backend, shape, T):
         r1 = min(rows, r0 + 8192)
         W = npq.dequantize(Q6K, raw[r0 * (k // 256) * 210:r1 * (k // 256) * 210], r1 - r0, k)
         exact[:, r0:r1] = f32_exact(W, x)
-    assert_parity(got, cpu, exact, 1e-5, what=f"Q6_K {shape} T={T}")
+    assert_parity(got, cpu, exact, 1e-5, what=f"Q6_K {shape} T={T}", correctly_rounded=True)
 
 
 # ------------------------------------------------------------ int8 mode ----
@@ -282,7 +282,7 @@ def test_fused_qkv_mixed_dtypes(backend):
     for (dt, r), o, i in zip(specs, outs, range(3)):
         raw = synth.weight(dt, r, k_in, i)
         cpu, exact = oracle_f32(dt, raw, r, k_in, x_h)
-        assert_parity(backend.download_f32(o), cpu, exact, 1e-5)
+        assert_parity(backend.download_f32(o), cpu, exact, 1e-5, correctly_rounded=True)
 
 
 @pytest.mark.parametrize("mode", [0, 1])
@@ -566,7 +566,7 @@ def test_q6k_head_matches_oracle(backend, mode, T, cached):
     cpu, exact = oracle_f32(Q6K, sub, idx.size, k, xq)
     rtol = 1e-3 if mode == "i8" else 1e-5
     rate = assert_parity(got[:, idx], cpu, exact, rtol, atol=1e-5 if mode == "i8" else 1e-6,
-                         what=f"head {mode} T={T} cached={cached}")
+                         what=f"head {mode} T={T} cached={cached}", correctly_rounded=mode == "f32")
     print(f"Q6_K head {mode} T={T} cached={cached}: plain pass rate {rate:.5f}")
     w.buf.close()
 
@@ -623,7 +623,7 @@ def test_raw_and_prepared_storage_agree_with_oracle(backend, dtype, T):
             y = backend.download_f32(yb)
             assert np.all(y[T * rows:] == CANARY), (name, mode)
             if mode == "f32":
-                assert_parity(y[:T * rows], cpu, exact, 1e-5, what=f"{name} f32 dtype={dtype} T={T}")
+                assert_parity(y[:T * rows], cpu, exact, 1e-5, what=f"{name} f32 dtype={dtype} T={T}", correctly_rounded=True)
             else:
                 assert_parity(y[:T * rows], cpu8, exact8, 1e-3, what=f"{name} i8 dtype={dtype} T={T}")
     # The embedding gather reads every storage layout the same way.

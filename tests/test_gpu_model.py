@@ -185,12 +185,21 @@ def test_int8_decode_norm_fusion_matches_separate_norm(backend, gqa):
 # requantized before every GEMV the device quantizes for; the reference's
 # "requantize, then CPU qmatmul" pattern, src/backend/rocm/decode/tests.rs:68-77).
 # Both sides are teacher-forced on the oracle's greedy tokens, so each step's
-# logits come from the same token sequence. They differ by f32 summation
-# order and by the int8 or f16 roundings that such an order difference can
-# flip (one activation quantum of amax/127 in one element); I8_LOGIT_RTOL is
-# the bound on max|dlogit| / max|logit| per step. A composition mistake (a
-# swapped norm, a dropped residual) moves logits by O(1) of that scale.
-I8_LOGIT_RTOL = 1e-2
+# logits come from the same token sequence. Every stage agrees with the
+# oracle to ~1e-6 on identical inputs (test_int8_prefill_stages_match_oracle),
+# but end to end the int8 mode amplifies that: a 1e-6 difference moves a
+# few activations per layer across a rounding boundary, and each such flip
+# changes one value by a whole quantum (amax/127), a GEMV output by ~1e-3
+# relative. On the grouped-query model the two int8 results measured 1.0%
+# apart (RMS) while the int8 oracle is 1.7% from the f32 one: flips are the
+# same size as the quantization error itself. I8_LOGIT_RTOL (max|dlogit| /
+# max|logit| per step) is set at that scale; the stage test carries the
+# tight check, and a composition mistake (a swapped norm, a dropped
+# residual) moves logits by O(1) of max|logit|.
+I8_LOGIT_RTOL = 3e-2
+# Greedy tokens are compared where the oracle's top-2 margin exceeds twice
+# the measured 1% gap.
+I8_TOKEN_MARGIN = 2e-2
 
 
 def teacher_forced(backend, path, prompt, forced, n_gen):
@@ -214,7 +223,7 @@ def test_int8_mode_decode_matches_int8_oracle(backend, tiny, gqa, which, n_promp
     gated gate/up, the residual-storing down projection, the int8 Q6_K head;
     a 20-token prompt takes the per-32 prefill GEMM) against the oracle's
     int8 mode. Greedy tokens must agree wherever the oracle's top-2 margin
-    exceeds twice the bound."""
+    exceeds I8_TOKEN_MARGIN."""
     path = tiny[1] if which == "tiny" else gqa
     vocab = 32000 if which == "tiny" else 2048
     p = synth.tokens(n_prompt, vocab, 2300 + n_prompt)
@@ -230,14 +239,14 @@ def test_int8_mode_decode_matches_int8_oracle(backend, tiny, gqa, which, n_promp
     print(f"int8 e2e {which} prompt {n_prompt}: per-step max|dlogit|/max|logit| {np.array2string(err, precision=2)}")
     assert np.all(err <= I8_LOGIT_RTOL), err
     top2 = np.sort(want, axis=1)[:, -2:]
-    clear = (top2[:, 1] - top2[:, 0]) / np.max(np.abs(want), axis=1) > 2 * I8_LOGIT_RTOL
+    clear = (top2[:, 1] - top2[:, 0]) / np.max(np.abs(want), axis=1) > I8_TOKEN_MARGIN
     assert np.array_equal(got.argmax(axis=1)[clear], toks[clear])
 
 
 def test_int8_batched_decode_matches_int8_oracle(backend, gqa):
     """Batched int8 decode (3 and 8 sequences: row teams and the matrix-core
     batch GEMV) against each sequence's int8-mode oracle run: tokens equal up
-    to the first step whose oracle top-2 margin is within twice the bound
+    to the first step whose oracle top-2 margin is within I8_TOKEN_MARGIN
     (past a near-tie the two greedy paths may part)."""
     r = gguf.Reader(gqa)
     n_gen = 16
@@ -254,7 +263,7 @@ def test_int8_batched_decode_matches_int8_oracle(backend, gqa):
                 want, logits = ffi.llama_run(r, prompts[b], n_gen, kv_f16=True, act_i8=True)
                 top2 = np.sort(logits, axis=1)[:, -2:]
                 tight = np.nonzero((top2[:, 1] - top2[:, 0]) / np.max(np.abs(logits), axis=1)
-                                   <= 2 * I8_LOGIT_RTOL)[0]
+                                   <= I8_TOKEN_MARGIN)[0]
                 upto = tight[0] + 1 if tight.size else n_gen
                 assert np.array_equal(got[b][:upto], want[:upto]), (B, b, got[b].tolist(), want.tolist())
                 checked += upto
@@ -262,6 +271,112 @@ def test_int8_batched_decode_matches_int8_oracle(backend, gqa):
         m.close()
     finally:
         backend.set_act_mode(ACT_F32)
+
+
+def test_int8_prefill_stages_match_oracle(backend, gqa):
+    """The int8 prefill of the grouped-query Q4_K_M model composed stage by
+    stage through the C ABI: every stage's output against the oracle's op
+    applied to that stage's own GPU input (GEMVs on x requantized per 256),
+    within STAGE_RTOL of the stage's largest |value| (measured at 1e-6 or
+    below). The driver's prefill logits must then be exactly this
+    composition's: the Llama driver runs the same int8 stages."""
+    from mdma_amd.backend import AttnSpec, KvView, RopeSpec
+    STAGE_RTOL = 2e-5
+    r = gguf.Reader(gqa)
+    E, H, KVH, hd, F, V, T = 512, 8, 2, 64, 1024, 2048, 8
+    be = backend
+
+    def W(name):
+        t = r.tensors[name]
+        return be.upload_weight(r.bytes_of(name), t.dtype, tuple(t.shape)), t
+
+    def Nh(name):
+        return np.frombuffer(r.bytes_of(name).tobytes(), np.float32).copy()
+
+    def xq(x, k):
+        return np.concatenate([ffi.dequantize_act(*ffi.quantize_act(x[t * k:(t + 1) * k], 256)[:2], 256)
+                               for t in range(x.size // k)])
+
+    def qm(name, x, k):
+        t = r.tensors[name]
+        return ffi.qmatmul(t.dtype, r.bytes_of(name), t.shape[0], t.shape[1], xq(x, k)).reshape(-1)
+
+    def chk(tag, got, want):
+        e = float(np.max(np.abs(got - want)) / np.max(np.abs(want)))
+        assert e <= STAGE_RTOL, f"{tag}: {e:.2e}"
+
+    D = be.download_f32
+    pr = synth.tokens(T, V, 2308)
+    be.set_act_mode(ACT_I8)
+    try:
+        x, xa, normed = be.alloc(T * E * 4), be.alloc(T * E * 4), be.alloc(T * E * 4)
+        q, k, v = be.alloc(T * H * hd * 4), be.alloc(T * KVH * hd * 4), be.alloc(T * KVH * hd * 4)
+        ao, proj = be.alloc(T * H * hd * 4), be.alloc(T * E * 4)
+        g, u, act = be.alloc(T * F * 4), be.alloc(T * F * 4), be.alloc(T * F * 4)
+        te, tt = W("token_embd.weight")
+        be.embed(te, pr, x)
+        assert np.array_equal(D(x), ffi.embed(tt.dtype, r.bytes_of("token_embd.weight"), V, E, pr).reshape(-1))
+        for i in range(2):
+            pre = f"blk.{i}."
+            wn = Nh(pre + "attn_norm.weight")
+            if i == 0:
+                xin = D(x)
+                be.rmsnorm(be.f32_buf(wn), x, normed, 1e-5)
+                chk(f"L{i} rmsnorm", D(normed), ffi.rmsnorm(wn, xin, 1e-5))
+            else:
+                a_, b_ = D(x), D(proj)
+                be.add_rmsnorm(be.f32_buf(wn), x, proj, xa, normed, 1e-5)
+                x, xa = xa, x
+                s_, y_ = ffi.add_rmsnorm(wn, a_, b_, 1e-5)
+                assert np.array_equal(D(x), s_)
+                chk(f"L{i} add_rmsnorm", D(normed), y_)
+            nin = D(normed)
+            names = [pre + n for n in ("attn_q.weight", "attn_k.weight", "attn_v.weight")]
+            ws = [W(n)[0] for n in names]
+            be.qmatmul_qkv(ws[0], ws[1], ws[2], normed, q, k, v)
+            for n, ob in zip(names, (q, k, v)):
+                chk(f"L{i} {n}", D(ob), qm(n, nin, E))
+            qh, kh = D(q), D(k)
+            kc, vc = be.alloc(T * KVH * hd * 2), be.alloc(T * KVH * hd * 2)
+            be.rope_kv_write(q, k, v, kc, vc, 0, 0, T, RopeSpec(hd, 500000.0), T * KVH * hd)
+            qr, kr = ffi.rope(qh, kh, 0, T, hd, 500000.0)
+            assert np.array_equal(D(q), qr)
+            kcache = be.download(kc, 0, T * KVH * hd * 2).view(np.float16).astype(np.float32)
+            vcache = be.download(vc, 0, T * KVH * hd * 2).view(np.float16).astype(np.float32)
+            assert np.array_equal(kcache, kr.astype(np.float16).astype(np.float32))
+            be.attn(q, KvView(kc, vc, T), AttnSpec(hd, H, KVH), ao)
+            chk(f"L{i} attn", D(ao), ffi.attention(D(q), kcache, vcache, T, hd, H, KVH))
+            aoh = D(ao)
+            be.qmatmul(W(pre + "attn_output.weight")[0], ao, proj)
+            chk(f"L{i} o", D(proj), qm(pre + "attn_output.weight", aoh, E))
+            fn = Nh(pre + "ffn_norm.weight")
+            a_, b_ = D(x), D(proj)
+            be.add_rmsnorm(be.f32_buf(fn), x, proj, xa, normed, 1e-5)
+            x, xa = xa, x
+            chk(f"L{i} ffn norm", D(normed), ffi.add_rmsnorm(fn, a_, b_, 1e-5)[1])
+            nin = D(normed)
+            be.ffn_gate_up(W(pre + "ffn_gate.weight")[0], W(pre + "ffn_up.weight")[0], normed, g, u, act)
+            chk(f"L{i} gate_up", D(act), ffi.silu_mul(qm(pre + "ffn_gate.weight", nin, E),
+                                                        qm(pre + "ffn_up.weight", nin, E)))
+            ah = D(act)
+            be.qmatmul(W(pre + "ffn_down.weight")[0], act, proj)
+            chk(f"L{i} down", D(proj), qm(pre + "ffn_down.weight", ah, F))
+        a_, b_ = D(x), D(proj)
+        be.add_rmsnorm(be.f32_buf(Nh("output_norm.weight")), x, proj, xa, normed, 1e-5)
+        last = D(normed)[(T - 1) * E:]
+        chk("final norm", last, ffi.add_rmsnorm(Nh("output_norm.weight"), a_, b_, 1e-5)[1][(T - 1) * E:])
+        lg = be.alloc(V * 4)
+        be.qmatmul(W("output.weight")[0], be.f32_buf(last), lg)
+        manual = D(lg)
+        chk("head", manual, qm("output.weight", last, E))
+        m = Model(be, gqa)
+        s = m.session(T + 1, 1, T)
+        driver = s.prefill(pr, 0)
+        s.close()
+        m.close()
+    finally:
+        be.set_act_mode(ACT_F32)
+    assert np.array_equal(driver, manual)
 
 
 def test_memory_plan_and_limits(backend, tiny):
