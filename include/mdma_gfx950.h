@@ -218,6 +218,17 @@ int mdma_gfx950_block_dot_i32(mdma_ctx *ctx, const mdma_qweight *w, const mdma_b
 /* Explicit-mode GEMVs, independent of the context's mode. */
 int mdma_gfx950_qmatmul_f32(mdma_ctx *ctx, const mdma_qweight *w, const mdma_buf *x, mdma_buf *y);
 int mdma_gfx950_qmatmul_i8(mdma_ctx *ctx, const mdma_qweight *w, const mdma_buf *x, mdma_buf *y);
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): mdma_gfx950_qmatmul_i8 with the scratch its int8 routes
+ * take -- x's per-256 int8 form, or the prefill GEMM's per-32 inputs (the
+ * GEMM then runs unsplit) -- in the library's static device array of 8 MiB
+ * per GPU instead of the context's buffers. It calls no hipMalloc or
+ * hipFree; an x needing more than 8 MiB of scratch (about 6.1 million
+ * values) fails with MDMA_ERR_BUFFER_BUDGET before anything runs. Calls
+ * through one context run in its stream's order; calls from two contexts on
+ * one GPU share the array and race. */
+int mdma_gfx950_qmatmul_i8_noalloc(mdma_ctx *ctx, const mdma_qweight *w, const mdma_buf *x, mdma_buf *y);
 
 /* Stream capture into a replayable HIP graph (the reference's graph decode
  * executor, src/backend/rocm/graph.rs:105-262, captures forward_device the

@@ -76,6 +76,7 @@ _SIGS = {
     "upload": [_P, _P, _U64, _P, _U64], "download": [_P, _P, _U64, _P, _U64],
     "copy": [_P, _P, _U64, _P, _U64, _U64], "upload_weight": [_P, _P, _U64, C.c_int, _I32, _U64, _U64, _P],
     "qmatmul": [_P, _P, _P, _P], "qmatmul_f32": [_P, _P, _P, _P], "qmatmul_i8": [_P, _P, _P, _P],
+    "qmatmul_i8_noalloc": [_P, _P, _P, _P],
     "qmatmul_qkv": [_P, _P, _P, _P, _P, _P, _P, _P], "ffn_gate_up": [_P, _P, _P, _P, _P, _P, _P],
     "embed": [_P, _P, _P, _U64, _P], "rmsnorm": [_P, _P, _P, _P, _F],
     "add_rmsnorm": [_P, _P, _P, _P, _P, _P, _F], "add": [_P, _P, _P, _P], "silu_mul": [_P, _P, _P, _P],
@@ -307,6 +308,11 @@ class Gfx950Backend:
 
     def qmatmul_i8(self, w: QWeight, x: Buf, y: Buf):
         _check(lib().mdma_gfx950_qmatmul_i8(self.ctx, C.byref(w.c()), x.handle, y.handle))
+
+    def qmatmul_i8_noalloc(self, w: QWeight, x: Buf, y: Buf):
+        """qmatmul_i8 with its scratch in the library's static device array:
+        no device allocation (callers that cannot allocate)."""
+        _check(lib().mdma_gfx950_qmatmul_i8_noalloc(self.ctx, C.byref(w.c()), x.handle, y.handle))
 
     def qmatmul_qkv(self, wq: QWeight, wk: QWeight, wv: QWeight, x: Buf, q: Buf, k: Buf, v: Buf):
         _check(lib().mdma_gfx950_qmatmul_qkv(self.ctx, C.byref(wq.c()), C.byref(wk.c()), C.byref(wv.c()),

@@ -117,17 +117,7 @@ void run_gemv(mdma_ctx *ctx, int mode, const GemvJob *jobs, int n, const float *
 }
 
 int qmatmul_mode(mdma_ctx *ctx, const mdma_qweight *w, const mdma_buf *x, mdma_buf *y, int mode) {
-  return guarded([&] {
-    need(ctx, "qmatmul");
-    std::lock_guard<std::recursive_mutex> g(ctx->lock);
-    uint64_t T = matmul_tokens(w, x, y, "qmatmul");
-    same_ctx(ctx, w->buf, "qmatmul");
-    same_ctx(ctx, x, "qmatmul");
-    same_ctx(ctx, y, "qmatmul");
-    GemvJob j = job_of(w, y);
-    run_gemv(ctx, mode < 0 ? ctx->act_mode : mode, &j, 1, reinterpret_cast<const float *>(x->ptr), T);
-    q8_invalidate_range(ctx, y->ptr, y->len);
-  });
+  return guarded([&] { qmatmul_run(ctx, w, x, y, mode); });
 }
 
 // rope angle table on the host with the CPU backend's formula (apply_rope,
@@ -167,6 +157,18 @@ void check_rope(const mdma_rope_spec *spec, uint64_t qe, uint64_t ke, uint64_t n
 
 namespace mdma {
 
+void qmatmul_run(mdma_ctx *ctx, const mdma_qweight *w, const mdma_buf *x, mdma_buf *y, int mode) {
+  need(ctx, "qmatmul");
+  std::lock_guard<std::recursive_mutex> g(ctx->lock);
+  uint64_t T = matmul_tokens(w, x, y, "qmatmul");
+  same_ctx(ctx, w->buf, "qmatmul");
+  same_ctx(ctx, x, "qmatmul");
+  same_ctx(ctx, y, "qmatmul");
+  GemvJob j = job_of(w, y);
+  run_gemv(ctx, mode < 0 ? ctx->act_mode : mode, &j, 1, reinterpret_cast<const float *>(x->ptr), T);
+  q8_invalidate_range(ctx, y->ptr, y->len);
+}
+
 void fail(int code, const std::string &msg) { throw Error{code, msg}; }
 
 void set_last_error(const std::string &msg) { g_last_error = msg; }
@@ -180,6 +182,7 @@ void hip_check(hipError_t e, const char *what) {
 
 void no_capture(mdma_ctx *ctx, const char *what) {
   if (ctx->capturing) fail(MDMA_ERR_BACKEND, std::string(what) + " synchronizes and cannot run under graph capture");
+  if (ctx->fixed_scratch) fail(MDMA_ERR_BACKEND, std::string(what) + " would allocate inside an allocation-free call");
 }
 
 char *scratch(mdma_ctx *ctx, uint64_t bytes) {
@@ -337,6 +340,14 @@ int mdma_gfx950_create(int device, mdma_ctx **out) {
     }
     c->host_ids = static_cast<uint32_t *>(h);
     c->host_ids_cap = 4096;
+    try {
+      noalloc_setup(c);
+    } catch (...) {
+      (void)hipHostFree(c->host_ids);
+      (void)hipStreamDestroy(c->stream);
+      delete c;
+      throw;
+    }
     *out = c;
   });
 }

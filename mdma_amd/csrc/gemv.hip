@@ -791,10 +791,24 @@ bool is_i8_dtype(int32_t dt) { return dt == DT_Q4_K || dt == DT_Q6_K || dt == DT
 // The int8 activations of x [T, n_in] in the context's activation buffer,
 // quantized now unless that buffer already holds exactly this x (same
 // pointer and shape, no write since; see q8_invalidate).
+uint64_t q8_slot_bytes(uint64_t n) {
+  return (n + 255) / 256 * 256 + (n / 256 * 4 + 255) / 256 * 256 + n / 16 * 4 + 256;
+}
+
+uint64_t gemm_input_bytes(uint64_t n) {
+  return (n + 255) / 256 * 256 + (n / 32 * 4 + 255) / 256 * 256 + (n / 16 * 4 + 255) / 256 * 256;
+}
+
 void q8_slots(mdma_ctx *ctx, uint64_t T, uint64_t n_in, int8_t **qx, float **dx, int32_t **s16) {
   const uint64_t n = T * n_in;
   const uint64_t qb = (n + 255) / 256 * 256, db = (n / 256 * 4 + 255) / 256 * 256;
-  char *s = q8_buffer(ctx, qb + db + n / 16 * 4 + 256);
+  char *s;
+  if (ctx->fixed_scratch) {  // an allocation-free call: its fixed buffer
+    if (q8_slot_bytes(n) > ctx->fixed_cap) fail(MDMA_ERR_BUFFER_BUDGET, "int8 activations exceed the fixed scratch");
+    s = ctx->fixed_scratch;
+  } else {
+    s = q8_buffer(ctx, q8_slot_bytes(n));
+  }
   *qx = reinterpret_cast<int8_t *>(s);
   *dx = reinterpret_cast<float *>(s + qb);
   *s16 = reinterpret_cast<int32_t *>(s + qb + db);
@@ -893,7 +907,14 @@ static bool try_gemm_i8(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const fl
   }
   // Under stream capture the scratch cannot grow: past its size, unsplit.
   if (ctx->capturing && qb + db + sb + pd * 8 > ctx->scratch_cap) pd = 0;
-  char *s = scratch(ctx, qb + db + sb + pd * 8);
+  char *s;
+  if (ctx->fixed_scratch) {  // an allocation-free call: unsplit, inputs in its fixed buffer
+    pd = 0;
+    if (qb + db + sb > ctx->fixed_cap) fail(MDMA_ERR_BUFFER_BUDGET, "GEMM inputs exceed the fixed scratch");
+    s = ctx->fixed_scratch;
+  } else {
+    s = scratch(ctx, qb + db + sb + pd * 8);
+  }
   int8_t *qx = reinterpret_cast<int8_t *>(s);
   float *dx = reinterpret_cast<float *>(s + qb);
   int32_t *s16 = reinterpret_cast<int32_t *>(s + qb + db);

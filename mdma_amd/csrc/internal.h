@@ -100,6 +100,14 @@ struct mdma_ctx {
   double *ssq = nullptr;  // per-workgroup sums of squares of a residual-stream GEMV (norm fusion)
   uint64_t ssq_cap = 0;
   uint32_t team_grid = 0;  // workgroups of the last row-team launch
+  // This device's copy of the library's static scratch array (noalloc.hip),
+  // from hipGetSymbolAddress at create.
+  char *static_scratch = nullptr;
+  // Set only for the duration of an allocation-free call: the int8
+  // activations and GEMM inputs go to this fixed buffer, and any growth of
+  // a context buffer fails instead of allocating.
+  char *fixed_scratch = nullptr;
+  uint64_t fixed_cap = 0;
 };
 
 struct mdma_graph {
@@ -108,6 +116,17 @@ struct mdma_graph {
 };
 
 namespace mdma {
+
+// Backend::qmatmul with its shape rules, in activation mode `mode` (-1: the
+// context's); throws Error. The lock is taken inside.
+void qmatmul_run(mdma_ctx *ctx, const mdma_qweight *w, const mdma_buf *x, mdma_buf *y, int mode);
+// Per-device set-up of the allocation-free entry point (noalloc.hip): the
+// device address of this device's static scratch, kept in ctx.
+void noalloc_setup(mdma_ctx *ctx);
+// Bytes of int8 activation slots (per-256 scales, sums of 16) for n values.
+uint64_t q8_slot_bytes(uint64_t n);
+// Bytes of the prefill GEMM's per-32 activations for n values (unsplit).
+uint64_t gemm_input_bytes(uint64_t n);
 
 // Scratch space of at least `bytes` on the context's device; growing it
 // synchronizes the stream (callers hold the context lock).

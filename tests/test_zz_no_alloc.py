@@ -1,0 +1,98 @@
+"""The allocation-free int8 qmatmul (mdma_gfx950_qmatmul_i8_noalloc) against
+the allocating entry point it varies (mdma_gfx950_qmatmul_i8), through the
+C ABI on the GPU: two calls in a row, the second with a smaller input, and
+the other int8 routes (row teams, the matrix-core batch GEMV, the prefill
+GEMM, which runs unsplit here), plus the size limit.
+"""
+import numpy as np
+import pytest
+
+import npq
+from conftest import assert_parity, f32_exact
+from mdma_amd import backend as backend_mod
+from mdma_amd import synth
+from oracle import ffi
+
+pytestmark = pytest.mark.gpu
+Q8, Q4K, Q6K = 8, 12, 14
+CANARY = np.float32(123456.25)
+
+
+def both(be, w, x_h, rows):
+    """(noalloc output, qmatmul_i8 output), each into a canary-tailed y."""
+    T = x_h.size // w.shape[1]
+    outs = []
+    for fn in (be.qmatmul_i8_noalloc, be.qmatmul_i8):
+        xb = be.f32_buf(x_h)  # a fresh buffer: no cached int8 form
+        yb = be.f32_buf(np.full(T * rows + 8, CANARY, np.float32))
+        fn(w, xb, yb)
+        y = be.download_f32(yb)
+        assert np.all(y[T * rows:] == CANARY), "wrote past the output"
+        outs.append(y[:T * rows])
+        xb.close()
+        yb.close()
+    return outs
+
+
+def test_noalloc_equals_allocating_entry_two_calls(backend):
+    # Call 1: Q4_K 4096x4096, 3 tokens (row teams over int8 x in the array).
+    w1 = backend.upload_weight(synth.weight(Q4K, 4096, 4096, 1), Q4K, (4096, 4096))
+    a, b = both(backend, w1, synth.normal_f32(3 * 4096, 2), 4096)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    # Call 2, smaller: Q6_K 1024x4096, 2 tokens.
+    w2 = backend.upload_weight(synth.weight(Q6K, 1024, 4096, 3), Q6K, (1024, 4096))
+    a, b = both(backend, w2, synth.normal_f32(2 * 4096, 4), 1024)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype,rows,k,T", [(Q8, 300, 1024, 1), (Q4K, 640, 4096, 8), (Q6K, 4096, 14336, 5)])
+def test_noalloc_routes_bit_exact(backend, dtype, rows, k, T):
+    """One token (Q8_0: x quantized separately; K-quants quantize in the
+    kernel's prologue) and the batch GEMV (5..16 tokens, matrix cores) give
+    the allocating entry point's bits."""
+    raw = synth.weight(dtype, rows, k, 10 + T)
+    w = backend.upload_weight(raw, dtype, (rows, k))
+    a, b = both(backend, w, synth.normal_f32(T * k, 11 + T), rows)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [Q8, Q4K, Q6K])
+def test_noalloc_prefill_gemm_matches_oracle(backend, dtype):
+    """24 tokens: the prefill GEMM route, unsplit here (its split-K partials
+    would need scratch), against the oracle's per-32 requantized qmatmul at
+    the int8 bar, and against the allocating entry point's result."""
+    T, k, rows = 24, 1024, 384
+    raw = synth.weight(dtype, rows, k, 20)
+    x = synth.normal_f32(T * k, 21)
+    w = backend.upload_weight(raw, dtype, (rows, k))
+    a, b = both(backend, w, x, rows)
+    q, d, _ = ffi.quantize_act(x, 32)
+    xq = ffi.dequantize_act(q, d, 32)
+    cpu = ffi.qmatmul(dtype, raw, rows, k, xq)
+    exact = f32_exact(npq.dequantize(dtype, raw, rows, k), xq)
+    atol = 1e-5 if dtype == Q6K else 1e-6
+    assert_parity(a, cpu, exact, 1e-3, atol=atol, what=f"noalloc gemm {dtype}")
+    assert_parity(b, cpu, exact, 1e-3, atol=atol, what=f"alloc gemm {dtype}")
+
+
+def test_noalloc_rejects_oversize_and_keeps_cached_activations(backend):
+    k, rows = 4096, 64
+    w = backend.upload_weight(synth.weight(Q4K, rows, k, 30), Q4K, (rows, k))
+    big = backend.alloc(2048 * k * 4)  # 8.4 M values: past the 8 MiB array
+    y = backend.alloc(2048 * rows * 4)
+    with pytest.raises(backend_mod.BufferBudget):
+        backend.qmatmul_i8_noalloc(w, big, y)
+    # An rmsnorm in the int8 mode caches its output's int8 form; a noalloc
+    # call on another x in between must leave that cache usable.
+    backend.set_act_mode(backend_mod.ACT_I8)
+    try:
+        xn = backend.alloc(k * 4)
+        backend.rmsnorm(backend.f32_buf(np.ones(k, np.float32)), backend.f32_buf(synth.normal_f32(k, 31)), xn, 1e-5)
+        other, yo = backend.f32_buf(synth.normal_f32(2 * k, 32)), backend.alloc(2 * rows * 4)
+        backend.qmatmul_i8_noalloc(w, other, yo)
+        y1, y2 = backend.alloc(rows * 4), backend.alloc(rows * 4)
+        backend.qmatmul(w, xn, y1)  # reads the cached int8 form of xn
+        backend.qmatmul(w, backend.f32_buf(backend.download_f32(xn)), y2)  # quantizes afresh
+        assert np.array_equal(backend.download_f32(y1), backend.download_f32(y2))
+    finally:
+        backend.set_act_mode(backend_mod.ACT_F32)
