@@ -53,7 +53,10 @@ typedef enum { MDMA_POOL_WEIGHTS = 0, MDMA_POOL_KV = 1, MDMA_POOL_SCRATCH = 2 } 
  * rearranged losslessly into 16-byte planes indexed by the 64-column unit
  * (32 for Q8_0) a lane owns, so every wave load reads 1 KiB of contiguous
  * memory. Each block keeps its byte count; rows are padded to 16 bytes. */
-typedef enum { MDMA_LAYOUT_GGUF = 0, MDMA_LAYOUT_GFX950 = 1 } mdma_layout;
+typedef enum { MDMA_LAYOUT_GGUF = 0, MDMA_LAYOUT_GFX950 = 1, MDMA_LAYOUT_ROCM_Q4K_V3 = 2 } mdma_layout;
+
+/* MemoryDomain (src/memory/buffers.rs:5-10): the two ledgers of a BufferBudget. */
+typedef enum { MDMA_DOMAIN_DEVICE = 0, MDMA_DOMAIN_HOST = 1 } mdma_memory_domain;
 
 /* Activation mode of the decode GEMV: f32 activations (exact parity mode) or
  * int8 activations quantized per 256 with an f32 scale. The reference's
@@ -111,10 +114,19 @@ uint64_t mdma_gfx950_max_head_dim(mdma_ctx *ctx);
 uint64_t mdma_gfx950_kv_elem_bytes(mdma_ctx *ctx);
 /* Backend::join_execution (:197): wait for all queued device work. */
 int mdma_gfx950_join_execution(mdma_ctx *ctx);
-/* Backend::set_buffer_budget (:352) with BufferBudget's per-pool device
- * quotas (src/memory/buffers.rs:32-99); UINT64_MAX = unlimited. */
-int mdma_gfx950_set_buffer_budget(mdma_ctx *ctx, uint64_t weights, uint64_t kv, uint64_t scratch);
-int mdma_gfx950_buffer_usage(mdma_ctx *ctx, int pool, uint64_t *used, uint64_t *limit);
+/* Backend::set_buffer_budget (:352) with a BufferBudget (src/memory/buffers.rs:32-99):
+ * quotas for the device and host domains, UINT64_MAX for none (BufferBudget::new's
+ * None), 0 to forbid a domain. Installed only while nothing is charged to the
+ * context's ledger (MDMA_ERR_BACKEND otherwise, as BufferBudget::replace). Charged
+ * to the device domain: every buffer from alloc / upload_weight (the requested
+ * bytes, at least one) and the context's own device scratch (int8 activations,
+ * partial results, counters, the RoPE table) as it grows; a charge that would
+ * pass the quota fails with MDMA_ERR_BUFFER_BUDGET before anything is allocated,
+ * and a buffer whose hipFree fails stays charged. The library allocates no host
+ * buffers after create, so the host domain stays at zero. */
+int mdma_gfx950_set_buffer_budget(mdma_ctx *ctx, uint64_t device_bytes, uint64_t host_bytes);
+/* BufferBudget::used / limit of one domain (mdma_memory_domain). */
+int mdma_gfx950_buffer_usage(mdma_ctx *ctx, int domain, uint64_t *used, uint64_t *limit);
 /* Extra: select the decode GEMV activation mode (default MDMA_ACT_F32). */
 int mdma_gfx950_set_act_mode(mdma_ctx *ctx, int mode);
 /* Extra: in the int8 mode's one-token decode, fuse each layer's attention
@@ -138,15 +150,26 @@ int mdma_gfx950_upload(mdma_ctx *ctx, mdma_buf *dst, uint64_t offset, const void
 int mdma_gfx950_download(mdma_ctx *ctx, const mdma_buf *src, uint64_t offset, void *dst, uint64_t len);
 int mdma_gfx950_copy(mdma_ctx *ctx, const mdma_buf *src, uint64_t src_off, mdma_buf *dst,
                      uint64_t dst_off, uint64_t len);
-/* Backend::upload_weight (src/backend.rs:228-237). `layout` names the format
- * of `bytes`. GGUF Q4_K / Q6_K / Q8_0 bytes are packed into the prepared
- * layout on the way (the buffer then holds prepared rows, as a buffer the
- * reference's HIP backend uploads with its packed flag does,
- * src/backend/rocm.rs:401-412); MDMA_LAYOUT_GFX950 bytes (from
- * mdma_gfx950_pack_weight, e.g. a model cache) are stored as they are. The
- * dtype and shape say what the bytes hold. */
-int mdma_gfx950_upload_weight(mdma_ctx *ctx, const void *bytes, uint64_t len, int layout,
-                              int32_t dtype, uint64_t rows, uint64_t cols, mdma_buf **out);
+/* Backend::upload_weight (src/backend.rs:228-237): the trait's (bytes, layout).
+ * MDMA_LAYOUT_GGUF bytes are stored raw and marked for repacking: the first op
+ * that reads the buffer as a Q4_K / Q6_K / Q8_0 QWeight of matching size
+ * repacks it on the device into the prepared layout, in place of the raw bytes
+ * (a buffer the reference's HIP backend uploads with its packed flag is read
+ * the same way, src/backend/rocm.rs:401-412). Until then, and where that op
+ * may not allocate (graph capture, the allocation-free call, a full budget),
+ * the raw-layout kernels read it. MDMA_LAYOUT_GFX950 bytes (from
+ * mdma_gfx950_pack_weight, e.g. a model cache) are stored as they are.
+ * MDMA_LAYOUT_ROCM_Q4K_V3 (the reference ROCm backend's packed Q4_K,
+ * src/cache/layout.rs:10-38) fails with MDMA_ERR_NOT_IMPLEMENTED, as the
+ * trait's default does for layouts a backend does not read. */
+int mdma_gfx950_upload_weight(mdma_ctx *ctx, const void *bytes, uint64_t len, int layout, mdma_buf **out);
+/* Extra, for loaders that know the tensor: upload_weight with the dtype and
+ * [rows, cols] given, so GGUF Q4_K / Q6_K / Q8_0 bytes are packed into the
+ * prepared layout on the host before the upload (no raw copy on the device). */
+int mdma_gfx950_upload_weight_typed(mdma_ctx *ctx, const void *bytes, uint64_t len, int layout,
+                                    int32_t dtype, uint64_t rows, uint64_t cols, mdma_buf **out);
+/* Extra: the layout a buffer holds now (mdma_layout), -1 for a null buffer. */
+int mdma_gfx950_buf_layout(const mdma_buf *buf);
 /* Host-side packing into / out of the prepared layout (pack_q4k of
  * src/cache/layout.rs:40-79 is the reference's counterpart): bytes of a
  * prepared [rows, cols] weight (0 if the dtype has no prepared layout), and
@@ -234,7 +257,12 @@ int mdma_gfx950_qmatmul_i8_noalloc(mdma_ctx *ctx, const mdma_qweight *w, const m
  * executor, src/backend/rocm/graph.rs:105-262, captures forward_device the
  * same way). Between begin and end, launches are recorded, not run; calls
  * that must synchronize (upload, download, scratch growth) fail with
- * MDMA_ERR_BACKEND instead. */
+ * MDMA_ERR_BACKEND instead. A graph holds the device addresses its launches
+ * used: graph_launch fails with MDMA_ERR_BACKEND once the context has
+ * replaced any buffer of its own since the capture (scratch growth, the
+ * repack of a weight from the trait-shaped upload_weight); reserve_scratch
+ * before capturing and capture again after. Buffers the caller frees must
+ * outlive the graphs that use them. */
 typedef struct mdma_graph mdma_graph;
 int mdma_gfx950_graph_begin(mdma_ctx *ctx);
 int mdma_gfx950_graph_end(mdma_ctx *ctx, mdma_graph **out);

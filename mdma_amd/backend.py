@@ -22,7 +22,8 @@ from .synth import BLOCK_SIZE, TYPE_SIZE, GGML_F32, GGML_F16, GGML_Q8_0, GGML_Q4
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmdma_gfx950.so")
 
 POOL_WEIGHTS, POOL_KV, POOL_SCRATCH = 0, 1, 2
-LAYOUT_GGUF, LAYOUT_GFX950 = 0, 1
+LAYOUT_GGUF, LAYOUT_GFX950, LAYOUT_ROCM_Q4K_V3 = 0, 1, 2
+DOMAIN_DEVICE, DOMAIN_HOST = 0, 1
 ACT_F32, ACT_I8 = 0, 1
 
 ERROR_NAMES = {1: "ContextLimit", 2: "ShapeMismatch", 3: "NotImplemented", 4: "UnsupportedModel",
@@ -69,12 +70,13 @@ _SIGS = {
     "create": [C.c_int, _P], "destroy": [_P], "last_error": [],
     "device_label": [_P, C.c_char_p, C.c_size_t], "total_device_bytes": [_P],
     "available_device_bytes": [_P, _P], "supports_weight_dtype": [_P, _I32], "max_head_dim": [_P],
-    "kv_elem_bytes": [_P], "join_execution": [_P], "set_buffer_budget": [_P, _U64, _U64, _U64],
+    "kv_elem_bytes": [_P], "join_execution": [_P], "set_buffer_budget": [_P, _U64, _U64],
     "buffer_usage": [_P, C.c_int, _P, _P], "set_act_mode": [_P, C.c_int],
     "set_norm_fusion": [_P, C.c_int], "stream": [_P],
     "alloc": [_P, _U64, C.c_int, _P], "free": [_P], "buf_len": [_P], "buf_view": [_P, _U64, _U64, _P],
     "upload": [_P, _P, _U64, _P, _U64], "download": [_P, _P, _U64, _P, _U64],
-    "copy": [_P, _P, _U64, _P, _U64, _U64], "upload_weight": [_P, _P, _U64, C.c_int, _I32, _U64, _U64, _P],
+    "copy": [_P, _P, _U64, _P, _U64, _U64], "upload_weight": [_P, _P, _U64, C.c_int, _P],
+    "upload_weight_typed": [_P, _P, _U64, C.c_int, _I32, _U64, _U64, _P], "buf_layout": [_P],
     "qmatmul": [_P, _P, _P, _P], "qmatmul_f32": [_P, _P, _P, _P], "qmatmul_i8": [_P, _P, _P, _P],
     "qmatmul_i8_noalloc": [_P, _P, _P, _P],
     "qmatmul_qkv": [_P, _P, _P, _P, _P, _P, _P, _P], "ffn_gate_up": [_P, _P, _P, _P, _P, _P, _P],
@@ -241,12 +243,16 @@ class Gfx950Backend:
     def join_execution(self):
         _check(lib().mdma_gfx950_join_execution(self.ctx))
 
-    def set_buffer_budget(self, weights=2**64 - 1, kv=2**64 - 1, scratch=2**64 - 1):
-        _check(lib().mdma_gfx950_set_buffer_budget(self.ctx, weights, kv, scratch))
+    def set_buffer_budget(self, device=None, host=None):
+        """Backend::set_buffer_budget with BufferBudget::new(device, host):
+        None tracks without a quota, 0 forbids the domain."""
+        unl = 2**64 - 1
+        _check(lib().mdma_gfx950_set_buffer_budget(self.ctx, unl if device is None else device,
+                                                   unl if host is None else host))
 
-    def buffer_usage(self, pool: int):
+    def buffer_usage(self, domain: int):
         u, l = C.c_uint64(), C.c_uint64()
-        _check(lib().mdma_gfx950_buffer_usage(self.ctx, pool, C.byref(u), C.byref(l)))
+        _check(lib().mdma_gfx950_buffer_usage(self.ctx, domain, C.byref(u), C.byref(l)))
         return u.value, l.value
 
     def set_act_mode(self, mode: int):
@@ -286,11 +292,26 @@ class Gfx950Backend:
         _check(lib().mdma_gfx950_copy(self.ctx, src.handle, src_off, dst.handle, dst_off, length))
 
     def upload_weight(self, raw, dtype: int, shape, layout: int = LAYOUT_GGUF) -> QWeight:
+        """upload_weight with the tensor's dtype and [rows, cols] given
+        (mdma_gfx950_upload_weight_typed): GGUF K-quant / Q8_0 bytes are
+        packed into the prepared layout on the host."""
         a = np.ascontiguousarray(raw).view(np.uint8).reshape(-1)
         h = C.c_void_p()
-        _check(lib().mdma_gfx950_upload_weight(self.ctx, a.ctypes.data, a.nbytes, layout, dtype, shape[0],
-                                               shape[1], C.byref(h)))
+        _check(lib().mdma_gfx950_upload_weight_typed(self.ctx, a.ctypes.data, a.nbytes, layout, dtype, shape[0],
+                                                     shape[1], C.byref(h)))
         return QWeight(dtype, tuple(shape), Buf(h.value, self))
+
+    def upload_weight_bytes(self, raw, layout: int = LAYOUT_GGUF) -> Buf:
+        """Backend::upload_weight(bytes, layout) as the trait declares it
+        (src/backend.rs:228-237): no dtype or shape; GGUF bytes are repacked
+        on the device by the first op that reads them as a QWeight."""
+        a = np.ascontiguousarray(raw).view(np.uint8).reshape(-1)
+        h = C.c_void_p()
+        _check(lib().mdma_gfx950_upload_weight(self.ctx, a.ctypes.data, a.nbytes, layout, C.byref(h)))
+        return Buf(h.value, self)
+
+    def buf_layout(self, buf: Buf) -> int:
+        return int(lib().mdma_gfx950_buf_layout(buf.handle))
 
     def f32_buf(self, values, pool: int = POOL_SCRATCH) -> Buf:
         a = np.ascontiguousarray(values, dtype=np.float32).reshape(-1)

@@ -160,6 +160,7 @@ namespace mdma {
 void qmatmul_run(mdma_ctx *ctx, const mdma_qweight *w, const mdma_buf *x, mdma_buf *y, int mode) {
   need(ctx, "qmatmul");
   std::lock_guard<std::recursive_mutex> g(ctx->lock);
+  prepare_weight(ctx, w);
   uint64_t T = matmul_tokens(w, x, y, "qmatmul");
   same_ctx(ctx, w->buf, "qmatmul");
   same_ctx(ctx, x, "qmatmul");
@@ -167,6 +168,39 @@ void qmatmul_run(mdma_ctx *ctx, const mdma_qweight *w, const mdma_buf *x, mdma_b
   GemvJob j = job_of(w, y);
   run_gemv(ctx, mode < 0 ? ctx->act_mode : mode, &j, 1, reinterpret_cast<const float *>(x->ptr), T);
   q8_invalidate_range(ctx, y->ptr, y->len);
+}
+
+void prepare_weight(mdma_ctx *ctx, const mdma_qweight *w) {
+  if (!w || !w->buf || !w->buf->repack_pending) return;
+  mdma_buf *b = const_cast<mdma_buf *>(w->buf);  // the representation changes, not the weight
+  if (!b->owner || b->ctx != ctx || !gfx950_layout_dtype(w->dtype)) return;
+  const uint64_t bs = block_size(w->dtype);
+  if (!w->rows || !w->cols || w->cols % bs || b->len != w->rows * (w->cols / bs) * type_size(w->dtype))
+    return;  // not this weight's raw bytes: the shape rules report it
+  if (ctx->capturing || ctx->fixed_scratch) return;  // no allocation now: the raw kernels read it
+  const uint64_t n = w->rows * gfx950_row_bytes(w->dtype, w->cols);
+  mdma_buf *p = nullptr;
+  if (mdma_gfx950_alloc(ctx, n, MDMA_POOL_WEIGHTS, &p)) return;  // no room in the budget or on the device: stays raw
+  try {
+    launch_repack(ctx, w->dtype, w->rows, w->cols, reinterpret_cast<const uint8_t *>(b->ptr),
+                  reinterpret_cast<uint8_t *>(p->ptr));
+  } catch (...) {
+    mdma_gfx950_free(p);
+    throw;
+  }
+  // The prepared copy takes the raw buffer's place (free drains the stream
+  // first, so the repack has finished reading the raw bytes). A graph
+  // captured while the weight was raw holds the freed address: the epoch
+  // makes it refuse to replay.
+  ctx->buf_epoch++;
+  std::swap(b->ptr, p->ptr);
+  std::swap(b->len, p->len);
+  std::swap(b->charged, p->charged);
+  b->layout = MDMA_LAYOUT_GFX950;
+  b->repack_pending = false;
+  p->repack_pending = false;
+  int st = mdma_gfx950_free(p);
+  if (st) fail(st, g_last_error);
 }
 
 void fail(int code, const std::string &msg) { throw Error{code, msg}; }
@@ -185,83 +219,89 @@ void no_capture(mdma_ctx *ctx, const char *what) {
   if (ctx->fixed_scratch) fail(MDMA_ERR_BACKEND, std::string(what) + " would allocate inside an allocation-free call");
 }
 
+void budget_charge(mdma_ctx *ctx, int domain, uint64_t bytes, const char *what) {
+  Ledger &l = ctx->budget[domain];
+  if (l.used + bytes < l.used || l.used + bytes > l.limit)
+    fail(MDMA_ERR_BUFFER_BUDGET,
+         fmt("%s: %s buffer budget exhausted: requested %llu bytes, used %llu, limit %llu", what,
+             domain == MDMA_DOMAIN_DEVICE ? "device" : "host", (unsigned long long)bytes,
+             (unsigned long long)l.used, (unsigned long long)l.limit));
+  l.used += bytes;
+}
+
+void budget_refund(mdma_ctx *ctx, int domain, uint64_t bytes) { ctx->budget[domain].used -= bytes; }
+
+// Replace a context-owned device buffer (buf, cap units of `unit` bytes)
+// by one of new_cap units: charged to the device budget first
+// (BufferBudget::allocate; a refusal leaves the old buffer as it was), the
+// stream drained so no queued kernel still reads the old memory, the old
+// buffer freed (its charge refunded only when the free succeeds), and the
+// context's buffer epoch bumped (graphs captured before refuse to replay).
+template <class T>
+static T *regrow(mdma_ctx *ctx, T *&buf, uint64_t &cap, uint64_t new_cap, uint64_t unit, const char *what) {
+  no_capture(ctx, what);
+  const uint64_t new_bytes = new_cap * unit;
+  budget_charge(ctx, MDMA_DOMAIN_DEVICE, new_bytes, what);
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    budget_refund(ctx, MDMA_DOMAIN_DEVICE, new_bytes);
+    hip_check(e, what);
+  }
+  if (buf) {
+    ctx->buf_epoch++;
+    e = hipFree(buf);
+    if (e == hipSuccess) budget_refund(ctx, MDMA_DOMAIN_DEVICE, cap * unit);  // else: the charge stays
+    buf = nullptr;
+    cap = 0;
+    if (e != hipSuccess) {
+      budget_refund(ctx, MDMA_DOMAIN_DEVICE, new_bytes);
+      hip_check(e, what);
+    }
+  }
+  void *p = nullptr;
+  e = hipMalloc(&p, new_bytes);
+  if (e != hipSuccess) {
+    budget_refund(ctx, MDMA_DOMAIN_DEVICE, new_bytes);
+    hip_check(e, what);
+  }
+  buf = static_cast<T *>(p);
+  cap = new_cap;
+  return buf;
+}
+
 char *scratch(mdma_ctx *ctx, uint64_t bytes) {
   if (bytes <= ctx->scratch_cap) return ctx->scratch;
-  no_capture(ctx, "scratch growth");
-  uint64_t cap = bytes < (1u << 20) ? (1u << 20) : bytes + bytes / 4;
-  hip_check(hipStreamSynchronize(ctx->stream), "scratch grow sync");
-  if (ctx->scratch) hip_check(hipFree(ctx->scratch), "scratch free");
-  ctx->scratch = nullptr;
-  ctx->scratch_cap = 0;
-  void *p = nullptr;
-  hip_check(hipMalloc(&p, cap), "scratch alloc");
-  ctx->scratch = static_cast<char *>(p);
-  ctx->scratch_cap = cap;
-  return ctx->scratch;
+  const uint64_t cap = bytes < (1u << 20) ? (1u << 20) : bytes + bytes / 4;
+  return regrow(ctx, ctx->scratch, ctx->scratch_cap, cap, 1, "scratch growth");
 }
 
 char *q8_buffer(mdma_ctx *ctx, uint64_t bytes) {
   if (bytes <= ctx->q8_cap) return ctx->q8;
-  no_capture(ctx, "int8 activation buffer growth");
-  uint64_t cap = bytes < (1u << 20) ? (1u << 20) : bytes + bytes / 4;
-  hip_check(hipStreamSynchronize(ctx->stream), "q8 grow sync");
-  if (ctx->q8) hip_check(hipFree(ctx->q8), "q8 free");
-  ctx->q8 = nullptr;
-  ctx->q8_cap = 0;
+  const uint64_t cap = bytes < (1u << 20) ? (1u << 20) : bytes + bytes / 4;
   ctx->q8_valid = false;
-  void *p = nullptr;
-  hip_check(hipMalloc(&p, cap), "q8 alloc");
-  ctx->q8 = static_cast<char *>(p);
-  ctx->q8_cap = cap;
-  return ctx->q8;
+  return regrow(ctx, ctx->q8, ctx->q8_cap, cap, 1, "int8 activation buffer growth");
 }
 
 char *argmax_parts(mdma_ctx *ctx, uint64_t chunks) {
   if (chunks <= ctx->argmax_part_cap) return ctx->argmax_part;
-  no_capture(ctx, "argmax buffer growth");
   const uint64_t cap = chunks < 4096 ? 4096 : chunks + chunks / 4;
-  hip_check(hipStreamSynchronize(ctx->stream), "argmax buffer grow sync");
-  if (ctx->argmax_part) hip_check(hipFree(ctx->argmax_part), "argmax buffer free");
-  ctx->argmax_part = nullptr;
-  ctx->argmax_part_cap = 0;
-  void *p = nullptr;
-  hip_check(hipMalloc(&p, cap * 12), "argmax buffer alloc");
-  ctx->argmax_part = static_cast<char *>(p);
-  ctx->argmax_part_cap = cap;
-  return ctx->argmax_part;
+  return regrow(ctx, ctx->argmax_part, ctx->argmax_part_cap, cap, 12, "argmax buffer growth");
 }
 
 double *ssq_parts(mdma_ctx *ctx, uint64_t n) {
   if (n <= ctx->ssq_cap) return ctx->ssq;
-  no_capture(ctx, "norm partials growth");
   const uint64_t cap = n < 4096 ? 4096 : n + n / 4;
-  hip_check(hipStreamSynchronize(ctx->stream), "norm partials grow sync");
-  if (ctx->ssq) hip_check(hipFree(ctx->ssq), "norm partials free");
-  ctx->ssq = nullptr;
-  ctx->ssq_cap = 0;
-  void *p = nullptr;
-  hip_check(hipMalloc(&p, cap * 8), "norm partials alloc");
-  ctx->ssq = static_cast<double *>(p);
-  ctx->ssq_cap = cap;
-  return ctx->ssq;
+  return regrow(ctx, ctx->ssq, ctx->ssq_cap, cap, 8, "norm partials growth");
 }
 
 // A zeroed uint32 buffer of at least n entries (grown outside capture only).
 static uint32_t *zeroed_counters(mdma_ctx *ctx, uint32_t *&buf, uint64_t &cap_, uint64_t n, const char *what) {
   if (n <= cap_) return buf;
-  no_capture(ctx, what);
   const uint64_t cap = n < 4096 ? 4096 : n + n / 4;
-  hip_check(hipStreamSynchronize(ctx->stream), "counter grow sync");
-  if (buf) hip_check(hipFree(buf), "counter free");
-  buf = nullptr;
-  cap_ = 0;
-  void *p = nullptr;
-  hip_check(hipMalloc(&p, cap * 4), "counter alloc");
+  regrow(ctx, buf, cap_, cap, 4, what);
   // On the context's stream (non-blocking: it does not wait for work on the
   // null stream), so the launches that use the counters follow the clear.
-  hip_check(hipMemsetAsync(p, 0, cap * 4, ctx->stream), "counter clear");
-  buf = static_cast<uint32_t *>(p);
-  cap_ = cap;
+  hip_check(hipMemsetAsync(buf, 0, cap * 4, ctx->stream), "counter clear");
   return buf;
 }
 
@@ -288,12 +328,9 @@ const float *rope_table(mdma_ctx *ctx, uint64_t max_pos, uint64_t hd, float thet
   uint64_t positions = need_pos < 4096 ? 4096 : need_pos + need_pos / 2;
   std::vector<float> host(positions * hd);
   fill_rope(host.data(), 0, positions, hd, theta);
-  hip_check(hipStreamSynchronize(ctx->stream), "rope table sync");
-  if (ctx->rope_tab) hip_check(hipFree(ctx->rope_tab), "rope table free");
-  ctx->rope_tab = nullptr;
-  void *p = nullptr;
-  hip_check(hipMalloc(&p, host.size() * 4), "rope table alloc");
-  ctx->rope_tab = static_cast<float *>(p);
+  ctx->rope_positions = 0;
+  regrow(ctx, ctx->rope_tab, ctx->rope_bytes, host.size() * 4, 1, "RoPE table growth");
+  void *p = ctx->rope_tab;
   hip_check(hipMemcpy(p, host.data(), host.size() * 4, hipMemcpyHostToDevice), "rope table upload");
   ctx->rope_positions = positions;
   ctx->rope_hd = hd;
@@ -405,27 +442,25 @@ int mdma_gfx950_join_execution(mdma_ctx *ctx) {
   });
 }
 
-int mdma_gfx950_set_buffer_budget(mdma_ctx *ctx, uint64_t weights, uint64_t kv, uint64_t scratch_) {
+int mdma_gfx950_set_buffer_budget(mdma_ctx *ctx, uint64_t device_bytes, uint64_t host_bytes) {
   return guarded([&] {
     need(ctx, "set_buffer_budget");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
-    uint64_t lim[3] = {weights, kv, scratch_};
-    for (int i = 0; i < 3; i++)
-      if (ctx->pools[i].used > lim[i])
-        fail(MDMA_ERR_BUFFER_BUDGET,
-             fmt("pool %d already holds %llu bytes, above the new limit %llu", i,
-                 (unsigned long long)ctx->pools[i].used, (unsigned long long)lim[i]));
-    for (int i = 0; i < 3; i++) ctx->pools[i].limit = lim[i];
+    // BufferBudget::replace (src/memory/buffers.rs:61-70): only an unused ledger.
+    if (ctx->budget[MDMA_DOMAIN_DEVICE].used || ctx->budget[MDMA_DOMAIN_HOST].used)
+      fail(MDMA_ERR_BACKEND, "buffer budget must be installed before allocations or sharing");
+    ctx->budget[MDMA_DOMAIN_DEVICE].limit = device_bytes;
+    ctx->budget[MDMA_DOMAIN_HOST].limit = host_bytes;
   });
 }
 
-int mdma_gfx950_buffer_usage(mdma_ctx *ctx, int pool, uint64_t *used, uint64_t *limit) {
+int mdma_gfx950_buffer_usage(mdma_ctx *ctx, int domain, uint64_t *used, uint64_t *limit) {
   return guarded([&] {
     need(ctx, "buffer_usage");
-    if (pool < 0 || pool > 2) shape_fail("buffer_usage: pool out of range");
+    if (domain != MDMA_DOMAIN_DEVICE && domain != MDMA_DOMAIN_HOST) shape_fail("buffer_usage: unknown domain");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
-    if (used) *used = ctx->pools[pool].used;
-    if (limit) *limit = ctx->pools[pool].limit;
+    if (used) *used = ctx->budget[domain].used;
+    if (limit) *limit = ctx->budget[domain].limit;
   });
 }
 
@@ -456,24 +491,26 @@ int mdma_gfx950_alloc(mdma_ctx *ctx, uint64_t bytes, int pool, mdma_buf **out) {
     if (pool < 0 || pool > 2) shape_fail("alloc: pool out of range");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
     // Allocations are rounded to 256 bytes so 16-byte vector loads of a
-    // buffer's last element never cross the allocation's end.
-    uint64_t charged = (bytes + 255) / 256 * 256;
-    if (charged < bytes) fail(MDMA_ERR_SIZE_OVERFLOW, "alloc: size overflows");
-    auto &p = ctx->pools[pool];
-    if (p.used + charged > p.limit || p.used + charged < p.used)
-      fail(MDMA_ERR_BUFFER_BUDGET, fmt("pool %d buffer budget exhausted: requested %llu bytes, "
-                                       "allocated %llu, limit %llu", pool, (unsigned long long)charged,
-                                       (unsigned long long)p.used, (unsigned long long)p.limit));
-    hip_check(hipSetDevice(ctx->device), "hipSetDevice");
+    // buffer's last element never cross the allocation's end; the budget is
+    // charged the requested bytes (at least one), as the reference's HIP
+    // buffers are (src/backend/rocm.rs:534-541, src/memory/buffers.rs:52-53).
+    const uint64_t charged = bytes ? bytes : 1;
+    const uint64_t rounded = (charged + 255) / 256 * 256;
+    if (rounded < charged) fail(MDMA_ERR_SIZE_OVERFLOW, "alloc: size overflows");
+    budget_charge(ctx, MDMA_DOMAIN_DEVICE, charged, "alloc");
     void *d = nullptr;
-    if (charged) hip_check(hipMalloc(&d, charged), "hipMalloc");
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e == hipSuccess) e = hipMalloc(&d, rounded);
+    if (e != hipSuccess) {
+      budget_refund(ctx, MDMA_DOMAIN_DEVICE, charged);
+      hip_check(e, "hipMalloc");
+    }
     auto *b = new mdma_buf();
     b->ctx = ctx;
     b->ptr = static_cast<char *>(d);
     b->len = bytes;
     b->charged = charged;
     b->pool = pool;
-    p.used += charged;
     *out = b;
   });
 }
@@ -494,12 +531,13 @@ int mdma_gfx950_free(mdma_buf *buf) {
     if (buf->ptr) {
       hipError_t e = hipFree(buf->ptr);
       if (e != hipSuccess) {
-        // Keep the charge: the memory may still be allocated.
+        // Keep the charge: the memory may still be allocated
+        // (src/backend/rocm/memory.rs:36-55).
         delete buf;
         hip_check(e, "hipFree");
       }
     }
-    ctx->pools[buf->pool].used -= buf->charged;
+    budget_refund(ctx, MDMA_DOMAIN_DEVICE, buf->charged);
     delete buf;
   });
 }
@@ -519,6 +557,7 @@ int mdma_gfx950_buf_view(mdma_buf *parent, uint64_t offset, uint64_t len, mdma_b
     b->pool = parent->pool;
     b->layout = parent->layout;
     b->owner = false;
+    b->repack_pending = false;  // a window of raw bytes is read by the raw kernels
     *out = b;
   });
 }
@@ -572,24 +611,52 @@ int mdma_gfx950_copy(mdma_ctx *ctx, const mdma_buf *src, uint64_t src_off, mdma_
   });
 }
 
-int mdma_gfx950_upload_weight(mdma_ctx *ctx, const void *bytes, uint64_t len, int layout, int32_t dtype,
-                              uint64_t rows, uint64_t cols, mdma_buf **out) {
+int mdma_gfx950_upload_weight(mdma_ctx *ctx, const void *bytes, uint64_t len, int layout, mdma_buf **out) {
   return guarded([&] {
     need(ctx, "upload_weight");
     need(out, "upload_weight");
     *out = nullptr;
+    // The trait's default stores GGUF bytes and refuses other layouts
+    // (src/backend.rs:228-237); this backend also takes its own prepared
+    // layout as it is. The reference ROCm backend's packed Q4_K is not read.
+    if (layout == MDMA_LAYOUT_ROCM_Q4K_V3)
+      fail(MDMA_ERR_NOT_IMPLEMENTED, "prepared weight layout for this backend");
     if (layout != MDMA_LAYOUT_GGUF && layout != MDMA_LAYOUT_GFX950)
       fail(MDMA_ERR_NOT_IMPLEMENTED, "upload_weight: unknown weight layout");
+    if (len) need(bytes, "upload_weight");
+    mdma_buf *b = nullptr;
+    int st = mdma_gfx950_alloc(ctx, len, MDMA_POOL_WEIGHTS, &b);
+    if (st) fail(st, g_last_error);
+    st = mdma_gfx950_upload(ctx, b, 0, bytes, len);
+    if (st) {
+      std::string m = g_last_error;
+      mdma_gfx950_free(b);
+      fail(st, m);
+    }
+    b->layout = layout;
+    b->repack_pending = layout == MDMA_LAYOUT_GGUF;
+    *out = b;
+  });
+}
+
+int mdma_gfx950_upload_weight_typed(mdma_ctx *ctx, const void *bytes, uint64_t len, int layout, int32_t dtype,
+                                    uint64_t rows, uint64_t cols, mdma_buf **out) {
+  return guarded([&] {
+    need(ctx, "upload_weight_typed");
+    need(out, "upload_weight_typed");
+    *out = nullptr;
+    if (layout != MDMA_LAYOUT_GGUF && layout != MDMA_LAYOUT_GFX950)
+      fail(MDMA_ERR_NOT_IMPLEMENTED, "upload_weight_typed: unknown weight layout");
     uint64_t bs = block_size(dtype);
-    if (!bs) fail(MDMA_ERR_NOT_IMPLEMENTED, fmt("upload_weight: dtype %d", dtype));
+    if (!bs) fail(MDMA_ERR_NOT_IMPLEMENTED, fmt("upload_weight_typed: dtype %d", dtype));
     if (layout == MDMA_LAYOUT_GFX950 && !gfx950_layout_dtype(dtype))
-      fail(MDMA_ERR_NOT_IMPLEMENTED, fmt("upload_weight: dtype %d has no prepared layout", dtype));
+      fail(MDMA_ERR_NOT_IMPLEMENTED, fmt("upload_weight_typed: dtype %d has no prepared layout", dtype));
     const uint64_t raw = cols % bs ? 0 : rows * (cols / bs) * type_size(dtype);
     const uint64_t want = layout == MDMA_LAYOUT_GFX950 ? rows * gfx950_row_bytes(dtype, cols) : raw;
     if (cols % bs || len != want)
-      shape_fail(fmt("upload_weight: %llu bytes do not hold a [%llu, %llu] weight", (unsigned long long)len,
+      shape_fail(fmt("upload_weight_typed: %llu bytes do not hold a [%llu, %llu] weight", (unsigned long long)len,
                      (unsigned long long)rows, (unsigned long long)cols));
-    if (len) need(bytes, "upload_weight");
+    if (len) need(bytes, "upload_weight_typed");
     // GGUF Q4_K / Q6_K / Q8_0 rows are stored in the prepared layout, which
     // every op on this backend reads; other dtypes keep their bytes.
     const bool pack = layout == MDMA_LAYOUT_GGUF && gfx950_layout_dtype(dtype);
@@ -616,6 +683,8 @@ int mdma_gfx950_upload_weight(mdma_ctx *ctx, const void *bytes, uint64_t len, in
   });
 }
 
+int mdma_gfx950_buf_layout(const mdma_buf *buf) { return buf ? buf->layout : -1; }
+
 int mdma_gfx950_qmatmul(mdma_ctx *ctx, const mdma_qweight *w, const mdma_buf *x, mdma_buf *y) {
   return qmatmul_mode(ctx, w, x, y, -1);
 }
@@ -634,6 +703,7 @@ int mdma_gfx950_qmatmul_qkv(mdma_ctx *ctx, const mdma_qweight *wq, const mdma_qw
   return guarded([&] {
     need(ctx, "qmatmul_qkv");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    for (const mdma_qweight *w : {wq, wk, wv}) prepare_weight(ctx, w);
     uint64_t T = matmul_tokens(wq, x, q, "qmatmul_qkv");
     if (matmul_tokens(wk, x, k, "qmatmul_qkv") != T || matmul_tokens(wv, x, v, "qmatmul_qkv") != T)
       shape_fail("qmatmul_qkv: projections disagree on n_tokens");
@@ -653,6 +723,8 @@ int mdma_gfx950_ffn_gate_up(mdma_ctx *ctx, const mdma_qweight *gate, const mdma_
   return guarded([&] {
     need(ctx, "ffn_gate_up");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    prepare_weight(ctx, gate);
+    prepare_weight(ctx, up);
     need(gate, "ffn_gate_up");
     need(up, "ffn_gate_up");
     if (gate->rows != up->rows || gate->cols != up->cols)
@@ -702,6 +774,7 @@ int mdma_gfx950_embed(mdma_ctx *ctx, const mdma_qweight *table, const uint32_t *
     need(ctx, "embed");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
     q8_invalidate(ctx);
+    prepare_weight(ctx, table);
     weight_row_bytes(table, "embed");
     uint64_t oe = f32_elems("embed", out);
     // shape::embed (shape.rs:92-110).
@@ -954,6 +1027,7 @@ int mdma_gfx950_block_dot_i32(mdma_ctx *ctx, const mdma_qweight *w, const mdma_b
     need(ctx, "block_dot_i32");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
     q8_invalidate(ctx);
+    prepare_weight(ctx, w);
     weight_row_bytes(w, "block_dot_i32");
     if (w->dtype != DT_Q4_K && w->dtype != DT_Q6_K && w->dtype != DT_Q8_0)
       fail(MDMA_ERR_NOT_IMPLEMENTED, "block_dot_i32: quantized dtypes only");
@@ -1010,6 +1084,9 @@ int mdma_gfx950_graph_begin(mdma_ctx *ctx) {
       ctx->lock.unlock();
       fail(MDMA_ERR_BACKEND, "graph_begin: capture already in progress");
     }
+    // A captured GEMV must not rely on int8 activations an earlier call left
+    // in the cache: a replay would read whatever the buffer then holds.
+    q8_invalidate(ctx);
     hipError_t e = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal);
     if (e != hipSuccess) {
       ctx->lock.unlock();
@@ -1032,6 +1109,8 @@ int mdma_gfx950_graph_end(mdma_ctx *ctx, mdma_graph **out) {
     hip_check(e, "hipStreamEndCapture");
     auto *g = new mdma_graph();
     g->graph = gr;
+    g->ctx = ctx;
+    g->epoch = ctx->buf_epoch;
     e = hipGraphInstantiate(&g->exec, gr, nullptr, nullptr, 0);
     if (e != hipSuccess) {
       (void)hipGraphDestroy(gr);
@@ -1049,6 +1128,11 @@ int mdma_gfx950_graph_launch(mdma_ctx *ctx, mdma_graph *graph) {
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
     q8_invalidate(ctx);
     no_capture(ctx, "graph_launch");
+    if (graph->ctx != ctx) fail(MDMA_ERR_BACKEND, "graph_launch: graph was captured on another context");
+    // The graph holds addresses of context buffers as they were at capture.
+    if (graph->epoch != ctx->buf_epoch)
+      fail(MDMA_ERR_BACKEND, "graph_launch: context buffers were reallocated since capture (reserve_scratch "
+                             "before capturing); capture again");
     hip_check(hipGraphLaunch(graph->exec, ctx->stream), "hipGraphLaunch");
   });
 }

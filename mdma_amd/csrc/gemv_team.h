@@ -425,6 +425,7 @@ struct TeamSet {
   // rows of y (f32 squares added in f64) in ssq[workgroup].
   const float *res;
   double *ssq;
+  uint32_t ssq_cap;  // entries of ssq; a grid past it is not launched
   // One token, PRO 5: x = rmsnorm(nsum) * nw, the sum of squares of nsum
   // being the n_part partials npart that its producer stored.
   const float *nsum, *nw;
@@ -837,6 +838,10 @@ void launch_iters(mdma_ctx *ctx, TeamSet ts, int tw, int pl, const float *xf, co
   const bool pro4 = PRO_OK && ts.pro && tw > 1 && pl == 1;
   const int wg = pro4 ? 64 * tw * MDMA_PRO4_TEAMS : WG, tpw = wg / 64 / tw;
   const dim3 grid((uint32_t)((teams + tpw - 1) / tpw)), block(wg);
+  if (ts.ssq && grid.x > ts.ssq_cap) {  // one sum-of-squares partial per workgroup: no room, no launch
+    ctx->team_grid = 0;
+    return;
+  }
   ctx->team_grid = grid.x;
   // With timing events set, the dispatch itself timestamps them (kernel-only
   // duration, as a profiler measures it); they apply to one launch.

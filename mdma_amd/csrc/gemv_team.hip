@@ -81,9 +81,11 @@ uint32_t launch_gemv_i8_residual(mdma_ctx *ctx, const GemvJob &job, const float 
   TeamNorm nm;
   nm.res = res;
   nm.ssq = ssq_parts(ctx, 65536);
+  nm.ssq_cap = (uint32_t)(ctx->ssq_cap < 65536 ? ctx->ssq_cap : 65536);
   ctx->team_grid = 0;
+  // The launcher makes no launch whose grid passes ssq_cap (team_grid stays
+  // 0: the caller takes the unfused path).
   launch_gemv_team(ctx, MDMA_ACT_I8, &job, 1, false, x, 1, nullptr, pro, &nm);
-  if (ctx->team_grid > 65536) fail(MDMA_ERR_BACKEND, "residual GEMV: more workgroups than norm partials");
   return ctx->team_grid;
 }
 
@@ -128,6 +130,7 @@ void launch_gemv_team(mdma_ctx *ctx, int mode, const GemvJob *jobs, int n_jobs, 
     if (nm) {  // one token only (the callers check)
       ts.res = nm->res;
       ts.ssq = nm->ssq;
+      ts.ssq_cap = nm->ssq_cap;
       ts.nsum = nm->nsum;
       ts.nw = nm->nw;
       ts.npart = nm->npart;

@@ -45,7 +45,9 @@ void hip_check(hipError_t e, const char *what);
 // The thread-local message mdma_gfx950_last_error() returns.
 void set_last_error(const std::string &msg);
 
-struct Pool {
+// One domain of a BufferBudget (src/memory/buffers.rs:32-99): requested
+// bytes of live buffers against an optional quota.
+struct Ledger {
   uint64_t used = 0;
   uint64_t limit = UINT64_MAX;
 };
@@ -56,17 +58,21 @@ struct mdma_buf {
   mdma_ctx *ctx = nullptr;
   char *ptr = nullptr;     // device address of element 0
   uint64_t len = 0;        // bytes visible to ops
-  uint64_t charged = 0;    // bytes charged to the pool (0 for views)
+  uint64_t charged = 0;    // bytes charged to the device budget (0 for views)
   int pool = MDMA_POOL_SCRATCH;
   int layout = MDMA_LAYOUT_GGUF;
   bool owner = true;       // false for views
+  // Weight bytes from the trait-shaped upload_weight: raw GGUF blocks whose
+  // dtype and shape the first op that reads them supplies; that op repacks
+  // them into the prepared layout (see prepare_weight).
+  bool repack_pending = false;
 };
 
 struct mdma_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   std::recursive_mutex lock;
-  mdma::Pool pools[3];
+  mdma::Ledger budget[2];  // MDMA_DOMAIN_DEVICE, MDMA_DOMAIN_HOST
   int act_mode = MDMA_ACT_F32;
   bool norm_fusion = true;  // one-token int8 decode: attention rmsnorm fused into the GEMVs around it
   std::string label;
@@ -83,6 +89,7 @@ struct mdma_ctx {
   uint64_t q8_n = 0, q8_n_in = 0;
   // Device RoPE cos/sin table: [positions][head_dim/2] for one (head_dim, theta).
   float *rope_tab = nullptr;
+  uint64_t rope_bytes = 0;
   uint64_t rope_positions = 0, rope_hd = 0;
   float rope_theta = 0.f;
   uint32_t *host_ids = nullptr;  // pinned staging for token ids / argmax result
@@ -100,6 +107,10 @@ struct mdma_ctx {
   double *ssq = nullptr;  // per-workgroup sums of squares of a residual-stream GEMV (norm fusion)
   uint64_t ssq_cap = 0;
   uint32_t team_grid = 0;  // workgroups of the last row-team launch
+  // Bumped whenever a context buffer a captured graph may point into is
+  // freed or replaced (scratch, int8 activations, counters, partials, RoPE
+  // table); a graph captured under another epoch refuses to replay.
+  uint64_t buf_epoch = 0;
   // This device's copy of the library's static scratch array (noalloc.hip),
   // from hipGetSymbolAddress at create.
   char *static_scratch = nullptr;
@@ -113,6 +124,8 @@ struct mdma_ctx {
 struct mdma_graph {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
+  mdma_ctx *ctx = nullptr;
+  uint64_t epoch = 0;  // the context's buf_epoch at capture
 };
 
 namespace mdma {
@@ -120,6 +133,19 @@ namespace mdma {
 // Backend::qmatmul with its shape rules, in activation mode `mode` (-1: the
 // context's); throws Error. The lock is taken inside.
 void qmatmul_run(mdma_ctx *ctx, const mdma_qweight *w, const mdma_buf *x, mdma_buf *y, int mode);
+// Charge / refund requested bytes to a budget domain of the context
+// (MDMA_ERR_BUFFER_BUDGET past its quota).
+void budget_charge(mdma_ctx *ctx, int domain, uint64_t bytes, const char *what);
+void budget_refund(mdma_ctx *ctx, int domain, uint64_t bytes);
+// A weight uploaded through the trait-shaped upload_weight holds raw GGUF
+// blocks until the first op that reads it with a Q4_K / Q6_K / Q8_0 QWeight
+// of matching size: that op repacks it on the device into the prepared
+// layout (a new buffer in place of the raw one). Under graph capture or in
+// an allocation-free call, or when the budget has no room, the weight stays
+// raw for now and the raw-layout kernels read it.
+void prepare_weight(mdma_ctx *ctx, const mdma_qweight *w);
+// Device repack of raw GGUF rows into the prepared layout (layout.cpp).
+void launch_repack(mdma_ctx *ctx, int32_t dtype, uint64_t rows, uint64_t cols, const uint8_t *src, uint8_t *dst);
 // Per-device set-up of the allocation-free entry point (noalloc.hip): the
 // device address of this device's static scratch, kept in ctx.
 void noalloc_setup(mdma_ctx *ctx);
@@ -205,6 +231,7 @@ void launch_gemv_batch(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, bool gate
 struct TeamNorm {
   const float *res = nullptr;
   double *ssq = nullptr;
+  uint32_t ssq_cap = 0;  // partials ssq holds: a launch of more workgroups is not made
   const float *nsum = nullptr, *nw = nullptr;
   const double *npart = nullptr;
   uint32_t n_part = 0;

@@ -26,6 +26,8 @@
 // Every block keeps its byte count (144, 210, 34); only the row padding is
 // added (none when the row is already a multiple of 16 bytes, as at every
 // Llama-3-8B shape).
+#include <hip/hip_runtime.h>
+
 #include <cstring>
 
 #include "internal.h"
@@ -80,6 +82,60 @@ void pack_gfx950(int32_t dtype, uint64_t rows, uint64_t cols, const uint8_t *src
       }
     }
   }
+}
+
+namespace {
+
+__device__ __forceinline__ void copy_bytes(uint8_t *d, const uint8_t *s, int n) {
+  for (int i = 0; i < n; i++) d[i] = s[i];
+}
+
+// pack_gfx950's byte moves for one (row, block), one thread each; the
+// thread of a row's block 0 also clears the row's padding.
+__global__ __launch_bounds__(256) void repack_kernel(int32_t dtype, uint64_t rows, uint64_t nb, uint32_t ts,
+                                                     uint64_t rbp, const uint8_t *__restrict__ src,
+                                                     uint8_t *__restrict__ dst) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * nb) return;
+  const uint64_t r = i / nb, b = i % nb;
+  const uint8_t *blk = src + i * ts;
+  uint8_t *d = dst + r * rbp;
+  if (b == 0)
+    for (uint64_t k = nb * ts; k < rbp; k++) d[k] = 0;
+  if (dtype == DT_Q4_K) {
+    const uint64_t U = 4 * nb;
+    for (int p = 0; p < 4; p++) {
+      copy_bytes(d + 16 * (4 * b + p), blk + 16 + 32 * p, 16);
+      copy_bytes(d + 16 * (U + 4 * b + p), blk + 32 + 32 * p, 16);
+    }
+    copy_bytes(d + 32 * U + 16 * b, blk, 16);
+  } else if (dtype == DT_Q6_K) {
+    const uint64_t U = 4 * nb;
+    const uint8_t *ql = blk, *qh = blk + 128, *sc = blk + 192;
+    for (int k = 0; k < 4; k++) {
+      const int n = k >> 1, h = k & 1;
+      const uint64_t u = 4 * b + k;
+      copy_bytes(d + 16 * u, ql + 64 * n + 16 * h, 16);
+      copy_bytes(d + 16 * (U + u), ql + 64 * n + 32 + 16 * h, 16);
+      copy_bytes(d + 16 * (2 * U + u), qh + 32 * n + 16 * h, 16);
+      for (int q = 0; q < 4; q++) d[48 * U + 4 * u + q] = sc[8 * n + 2 * q + h];
+    }
+    copy_bytes(d + 52 * U + 2 * b, blk + 208, 2);
+  } else {
+    copy_bytes(d + 16 * b, blk + 2, 16);
+    copy_bytes(d + 16 * (nb + b), blk + 18, 16);
+    copy_bytes(d + 32 * nb + 2 * b, blk, 2);
+  }
+}
+
+}  // namespace
+
+void launch_repack(mdma_ctx *ctx, int32_t dtype, uint64_t rows, uint64_t cols, const uint8_t *src, uint8_t *dst) {
+  const uint64_t nb = cols / block_size(dtype), total = rows * nb;
+  if (!total) return;
+  repack_kernel<<<dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, ctx->stream>>>(
+      dtype, rows, nb, (uint32_t)type_size(dtype), gfx950_row_bytes(dtype, cols), src, dst);
+  hip_check(hipGetLastError(), "repack launch");
 }
 
 void unpack_gfx950(int32_t dtype, uint64_t rows, uint64_t cols, const uint8_t *src, uint8_t *dst) {

@@ -322,7 +322,8 @@ Weight load_weight(mdma_model *m, Gguf &g, const std::string &name, std::vector<
   w.dtype = t.dtype;
   w.rows = t.rows;
   w.cols = t.cols;
-  int st = mdma_gfx950_upload_weight(m->ctx, tmp.data(), t.bytes, MDMA_LAYOUT_GGUF, t.dtype, t.rows, t.cols, &w.buf);
+  int st = mdma_gfx950_upload_weight_typed(m->ctx, tmp.data(), t.bytes, MDMA_LAYOUT_GGUF, t.dtype, t.rows, t.cols,
+                                           &w.buf);
   if (st) fail(st, mdma_gfx950_last_error());
   m->owned.push_back(w.buf);
   return w;
