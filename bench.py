@@ -4,12 +4,13 @@
 Workload (the Q4_K decode-GEMV benchmark configuration): one step is one pass over a Llama-3-8B layer's
 seven Q4_K matrix-vector products at batch 1 (q and o 4096x4096, k and v
 1024x4096, gate and up 14336x4096, down 4096x14336), issued the way the decode
-path issues them: fused QKV, o, fused gate/up + SiLU, down -- four launches.
-The three 4096-wide launches read one input whose int8 form was written by the
-rmsnorm that produced it (the decode path fuses the quantization into the
-producers of these inputs: rmsnorm and attention), made once before the timed
-region; the down projection reads an f32 input and quantizes it in its own
-prologue, as in the decode path. Weights are synthetic (f16 d, dmin = |N(0,1)|*1e-3,
+path issues them: fused QKV, o, fused gate/up + SiLU, down -- four launches,
+after the rmsnorm that writes their 4096-wide input. The three 4096-wide
+launches read that input's int8 form, which the rmsnorm writes beside it (the
+decode path fuses the quantization into the producers of these inputs:
+rmsnorm and attention); the down projection reads an f32 input and quantizes
+it in its own prologue, as in the decode path. The rmsnorm is part of every
+step (and of its bytes), so each graph replay rewrites what the GEMVs read. Weights are synthetic (f16 d, dmin = |N(0,1)|*1e-3,
 six-bit scales and mins uniform in [0,63], nibbles uniform in [0,15]) and rotate over >= 1 GiB of distinct device copies so the 256 MB
 Infinity Cache cannot serve them. Each step is one replay of a captured HIP
 graph; the timed region is bracketed by stream synchronisation and HIP events
@@ -141,8 +142,22 @@ class Workload:
             be.qmatmul(L["down"], self.x["down"], self.y["down"])
 
     def step(self, be, L):
+        """One layer step: the rmsnorm that writes the 4096-wide input and, in
+        the int8 mode, its int8 form (captured with the GEMVs, so every
+        replay rewrites what they read), then the four GEMV launches."""
+        self.prepare(be)
         for name, _, _, _ in LAUNCHES:
             self.launch(be, L, name)
+
+
+def norm_bytes(mode):
+    """The step's rmsnorm: x and the norm weight read, y written, and in the
+    int8 mode y's int8 form (values, per-256 scales, per-16 sums)."""
+    return 3 * 4096 * 4 + (x_bytes(4096, "i8") if mode == "i8" else 0)
+
+
+def step_bytes(mode):
+    return sum(launch_bytes(l, mode) for l in LAUNCHES) + norm_bytes(mode)
 
 
 def time_graphs(be, ev, graphs, steps, warmup):
@@ -173,8 +188,9 @@ def per_launch(be, ev, wl, mode, reps):
     starts, stops = [ev.event() for _ in range(n)], [ev.event() for _ in range(n)]
     for launch in LAUNCHES:
         name = launch[0]
-        wl.prepare(be)
-        g = be.capture(lambda: [wl.launch(be, L, name) for L in wl.layers])
+        # The graph starts with the rmsnorm writing the launches' input (and
+        # its int8 form): us_graph includes a ninth of that kernel.
+        g = be.capture(lambda: [wl.prepare(be)] + [wl.launch(be, L, name) for L in wl.layers])
         ms = time_graphs(be, ev, [g], reps, 2)
         g.close()
         us_graph = ms * 1e3 / n
@@ -189,9 +205,11 @@ def per_launch(be, ev, wl, mode, reps):
                 wl.launch(be, L, name)
                 i += 1
         be.join_execution()
-        us = sum(ev.elapsed_ms(starts[k], stops[k]) for k in range(n)) * 1e3 / n
+        durs = [ev.elapsed_ms(starts[k], stops[k]) * 1e3 for k in range(n)]
+        us = sum(durs) / n
         b = launch_bytes(launch, mode)
-        out[name] = {"us_kernel": round(us, 3), "GBps_kernel": round(b / us / 1e3, 1),
+        out[name] = {"us_kernel": round(us, 3), "us_kernel_median": round(float(np.median(durs)), 3),
+                     "GBps_kernel": round(b / us / 1e3, 1),
                      "us_graph": round(us_graph, 3), "GBps_graph": round(b / us_graph / 1e3, 1),
                      "bytes_per_launch": b, "launches_timed": n}
     for e in starts + stops:
@@ -314,7 +332,10 @@ def prefill_gemms(be, ev, reps):
     return out
 
 
-def e2e_decode(be, n_prompt=512, n_gen=256, batches=(1, 8), path="/tmp/mdma_bench_llama3_8b_q4km.gguf"):
+E2E_PATH = "/tmp/mdma_bench_llama3_8b_q4km.gguf"
+
+
+def e2e_decode(be, n_prompt=512, n_gen=256, batches=(1, 8), path=E2E_PATH):
     """Llama-3-8B geometry, Q4_K_M mix (attention and down Q6_K, gate/up and
     token_embd Q4_K, head Q6_K), random init written as GGUF; a 512-token
     random prompt prefill, then greedy decode at batch 1 and 8, int8
@@ -378,17 +399,30 @@ def copy_probe(be, ev, nbytes=1 << 30, reps=10):
             "GBps_read_plus_write": round(2 * nbytes * reps / (ms * 1e-3) / 1e9, 1)}
 
 
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(raws, budget_s):
+    """The CPU oracle (oracle/oracle.c, restating CpuBackend::qmatmul:
+    rows over threads, each row dequantized to f32, a sequential f32 dot)
+    on every core this process may run on (sched_getaffinity), for about
+    budget_s seconds of the same layer step (f32 activations)."""
     from oracle import ffi
 
     try:
         cores = len(os.sched_getaffinity(0))
     except AttributeError:
         cores = os.cpu_count() or 1
-    cores = max(1, min(cores, 16))
     rng = np.random.default_rng(1)
     xs = {4096: rng.standard_normal(4096).astype(np.float32), 14336: rng.standard_normal(14336).astype(np.float32)}
-    step_bytes = sum(launch_bytes(l, "f32") for l in LAUNCHES)
+    gemv_bytes = sum(launch_bytes(l, "f32") for l in LAUNCHES)
     ffi.qmatmul(Q4K, raws["q"], 4096, 4096, xs[4096], threads=cores)  # warm
     n, t0 = 0, time.perf_counter()
     while True:
@@ -398,10 +432,95 @@ def cpu_baseline(raws, budget_s):
         el = time.perf_counter() - t0
         if el >= budget_s:
             break
-    return {"value": round(step_bytes * n / el / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+    return {"value": round(gemv_bytes * n / el / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "cpu": cpu_model(),
             "sample": f"{n} full Q4_K layer steps (the same 7 GEMV shapes, f32 activations), {el:.1f} s, "
                       "oracle/oracle.c restating CpuBackend::qmatmul (row-parallel, sequential f32 dot)",
             "ms_per_step": round(el * 1e3 / n, 2)}
+
+
+def cpu_e2e(path_8b, cores):
+    """End-to-end greedy decode on the host cores, the oracle restating
+    Model::forward / Llama::run_layers (f32 activations, f16-rounded KV):
+      - config 1 (TinyStories-15M geometry, Q8_0): 8-token prompt, 64 tokens;
+      - config 5 (Llama-3-8B geometry, Q4_K_M), a bounded sample: a
+        16-token prompt and 3 decode steps (each step streams all 5.2 GB of
+        weights through the row-parallel dequantize-and-dot)."""
+    import tempfile
+
+    from mdma_amd import gguf, llama_synth, synth
+    from oracle import ffi
+
+    out = {"cores": cores, "cpu": cpu_model(), "kind": "port"}
+    with tempfile.TemporaryDirectory() as d:
+        p1 = os.path.join(d, "tiny.gguf")
+        llama_synth.write(p1, llama_synth.TINYSTORIES, llama_synth.Q8_ALL, 1)
+        r = gguf.Reader(p1)
+        ffi.llama_timed(r, synth.tokens(8, 32000, 1001), 4, threads=cores)  # warm
+        _, secs = ffi.llama_timed(r, synth.tokens(8, 32000, 1001), 64, threads=cores)
+        dec = secs[1:]
+        out["config1"] = {"prompt_tokens": 8, "decode_tokens": 63, "prefill_ms": round(secs[0] * 1e3, 2),
+                          "decode_tok_s": round(len(dec) / dec.sum(), 1),
+                          "decode_ms_per_step_p50": round(float(np.median(dec)) * 1e3, 2)}
+    r = gguf.Reader(path_8b)
+    _, secs = ffi.llama_timed(r, synth.tokens(16, 128256, SEED + 60), 4, threads=cores)
+    dec = secs[1:]
+    out["config5_sample"] = {"prompt_tokens": 16, "decode_tokens": len(dec), "prefill_s": round(secs[0], 2),
+                             "decode_tok_s": round(len(dec) / dec.sum(), 3),
+                             "decode_s_per_step_p50": round(float(np.median(dec)), 3)}
+    print(f"[bench] cpu e2e: {out}", file=sys.stderr, flush=True)
+    return out
+
+
+def mdma_bench(be, path, init_seconds, prompt_len=512, steps=256, repetitions=2):
+    """The reference's mdma-bench protocol (src/bin/mdma-bench.rs:19-116) on
+    the same model: load with a memory budget, then one untimed warmup trial
+    and `repetitions` timed trials, each on a fresh KV cache: a prefill of
+    prompt_len tokens, then `steps` decode steps, each downloading the
+    logits and taking the host's greedy argmax (the eager decoder), in the
+    int8 mode. Its JSON fields; the prompt is seeded token ids (no
+    tokenizer)."""
+    from mdma_amd import synth
+    from mdma_amd.backend import ACT_I8
+    from mdma_amd.model import Model
+
+    be.set_act_mode(ACT_I8)
+    t0 = time.perf_counter()
+    m = Model(be, path)
+    load_s = time.perf_counter() - t0
+    cap = prompt_len + steps
+    tokens = synth.tokens(prompt_len, 128256, SEED + 70)
+    plan_p, plan_d = m.plan(cap, 1, prompt_len), m.plan(cap, 1, 1)
+    trials = []
+    for trial in range(repetitions + 1):
+        s = m.session(cap, 1, prompt_len)
+        be.join_execution()
+        a = time.perf_counter()
+        logits = s.prefill(tokens, 0)
+        pre = time.perf_counter() - a
+        a = time.perf_counter()
+        for i in range(steps):
+            logits = s.forward(int(np.argmax(logits)), prompt_len + i)
+        dec = time.perf_counter() - a
+        assert np.all(np.isfinite(logits))
+        s.close()
+        if trial > 0:
+            trials.append({"prefill_seconds": round(pre, 5), "decode_seconds": round(dec, 5),
+                           "prefill_tokens_per_second": round(prompt_len / pre, 1),
+                           "decode_tokens_per_second": round(steps / dec, 1)})
+    out = {"backend": "gfx950", "architecture": "llama", "model": os.path.basename(path), "execution": "eager",
+           "artifact_bytes": os.path.getsize(path), "backend_init_seconds": round(init_seconds, 4),
+           "load_seconds": round(load_s, 3), "prompt_tokens": prompt_len, "decode_steps": steps,
+           "context_capacity": cap, "kv_element_bytes": be.kv_elem_bytes(),
+           "native_weight_bytes": int(plan_p.weight_bytes), "native_kv_bytes": int(plan_p.kv_bytes),
+           "native_prefill_workspace_bytes": int(plan_p.workspace_bytes),
+           "native_decode_workspace_bytes": int(plan_d.workspace_bytes),
+           "native_peak_tensor_bytes": int(plan_p.weight_bytes + plan_p.kv_bytes +
+                                           max(plan_p.workspace_bytes, plan_d.workspace_bytes)),
+           "warmup_trials": 1, "trials": trials}
+    m.close()
+    print(f"[bench] mdma-bench: {trials}", file=sys.stderr, flush=True)
+    return out
 
 
 def main():
@@ -423,7 +542,9 @@ def main():
 
     from mdma_amd.backend import ACT_F32, ACT_I8, Gfx950Backend
 
+    t0 = time.perf_counter()
     be = Gfx950Backend(0)
+    init_s = time.perf_counter() - t0
     if args.e2e_only:
         print(json.dumps({"e2e_llama3_8b": e2e_decode(be), "device": be.device_label()}), flush=True)
         return
@@ -434,14 +555,13 @@ def main():
     results = {}
     for mode, code in (("i8", ACT_I8), ("f32", ACT_F32)):
         be.set_act_mode(code)
-        wl.prepare(be)
         graphs = [be.capture(lambda L=L: wl.step(be, L)) for L in wl.layers]
         ms = time_graphs(be, ev, graphs, args.steps, args.warmup)
         for g in graphs:
             g.close()
-        step_bytes = sum(launch_bytes(l, mode) for l in LAUNCHES)
-        results[mode] = {"ms_per_step": ms / args.steps, "GBps": step_bytes * args.steps / (ms * 1e-3) / 1e9,
-                         "step_bytes": step_bytes, "per_launch": per_launch(be, ev, wl, mode, args.reps)}
+        sb = step_bytes(mode)
+        results[mode] = {"ms_per_step": ms / args.steps, "GBps": sb * args.steps / (ms * 1e-3) / 1e9,
+                         "step_bytes": sb, "per_launch": per_launch(be, ev, wl, mode, args.reps)}
     be.set_act_mode(ACT_I8)
     q6 = q6k_gemvs(be, ev, max(2, args.reps // 4))
     gemm = prefill_gemms(be, ev, max(2, args.reps // 4))
@@ -457,6 +577,10 @@ def main():
             "kernel": "gemv_team<Q4G, int8, gated, x staged in LDS> (fused ffn gate/up + SiLU, 2 x 14336x4096 Q4_K, "
                       "x's int8 form from the fused rmsnorm)",
             "bytes_per_launch": dom["bytes_per_launch"], "us_per_launch": dom["us_kernel"],
+            "us_per_launch_median": dom["us_kernel_median"],
+            "timing": (f"achieved = bytes_per_launch / us_per_launch, us_per_launch the mean of "
+                       f"{dom['launches_timed']} kernel-only durations from the dispatches' own start/end "
+                       "timestamps (the statistic rocprofv3 --stats reports as its average)"),
             "x_quantized_in_kernel": {"kernel": "gemv_team<Q4G, int8, gated, x-quant> (f32 x quantized in the prologue)",
                                       "us_per_launch": round(us_xk, 3),
                                       "achieved": round(b_xk / us_xk / 1e3, 1),
@@ -465,16 +589,20 @@ def main():
         for w in L.values():
             w.buf.close()
     e2e = None if args.no_e2e else e2e_decode(be)
+    protocol = None if args.no_e2e else mdma_bench(be, E2E_PATH, init_s)
     cpu = None if args.no_cpu else cpu_baseline(wl.raws, args.cpu_seconds)
+    if cpu is not None and not args.no_e2e:
+        cpu["e2e"] = cpu_e2e(E2E_PATH, cpu["cores"])
     f = results["f32"]
     line = {
         "metric": "Q4_K GEMV HBM GB/s (% of peak) @8B shapes; decode tok/s, 1 MI355X",
         "value": round(main_mode["GBps"], 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(main_mode["ms_per_step"], 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "i8", "data": "synthetic",
-        "config": {"workload": "Q4_K decode GEMV, one Llama-3-8B layer (fused qkv, o, fused gate/up+SiLU, down), "
-                               "batch 1, int8 activations (qkv/o/gate_up read x's int8 form from its producer; "
-                               "down quantizes its f32 x in the kernel)", "global_batch": 1, "seq_len": 1, "parallelism": "none",
+        "config": {"workload": "Q4_K decode GEMV, one Llama-3-8B layer (rmsnorm writing x and its int8 form, "
+                               "then fused qkv, o, fused gate/up+SiLU reading that int8 form, and the down "
+                               "projection quantizing its f32 input in the kernel), batch 1, int8 activations",
+                   "global_batch": 1, "seq_len": 1, "parallelism": "none",
                    "weight_copies": wl.copies, "rotated_bytes": wl.copies * wl.layer_bytes, "seed": SEED},
         "pct_of_hbm_peak": round(100 * main_mode["GBps"] / HBM_PEAK_GBS, 2),
         "roofline": roof,
@@ -485,6 +613,7 @@ def main():
         "q6k_gemv": q6,
         "prefill_gemm_i8": gemm,
         "e2e_llama3_8b": e2e,
+        "mdma_bench": protocol,
         "copy_probe": probe,
         "device": be.device_label(),
     }

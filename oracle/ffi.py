@@ -42,6 +42,7 @@ def lib():
             "orc_block_dot_i32": (C.c_int, [C.c_int, _P, _Z, _Z, _Z, _P, _Z, _P]),
             "orc_llama_generate": (C.c_int, [_P, _P, _Z, _Z, _P, _P]),
             "orc_llama_run": (C.c_int, [_P, _P, _Z, _Z, _P, _P, _P]),
+            "orc_llama_run_timed": (C.c_int, [_P, _P, _Z, _Z, _P, _P, _P, _P]),
             "orc_i8_group": (_Z, [C.c_int, _Z, _Z, _Z]),
         }
         for name, (res, args) in sig.items():
@@ -281,3 +282,16 @@ def llama_run(gguf_reader, prompt, n_gen: int, forced=None, kv_f16: bool = True,
     _chk("llama_run", lib().orc_llama_run(C.byref(m), _p(prompt), prompt.size, n_gen, fp, _p(out), _p(logits)))
     del keep
     return out, logits
+
+
+def llama_timed(gguf_reader, prompt, n_gen: int, threads: int = 0, act_i8: bool = False):
+    """(greedy tokens [n_gen], wall seconds per step [n_gen]: [0] prefill
+    and head, [i] decode step i), f16-rounded KV; the CPU baseline's run."""
+    m, keep, vocab = _model(gguf_reader, True, threads, act_i8)
+    prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+    out = np.zeros(n_gen, dtype=np.uint32)
+    secs = np.zeros(n_gen, dtype=np.float64)
+    _chk("llama_run_timed", lib().orc_llama_run_timed(C.byref(m), _p(prompt), prompt.size, n_gen, None, _p(out),
+                                                      None, _p(secs)))
+    del keep
+    return out, secs

@@ -19,6 +19,7 @@
 #include "oracle.h"
 
 #include <math.h>
+#include <time.h>
 #include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
@@ -710,8 +711,23 @@ static int nonfinite(const float *v, size_t n) {
  * i (teacher forcing: every step's logits are then those of one fixed token
  * sequence); out_tokens still receives each step's greedy token.
  * step_logits (nullable) receives the logits of every step, [n_gen][vocab]. */
+static double now_s(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
+
 int orc_llama_run(const orc_model *m, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
                   const uint32_t *forced, uint32_t *out_tokens, float *step_logits) {
+    return orc_llama_run_timed(m, prompt, n_prompt, n_gen, forced, out_tokens, step_logits, NULL);
+}
+
+/* orc_llama_run that also records wall seconds per step (nullable): [0] the
+ * prefill and its head, [i] decode step i (forward + head); the CPU
+ * baseline's timing. */
+int orc_llama_run_timed(const orc_model *m, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
+                        const uint32_t *forced, uint32_t *out_tokens, float *step_logits,
+                        double *step_seconds) {
     if (!n_prompt || !n_gen || n_prompt + n_gen > m->n_ctx)
         return 1; /* ContextLimit */
     size_t E = m->n_embd, kvw = m->n_kv_heads * m->head_dim, qw = m->n_heads * m->head_dim;
@@ -735,9 +751,12 @@ int orc_llama_run(const orc_model *m, const uint32_t *prompt, size_t n_prompt, s
     ws.up = (float *)calloc(T * F, 4);
     ws.act = (float *)calloc(T * F, 4);
     float *logits = (float *)calloc(m->vocab, 4);
+    double t0 = now_s();
     int st = run(m, &ws, kc, vc, prompt, T, 0);
     if (!st)
         st = qm(m, &m->output, ws.normed + (T - 1) * E, 1, logits);
+    if (step_seconds)
+        step_seconds[0] = now_s() - t0;
     for (size_t i = 0; !st && i < n_gen; i++) {
         if (nonfinite(logits, m->vocab)) {
             st = 10; /* Backend("empty or nonfinite logits") */
@@ -753,9 +772,12 @@ int orc_llama_run(const orc_model *m, const uint32_t *prompt, size_t n_prompt, s
                 st = 2;
                 break;
             }
+            t0 = now_s();
             st = run(m, &ws, kc, vc, &feed, 1, (uint32_t)(n_prompt + i));
             if (!st)
                 st = qm(m, &m->output, ws.normed, 1, logits);
+            if (step_seconds)
+                step_seconds[i + 1] = now_s() - t0;
         }
     }
     for (size_t i = 0; i < m->n_layers; i++) {

@@ -83,6 +83,9 @@ enum { ORC_I8_QKV = 1, ORC_I8_O = 2, ORC_I8_GATE_UP = 4, ORC_I8_DOWN = 8, ORC_I8
 size_t orc_i8_group(int dtype, size_t n_out, size_t n_in, size_t T);
 int orc_llama_run(const orc_model *m, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
                   const uint32_t *forced, uint32_t *out_tokens, float *step_logits);
+int orc_llama_run_timed(const orc_model *m, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
+                        const uint32_t *forced, uint32_t *out_tokens, float *step_logits,
+                        double *step_seconds);
 int orc_llama_generate(const orc_model *m, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
                        uint32_t *out_tokens, float *last_logits);
 

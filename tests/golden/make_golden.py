@@ -8,8 +8,15 @@
   /root/reference/src/backend/rocm/decode/tests.rs:81-96), each output checked
   here against an f64 dot product of the dequantized rows before it is written.
 - int8_small.npz: activations, their int8 quantization and block dots.
+- config5_steps.json (`config5` argument; about a minute of CPU): the
+  Llama-3-8B geometry with the Q4_K_M mix (random init, written by
+  mdma_amd.llama_synth with fast=True and CONFIG5_SEED), f32 activations,
+  f16-rounded KV. A 16-token prompt (the prefill GEMM route in the int8
+  mode), then 15 teacher-forced random tokens: every step's greedy token,
+  top-2 margin, largest |logit| and top-8 (token, logit) pairs, in the f32
+  mode and in the int8 mode (x requantized before every GEMV).
 
-Run from the repository root: python tests/golden/make_golden.py
+Run from the repository root: python tests/golden/make_golden.py [config5]
 """
 import json
 import os
@@ -25,6 +32,34 @@ from mdma_amd import gguf, llama_synth, synth  # noqa: E402
 from oracle import ffi  # noqa: E402
 
 HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+CONFIG5_SEED = 20261202
+CONFIG5_PROMPT, CONFIG5_STEPS = 16, 16
+
+
+def config5(path="/tmp/mdma_config5.gguf"):
+    if not os.path.exists(path):
+        llama_synth.write(path, llama_synth.LLAMA3_8B, llama_synth.Q4_K_M, CONFIG5_SEED, fast=True)
+    r = gguf.Reader(path)
+    V = llama_synth.LLAMA3_8B["vocab"]
+    prompt = synth.tokens(CONFIG5_PROMPT, V, CONFIG5_SEED + 1)
+    forced = synth.tokens(CONFIG5_STEPS - 1, V, CONFIG5_SEED + 2)
+    out = {"seed": CONFIG5_SEED, "prompt": prompt.tolist(), "forced": forced.tolist()}
+    for mode, act_i8 in (("f32", False), ("i8", True)):
+        toks, logits = ffi.llama_run(r, prompt, CONFIG5_STEPS, forced=forced, kv_f16=True, act_i8=act_i8)
+        steps = []
+        for i in range(CONFIG5_STEPS):
+            lg = logits[i]
+            order = np.argsort(lg)[::-1][:8]
+            steps.append({"greedy": int(toks[i]), "margin": float(lg[order[0]] - lg[order[1]]),
+                          "max_abs": float(np.max(np.abs(lg))),
+                          "top8": [[int(t), float(lg[t])] for t in order]})
+            assert steps[-1]["greedy"] == int(order[0])
+        out[mode] = steps
+        print(f"config5 {mode} margins / max|logit|:", [round(s["margin"] / s["max_abs"], 5) for s in steps])
+    with open(os.path.join(HERE, "config5_steps.json"), "w") as f:
+        json.dump(out, f)
 
 
 def main():
@@ -71,4 +106,7 @@ def main():
 
 
 if __name__ == "__main__":
-    main()
+    if len(sys.argv) > 1 and sys.argv[1] == "config5":
+        config5()
+    else:
+        main()

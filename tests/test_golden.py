@@ -61,3 +61,15 @@ def test_oracle_decode_is_prefill_consistent(tmp_path):
     # Batched (prefill) attention and step-wise attention are the same sums in the
     # oracle only up to rounding of different softmax lengths, so compare tokens.
     assert a[1:].tolist() == b.tolist()
+
+
+def test_config5_fixture_inputs_regenerate_from_its_seed():
+    """The config-5 fixture's prompt and forced tokens are the seeded
+    generator's (the GPU test rebuilds the model from the same seed)."""
+    fx = json.load(open(os.path.join(G, "config5_steps.json")))
+    assert fx["prompt"] == synth.tokens(16, 128256, fx["seed"] + 1).tolist()
+    assert fx["forced"] == synth.tokens(15, 128256, fx["seed"] + 2).tolist()
+    for mode in ("f32", "i8"):
+        assert len(fx[mode]) == 16
+        for st in fx[mode]:
+            assert st["greedy"] == st["top8"][0][0] and st["margin"] > 0

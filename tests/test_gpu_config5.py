@@ -1,0 +1,97 @@
+"""Config 5 end to end: the full Llama-3-8B geometry with the Q4_K_M mix
+(32 layers, dim 4096, 32 query / 8 KV heads, FFN 14336, vocab 128256; random
+init written as GGUF with the fixture's seed), against the CPU oracle's run
+of the same model committed in tests/golden/config5_steps.json.
+
+A 16-token prompt, then 15 teacher-forced random tokens (a random model left
+to itself repeats one token; forcing makes every step a new context). In
+both modes every step's logits at the oracle's top-8 tokens must agree, and
+the greedy token must be the oracle's where its top-2 margin is clear:
+  - f32 activations: within F32_LOGIT_RTOL of max|logit| (both sides round
+    K/V to f16 through 32 layers; a value an ulp apart may round to the
+    neighbouring half, a 2^-11 step);
+  - int8 activations (the production path; the 16-token prompt takes the
+    prefill GEMM): within I8_LOGIT_RTOL, the activation-flip scale measured
+    on the small models (tests/test_gpu_model.py).
+Batched decode of 8 sequences must give each sequence's single-sequence
+tokens (f32 mode: every GEMV is the correctly rounded dot product, whatever
+the batch).
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from mdma_amd import llama_synth, synth
+from mdma_amd.backend import ACT_F32, ACT_I8
+from mdma_amd.model import Model
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "config5_steps.json")
+F32_LOGIT_RTOL = 1e-3
+I8_LOGIT_RTOL = 3e-2
+I8_TOKEN_MARGIN = 2e-2
+
+
+@pytest.fixture(scope="module")
+def config5(tmp_path_factory):
+    fx = json.load(open(GOLDEN))
+    p = str(tmp_path_factory.mktemp("c5") / "llama3_8b_q4km.gguf")
+    llama_synth.write(p, llama_synth.LLAMA3_8B, llama_synth.Q4_K_M, fx["seed"], fast=True)
+    yield p, fx
+    os.remove(p)
+
+
+def forced_logits(backend, path, prompt, forced):
+    m = Model(backend, path)
+    s = m.session(len(prompt) + len(forced) + 1, 1, len(prompt))
+    out = [s.prefill(prompt, 0)]
+    for i, t in enumerate(forced):
+        out.append(s.forward(int(t), len(prompt) + i))
+    s.close()
+    m.close()
+    return np.stack(out)
+
+
+@pytest.mark.parametrize("mode", ["f32", "i8"])
+def test_config5_teacher_forced_steps_match_oracle(backend, config5, mode):
+    path, fx = config5
+    backend.set_act_mode(ACT_F32 if mode == "f32" else ACT_I8)
+    try:
+        got = forced_logits(backend, path, np.array(fx["prompt"], np.uint32), np.array(fx["forced"], np.uint32))
+    finally:
+        backend.set_act_mode(ACT_F32)
+    steps = fx[mode]
+    assert got.shape == (len(steps), 128256) and np.all(np.isfinite(got))
+    rtol = F32_LOGIT_RTOL if mode == "f32" else I8_LOGIT_RTOL
+    margin = 2 * F32_LOGIT_RTOL if mode == "f32" else I8_TOKEN_MARGIN
+    worst, compared = 0.0, 0
+    for i, st in enumerate(steps):
+        toks = np.array([t for t, _ in st["top8"]])
+        want = np.array([v for _, v in st["top8"]])
+        err = float(np.max(np.abs(got[i, toks] - want)) / st["max_abs"])
+        worst = max(worst, err)
+        assert err <= rtol, (mode, i, err)
+        if st["margin"] / st["max_abs"] > margin:
+            assert int(np.argmax(got[i])) == st["greedy"], (mode, i)
+            compared += 1
+    print(f"config5 {mode}: worst top-8 |dlogit|/max|logit| {worst:.2e}; greedy compared at {compared} steps")
+    assert compared >= len(steps) // 2, "test case too close to ties"
+
+
+def test_config5_batched_decode_equals_single_sequences(backend, config5):
+    path, fx = config5
+    backend.set_act_mode(ACT_F32)
+    prompts = np.stack([synth.tokens(16, 128256, fx["seed"] + 10 + b) for b in range(8)])
+    m = Model(backend, path)
+    s = m.session(16 + 8, 8, 16)
+    batched, _ = s.generate(prompts, 8)
+    s.close()
+    s = m.session(16 + 8, 1, 16)
+    for b in range(8):
+        s.reset()
+        one, _ = s.generate(prompts[b:b + 1], 8)
+        assert np.array_equal(one[0], batched[b]), b
+    s.close()
+    m.close()
