@@ -135,6 +135,14 @@ int mdma_gfx950_set_act_mode(mdma_ctx *ctx, int mode);
  * Default on; off runs the separate norm kernel (for A/B measurement and
  * the parity test of the fused path). */
 int mdma_gfx950_set_norm_fusion(mdma_ctx *ctx, int on);
+/* Extra: the int8 mode's prefill GEMM kernel (calls of 16 or more tokens).
+ * AUTO (default) takes the f16-path GEMM where it covers the weight (Q4_K
+ * rows of whole 256-column blocks) and the int8 MFMA GEMM elsewhere; I8
+ * forces the int8 MFMA GEMM (for A/B measurement and parity of both).
+ * Both compute the per-32-quantized product of the reference's
+ * qmatmul_i8 (src/backend/rocm.rs:1759-1918). */
+typedef enum { MDMA_PREFILL_AUTO = 0, MDMA_PREFILL_I8 = 1 } mdma_prefill_kernel;
+int mdma_gfx950_set_prefill_kernel(mdma_ctx *ctx, int kind);
 /* Extra: the HIP stream (hipStream_t) every launch of this context uses. */
 void *mdma_gfx950_stream(mdma_ctx *ctx);
 

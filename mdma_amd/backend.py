@@ -25,6 +25,7 @@ POOL_WEIGHTS, POOL_KV, POOL_SCRATCH = 0, 1, 2
 LAYOUT_GGUF, LAYOUT_GFX950, LAYOUT_ROCM_Q4K_V3 = 0, 1, 2
 DOMAIN_DEVICE, DOMAIN_HOST = 0, 1
 ACT_F32, ACT_I8 = 0, 1
+PREFILL_AUTO, PREFILL_I8 = 0, 1  # mdma_prefill_kernel
 
 ERROR_NAMES = {1: "ContextLimit", 2: "ShapeMismatch", 3: "NotImplemented", 4: "UnsupportedModel",
                5: "MemoryBudget", 6: "BufferBudget", 7: "InsufficientMemory", 8: "OutOfMemory",
@@ -72,7 +73,7 @@ _SIGS = {
     "available_device_bytes": [_P, _P], "supports_weight_dtype": [_P, _I32], "max_head_dim": [_P],
     "kv_elem_bytes": [_P], "join_execution": [_P], "set_buffer_budget": [_P, _U64, _U64],
     "buffer_usage": [_P, C.c_int, _P, _P], "set_act_mode": [_P, C.c_int],
-    "set_norm_fusion": [_P, C.c_int], "stream": [_P],
+    "set_norm_fusion": [_P, C.c_int], "set_prefill_kernel": [_P, C.c_int], "stream": [_P],
     "alloc": [_P, _U64, C.c_int, _P], "free": [_P], "buf_len": [_P], "buf_view": [_P, _U64, _U64, _P],
     "upload": [_P, _P, _U64, _P, _U64], "download": [_P, _P, _U64, _P, _U64],
     "copy": [_P, _P, _U64, _P, _U64, _U64], "upload_weight": [_P, _P, _U64, C.c_int, _P],
@@ -260,6 +261,11 @@ class Gfx950Backend:
 
     def set_norm_fusion(self, on: bool):
         _check(lib().mdma_gfx950_set_norm_fusion(self.ctx, int(bool(on))))
+
+    def set_prefill_kernel(self, kind: int):
+        """PREFILL_AUTO: the f16-path GEMM for Q4_K prefill calls, the int8
+        MFMA GEMM elsewhere; PREFILL_I8: the int8 MFMA GEMM for all."""
+        _check(lib().mdma_gfx950_set_prefill_kernel(self.ctx, int(kind)))
 
     def stream(self) -> int:
         return int(lib().mdma_gfx950_stream(self.ctx) or 0)

@@ -473,6 +473,15 @@ int mdma_gfx950_set_act_mode(mdma_ctx *ctx, int mode) {
   });
 }
 
+int mdma_gfx950_set_prefill_kernel(mdma_ctx *ctx, int kind) {
+  return guarded([&] {
+    need(ctx, "set_prefill_kernel");
+    if (kind != MDMA_PREFILL_AUTO && kind != MDMA_PREFILL_I8) shape_fail("set_prefill_kernel: unknown kind");
+    std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    ctx->prefill_kernel = kind;
+  });
+}
+
 int mdma_gfx950_set_norm_fusion(mdma_ctx *ctx, int on) {
   return guarded([&] {
     need(ctx, "set_norm_fusion");

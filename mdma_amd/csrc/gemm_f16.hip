@@ -1,0 +1,440 @@
+// Prefill GEMM on gfx950 with the int8 activations and integer weight
+// values carried on the f16 matrix path.
+//
+// Y[m, n] = sum_k X[m, k] * deq(W)[n, k]   (reference HipBackend::qmatmul_i8,
+// /root/reference/src/backend/rocm.rs:1759-1918; CPU oracle
+// src/backend/cpu.rs:335-368 on the requantized activations)
+//
+// Activations are quantized per 32 columns to int8 with an f32 scale (the
+// int8 mode's prefill configuration, the arithmetic of quantize_act_kernel
+// bit for bit). Every int8 value is an exact f16 (|q| <= 127 < 2^11), and so
+// is every Q4_K weight value q * sc (q <= 15, sc <= 63: at most 945): each
+// product of the f16 MFMA is exact and each 32-column block's dot product,
+// at most 2^23 in magnitude, is summed exactly in its f32 accumulator. So
+// v_mfma_f32_32x32x16_f16 computes the same integer block dots as an int8
+// MFMA, but hands them over as exact f32 with the 6-bit sub-scale already
+// applied: the float epilogue is one FMA per output and block,
+//   part += s_x[m, b] * C_b[n, m]
+// where the i32 MFMA would need a conversion, the sub-scale and the
+// activation scale on the VALU (3 to 4 operations per output and block;
+// without packed FP32 that caps it near 15% of the int8 peak).
+//
+// Q4_K, per super-block sb (256 columns, 8 blocks):
+//   Y += d[n] * part - dmin[n] * sum_b m[n, b] * P[m, b]
+// with P[m, b] = s_x[m, b] * sum_{k in b} q_x[m, k]. The min term is one
+// more MFMA per super-block: its 16 columns pair the 8 six-bit mins m[n, b]
+// (exact) with P[m, b] split into two f16 (hi + lo, 22 bits), P scaled per
+// token row by a power of two 2^e[m] that keeps it in f16 range (divided
+// out in the epilogue). The weight operand is q * sc itself, not an offset
+// form: an offset (1024 + q*sc, the plain bit-pattern conversion) would add
+// 1024 * sum_b P to part, a term several times larger than the result that
+// the epilogue would have to subtract again, losing its low bits.
+//
+// Rounding: part and Y are f32 sums of terms at the scale of the dot
+// product's partial sums, so each output is within about u * sum_k |x_k w_k|
+// (u = 2^-24) of the exact product of the quantized operands.
+//
+// Tiling: a 256-thread workgroup computes 128 weight rows x 128 tokens; each
+// of its 4 waves 64 x 64 (2 x 2 MFMA tiles of 32 x 32). The weight rows are
+// the MFMA's first operand, so each lane holds one token's column of a tile:
+// the activation scale s_x is a per-lane scalar, and each output of a lane
+// is one weight row. K advances 64 columns (one Q4_K sub-block pair) per
+// stage through two LDS buffers: while a stage computes from one, the next
+// is converted into the other and the one after is in flight from global
+// memory, with one barrier per stage. About 76 KB of LDS: two workgroups
+// per CU.
+#include <hip/hip_ext.h>
+
+#include "kernels.h"
+
+namespace mdma {
+namespace {
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int TN = 128, TM = 128, SK = 64, MAX_BLOCKS = 16384 / 32;
+
+// ---------------------------------------------------------- prologue ----
+// One workgroup per token row: q = round(x * 127 / amax) per 32 columns (the
+// quantize_act_kernel arithmetic), written as f16; s_x = amax / 127. With P
+// (Q4_K): P = s_x * sum q per block, stored as f16 hi + lo of P * 2^e where
+// 2^e brings the row's largest |P| into [512, 1024); inv[m] = 2^-e.
+__global__ __launch_bounds__(256) void gemm_act_kernel(const float *__restrict__ x, uint32_t K,
+                                                       _Float16 *__restrict__ xh, float *__restrict__ sx,
+                                                       _Float16 *__restrict__ ph, _Float16 *__restrict__ pl,
+                                                       float *__restrict__ inv) {
+#pragma clang fp contract(off)
+  __shared__ float bs[MAX_BLOCKS], bp[MAX_BLOCKS];
+  __shared__ float wmax[4];
+  const uint32_t m = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+  const float *xr = x + (size_t)m * K;
+  const uint32_t nch = K / 4, nb = K / 32;
+  float pmax = 0.f;
+  for (uint32_t c0 = 0; c0 < nch; c0 += 256) {
+    // Chunks of 4 columns; the 8 chunks of a block sit on 8 consecutive
+    // lanes, all live or all past the row (K is whole blocks).
+    const uint32_t c = c0 + tid;
+    const bool live = c < nch;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (live) {
+      const float4 t = *reinterpret_cast<const float4 *>(xr + 4 * (size_t)c);
+      v[0] = t.x, v[1] = t.y, v[2] = t.z, v[3] = t.w;
+    }
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    amax = dpp_max<0xB1, 0xF>(amax);
+    amax = dpp_max<0x4E, 0xF>(amax);
+    amax = dpp_max<0x141, 0xF>(amax);  // half-row mirror: the 8 lanes of the block
+    const float iv = amax == 0.f ? 0.f : 127.0f / amax;
+    int qi[4], sum = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      qi[k] = q8_round(v[k] * iv);
+      sum += qi[k];
+    }
+    sum += (int)dpp_u32<0xB1, 0xF>((uint32_t)sum);
+    sum += (int)dpp_u32<0x4E, 0xF>((uint32_t)sum);
+    sum += (int)dpp_u32<0x141, 0xF>((uint32_t)sum);
+    const float s = amax / 127.0f, p = s * (float)sum;
+    if (live) {
+      const v4h h = {(_Float16)(float)qi[0], (_Float16)(float)qi[1], (_Float16)(float)qi[2], (_Float16)(float)qi[3]};
+      *reinterpret_cast<v4h *>(xh + (size_t)m * K + 4 * (size_t)c) = h;
+      if ((lane & 7) == 0) {
+        bs[c >> 3] = s;
+        bp[c >> 3] = p;
+      }
+      pmax = fmaxf(pmax, fabsf(p));
+    }
+  }
+  pmax = wave_max_all(pmax);
+  if (lane == 0) wmax[tid >> 6] = pmax;
+  __syncthreads();
+  const float pm = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  int e = 0;
+  if (pm > 0.f) {
+    int ex;
+    frexpf(pm, &ex);  // pm = f * 2^ex, f in [0.5, 1)
+    e = min(max(10 - ex, -100), 100);
+  }
+  for (uint32_t b = tid; b < nb; b += 256) {
+    sx[(size_t)m * nb + b] = bs[b];
+    if (ph) {
+      const float p = ldexpf(bp[b], e);
+      const _Float16 hi = (_Float16)p;
+      ph[(size_t)m * nb + b] = hi;
+      pl[(size_t)m * nb + b] = (_Float16)(p - (float)hi);
+    }
+  }
+  if (tid == 0 && inv) inv[m] = ldexpf(1.0f, -e);
+}
+
+// ------------------------------------------------------------- GEMM ----
+
+struct F16Args {
+  const _Float16 *xh;  // [M, K] int8 values as f16
+  const float *sx;     // [M, K/32]
+  const _Float16 *p;   // [M, K/32] Q4_K: P * 2^e, hi; the lo array p_lo elements further
+  uint32_t p_lo;
+  const float *inv;    // [M] Q4_K: 2^-e
+  const uint8_t *w;    // prepared rows, row_bytes apart
+  float *y;            // [M, N]
+  uint32_t M, N, K;
+  uint64_t row_bytes;
+};
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+// Global memory straight into LDS (global_load_lds): each lane of the wave
+// moves 16 (or 4) bytes from base + off to LDS address lds + 16 (4) * lane.
+// Issued as inline assembly so that the compiler does not track it: its own
+// LDS-DMA tracking cannot tell runtime-indexed LDS buffers apart and would
+// wait for these loads before every LDS read of the other buffer. The
+// kernel waits for them itself (lds_wait_dma) before reading what they
+// wrote or publishing it at a barrier.
+__device__ __forceinline__ uint32_t lds_addr(const void *lds) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);  // the LDS offset: low bits of the address
+}
+__device__ __forceinline__ void lds_dma16(const void *base, uint32_t off, const void *lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds_addr(lds))
+               : "memory");
+}
+__device__ __forceinline__ void lds_dma4(const void *base, uint32_t off, const void *lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds_addr(lds))
+               : "memory");
+}
+__device__ __forceinline__ void lds_wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Physical 16-byte chunk of logical chunk c (0..7) of LDS row r: rows are
+// 128 bytes, so 16 lanes reading one chunk of 16 consecutive rows would hit
+// the same 4 banks every second row; XOR-ing the chunk with bits 1..3 of the
+// row spreads them over all 64 banks.
+__device__ __forceinline__ int swz(int r, int c) { return (c ^ (r >> 1)) & 7; }
+
+// Eight 4-bit quants q (one dword: bytes b, low nibble then high nibble)
+// times a sub-block scale, as f16 pairs: v_perm_b32 puts each nibble under
+// the exponent byte 0x64 (the f16 1024 + q), and one packed f16 FMA forms
+// (1024 + q) * sc - 1024 * sc = q * sc, exact (the FMA rounds once, and
+// q * sc <= 945 is an f16 integer).
+__device__ __forceinline__ void q4_f16(uint32_t q, h2 sa, h2 na, h2 sb, h2 nb_, uint32_t lo[2], uint32_t hi[2]) {
+  const uint32_t t = q & 0x0F0F0F0Fu, u = (q >> 4) & 0x0F0F0F0Fu;
+  const uint32_t c = 0x64646464u;
+  auto f = [](uint32_t bits, h2 s, h2 n) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(h2, bits), s, n));
+  };
+  lo[0] = f(__builtin_amdgcn_perm(c, t, 0x04010400u), sa, na);  // quants 0, 1
+  lo[1] = f(__builtin_amdgcn_perm(c, t, 0x04030402u), sa, na);  // quants 2, 3
+  hi[0] = f(__builtin_amdgcn_perm(c, u, 0x04010400u), sb, nb_);
+  hi[1] = f(__builtin_amdgcn_perm(c, u, 0x04030402u), sb, nb_);
+}
+
+template <int DT>
+__global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
+  __shared__ __attribute__((aligned(16))) _Float16 ws[2][TN][SK];  // weights, f16 q * sc
+  __shared__ __attribute__((aligned(16))) _Float16 xs[2][TM][SK];  // activations, f16 int8 values
+  __shared__ __attribute__((aligned(16))) uint8_t wraw[TN][32];    // the stage's quant bytes (planes A, B)
+  __shared__ __attribute__((aligned(16))) uint8_t whd[TN][16];     // the super-block's row headers
+  __shared__ __attribute__((aligned(16))) float sxs[2][2][TM];      // s_x of the stage's two blocks
+  __shared__ __attribute__((aligned(16))) _Float16 xmin[2][TM][8];  // P hi / lo of the super-block
+  __shared__ __attribute__((aligned(16))) _Float16 wmin[TN][8];     // the rows' 8 mins
+  __shared__ __attribute__((aligned(16))) float dvs[TN], dms[TN];
+  __shared__ float invs[TM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t bn = blockIdx.x * TN, bm = blockIdx.y * TM;
+  const int wn = (wave & 1) * 64, wm = (wave >> 1) * 64;
+  // 16 x 16 MFMA tiles: lane l holds column l % 16 (a token) and K chunk
+  // l / 16 of its operands, and rows 4 (l / 16) .. + 3 of its result.
+  const int l16 = lane & 15, lq = lane >> 4;
+  const uint32_t K = a.K, nb = K / 32, nst = K / SK, U = K / 64, rb = (uint32_t)a.row_bytes;
+
+  // Byte offsets of each lane's DMA sources (32-bit: the launcher keeps the
+  // activations below 2^31 elements and the weights below 2^32 bytes).
+  // X: the wave's i-th load fills rows 32 wave + 8 i + l / 8, physical chunk
+  // l % 8 (LDS byte 16 l), with the logical chunk the swizzle places there.
+  uint32_t xo[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int row = 32 * wave + 8 * i + (lane >> 3);
+    xo[i] = 2 * (min(bm + row, a.M - 1) * K + 8 * swz(row, lane & 7));
+  }
+  // Per thread (LDS byte 16 tid or 4 tid): token s_tok's block s_blk (s_x)
+  // or hi / lo half (P); weight row w_row's plane w_plane.
+  const int s_tok = tid & 127, s_blk = tid >> 7;
+  const uint32_t s_row = min(bm + s_tok, a.M - 1);
+  const uint32_t so = 4 * (s_row * nb + s_blk), po = 2 * (s_row * nb + (s_blk ? a.p_lo : 0));
+  const int w_row = tid >> 1, w_plane = tid & 1;
+  const uint32_t wrow = min(bn + w_row, a.N - 1) * rb;
+  const uint32_t wo = wrow + 16 * (w_plane ? U : 0);
+  // Headers: lanes 0..31 of wave w load rows 32 w + lane (the rows of the
+  // wave's own threads).
+  const uint32_t ho = min(bn + 32 * wave + (lane & 31), a.N - 1) * rb + 32 * U;
+  if (tid < TM) invs[tid] = a.inv[min(bm + tid, a.M - 1)];
+
+  // Stage st's operands into LDS: X into xs[st & 1], s_x into sxs[st & 1],
+  // the quant bytes into wraw; at a super-block's first stage its headers.
+  auto gload = [&](uint32_t st) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) lds_dma16(a.xh, xo[i] + 128 * st, &xs[st & 1][32 * wave + 8 * i][0]);
+    lds_dma4(a.sx, so + 8 * st, &sxs[st & 1][0][64 * wave]);
+    lds_dma16(a.w, wo + 16 * st, &wraw[32 * wave][0]);
+    if (st % 4 == 0 && lane < 32) lds_dma16(a.w, ho + 4 * st, &whd[32 * wave][0]);
+  };
+  // P of super-block sb into xmin (its previous contents, the last
+  // super-block's, are read by that super-block's epilogue: issued after it).
+  auto pload = [&](uint32_t sb) { lds_dma16(a.p, po + 16 * sb, &xmin[0][0][0] + 512 * wave); };
+  // The stage's weights into ws[st & 1] as f16 q * sc (each thread converts
+  // the 16 bytes it loaded).
+  auto wstore = [&](uint32_t st) {
+    const uint4 gq = *reinterpret_cast<const uint4 *>(&wraw[w_row][16 * w_plane]);
+    const uint4 hd = *reinterpret_cast<const uint4 *>(&whd[w_row][0]);
+    int sca, scb, ma, mb;
+    q4k_scales_i(hd, st & 3, sca, scb, ma, mb);
+    const _Float16 fa = (_Float16)(float)sca, fb = (_Float16)(float)scb;
+    const h2 sa = {fa, fa}, sb = {fb, fb};
+    const h2 na = {(_Float16)(-1024.0f * (float)sca), (_Float16)(-1024.0f * (float)sca)};
+    const h2 nbv = {(_Float16)(-1024.0f * (float)scb), (_Float16)(-1024.0f * (float)scb)};
+    // 16 bytes: low nibbles -> sub-block 2p columns [16*plane, +16),
+    // high nibbles -> sub-block 2p+1 columns [32 + 16*plane, +16).
+    const uint32_t qw[4] = {gq.x, gq.y, gq.z, gq.w};
+    uint32_t lo[8], hi[8];
+#pragma unroll
+    for (int d = 0; d < 4; d++) q4_f16(qw[d], sa, na, sb, nbv, &lo[2 * d], &hi[2 * d]);
+    _Float16 *wr = &ws[st & 1][w_row][0];
+    *reinterpret_cast<uint4 *>(wr + 8 * swz(w_row, 2 * w_plane)) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    *reinterpret_cast<uint4 *>(wr + 8 * swz(w_row, 2 * w_plane + 1)) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
+    *reinterpret_cast<uint4 *>(wr + 8 * swz(w_row, 4 + 2 * w_plane)) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    *reinterpret_cast<uint4 *>(wr + 8 * swz(w_row, 5 + 2 * w_plane)) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+  };
+  // The super-block's epilogue operands from its headers: the 8 mins of each
+  // row (f16), d and dmin.
+  auto hstore = [&]() {
+    const uint4 hd = *reinterpret_cast<const uint4 *>(&whd[w_row][0]);
+    if (w_plane == 0) {
+      int mn[8], sc;
+#pragma unroll
+      for (int j = 0; j < 4; j++) q4k_scales_i(hd, j, sc, sc, mn[2 * j], mn[2 * j + 1]);
+      const v8h mv = {(_Float16)(float)mn[0], (_Float16)(float)mn[1], (_Float16)(float)mn[2], (_Float16)(float)mn[3],
+                      (_Float16)(float)mn[4], (_Float16)(float)mn[5], (_Float16)(float)mn[6], (_Float16)(float)mn[7]};
+      *reinterpret_cast<v8h *>(&wmin[w_row][0]) = mv;
+      dvs[w_row] = h2f(hd.x);
+    } else {
+      dms[w_row] = h2f(hd.x >> 16);
+    }
+  };
+
+  // part: the super-block's sum of s_x * block dot; acc: the outputs.
+  float acc[4][4][4], part[4][4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) acc[i][j][r] = 0.f, part[i][j][r] = 0.f;
+
+  gload(0);
+  pload(0);
+  lds_wait_dma();
+  wstore(0);
+  hstore();
+  lds_barrier();
+  for (uint32_t st = 0; st < nst; st++) {
+    // Stage st + 1's loads in flight over this stage's MFMAs, into the other
+    // buffers (last read by stage st - 1, before the barrier). A
+    // super-block's P goes in at its second stage, after the previous
+    // super-block's epilogue.
+    if (st + 1 < nst) gload(st + 1);
+    if (st % 4 == 0 && st > 0) pload(st / 4);
+    const int buf = st & 1;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {  // the stage's two blocks, one 16x16x32 MFMA per tile each
+      v8h A[4], B[4];
+      float s[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int r = wn + 16 * i + l16;
+        A[i] = *reinterpret_cast<const v8h *>(&ws[buf][r][8 * swz(r, 4 * h + lq)]);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int r = wm + 16 * j + l16;
+        B[j] = *reinterpret_cast<const v8h *>(&xs[buf][r][8 * swz(r, 4 * h + lq)]);
+        s[j] = sxs[buf][h][r];
+      }
+      // Software-pipelined: tile t + 1's MFMA is issued before tile t's
+      // FMAs, so the matrix core and the VALU overlap.
+      v4f c[2];
+      c[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0], B[0], v4f{}, 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < 16; t++) {
+        if (t + 1 < 16)
+          c[(t + 1) & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[(t + 1) >> 2], B[(t + 1) & 3], v4f{}, 0, 0, 0);
+        const int i = t >> 2, j = t & 3;
+#pragma unroll
+        for (int r = 0; r < 4; r++) part[i][j][r] = fmaf(s[j], c[t & 1][r], part[i][j][r]);
+      }
+    }
+    if (st % 4 == 3) {  // the super-block's last stage: d and the min term
+      // Min MFMA (16x16x16): K chunk lq of 4 columns; chunks 0, 1 pair the
+      // 8 mins with P hi, chunks 2, 3 the same mins with P lo.
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int rw = wn + 16 * i;
+        const v4h Am = *reinterpret_cast<const v4h *>(&wmin[rw + l16][4 * (lq & 1)]);
+        const float4 d4 = *reinterpret_cast<const float4 *>(&dvs[rw + 4 * lq]);
+        const float4 m4 = *reinterpret_cast<const float4 *>(&dms[rw + 4 * lq]);
+        const float dv[4] = {d4.x, d4.y, d4.z, d4.w}, dm[4] = {m4.x, m4.y, m4.z, m4.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const int t = wm + 16 * j + l16;
+          const v4h Bm = *reinterpret_cast<const v4h *>(&xmin[lq >> 1][t][4 * (lq & 1)]);
+          const v4f cm = __builtin_amdgcn_mfma_f32_16x16x16f16(Am, Bm, v4f{}, 0, 0, 0);
+          const float iv = invs[t];
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            acc[i][j][r] = fmaf(dv[r], part[i][j][r], acc[i][j][r]);
+            acc[i][j][r] = fmaf(-dm[r] * iv, cm[r], acc[i][j][r]);
+            part[i][j][r] = 0.f;
+          }
+        }
+      }
+    }
+    lds_wait_dma();
+    if (st + 1 < nst) wstore(st + 1);
+    // A super-block's epilogue operands go to LDS once the previous
+    // super-block's epilogue (stage st - 1) has passed the barrier.
+    if (st % 4 == 0 && st > 0) hstore();
+    lds_barrier();
+  }
+  // ---- store: lane = token; a tile's 4 outputs are 4 consecutive rows ----
+  const bool vec = (a.N & 3) == 0;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint32_t m = bm + wm + 16 * j + l16;
+    if (m >= a.M) continue;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t n = bn + wn + 16 * i + 4 * lq;
+      float *yp = a.y + (size_t)m * a.N + n;
+      if (vec && n + 3 < a.N) {
+        *reinterpret_cast<float4 *>(yp) = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+          if (n + t < a.N) yp[t] = acc[i][j][t];
+      }
+    }
+  }
+}
+
+}  // namespace
+
+bool gemm_f16_supported(int32_t dtype, int layout, uint64_t n_in, uint64_t n_out) {
+  if (layout != MDMA_LAYOUT_GFX950 || dtype != DT_Q4_K) return false;
+  if (n_in % 256 || n_in > 32 * (uint64_t)MAX_BLOCKS) return false;
+  // Weight offsets are 32-bit inside the kernel.
+  return n_out * gfx950_row_bytes(dtype, n_in) < (1ull << 32);
+}
+
+namespace {
+uint64_t r256(uint64_t b) { return (b + 255) / 256 * 256; }
+}  // namespace
+
+uint64_t gemm_f16_input_bytes(uint64_t M, uint64_t K) {
+  return r256(M * K * 2) + r256(M * (K / 32) * 4) + 2 * r256(M * (K / 32) * 2) + r256(M * 4);
+}
+
+void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t M, char *s) {
+  const uint64_t K = jobs[0].n_in, nb = K / 32;
+  _Float16 *xh = reinterpret_cast<_Float16 *>(s);
+  s += r256(M * K * 2);
+  float *sx = reinterpret_cast<float *>(s);
+  s += r256(M * nb * 4);
+  _Float16 *ph = reinterpret_cast<_Float16 *>(s);
+  s += r256(M * nb * 2);
+  _Float16 *pl = reinterpret_cast<_Float16 *>(s);
+  s += r256(M * nb * 2);
+  float *inv = reinterpret_cast<float *>(s);
+  gemm_act_kernel<<<dim3((uint32_t)M), dim3(256), 0, ctx->stream>>>(x, (uint32_t)K, xh, sx, ph, pl, inv);
+  hip_check(hipGetLastError(), "gemm activation launch");
+  // Token rows per launch: activation offsets are 32-bit inside the kernel.
+  const uint64_t rows = ((1ull << 31) / K) / TM * TM;
+  hipEvent_t t0 = ctx->time_start, t1 = ctx->time_stop;
+  ctx->time_start = ctx->time_stop = nullptr;
+  for (int i = 0; i < n_jobs; i++) {
+    const GemvJob &w = jobs[i];
+    for (uint64_t m0 = 0; m0 < M; m0 += rows) {
+      const uint64_t Mc = M - m0 < rows ? M - m0 : rows;
+      F16Args a{xh + m0 * K, sx + m0 * nb, ph + m0 * nb, (uint32_t)(pl - ph), inv + m0, w.w, w.y + m0 * w.n_out,
+                (uint32_t)Mc, (uint32_t)w.n_out, (uint32_t)K, gfx950_row_bytes(w.dtype, K)};
+      const dim3 grid((uint32_t)((w.n_out + TN - 1) / TN), (uint32_t)((Mc + TM - 1) / TM)), block(256);
+      // Timing events bracket the calls' GEMM launches (not the prologue).
+      const hipEvent_t e0 = i == 0 && m0 == 0 ? t0 : nullptr, e1 = i == n_jobs - 1 && m0 + Mc >= M ? t1 : nullptr;
+      if (e0 || e1) hipExtLaunchKernelGGL(gemm_f16_kernel<DT_Q4_K>, grid, block, 0, ctx->stream, e0, e1, 0, a);
+      else gemm_f16_kernel<DT_Q4_K><<<grid, block, 0, ctx->stream>>>(a);
+      hip_check(hipGetLastError(), "gemm f16 launch");
+    }
+  }
+}
+
+}  // namespace mdma

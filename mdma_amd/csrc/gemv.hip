@@ -888,8 +888,31 @@ void launch_gemv_f32_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up
 // Prefill-sized int8 calls (T >= GEMM_MIN_TOKENS) on prepared Q8_0 / Q4_K
 // weights run the MFMA GEMM with activations quantized per 32 (quantized
 // once for every job sharing x). Returns false when a job is not covered.
+// Q4_K jobs take the f16-path GEMM unless the context asks for the int8
+// one, or its inputs do not fit where they must go (a capture's fixed-size
+// scratch, an allocation-free call's buffer).
+static bool try_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t T) {
+  if (ctx->prefill_kernel != MDMA_PREFILL_AUTO) return false;
+  for (int i = 0; i < n_jobs; i++)
+    if (!gemm_f16_supported(jobs[i].dtype, jobs[i].layout, jobs[i].n_in, jobs[i].n_out) ||
+        jobs[i].n_in != jobs[0].n_in)
+      return false;
+  const uint64_t need = gemm_f16_input_bytes(T, jobs[0].n_in);
+  char *s;
+  if (ctx->fixed_scratch) {
+    if (need > ctx->fixed_cap) return false;
+    s = ctx->fixed_scratch;
+  } else {
+    if (ctx->capturing && need > ctx->scratch_cap) return false;
+    s = scratch(ctx, need);
+  }
+  launch_gemm_f16(ctx, jobs, n_jobs, x, T, s);
+  return true;
+}
+
 static bool try_gemm_i8(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t T) {
   if (T < GEMM_MIN_TOKENS) return false;
+  if (try_gemm_f16(ctx, jobs, n_jobs, x, T)) return true;
   for (int i = 0; i < n_jobs; i++)
     if (!gemm_i8_supported(jobs[i].dtype, jobs[i].layout, jobs[i].n_in, jobs[i].n_out) ||
         jobs[i].n_in != jobs[0].n_in)

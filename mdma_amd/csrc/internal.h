@@ -95,6 +95,7 @@ struct mdma_ctx {
   uint32_t *host_ids = nullptr;  // pinned staging for token ids / argmax result
   uint64_t host_ids_cap = 0;
   bool capturing = false;        // stream capture in progress: no synchronizing calls
+  int prefill_kernel = MDMA_PREFILL_AUTO;  // mdma_gfx950_set_prefill_kernel
   // Events the next GEMV kernel's dispatch timestamps (mdma_gfx950_time_next_gemv).
   hipEvent_t time_start = nullptr, time_stop = nullptr;
   // Per-chunk partial results of the two-pass argmax (12 bytes per chunk).
@@ -275,6 +276,14 @@ void launch_gemm_i8(mdma_ctx *ctx, const GemvJob &w, const int8_t *qx, const flo
                     uint64_t M, float *y, double *part, uint64_t part_doubles, uint32_t *cnt, uint64_t counters);
 // Token count from which the int8 mode runs the MFMA GEMM instead of the GEMV.
 constexpr uint64_t GEMM_MIN_TOKENS = 16;
+// Prefill GEMM on the f16 matrix path (gemm_f16.hip): the same per-32 int8
+// activations, carried as exact f16 integers with the Q4_K weights' 6-bit
+// sub-scales folded into the weight operand. Whether it covers (dtype,
+// layout, n_in, n_out); the scratch bytes its inputs take for M tokens; the
+// launch (quantization prologue, then each job's GEMM) with that scratch.
+bool gemm_f16_supported(int32_t dtype, int layout, uint64_t n_in, uint64_t n_out);
+uint64_t gemm_f16_input_bytes(uint64_t M, uint64_t K);
+void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t M, char *scratch);
 void launch_quantize_act(mdma_ctx *ctx, const float *x, uint64_t n, uint64_t group, int8_t *q,
                          float *d, int32_t *sum16);
 void launch_block_dot(mdma_ctx *ctx, const GemvJob &w, const int8_t *qx, uint64_t T, int32_t *out);

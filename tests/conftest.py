@@ -30,7 +30,18 @@ def f32_exact(W: np.ndarray, x: np.ndarray) -> np.ndarray:
 PARITY_LOG = []
 
 
-def assert_parity(got, cpu, exact, rtol, atol=1e-6, what="", correctly_rounded=False):
+U32 = 2.0 ** -24  # unit roundoff of f32
+
+
+def abs_dot(W, x):
+    """sum_k |x[t, k]| |W[r, k]| in f64, [T, rows]: the scale of a dot
+    product's partial sums, which sets its rounding error (the CPU's
+    sequential f32 sum is guaranteed only within K * u of it)."""
+    k = W.shape[1]
+    return np.abs(np.asarray(x, np.float64).reshape(-1, k)) @ np.abs(np.asarray(W, np.float64)).T
+
+
+def assert_parity(got, cpu, exact, rtol, atol=1e-6, what="", correctly_rounded=False, abs_sum=None, k_u=2.0):
     """Per-element parity against the CPU oracle.
 
     The oracle sums each dot product sequentially in f32 (reference
@@ -51,6 +62,13 @@ def assert_parity(got, cpu, exact, rtol, atol=1e-6, what="", correctly_rounded=F
     products and sums) and round once, so every element must be at least as
     close to exact as the CPU's sequential f32 sum, which no rounding of the
     exact value can lose to: |gpu - exact| <= |cpu - exact| everywhere.
+
+    abs_sum (per element sum_k |x_k w_k|, see abs_dot): for kernels that sum
+    in f32 at the scale of the partial sums (the prefill GEMMs), the slack
+    gains k_u * u * abs_sum, k_u roundings at that scale. Without it an
+    output that cancels to near zero would have to match to about 1e-6
+    while its terms are ~10: tighter than one ulp of the partial sums, a
+    bound the CPU's own sum (within K * u * abs_sum) does not meet either.
     """
     got = np.asarray(got, dtype=np.float64).reshape(-1)
     cpu = np.asarray(cpu, dtype=np.float64).reshape(-1)
@@ -58,6 +76,8 @@ def assert_parity(got, cpu, exact, rtol, atol=1e-6, what="", correctly_rounded=F
     assert got.shape == cpu.shape == exact.shape
     assert np.all(np.isfinite(got)), f"{what}: non-finite GPU output"
     bound = atol + rtol * np.abs(cpu) + np.abs(cpu - exact)
+    if abs_sum is not None:
+        bound = bound + k_u * U32 * np.asarray(abs_sum, dtype=np.float64).reshape(-1)
     err = np.abs(got - cpu)
     bad = np.nonzero(~(err <= bound))[0]
     assert bad.size == 0, (f"{what}: {bad.size}/{got.size} elements outside tolerance; first {bad[:5]}: "

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import npq
-from conftest import assert_parity, f32_exact
+from conftest import abs_dot, assert_parity, f32_exact
 from mdma_amd import synth
 from mdma_amd import backend as backend_mod
 from mdma_amd.backend import LAYOUT_GFX950, POOL_WEIGHTS, QWeight, ShapeMismatch, pack_weight
@@ -192,9 +192,10 @@ def test_i8_mode_batched(backend, T):
         g = 32 if T >= 16 else 256
         q = np.concatenate([ffi.quantize_act(x[t * k:(t + 1) * k], g)[0] for t in range(T)])
         d = np.concatenate([ffi.quantize_act(x[t * k:(t + 1) * k], g)[1] for t in range(T)])
-        cpu, exact = oracle_f32(dtype, raw, rows, k, ffi.dequantize_act(q, d, g))
-        assert_parity(got, cpu, exact, 1e-3, atol=gemm_atol(dtype) if T >= 16 else 1e-6,
-                      what=f"i8 batched {dtype} T={T}")
+        xq = ffi.dequantize_act(q, d, g)
+        cpu, exact = oracle_f32(dtype, raw, rows, k, xq)
+        absum = abs_dot(npq.dequantize(dtype, raw, rows, k), xq) if T >= 16 else None
+        assert_parity(got, cpu, exact, 1e-3, abs_sum=absum, what=f"i8 batched {dtype} T={T}")
 
 
 @pytest.mark.parametrize("dtype,shape,T", [(Q6K, (4096, 14336), 4), (Q6K, (4096, 14336), 8),
@@ -643,38 +644,81 @@ def test_packed_upload_rejects_wrong_sizes(backend):
 
 
 # ------------------------------------------------------- prefill GEMM ----
-# int8 mode with T >= 16 tokens on prepared Q8_0 / Q4_K / Q6_K weights runs the
-# int8 MFMA GEMM: activations quantized per 32 with an f32 scale. Oracle: the
-# reference's "requantize, then CPU qmatmul" (src/backend/rocm/decode/tests.rs:68-130).
+# int8 mode with T >= 16 tokens on prepared Q8_0 / Q4_K / Q6_K weights runs a
+# prefill GEMM on activations quantized per 32 with an f32 scale: the
+# f16-path GEMM for Q4_K (default), the int8 MFMA GEMM otherwise or when
+# asked. Oracle: the reference's "requantize, then CPU qmatmul"
+# (src/backend/rocm/decode/tests.rs:68-130).
 
 def oracle_i8_32(dtype, raw, rows, k, x):
+    """(CPU oracle, exact, sum_k |x_k w_k|) of the per-32 requantized product."""
     q, d, _ = ffi.quantize_act(x, 32)
-    return oracle_f32(dtype, raw, rows, k, ffi.dequantize_act(q, d, 32))
+    xq = ffi.dequantize_act(q, d, 32)
+    cpu, exact = oracle_f32(dtype, raw, rows, k, xq)
+    return cpu, exact, abs_dot(npq.dequantize(dtype, raw, rows, k), xq)
 
 
-def gemm_atol(dtype):
-    """Absolute slack for outputs that cancel to near zero. Q6_K weights of
-    the synthetic distribution (scales up to 64, values up to 32) give dot
-    products about ten times larger than Q4_K / Q8_0 ones, and the GEMM sums
-    each 128-column stage in f32 before its f64 total, so an output near zero
-    carries f32 rounding of those larger terms: 1e-5 is a few ulps at their
-    scale (|y| ~ 10)."""
-    return 1e-5 if dtype == Q6K else 1e-6
+# (dtype, prefill kernel): both kernels for Q4_K, the int8 one elsewhere.
+GEMM_CASES = [(Q8, backend_mod.PREFILL_I8), (Q4K, backend_mod.PREFILL_AUTO), (Q4K, backend_mod.PREFILL_I8),
+              (Q6K, backend_mod.PREFILL_I8)]
+GEMM_IDS = ["q8-i8", "q4k-f16", "q4k-i8", "q6k-i8"]
 
 
-@pytest.mark.parametrize("shape", [(16, 256, 64), (37, 512, 200), (130, 1024, 257), (64, 4096, 384)])
-@pytest.mark.parametrize("dtype", [Q8, Q4K, Q6K])
-def test_prefill_gemm_i8(backend, dtype, shape):
+@pytest.fixture
+def prefill_kernel(backend, request):
+    backend.set_prefill_kernel(request.param)
+    yield request.param
+    backend.set_prefill_kernel(backend_mod.PREFILL_AUTO)
+
+
+def gemm_cases(f):
+    f = pytest.mark.parametrize("dtype,prefill_kernel", GEMM_CASES, ids=GEMM_IDS, indirect=["prefill_kernel"])(f)
+    return f
+
+
+@pytest.mark.parametrize("shape", [(16, 256, 64), (37, 512, 200), (130, 1024, 257), (64, 4096, 384),
+                                   (300, 768, 130)])
+@gemm_cases
+def test_prefill_gemm_i8(backend, dtype, prefill_kernel, shape):
     T, k, rows = shape
     raw = synth.weight(dtype, rows, k, 300 + T)
     x = synth.normal_f32(T * k, 301 + rows)
     got = run_qmatmul(backend, dtype, raw, rows, k, x, "i8")
-    cpu, exact = oracle_i8_32(dtype, raw, rows, k, x)
-    assert_parity(got, cpu, exact, 1e-3, atol=gemm_atol(dtype), what=f"gemm dtype={dtype} T={T} k={k} rows={rows}")
+    cpu, exact, absum = oracle_i8_32(dtype, raw, rows, k, x)
+    assert_parity(got, cpu, exact, 1e-3, abs_sum=absum,
+                  what=f"gemm dtype={dtype} kernel={prefill_kernel} T={T} k={k} rows={rows}")
 
 
-@pytest.mark.parametrize("dtype", [Q8, Q4K, Q6K])
-def test_prefill_gemm_config4_shapes_sampled_rows(backend, dtype):
+@gemm_cases
+def test_prefill_gemm_activation_ranges(backend, dtype, prefill_kernel):
+    """Token rows over 50 decades of magnitude, an all-zero row, a row of one
+    non-zero, rows whose blocks quantize to the int8 extremes +-127 (and a
+    block of equal values, all at 127) and mixed block magnitudes within a
+    row: the f16-path GEMM rescales each row's block sums by a power of two
+    to keep them in f16 range, and must agree with the oracle throughout."""
+    T, k, rows = 40, 512, 136
+    raw = synth.weight(dtype, rows, k, 320)
+    x = synth.normal_f32(T * k, 321).reshape(T, k)
+    for t in range(24):
+        x[t] *= np.float32(10.0 ** (2 * t - 25))
+    x[24] = 0
+    x[25] = 0
+    x[25, 300] = -3.5
+    x[26] = np.sign(x[26]) * 2.0  # every block all at +-127
+    x[27] = 1.25                  # equal values: 127 everywhere
+    x[28, :256] *= np.float32(1e-6)  # one super-block 10^6 smaller than the next
+    x[29, ::32] = 1e4             # one outlier per block
+    x = x.reshape(-1)
+    got = run_qmatmul(backend, dtype, raw, rows, k, x, "i8")
+    cpu, exact, absum = oracle_i8_32(dtype, raw, rows, k, x)
+    # The slack of each element scales with its own terms (abs_sum): rows of
+    # 1e-25 and of 1e21 are held to the same relative bar.
+    assert_parity(got, cpu, exact, 1e-3, atol=0.0, abs_sum=absum, what=f"gemm ranges kernel={prefill_kernel}")
+    assert np.all(got[24] == 0)
+
+
+@gemm_cases
+def test_prefill_gemm_config4_shapes_sampled_rows(backend, dtype, prefill_kernel):
     """Full config-4 shapes on the GPU; the oracle checks a sample of output
     rows (the weight rows are contiguous, so a row slice is its own weight)."""
     for T, k, rows in ((512, 4096, 14336), (2048, 14336, 4096)):
@@ -687,10 +731,10 @@ def test_prefill_gemm_config4_shapes_sampled_rows(backend, dtype):
         rb = len(raw) // rows
         for r0 in (0, rows // 2 + 13, rows - 16):
             sl = raw[r0 * rb:(r0 + 16) * rb]
-            tok = np.r_[0:8, T - 8:T]
-            cpu, exact = oracle_i8_32(dtype, sl, 16, k, x.reshape(T, k)[tok].reshape(-1))
-            assert_parity(y[tok, r0:r0 + 16].reshape(-1), cpu, exact, 1e-3, atol=gemm_atol(dtype),
-                          what=f"gemm config4 dtype={dtype} T={T} rows {r0}..")
+            tok = np.r_[0:8, 130:133, T - 8:T]
+            cpu, exact, absum = oracle_i8_32(dtype, sl, 16, k, x.reshape(T, k)[tok].reshape(-1))
+            assert_parity(y[tok, r0:r0 + 16].reshape(-1), cpu, exact, 1e-3, abs_sum=absum,
+                          what=f"gemm config4 dtype={dtype} kernel={prefill_kernel} T={T} rows {r0}..")
         w.buf.close(), xb.close(), yb.close()
 
 
@@ -706,8 +750,8 @@ def test_prefill_gemm_fused_calls(backend, dtype):
         outs = [backend.alloc(T * n * 4) for _ in range(3)]
         backend.qmatmul_qkv(ws[0], ws[1], ws[2], xb, *outs)
         for i in range(3):
-            cpu, exact = oracle_i8_32(dtype, raws[i], n, k, x)
-            assert_parity(backend.download_f32(outs[i]), cpu, exact, 1e-3, atol=gemm_atol(dtype),
+            cpu, exact, absum = oracle_i8_32(dtype, raws[i], n, k, x)
+            assert_parity(backend.download_f32(outs[i]), cpu, exact, 1e-3, abs_sum=absum,
                           what=f"gemm qkv {i}")
         y = backend.alloc(T * n * 4)
         backend.ffn_gate_up(ws[0], ws[1], xb, outs[0], outs[1], y)

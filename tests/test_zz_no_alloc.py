@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 import npq
-from conftest import assert_parity, f32_exact
+from conftest import abs_dot, assert_parity, f32_exact
 from mdma_amd import backend as backend_mod
 from mdma_amd import synth
 from oracle import ffi
@@ -69,10 +69,10 @@ def test_noalloc_prefill_gemm_matches_oracle(backend, dtype):
     q, d, _ = ffi.quantize_act(x, 32)
     xq = ffi.dequantize_act(q, d, 32)
     cpu = ffi.qmatmul(dtype, raw, rows, k, xq)
-    exact = f32_exact(npq.dequantize(dtype, raw, rows, k), xq)
-    atol = 1e-5 if dtype == Q6K else 1e-6
-    assert_parity(a, cpu, exact, 1e-3, atol=atol, what=f"noalloc gemm {dtype}")
-    assert_parity(b, cpu, exact, 1e-3, atol=atol, what=f"alloc gemm {dtype}")
+    W = npq.dequantize(dtype, raw, rows, k)
+    exact, absum = f32_exact(W, xq), abs_dot(W, xq)
+    assert_parity(a, cpu, exact, 1e-3, abs_sum=absum, what=f"noalloc gemm {dtype}")
+    assert_parity(b, cpu, exact, 1e-3, abs_sum=absum, what=f"alloc gemm {dtype}")
 
 
 def test_noalloc_rejects_oversize_and_keeps_cached_activations(backend):
