@@ -25,9 +25,10 @@ sums).
 
 Also reported: per-launch rates (kernel-only from the dispatch's own
 timestamps, and back to back in a graph), the roofline of the dominant
-kernel (the fused gate/up GEMV, 66 MB per launch), the prefill int8 MFMA
-GEMM (512x4096->14336 and 2048x14336->4096, Q4_K and Q8_0 weights; TOPS
-against the 5.0 POPS int8 peak), the Q6_K GEMVs of
+kernel (the fused gate/up GEMV, 66 MB per launch), the prefill GEMMs
+(512x4096->14336 and 2048x14336->4096: Q4_K on the f16-path GEMM and on the
+int8 MFMA GEMM, Q8_0 and Q6_K on the int8 MFMA GEMM; TOPS against the 5.0
+POPS int8 and 2.5 PFLOP/s f16 dense peaks), the Q6_K GEMVs of
 the Q6_K configuration (output head 128256x4096 and down 4096x14336 at batch 1, 4
 and 8), a device copy-bandwidth probe, and the CPU baseline (the C
 restatement of CpuBackend::qmatmul on this host's cores, on a bounded sample
@@ -286,23 +287,28 @@ def q6k_gemvs(be, ev, reps):
 
 
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POPS
+F16_PEAK_TOPS = 2500.0   # MI355X dense f16 MFMA, 2.5 PFLOP/s
 GEMM_SHAPES = [(512, 4096, 14336), (2048, 14336, 4096)]  # (M tokens, K, N)
 
 
 def prefill_gemms(be, ev, reps):
-    """Prefill int8 MFMA GEMM at the two prefill shapes, Q4_K and Q8_0
-    weights (and Q6_K, the Q4_K_M mix's attention and down type): kernel-only GEMM duration (dispatch timestamps) and the whole
-    qmatmul call (per-32 activation quantization + GEMM) timed by events on
-    the stream. TOPS = 2*M*N*K / time."""
+    """Prefill GEMMs at the two prefill shapes: Q4_K weights on the f16-path
+    GEMM (the default for Q4_K) and on the int8 MFMA GEMM, Q8_0 and Q6_K (the
+    Q4_K_M mix's attention and down type) on the int8 MFMA GEMM.
+    Kernel-only GEMM duration (dispatch timestamps) and the whole qmatmul
+    call (per-32 activation quantization + GEMM) timed by events on the
+    stream. TOPS = 2*M*N*K / time, against the int8 and the f16 dense peaks."""
     from mdma_amd import synth
-    from mdma_amd.backend import ACT_I8
+    from mdma_amd.backend import ACT_I8, PREFILL_AUTO, PREFILL_I8
 
     be.set_act_mode(ACT_I8)
     out = {}
     for M, K, N in GEMM_SHAPES:
         x = be.f32_buf(synth.normal_f32(M * K, SEED + 20))
         y = be.alloc(M * N * 4)
-        for dt, name in ((12, "q4k"), (8, "q8_0"), (14, "q6k")):
+        for dt, name, kind in ((12, "q4k_f16path", PREFILL_AUTO), (12, "q4k_i8", PREFILL_I8), (8, "q8_0", PREFILL_I8),
+                               (14, "q6k", PREFILL_I8)):
+            be.set_prefill_kernel(kind)
             raw = synth.weight(dt, N, K, SEED + 21)
             w = be.upload_weight(raw, dt, (N, K))
             be.qmatmul(w, x, y)
@@ -325,10 +331,12 @@ def prefill_gemms(be, ev, reps):
             out[f"{name}_M{M}_K{K}_N{N}"] = {
                 "us_kernel": round(us, 2), "TOPS_kernel": round(ops / us / 1e6, 1),
                 "pct_of_int8_peak": round(100 * ops / us / 1e6 / INT8_PEAK_TOPS, 2),
+                "pct_of_f16_peak": round(100 * ops / us / 1e6 / F16_PEAK_TOPS, 2),
                 "us_call": round(us_call, 2), "TOPS_call": round(ops / us_call / 1e6, 1), "launches_timed": reps}
             w.buf.close()
         x.close()
         y.close()
+    be.set_prefill_kernel(PREFILL_AUTO)
     return out
 
 
