@@ -143,6 +143,18 @@ int mdma_gfx950_set_norm_fusion(mdma_ctx *ctx, int on);
  * qmatmul_i8 (src/backend/rocm.rs:1759-1918). */
 typedef enum { MDMA_PREFILL_AUTO = 0, MDMA_PREFILL_I8 = 1 } mdma_prefill_kernel;
 int mdma_gfx950_set_prefill_kernel(mdma_ctx *ctx, int kind);
+/* Extra (for tests; the reference pins its int8 matrix-core fragments the
+ * same way, src/backend/rocm/tests.rs:1861-1925): block-dot capture. With
+ * out set (NULL: off), every later int8-mode qmatmul, qmatmul_qkv and
+ * ffn_gate_up on prepared-layout Q4_K / Q6_K / Q8_0 weights also stores
+ * the int32 sub-block dots its production kernels form, for each weight of
+ * the call in order: [T][rows][n_sub], n_sub = cols/16 for Q6_K (sum of
+ * (q - 32) * x over 16 columns) and cols/32 otherwise (sum of q * x; Q4_K q
+ * the 4-bit value). The f16-path prefill GEMM stores sc * dot, the integer
+ * it forms with the Q4_K sub-block scale folded in. A call whose slots
+ * exceed out fails with MDMA_ERR_SHAPE_MISMATCH; f32-mode calls and raw
+ * GGUF-layout weights store nothing. */
+int mdma_gfx950_capture_block_dots(mdma_ctx *ctx, mdma_buf *out);
 /* Extra: the HIP stream (hipStream_t) every launch of this context uses. */
 void *mdma_gfx950_stream(mdma_ctx *ctx);
 

@@ -109,6 +109,18 @@ GemvJob job_of(const mdma_qweight *w, mdma_buf *y) {
                  reinterpret_cast<float *>(y->ptr), w->buf->layout};
 }
 
+// Block-dot capture: the jobs' slots, one region after another.
+void attach_dots(mdma_ctx *ctx, GemvJob *jobs, int n, uint64_t T) {
+  if (!ctx->dots) return;
+  uint64_t off = 0;
+  for (int i = 0; i < n; i++) {
+    const uint64_t need = T * jobs[i].n_out * dot_subs(jobs[i].dtype, jobs[i].n_in);
+    if (off + need > ctx->dots_cap) shape_fail("block-dot capture: the call's dots exceed the capture buffer");
+    jobs[i].dots = ctx->dots + off;
+    off += need;
+  }
+}
+
 void run_gemv(mdma_ctx *ctx, int mode, const GemvJob *jobs, int n, const float *x, uint64_t T) {
   if (mode == MDMA_ACT_I8)
     launch_gemv_i8(ctx, jobs, n, x, T);
@@ -166,6 +178,7 @@ void qmatmul_run(mdma_ctx *ctx, const mdma_qweight *w, const mdma_buf *x, mdma_b
   same_ctx(ctx, x, "qmatmul");
   same_ctx(ctx, y, "qmatmul");
   GemvJob j = job_of(w, y);
+  attach_dots(ctx, &j, 1, T);
   run_gemv(ctx, mode < 0 ? ctx->act_mode : mode, &j, 1, reinterpret_cast<const float *>(x->ptr), T);
   q8_invalidate_range(ctx, y->ptr, y->len);
 }
@@ -473,6 +486,19 @@ int mdma_gfx950_set_act_mode(mdma_ctx *ctx, int mode) {
   });
 }
 
+int mdma_gfx950_capture_block_dots(mdma_ctx *ctx, mdma_buf *out) {
+  return guarded([&] {
+    need(ctx, "capture_block_dots");
+    std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    if (out) {
+      same_ctx(ctx, out, "capture_block_dots");
+      if (reinterpret_cast<uintptr_t>(out->ptr) % 4) shape_fail("capture_block_dots: buffer must be 4-byte aligned");
+    }
+    ctx->dots = out ? reinterpret_cast<int32_t *>(out->ptr) : nullptr;
+    ctx->dots_cap = out ? out->len / 4 : 0;
+  });
+}
+
 int mdma_gfx950_set_prefill_kernel(mdma_ctx *ctx, int kind) {
   return guarded([&] {
     need(ctx, "set_prefill_kernel");
@@ -720,6 +746,7 @@ int mdma_gfx950_qmatmul_qkv(mdma_ctx *ctx, const mdma_qweight *wq, const mdma_qw
                               (const mdma_buf *)v})
       same_ctx(ctx, b, "qmatmul_qkv");
     GemvJob jobs[3] = {job_of(wq, q), job_of(wk, k), job_of(wv, v)};
+    attach_dots(ctx, jobs, 3, T);
     run_gemv(ctx, ctx->act_mode, jobs, 3, reinterpret_cast<const float *>(x->ptr), T);
     for (const mdma_buf *o : {(const mdma_buf *)q, (const mdma_buf *)k, (const mdma_buf *)v})
       q8_invalidate_range(ctx, o->ptr, o->len);
@@ -747,7 +774,9 @@ int mdma_gfx950_ffn_gate_up(mdma_ctx *ctx, const mdma_qweight *gate, const mdma_
     for (const mdma_buf *b : {gate->buf, up->buf, x, (const mdma_buf *)gate_scratch,
                               (const mdma_buf *)up_scratch, (const mdma_buf *)y})
       same_ctx(ctx, b, "ffn_gate_up");
-    GemvJob gj = job_of(gate, gate_scratch), uj = job_of(up, up_scratch);
+    GemvJob gu_jobs[2] = {job_of(gate, gate_scratch), job_of(up, up_scratch)};
+    attach_dots(ctx, gu_jobs, 2, T);
+    GemvJob gj = gu_jobs[0], uj = gu_jobs[1];
     const float *xp = reinterpret_cast<const float *>(x->ptr);
     float *yp = reinterpret_cast<float *>(y->ptr);
     struct Inval {  // runs when the call returns, after the launches below

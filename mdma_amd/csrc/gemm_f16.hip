@@ -45,6 +45,8 @@
 // per CU.
 #include <hip/hip_ext.h>
 
+#include <type_traits>
+
 #include "kernels.h"
 
 namespace mdma {
@@ -90,7 +92,7 @@ __global__ __launch_bounds__(256) void gemm_act_kernel(const float *__restrict__
     int qi[4], sum = 0;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-      qi[k] = q8_round(v[k] * iv);
+      qi[k] = q8_quant(v[k], iv);
       sum += qi[k];
     }
     sum += (int)dpp_u32<0xB1, 0xF>((uint32_t)sum);
@@ -141,6 +143,7 @@ struct F16Args {
   float *y;            // [M, N]
   uint32_t M, N, K;
   uint64_t row_bytes;
+  int32_t *dots;       // block-dot capture [M, N, K/32] (sc * block dot) or null
 };
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -188,7 +191,8 @@ __device__ __forceinline__ void q4_f16(uint32_t q, h2 sa, h2 na, h2 sb, h2 nb_, 
   hi[1] = f(__builtin_amdgcn_perm(c, u, 0x04030402u), sb, nb_);
 }
 
-template <int DT>
+// CAP: the block-dot capture instantiation (F16Args::dots set).
+template <int DT, bool CAP = false>
 __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
   __shared__ __attribute__((aligned(16))) _Float16 ws[2][TN][SK];  // weights, f16 q * sc
   __shared__ __attribute__((aligned(16))) _Float16 xs[2][TM][SK];  // activations, f16 int8 values
@@ -306,8 +310,9 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
     if (st + 1 < nst) gload(st + 1);
     if (st % 4 == 0 && st > 0) pload(st / 4);
     const int buf = st & 1;
-#pragma unroll
-    for (int h = 0; h < 2; h++) {  // the stage's two blocks, one 16x16x32 MFMA per tile each
+    // One block (h) of the stage: one 16x16x32 MFMA per tile, then
+    // part += s_x * dot. FIRST (a super-block's first block): part = s_x * dot.
+    auto block = [&](int h, auto first) {
       v8h A[4], B[4];
       float s[4];
 #pragma unroll
@@ -321,19 +326,33 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
         B[j] = *reinterpret_cast<const v8h *>(&xs[buf][r][8 * swz(r, 4 * h + lq)]);
         s[j] = sxs[buf][h][r];
       }
-      // Software-pipelined: tile t + 1's MFMA is issued before tile t's
-      // FMAs, so the matrix core and the VALU overlap.
-      v4f c[2];
+      // Software-pipelined two tiles deep: tile t + 2's MFMA is issued before
+      // tile t's FMAs, whose MFMA result is then long complete, so the
+      // matrix core and the VALU overlap.
+      v4f c[3];
       c[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0], B[0], v4f{}, 0, 0, 0);
+      c[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0], B[1], v4f{}, 0, 0, 0);
 #pragma unroll
       for (int t = 0; t < 16; t++) {
-        if (t + 1 < 16)
-          c[(t + 1) & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[(t + 1) >> 2], B[(t + 1) & 3], v4f{}, 0, 0, 0);
+        if (t + 2 < 16)
+          c[(t + 2) % 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[(t + 2) >> 2], B[(t + 2) & 3], v4f{}, 0, 0, 0);
         const int i = t >> 2, j = t & 3;
+        if constexpr (CAP) {  // block-dot capture: the exact integer sc * dot of each output's block
+          const uint32_t m = bm + wm + 16 * j + l16;
 #pragma unroll
-        for (int r = 0; r < 4; r++) part[i][j][r] = fmaf(s[j], c[t & 1][r], part[i][j][r]);
+          for (int r = 0; r < 4; r++) {
+            const uint32_t n = bn + wn + 16 * i + 4 * lq + r;
+            if (m < a.M && n < a.N) a.dots[((size_t)m * a.N + n) * nb + 2 * st + h] = (int)c[t % 3][r];
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          part[i][j][r] = first ? s[j] * c[t % 3][r] : fmaf(s[j], c[t % 3][r], part[i][j][r]);
       }
-    }
+    };
+    if (st % 4 == 0) block(0, std::true_type{});
+    else block(0, std::false_type{});
+    block(1, std::false_type{});
     if (st % 4 == 3) {  // the super-block's last stage: d and the min term
       // Min MFMA (16x16x16): K chunk lq of 4 columns; chunks 0, 1 pair the
       // 8 mins with P hi, chunks 2, 3 the same mins with P lo.
@@ -354,7 +373,6 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
           for (int r = 0; r < 4; r++) {
             acc[i][j][r] = fmaf(dv[r], part[i][j][r], acc[i][j][r]);
             acc[i][j][r] = fmaf(-dm[r] * iv, cm[r], acc[i][j][r]);
-            part[i][j][r] = 0.f;
           }
         }
       }
@@ -426,11 +444,13 @@ void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float
     for (uint64_t m0 = 0; m0 < M; m0 += rows) {
       const uint64_t Mc = M - m0 < rows ? M - m0 : rows;
       F16Args a{xh + m0 * K, sx + m0 * nb, ph + m0 * nb, (uint32_t)(pl - ph), inv + m0, w.w, w.y + m0 * w.n_out,
-                (uint32_t)Mc, (uint32_t)w.n_out, (uint32_t)K, gfx950_row_bytes(w.dtype, K)};
+                (uint32_t)Mc, (uint32_t)w.n_out, (uint32_t)K, gfx950_row_bytes(w.dtype, K),
+                w.dots ? w.dots + m0 * w.n_out * (K / 32) : nullptr};
       const dim3 grid((uint32_t)((w.n_out + TN - 1) / TN), (uint32_t)((Mc + TM - 1) / TM)), block(256);
       // Timing events bracket the calls' GEMM launches (not the prologue).
       const hipEvent_t e0 = i == 0 && m0 == 0 ? t0 : nullptr, e1 = i == n_jobs - 1 && m0 + Mc >= M ? t1 : nullptr;
-      if (e0 || e1) hipExtLaunchKernelGGL(gemm_f16_kernel<DT_Q4_K>, grid, block, 0, ctx->stream, e0, e1, 0, a);
+      if (a.dots) gemm_f16_kernel<DT_Q4_K, true><<<grid, block, 0, ctx->stream>>>(a);
+      else if (e0 || e1) hipExtLaunchKernelGGL(gemm_f16_kernel<DT_Q4_K>, grid, block, 0, ctx->stream, e0, e1, 0, a);
       else gemm_f16_kernel<DT_Q4_K><<<grid, block, 0, ctx->stream>>>(a);
       hip_check(hipGetLastError(), "gemm f16 launch");
     }

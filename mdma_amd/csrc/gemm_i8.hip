@@ -62,9 +62,11 @@ struct GemmArgs {
   uint32_t M, N, K;
   uint32_t ks;         // columns per split (a multiple of BK)
   uint64_t row_bytes;
+  int32_t *dots;       // block-dot capture [M, N, n_sub] or null
 };
 
-template <int DT>
+// CAP: the block-dot capture instantiation (GemmArgs::dots set).
+template <int DT, bool CAP = false>
 __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(16))) int8_t xs[KB][BM][LDR];
   __shared__ __attribute__((aligned(16))) int8_t ws[KB][BN][LDR];
@@ -249,6 +251,13 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
     for (int r = 0; r < 16; r++) acc[j][r] = 0.0;
 
   const int lr = lane & 31, lk = lane >> 5;  // operand row/column, K half
+  // Block-dot capture: result register r of tile j holds token row
+  // (r&3) + 4*lk + 8*(r>>2) of the wave's 32 and weight row 32 j + lane%32.
+  const uint32_t nsub = DT == DT_Q6_K ? K / 16 : K / 32;
+  auto capture = [&](int j, int r, uint32_t sub, int v) {
+    const uint32_t m = bm + wm + (r & 3) + 4 * lk + 8 * (r >> 2), n = bn + wn + 32 * j + lr;
+    if (m < a.M && n < a.N) a.dots[((size_t)m * a.N + n) * nsub + sub] = v;
+  };
   // The barriers order LDS only: the prefetched stages' global loads stay in
   // flight across them (a full __syncthreads would wait for them).
   auto stage = [&](Stage &S, uint32_t k0) {
@@ -283,6 +292,11 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
               __builtin_amdgcn_mfma_i32_32x32x16_i8(a0, *reinterpret_cast<const long *>(wr + 8 * lk), v16i{}, 0, 0, 0);
           const v16i c1 = __builtin_amdgcn_mfma_i32_32x32x16_i8(
               a1, *reinterpret_cast<const long *>(wr + 16 + 8 * lk), v16i{}, 0, 0, 0);
+          if constexpr (CAP) {
+            const uint32_t sub = (k0 + 32 * kb) / 16;
+#pragma unroll
+            for (int r = 0; r < 16; r++) capture(j, r, sub, c0[r]), capture(j, r, sub + 1, c1[r]);
+          }
           const int2 sc = s6[kb][wn + 32 * j + lr];
 #pragma unroll
           for (int r = 0; r < 16; r++) {
@@ -317,6 +331,10 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
       for (int j = 0; j < 2; j++) {
         v16i c = {};
         c = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[j], c, 0, 0, 0);
+        if constexpr (CAP) {
+#pragma unroll
+          for (int r = 0; r < 16; r++) capture(j, r, (k0 + 32 * kb) / 32, c[r]);
+        }
         const float sw = sws[kb][wn + 32 * j + lr];
         const float dm = DT == DT_Q4_K ? dms[kb][wn + 32 * j + lr] : 0.f;
 #pragma unroll
@@ -469,11 +487,15 @@ void launch_gemm_i8(mdma_ctx *ctx, const GemvJob &w, const int8_t *qx, const flo
       sp = Split{1, (uint32_t)K};
     GemmArgs a{qx + m0 * K, sx + m0 * (K / 32), s16 + m0 * (K / 16), w.w, y + m0 * N,
                sp.S > 1 ? part : nullptr, sp.S > 1 ? cnt : nullptr, (uint32_t)Mc, (uint32_t)N, (uint32_t)K,
-               sp.ks, gfx950_row_bytes(w.dtype, K)};
+               sp.ks, gfx950_row_bytes(w.dtype, K), w.dots ? w.dots + m0 * N * dot_subs(w.dtype, K) : nullptr};
     const dim3 grid((uint32_t)((N + BN - 1) / BN), (uint32_t)((Mc + BM - 1) / BM), sp.S), block(256);
     // Timing events (one launch) bracket the first chunk.
     const hipEvent_t e0 = m0 == 0 ? t0 : nullptr, e1 = m0 + Mc >= M ? t1 : nullptr;
-    if (w.dtype == DT_Q8_0) {
+    if (a.dots) {
+      if (w.dtype == DT_Q8_0) gemm_i8_kernel<DT_Q8_0, true><<<grid, block, 0, ctx->stream>>>(a);
+      else if (w.dtype == DT_Q6_K) gemm_i8_kernel<DT_Q6_K, true><<<grid, block, 0, ctx->stream>>>(a);
+      else gemm_i8_kernel<DT_Q4_K, true><<<grid, block, 0, ctx->stream>>>(a);
+    } else if (w.dtype == DT_Q8_0) {
       if (e0 || e1) hipExtLaunchKernelGGL(gemm_i8_kernel<DT_Q8_0>, grid, block, 0, ctx->stream, e0, e1, 0, a);
       else gemm_i8_kernel<DT_Q8_0><<<grid, block, 0, ctx->stream>>>(a);
     } else if (w.dtype == DT_Q6_K) {

@@ -638,7 +638,7 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const float *__restri
   int qi[4], sum = 0;
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    qi[k] = q8_round(v[k] * inv);
+    qi[k] = q8_quant(v[k], inv);
     sum += qi[k];
   }
   sum += (int)dpp_u32<0xB1, 0xF>((uint32_t)sum);  // 16 values = 4 lanes
@@ -781,6 +781,7 @@ void by_chunks(uint64_t T, F &&f) {
 GemvJob offset_job(const GemvJob &j, uint64_t t0) {
   GemvJob o = j;
   if (o.y) o.y += t0 * j.n_out;
+  if (o.dots) o.dots += t0 * j.n_out * dot_subs(j.dtype, j.n_in);
   return o;
 }
 

@@ -59,6 +59,17 @@ __device__ __forceinline__ v4i mma(uint64_t x, uint64_t w, v4i c) {
   return __builtin_amdgcn_mfma_i32_16x16x32_i8((long)x, (long)w, c, 0, 0, 0);
 }
 
+// Block-dot capture (GemvJob::dots): the row's slots for the block being
+// computed (p: null when off), tokens stride apart, the first T live.
+struct Dots {
+  int32_t *p;
+  size_t stride;
+  uint32_t T;
+  __device__ void put(uint32_t tok, uint32_t s, int v) const {
+    if (tok < T) p[tok * stride + s] = v;
+  }
+};
+
 // Activation bytes of the lane's token at column col.
 struct XRow {
   const int8_t *p;
@@ -111,7 +122,8 @@ struct BQ4 {
       x.hi[p] = xr(col + 32);
     }
   }
-  __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, float *c) {
+  static constexpr uint32_t SUBS = 8;  // capture slots per 256-column block
+  __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, float *c, const Dots &dc) {
     const uint32_t n = l & 15, g = l >> 4;
     const uint4 h = *reinterpret_cast<const uint4 *>(lds + 16 * RS + 16 * n);
     constexpr uint64_t M4 = 0x0F0F0F0F0F0F0F0Full;
@@ -122,6 +134,9 @@ struct BQ4 {
       const v4i z = {};
       const v4i da = mma(x.lo[p], w & M4, z);
       const v4i db = mma(x.hi[p], (w >> 4) & M4, z);
+      if (dc.p)
+#pragma unroll
+        for (int j = 0; j < 4; j++) dc.put(4 * g + j, 2 * p, da[j]), dc.put(4 * g + j, 2 * p + 1, db[j]);
       int sca, scb, ma, mb;
       q4k_scales_i(h, p, sca, scb, ma, mb);
       // 24-bit multiplies (full rate): |isum| <= 15*127*32.
@@ -196,7 +211,8 @@ struct BQ6 {
 #pragma unroll
       for (int r = 0; r < 4; r++) x.q[v][r] = xr(col(4 * b + 2 * v + (g >> 1), r) + 8 * (g & 1));
   }
-  __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, float *c) {
+  static constexpr uint32_t SUBS = 16;
+  __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, float *c, const Dots &dc) {
     const uint32_t n = l & 15, g = l >> 4;
     const uint4 sc4 = *reinterpret_cast<const uint4 *>(lds + 16 * RS + 16 * n);
     const uint32_t scw[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
@@ -216,6 +232,10 @@ struct BQ6 {
         const v4i z = {};
         const v4i d0 = mma(g < 2 ? x.q[v][r] : 0ull, wv, z);
         const v4i d1 = mma(g < 2 ? 0ull : x.q[v][r], wv, z);
+        // Sub-block (16 columns) of unit 4b + 2v + e, quarter r: 8v + 2r + e.
+        if (dc.p)
+#pragma unroll
+          for (int j = 0; j < 4; j++) dc.put(4 * g + j, 8 * v + 2 * r, d0[j]), dc.put(4 * g + j, 8 * v + 2 * r + 1, d1[j]);
         const int s0 = (int)(int8_t)((scw[2 * v] >> (8 * r)) & 0xff);
         const int s1 = (int)(int8_t)((scw[2 * v + 1] >> (8 * r)) & 0xff);
         // 24-bit multiplies (full rate): |isum| <= 32*127*16.
@@ -266,7 +286,8 @@ struct BQ8 {
 #pragma unroll
     for (int i = 0; i < 8; i++) x.q[i] = xr(256 * b + 32 * i + 8 * g);
   }
-  __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, float *c) {
+  static constexpr uint32_t SUBS = 8;
+  __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, float *c, const Dots &dc) {
     const uint32_t n = l & 15, g = l >> 4;
     const uint4 d4 = *reinterpret_cast<const uint4 *>(lds + 16 * RS + 16 * n);
     const uint32_t dw[4] = {d4.x, d4.y, d4.z, d4.w};
@@ -277,6 +298,9 @@ struct BQ8 {
       const uint64_t w = *reinterpret_cast<const uint64_t *>(lds + n * RS + 32 * i + 8 * g);
       const v4i z = {};
       const v4i dq = mma(x.q[i], w, z);
+      if (dc.p)
+#pragma unroll
+        for (int j = 0; j < 4; j++) dc.put(4 * g + j, i, dq[j]);
       const float d = h2f(dw[i >> 1] >> (16 * (i & 1)));
 #pragma unroll
       for (int j = 0; j < 4; j++) c[j] = fmaf(d, (float)dq[j], c[j]);
@@ -288,6 +312,7 @@ struct BatchJob {
   const uint8_t *w;
   float *y;
   uint32_t n_out, tiles;
+  int32_t *dots;  // block-dot capture or null
 };
 struct BatchSet {
   BatchJob j[3];
@@ -305,7 +330,8 @@ constexpr int NCHMAX = 8;
 #ifndef MDMA_BATCH_NS
 #define MDMA_BATCH_NS 2
 #endif
-template <class F, int TW, bool GATED, int NS>
+// CAP: the block-dot capture instantiation (BatchJob::dots set).
+template <class F, int TW, bool GATED, int NS, bool CAP = false>
 __global__ __launch_bounds__(64 * TW) void gemv_batch(BatchSet bs, const int8_t *__restrict__ qx,
                                                       const float *__restrict__ dx, uint32_t T,
                                                       float *__restrict__ ygated) {
@@ -354,8 +380,16 @@ __global__ __launch_bounds__(64 * TW) void gemv_batch(BatchSet bs, const int8_t 
     typename F::Raw w[NR];
     typename F::X x;
     float s[NJ];
+    uint32_t b;
   };
+  // Block-dot capture: the lane's row (of gate, of up), one slot per
+  // sub-block; tokens n_out * n_sub apart.
+  const uint32_t nsub = n_in / (256 / F::SUBS);
+  int32_t *dcap[NR];
+  dcap[0] = J.dots;
+  if (GATED) dcap[NR - 1] = bs.j[1].dots;
   auto fill = [&](Slot &sl, uint32_t b) {
+    sl.b = b;
 #pragma unroll
     for (int r = 0; r < NR; r++) F::gload(prow[r], hrow[r], U, b, lane, sl.w[r]);
     F::loadx(xr, b, g, sl.x);
@@ -373,7 +407,11 @@ __global__ __launch_bounds__(64 * TW) void gemv_batch(BatchSet bs, const int8_t 
 #pragma unroll
     for (int r = 0; r < NR; r++) {
       float c[NJ];
-      F::compute(stage[wave][r], sl.x, lane, c);
+      Dots dc{nullptr, (size_t)n_out * nsub, T};
+      if constexpr (CAP) {
+        if (r_lane < n_out) dc.p = dcap[r] + (size_t)r_lane * nsub + F::SUBS * sl.b;
+      }
+      F::compute(stage[wave][r], sl.x, lane, c, dc);
 #pragma unroll
       for (int j = 0; j < NJ; j++) acc[r][j] = fmaf(sl.s[j], c[j], acc[r][j]);
     }
@@ -454,7 +492,10 @@ void launch_tw(mdma_ctx *ctx, const BatchSet &bs, uint32_t tiles, bool gated, co
   hipEvent_t t0 = ctx->time_start, t1 = ctx->time_stop;
   ctx->time_start = ctx->time_stop = nullptr;
   const dim3 grid(tiles), block(64 * TW);
-  if (gated) {
+  if (bs.j[0].dots) {
+    if (gated) gemv_batch<F, TW, true, NS, true><<<grid, block, 0, ctx->stream>>>(bs, qx, dx, T, yg);
+    else gemv_batch<F, TW, false, NS, true><<<grid, block, 0, ctx->stream>>>(bs, qx, dx, T, yg);
+  } else if (gated) {
     if (t0 || t1)
       hipExtLaunchKernelGGL(gemv_batch<F, TW, true, NS>, grid, block, 0, ctx->stream, t0, t1, 0, bs, qx, dx, T, yg);
     else
@@ -512,6 +553,7 @@ void launch_gemv_batch(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, bool gate
   for (int i = 0; i < (gated ? 2 : n_jobs); i++) {
     bs.j[i].w = jobs[i].w;
     bs.j[i].y = jobs[i].y;
+    bs.j[i].dots = jobs[i].dots;
     bs.j[i].n_out = (uint32_t)jobs[i].n_out;
     bs.j[i].tiles = (uint32_t)((jobs[i].n_out + TROWS - 1) / TROWS);
     if (i < bs.n) tiles += bs.j[i].tiles;

@@ -125,7 +125,9 @@ struct Q4G {
     r.sb = sum_f64(r.xb, 32);
     return r;
   }
-  __device__ static float dot_i8(const W &w, const XI &x, uint32_t u) {
+  // dots: the unit's int32 sub-block dots (sum q * x of sub-blocks 2(u%4)
+  // and 2(u%4)+1), for the block-dot capture.
+  __device__ static float dot_i8(const W &w, const XI &x, uint32_t u, int (&dots)[4]) {
     const uint4 hd = header(w.h);
     const uint32_t q[8] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w};
     const uint32_t xa[8] = {x.a0.x, x.a0.y, x.a0.z, x.a0.w, x.a1.x, x.a1.y, x.a1.z, x.a1.w};
@@ -136,6 +138,7 @@ struct Q4G {
       ia = __builtin_amdgcn_sdot4((int)(q[k] & 0x0F0F0F0Fu), (int)xa[k], ia, false);
       ib = __builtin_amdgcn_sdot4((int)((q[k] >> 4) & 0x0F0F0F0Fu), (int)xb[k], ib, false);
     }
+    dots[0] = ia, dots[1] = ib;
     int sca, scb, ma, mb;
     q4k_scales_i(hd, u & 3, sca, scb, ma, mb);
     // 24-bit multiplies (full rate): |isum| <= 15*127*32, |xsum| <= 127*32.
@@ -143,6 +146,11 @@ struct Q4G {
     const int B = __mul24(ma, x.sa) + __mul24(mb, x.sb);
     const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
     return x.d8 * fmaf(d, (float)A, -dmin * (float)B);
+  }
+  __device__ static uint32_t n_sub(uint32_t n_in) { return n_in / 32; }
+  __device__ static void put_dots(int32_t *o, const int (&dots)[4], uint32_t u) {
+    o[2 * u] = dots[0];
+    o[2 * u + 1] = dots[1];
   }
   __device__ static double dot_f32(const W &w, const XF &x, uint32_t u) {
     const uint4 hd = header(w.h);
@@ -230,7 +238,8 @@ struct Q6G {
       default: return ((qb >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u);
     }
   }
-  __device__ static float dot_i8(const W &w, const XI &x, uint32_t) {
+  // dots: the unit's four 16-column dots sum (q - 32) * x (quarters r).
+  __device__ static float dot_i8(const W &w, const XI &x, uint32_t, int (&dots)[4]) {
     int A = 0;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -239,9 +248,15 @@ struct Q6G {
 #pragma unroll
       for (int k = 0; k < 4; k++) s = __builtin_amdgcn_sdot4((int)u6(w, r, k), (int)xv[k], s, false);
       // 24-bit multiply (full rate): |s - 32*xsum| <= 63*127*16 + 32*127*16.
-      A += __mul24((int)(int8_t)((w.sc >> (8 * r)) & 0xff), s - 32 * x.sq[r]);
+      dots[r] = s - 32 * x.sq[r];
+      A += __mul24((int)(int8_t)((w.sc >> (8 * r)) & 0xff), dots[r]);
     }
     return x.d8 * (h2f(w.d) * (float)A);
+  }
+  __device__ static uint32_t n_sub(uint32_t n_in) { return n_in / 16; }
+  __device__ static void put_dots(int32_t *o, const int (&dots)[4], uint32_t u) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) o[col(u, r) / 16] = dots[r];
   }
   __device__ static double dot_f32(const W &w, const XF &x, uint32_t) {
     double r = 0.0;
@@ -288,7 +303,7 @@ struct Q8G {
     r.s = sum_f64(r.x, 32);
     return r;
   }
-  __device__ static float dot_i8(const W &w, const XI &x, uint32_t) {
+  __device__ static float dot_i8(const W &w, const XI &x, uint32_t, int (&dots)[4]) {
     int s = __builtin_amdgcn_sdot4((int)w.a.x, (int)x.x0.x, 0, false);
     s = __builtin_amdgcn_sdot4((int)w.a.y, (int)x.x0.y, s, false);
     s = __builtin_amdgcn_sdot4((int)w.a.z, (int)x.x0.z, s, false);
@@ -297,8 +312,11 @@ struct Q8G {
     s = __builtin_amdgcn_sdot4((int)w.b.y, (int)x.x1.y, s, false);
     s = __builtin_amdgcn_sdot4((int)w.b.z, (int)x.x1.z, s, false);
     s = __builtin_amdgcn_sdot4((int)w.b.w, (int)x.x1.w, s, false);
+    dots[0] = s;
     return x.d8 * (h2f(w.d) * (float)s);
   }
+  __device__ static uint32_t n_sub(uint32_t n_in) { return n_in / 32; }
+  __device__ static void put_dots(int32_t *o, const int (&dots)[4], uint32_t u) { o[u] = dots[0]; }
   __device__ static double dot_f32(const W &w, const XF &x, uint32_t) {
     const uint32_t q[8] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w};
     double a = 0.0;
@@ -344,8 +362,8 @@ __device__ typename F::XI prologue_quant(const float (&v)[4][16]) {
     int sm = 0;
 #pragma unroll
     for (int k = 0; k < 16; k += 4) {
-      const int q0 = q8_round(v[c][k] * inv), q1 = q8_round(v[c][k + 1] * inv);
-      const int q2 = q8_round(v[c][k + 2] * inv), q3 = q8_round(v[c][k + 3] * inv);
+      const int q0 = q8_quant(v[c][k], inv), q1 = q8_quant(v[c][k + 1], inv);
+      const int q2 = q8_quant(v[c][k + 2], inv), q3 = q8_quant(v[c][k + 3], inv);
       sm += (q0 + q1) + (q2 + q3);
       w4[k >> 2] = pack4_i8(q0, q1, q2, q3);
     }
@@ -392,8 +410,8 @@ __device__ typename F::XI prologue_wg_quant(const float (&v)[16], uint32_t U, ui
   int sm = 0;
 #pragma unroll
   for (int k = 0; k < 16; k += 4) {
-    const int q0 = q8_round(v[k] * inv), q1 = q8_round(v[k + 1] * inv);
-    const int q2 = q8_round(v[k + 2] * inv), q3 = q8_round(v[k + 3] * inv);
+    const int q0 = q8_quant(v[k], inv), q1 = q8_quant(v[k + 1], inv);
+    const int q2 = q8_quant(v[k + 2], inv), q3 = q8_quant(v[k + 3], inv);
     sm += (q0 + q1) + (q2 + q3);
     w4[k >> 2] = pack4_i8(q0, q1, q2, q3);
   }
@@ -414,6 +432,7 @@ struct TeamJob {
   const uint8_t *w;
   float *y;
   uint32_t n_out, teams;
+  int32_t *dots;  // block-dot capture (GemvJob::dots) or null
 };
 struct TeamSet {
   TeamJob j[3];
@@ -466,7 +485,10 @@ constexpr int nbuf() {
 #endif
 constexpr int team_wg(int pro, int tw) { return pro == 4 ? 64 * tw * MDMA_PRO4_TEAMS : WG; }
 
-template <class F, bool F32, int R, int ITERS, int TW, int PL, int TT, bool GATED, int PRO = 0>
+// CAP: the block-dot capture instantiation (TeamJob::dots set), which also
+// stores each int32 sub-block dot; the production instantiations have none
+// of its code.
+template <class F, bool F32, int R, int ITERS, int TW, int PL, int TT, bool GATED, int PRO = 0, bool CAP = false>
 __global__ __launch_bounds__(team_wg(PRO, TW)) void gemv_team(TeamSet ts, const float *__restrict__ xf,
                                                 const int8_t *__restrict__ qx, const float *__restrict__ dx,
                                                 const int32_t *__restrict__ s16, uint32_t T,
@@ -507,6 +529,7 @@ __global__ __launch_bounds__(team_wg(PRO, TW)) void gemv_team(TeamSet ts, const 
   J.y = in2 ? ts.j[2].y : (in1 ? ts.j[1].y : ts.j[0].y);
   J.n_out = in2 ? ts.j[2].n_out : (in1 ? ts.j[1].n_out : ts.j[0].n_out);
   J.teams = in2 ? ts.j[2].teams : (in1 ? t1 : t0);
+  J.dots = in2 ? ts.j[2].dots : (in1 ? ts.j[1].dots : ts.j[0].dots);
   // A team past its job's end (the grid's last workgroup) runs the loop for
   // the barriers of its workgroup but stores nothing.
   const bool team_live = team < J.teams;
@@ -554,8 +577,16 @@ __global__ __launch_bounds__(team_wg(PRO, TW)) void gemv_team(TeamSet ts, const 
           if (t >= (int)T) break;
 #pragma unroll
           for (int r = 0; r < NR; r++) {
-            const float v = F::dot_i8(w[p][r], xi[p][t], uid[p]);
+            int dots[4];
+            const float v = F::dot_i8(w[p][r], xi[p][t], uid[p], dots);
             s[r][t] += uok[p] ? v : 0.f;
+            if constexpr (CAP) {
+              int32_t *dcap = r < R ? J.dots : ts.j[1].dots;  // the gated kernel's up rows: job 1
+              if (team_live && uok[p]) {
+                const uint32_t row = min(r0 + (r % R), r_last);
+                F::put_dots(dcap + ((size_t)t * n_out + row) * F::n_sub(n_in), dots, uid[p]);
+              }
+            }
           }
         }
       } else if constexpr (TT == 1) {
@@ -717,8 +748,8 @@ __global__ __launch_bounds__(team_wg(PRO, TW)) void gemv_team(TeamSet ts, const 
       int sm = 0;
 #pragma unroll
       for (int k = 0; k < 16; k += 4) {
-        const int q0 = q8_round(v[p][k] * inv), q1 = q8_round(v[p][k + 1] * inv);
-        const int q2 = q8_round(v[p][k + 2] * inv), q3 = q8_round(v[p][k + 3] * inv);
+        const int q0 = q8_quant(v[p][k], inv), q1 = q8_quant(v[p][k + 1], inv);
+        const int q2 = q8_quant(v[p][k + 2], inv), q3 = q8_quant(v[p][k + 3], inv);
         sm += (q0 + q1) + (q2 + q3);
         w4[k >> 2] = pack4_i8(q0, q1, q2, q3);
       }
@@ -853,6 +884,13 @@ void launch_iters(mdma_ctx *ctx, TeamSet ts, int tw, int pl, const float *xf, co
   constexpr bool NORM_OK = !F32 && TT == 1 && !GATED && !std::is_same<F, Q8G>::value;
 #define MDMA_TEAM_GO(TW_, PL_, PRO_)                                                                              \
   do {                                                                                                            \
+    if constexpr (!F32) {                                                                                         \
+      if (ts.j[0].dots) {                                                                                         \
+        gemv_team<F, F32, R, ITERS, TW_, PL_, TT, GATED, PRO_, true><<<grid, block, 0, ctx->stream>>>(          \
+            ts, xf, qx, dx, s16, T, yg);                                                                          \
+        break;                                                                                                    \
+      }                                                                                                           \
+    }                                                                                                             \
     if (t0 || t1)                                                                                                 \
       hipExtLaunchKernelGGL(gemv_team<F, F32, R, ITERS, TW_, PL_, TT, GATED, PRO_>, grid, block, 0, ctx->stream,  \
                             t0, t1, 0, ts, xf, qx, dx, s16, T, yg);                                               \

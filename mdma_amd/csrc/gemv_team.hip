@@ -143,6 +143,7 @@ void launch_gemv_team(mdma_ctx *ctx, int mode, const GemvJob *jobs, int n_jobs, 
       ts.j[i].w = jobs[i].w;
       ts.j[i].y = jobs[i].y ? jobs[i].y + t0 * jobs[i].n_out : nullptr;
       ts.j[i].n_out = (uint32_t)jobs[i].n_out;
+      ts.j[i].dots = jobs[i].dots ? jobs[i].dots + t0 * jobs[i].n_out * dot_subs(dt, n_in) : nullptr;
     }
     const float *xt = x + t0 * n_in;
     const int8_t *qt = qx ? qx + t0 * n_in : nullptr;

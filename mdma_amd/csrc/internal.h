@@ -96,6 +96,9 @@ struct mdma_ctx {
   uint64_t host_ids_cap = 0;
   bool capturing = false;        // stream capture in progress: no synchronizing calls
   int prefill_kernel = MDMA_PREFILL_AUTO;  // mdma_gfx950_set_prefill_kernel
+  // Block-dot capture (mdma_gfx950_capture_block_dots): int32 slots or null.
+  int32_t *dots = nullptr;
+  uint64_t dots_cap = 0;
   // Events the next GEMV kernel's dispatch timestamps (mdma_gfx950_time_next_gemv).
   hipEvent_t time_start = nullptr, time_stop = nullptr;
   // Per-chunk partial results of the two-pass argmax (12 bytes per chunk).
@@ -189,7 +192,15 @@ struct GemvJob {
   uint64_t n_out, n_in;
   float *y;        // [T, n_out], row stride n_out
   int layout = MDMA_LAYOUT_GGUF;  // MDMA_LAYOUT_GFX950: prepared rows (layout.cpp)
+  // Block-dot capture (mdma_gfx950_capture_block_dots): when set, the int8
+  // kernels over prepared rows also store every int32 sub-block dot they
+  // form, dots[(t * n_out + row) * n_sub + s] (n_sub = n_in / 16 for Q6_K,
+  // n_in / 32 otherwise); the f16-path GEMM stores its block dot times the
+  // Q4_K sub-block scale, the integer it forms.
+  int32_t *dots = nullptr;
 };
+// Sub-blocks per row in the block-dot capture layout.
+inline uint64_t dot_subs(int32_t dtype, uint64_t n_in) { return dtype == DT_Q6_K ? n_in / 16 : n_in / 32; }
 
 // ---- prepared weight layout (layout.cpp) ----
 // Bytes of one prepared row (0 if cols is not whole blocks).

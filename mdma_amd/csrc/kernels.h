@@ -55,15 +55,20 @@ __device__ __forceinline__ uint32_t q6_centre4(uint32_t v) {
   return ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
 }
 
-// The int8 of an activation already scaled by 127/amax: round half away from
-// zero, clamped to [-127, 127] (a NaN gives -127, as fminf(fmaxf(NaN, -127),
-// 127) does). trunc(r + copysign(0.5 - 2^-25, r)) equals roundf(r) for every
-// float |r| < 2^22: a tie k + 0.5 sums to k + 1 - 2^-25, which rounds to
-// k + 1; below a tie the sum stays more than half an ulp under k + 1; above
-// it the sum is at least k + 1. (Adding 0.5 itself fails at 0.5 - 2^-25,
-// whose sum rounds up to 1.) Five instructions instead of roundf's seven
-// plus the clamp.
-__device__ __forceinline__ int q8_round(float r) {
+// The int8 of activation v at scale inv = 127/amax: v * inv rounded half
+// away from zero, clamped to [-127, 127] (a NaN gives -127, as
+// fminf(fmaxf(NaN, -127), 127) does). trunc(r + copysign(0.5 - 2^-25, r))
+// equals roundf(r) for every float |r| < 2^22: a tie k + 0.5 sums to
+// k + 1 - 2^-25, which rounds to k + 1; below a tie the sum stays more than
+// half an ulp under k + 1; above it the sum is at least k + 1. (Adding 0.5
+// itself fails at 0.5 - 2^-25, whose sum rounds up to 1.) Five instructions
+// instead of roundf's seven plus the clamp. The product is rounded to f32
+// before the addition, as the CPU computes it: contraction into one FMA
+// (which HIP's default fp-contract allows across statements) would skip
+// that rounding and move rare values across a tie.
+__device__ __forceinline__ int q8_quant(float v, float inv) {
+#pragma clang fp contract(off)
+  const float r = v * inv;
   const float t = r + __builtin_copysignf(0x1.fffffep-2f, r);
   return (int)fminf(fmaxf(t, -127.f), 127.f);
 }

@@ -212,7 +212,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_row_kernel(const float *__restri
       int qi[4], sm = 0;
 #pragma unroll
       for (int k = 0; k < 4; k++) {
-        qi[k] = q8_round(r[k] * inv);
+        qi[k] = q8_quant(r[k], inv);
         sm += qi[k];
       }
       // sums of 16 columns: the quad of lanes, every lane of it
@@ -767,7 +767,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
       if (256 * k >= G * hd) break;
       const float amax = fmaxf(fmaxf(gmax[k][0], gmax[k][1]), fmaxf(gmax[k][2], gmax[k][3]));
       const float inv = amax == 0.f ? 0.f : 127.0f / amax;
-      const int qi = q8_round(out[k] * inv);
+      const int qi = q8_quant(out[k], inv);
       // sum of 16 columns: quads, then half rows and rows (every lane)
       int sm = qi;
       sm += (int)dpp_u32<0xB1, 0xF>((uint32_t)sm);

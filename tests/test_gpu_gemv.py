@@ -12,6 +12,7 @@ import pytest
 
 import npq
 from conftest import abs_dot, assert_parity, f32_exact
+from ties import near_tie_x
 from mdma_amd import synth
 from mdma_amd import backend as backend_mod
 from mdma_amd.backend import LAYOUT_GFX950, POOL_WEIGHTS, QWeight, ShapeMismatch, pack_weight
@@ -221,6 +222,9 @@ def test_quantize_act_bit_exact(backend, group):
     x = synth.normal_f32(8 * 1024, 77) * 3
     x[:group] = 0
     x[group:2 * group] = np.linspace(-1, 1, group, dtype=np.float32) * 127  # .5 ties
+    # Activations whose quantization depends on rounding the product before
+    # the half-way offset (a quantizer fusing them into one FMA fails here).
+    x[2 * group:18 * group] = near_tie_x(16, group, 78)
     n = x.size
     xb = backend.f32_buf(x)
     qb, db, sb = backend.alloc(n), backend.alloc(n // group * 4), backend.alloc(n // 16 * 4)

@@ -55,3 +55,24 @@ def test_adding_half_fails_below_one_half():
     # The plain r + 0.5 form rounds 0.5 - 2^-25 up to 1: the case the constant avoids.
     r = np.float32([0.5 - 2.0 ** -25])
     assert device_rule(r, np.float32(0.5))[0] == 1 and oracle_rule(r)[0] == 0 and device_rule(r)[0] == 0
+
+
+def test_near_tie_activations_depend_on_the_product_rounding():
+    """The fixture behind the GPU quantizer tests: near-tie activations exist
+    in quantity, their oracle quantization is the product-first rounding,
+    and a quantizer fusing the multiply into the offset addition (planted
+    here on the CPU) disagrees with the oracle on them."""
+    from oracle import ffi
+    from ties import C, near_tie_x
+
+    x = near_tie_x(16, 32, 5)
+    q, d, _ = ffi.quantize_act(x, 32)
+    xs = x.reshape(16, 32)
+    amax = np.abs(xs).max(axis=1)
+    inv = (np.float32(127.0) / amax).astype(np.float32)
+    r = (xs * inv[:, None]).astype(np.float32)
+    assert np.array_equal(q.reshape(16, 32), device_rule(r))
+    fused = np.trunc((xs.astype(np.float64) * inv[:, None].astype(np.float64)
+                      + np.copysign(np.float64(C), r)).astype(np.float32))
+    fused = np.clip(fused, -127, 127).astype(np.int32)
+    assert np.count_nonzero(fused != q.reshape(16, 32)) >= 32  # about 5 per group
