@@ -351,6 +351,26 @@ int mdma_gfx950_forward(mdma_session *s, uint64_t seq, uint32_t token, uint32_t 
 int mdma_gfx950_generate(mdma_session *s, const uint32_t *prompts, uint64_t n_prompt, uint64_t n_gen,
                          uint32_t *out_tokens, double *step_seconds);
 
+/* Graph decode executor (HipDecoder / Decoder::forward,
+ * src/backend/rocm/graph.rs:105-262): one decode step of sequence `seq`
+ * captured into a HIP graph whose token and position are read from device
+ * memory, replayed by every later forward. Its logits equal
+ * mdma_gfx950_forward's bit for bit, with the same validation
+ * (Model::validate_decode) and the same KV update. A forward after the
+ * context replaced a buffer the graph captured (scratch growth, a prefill
+ * of more tokens) runs that step eagerly and captures again. Free the
+ * decoder before its session. */
+typedef struct mdma_decoder mdma_decoder;
+int mdma_gfx950_decoder_new(mdma_session *s, uint64_t seq, mdma_decoder **out);
+int mdma_gfx950_decoder_forward(mdma_decoder *d, uint32_t token, uint32_t pos, float *logits);
+/* Whether the decoder's last forward replayed its graph (1) or ran eagerly (0). */
+int mdma_gfx950_decoder_replayed(const mdma_decoder *d);
+void mdma_gfx950_decoder_free(mdma_decoder *d);
+/* Extra: whether generate captures its decode step into a HIP graph and
+ * replays it (default on; off runs every step eagerly, for A/B measurement
+ * and the test that both give the same tokens). */
+int mdma_gfx950_set_graph_decode(mdma_ctx *ctx, int on);
+
 #ifdef __cplusplus
 }
 #endif

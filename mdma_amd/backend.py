@@ -73,7 +73,7 @@ _SIGS = {
     "available_device_bytes": [_P, _P], "supports_weight_dtype": [_P, _I32], "max_head_dim": [_P],
     "kv_elem_bytes": [_P], "join_execution": [_P], "set_buffer_budget": [_P, _U64, _U64],
     "buffer_usage": [_P, C.c_int, _P, _P], "set_act_mode": [_P, C.c_int],
-    "set_norm_fusion": [_P, C.c_int], "set_prefill_kernel": [_P, C.c_int], "capture_block_dots": [_P, _P], "stream": [_P],
+    "set_norm_fusion": [_P, C.c_int], "set_prefill_kernel": [_P, C.c_int], "capture_block_dots": [_P, _P], "set_graph_decode": [_P, C.c_int], "stream": [_P],
     "alloc": [_P, _U64, C.c_int, _P], "free": [_P], "buf_len": [_P], "buf_view": [_P, _U64, _U64, _P],
     "upload": [_P, _P, _U64, _P, _U64], "download": [_P, _P, _U64, _P, _U64],
     "copy": [_P, _P, _U64, _P, _U64, _U64], "upload_weight": [_P, _P, _U64, C.c_int, _P],
@@ -261,6 +261,10 @@ class Gfx950Backend:
 
     def set_norm_fusion(self, on: bool):
         _check(lib().mdma_gfx950_set_norm_fusion(self.ctx, int(bool(on))))
+
+    def set_graph_decode(self, on: bool):
+        """generate's decode steps replayed from one captured HIP graph (default) or run eagerly."""
+        _check(lib().mdma_gfx950_set_graph_decode(self.ctx, int(bool(on))))
 
     def capture_block_dots(self, out):
         """Block-dot capture into the int32 buffer out (None: off); see

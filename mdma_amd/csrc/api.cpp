@@ -499,6 +499,14 @@ int mdma_gfx950_capture_block_dots(mdma_ctx *ctx, mdma_buf *out) {
   });
 }
 
+int mdma_gfx950_set_graph_decode(mdma_ctx *ctx, int on) {
+  return guarded([&] {
+    need(ctx, "set_graph_decode");
+    std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    ctx->graph_decode = on != 0;
+  });
+}
+
 int mdma_gfx950_set_prefill_kernel(mdma_ctx *ctx, int kind) {
   return guarded([&] {
     need(ctx, "set_prefill_kernel");

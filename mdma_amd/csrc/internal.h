@@ -96,6 +96,7 @@ struct mdma_ctx {
   uint64_t host_ids_cap = 0;
   bool capturing = false;        // stream capture in progress: no synchronizing calls
   int prefill_kernel = MDMA_PREFILL_AUTO;  // mdma_gfx950_set_prefill_kernel
+  bool graph_decode = true;                // mdma_gfx950_set_graph_decode
   // Block-dot capture (mdma_gfx950_capture_block_dots): int32 slots or null.
   int32_t *dots = nullptr;
   uint64_t dots_cap = 0;
@@ -341,10 +342,21 @@ bool launch_attn_q8(mdma_ctx *ctx, const float *q, const uint16_t *k, const uint
 // seq_stride 0), all at rope position pos = kv_len - 1. The rotated key and
 // the value are written to the caches at that position, with the values
 // launch_rope_kv_write writes. int8_out: as launch_attn_q8. False, launching
-// nothing, when the shape has no such variant.
+// nothing, when the shape has no such variant. pos_dev (a captured decode
+// step): the kernel reads the position from device memory instead, and
+// kv_len is the cache capacity the launch is sized for; the results equal a
+// launch with that position and kv_len = position + 1, bit for bit.
 bool launch_attn_rope(mdma_ctx *ctx, const float *q, const float *k, const float *v, const float *tab, uint32_t pos,
                       uint16_t *kc, uint16_t *vc, float *o, uint64_t n_q, uint64_t kv_len, uint64_t hd,
-                      uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride, bool int8_out);
+                      uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride, bool int8_out,
+                      const uint32_t *pos_dev = nullptr);
+// A captured decode step's device parameters: p[0..n) = vals (one thread).
+void launch_set_u32(mdma_ctx *ctx, uint32_t *p, const uint32_t *vals, int n);
+// After a captured generate step: hist[step * B + b] = cur[b] and
+// hist_flag[...] = cur_flag[b] for the step in params[1]; then the position
+// params[0] and step params[1] advance by one.
+void launch_step_record(mdma_ctx *ctx, uint32_t *params, const uint32_t *cur, const uint32_t *cur_flag,
+                        uint32_t *hist, uint32_t *hist_flag, uint32_t B);
 void launch_argmax_rows(mdma_ctx *ctx, const float *x, uint64_t rows, uint64_t n, uint32_t *idx,
                         uint32_t *flag);
 

@@ -19,6 +19,8 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
+#include <functional>
 #include <map>
 #include <memory>
 #include <string>
@@ -363,12 +365,17 @@ void gemv_gated(mdma_ctx *ctx, const GemvJob &g, const GemvJob &u, const float *
 // (prefill or decode). seq_stride > 0: row t is the single decode token of
 // sequence t, all at position pos (batched decode). Leaves the final-normed
 // rows in s->normed.
-void run_layers(mdma_session *s, uint64_t T, uint32_t pos, uint64_t seq, bool batched) {
+// pos_dev (a captured decode step, T new tokens of one position): the
+// position is read from device memory at run time and pos is unused; the
+// RoPE table then covers the whole cache, and a shape whose attention has no
+// such launch fails instead of falling back.
+void run_layers(mdma_session *s, uint64_t T, uint32_t pos, uint64_t seq, bool batched,
+                const uint32_t *pos_dev = nullptr) {
   mdma_model *m = s->m;
   mdma_ctx *ctx = m->ctx;
   const mdma_model_config &c = m->cfg;
   const uint64_t E = c.n_embd, hd = c.head_dim, kvw = c.n_kv_heads * hd;
-  const float *tab = rope_table(ctx, pos + (batched ? 0 : T - 1), hd, c.rope_theta);
+  const float *tab = rope_table(ctx, pos_dev ? s->capacity - 1 : pos + (batched ? 0 : T - 1), hd, c.rope_theta);
   mdma_buf *x = s->x, *x_alt = s->x_alt;
   const uint64_t cache_stride = s->capacity * kvw;
   // In the int8 mode, decode-sized rows get their int8 form from the
@@ -390,14 +397,19 @@ void run_layers(mdma_session *s, uint64_t T, uint32_t pos, uint64_t seq, bool ba
   };
   // One new token per sequence (a decode step): RoPE, the K/V cache write
   // and attention in one launch.
+  // The int8 output form first (when this mode wants it), else f32 output.
   auto decode_attend = [&](uint16_t *kc, uint16_t *vc, uint64_t stride) {
     q8_invalidate(ctx);
-    const bool q8 = fuse_q8;
-    if (!launch_attn_rope(ctx, fp(s->q), fp(s->k), fp(s->v), tab, (uint32_t)pos, kc, vc, fp(s->attn_out), T, pos + 1,
-                          hd, c.n_heads, c.n_kv_heads, stride, q8))
-      return false;
-    fresh = q8;
-    return true;
+    for (bool q8 : {fuse_q8, false}) {
+      if (launch_attn_rope(ctx, fp(s->q), fp(s->k), fp(s->v), tab, (uint32_t)pos, kc, vc, fp(s->attn_out), T,
+                           pos_dev ? s->capacity : pos + 1, hd, c.n_heads, c.n_kv_heads, stride, q8, pos_dev)) {
+        fresh = q8;
+        return true;
+      }
+      if (!q8) break;
+    }
+    if (pos_dev) fail(MDMA_ERR_BACKEND, "graph decode: no captured attention launch for this shape");
+    return false;
   };
   // One token per step (decode of one sequence): the attention rmsnorm of
   // layers after the first is fused into the GEMVs around it. The previous
@@ -698,6 +710,108 @@ int mdma_gfx950_forward(mdma_session *s, uint64_t seq, uint32_t token, uint32_t 
   });
 }
 
+}  // extern "C"
+
+// The graph decode executor's state: the session's sequence, the device
+// parameters [token, position] of the captured step, and its graph.
+struct mdma_decoder {
+  mdma_session *s = nullptr;
+  uint64_t seq = 0;
+  mdma_buf *params = nullptr;
+  mdma_graph *graph = nullptr;
+  bool replayed = false;
+  ~mdma_decoder() {
+    if (graph) {
+      (void)hipStreamSynchronize(s->m->ctx->stream);  // a replay may still run
+      mdma_gfx950_graph_destroy(graph);
+    }
+    if (params) mdma_gfx950_free(params);
+  }
+};
+
+namespace {
+
+// Captures step() on the context's stream into a graph (nullptr when the
+// step cannot be captured, e.g. a buffer it needs would have to grow; the
+// stream is back to eager launches either way).
+mdma_graph *capture_step(mdma_ctx *ctx, const std::function<void()> &step) {
+  if (mdma_gfx950_graph_begin(ctx)) return nullptr;
+  bool ok = true;
+  try {
+    step();
+  } catch (...) {
+    ok = false;
+  }
+  mdma_graph *g = nullptr;
+  if (mdma_gfx950_graph_end(ctx, &g) || !ok) {
+    if (g) mdma_gfx950_graph_destroy(g);
+    return nullptr;
+  }
+  return g;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mdma_gfx950_decoder_new(mdma_session *s, uint64_t seq, mdma_decoder **out) {
+  return guarded([&] {
+    if (!s || !out) shape_fail("decoder_new: null argument");
+    if (seq >= s->batch) shape_fail("decoder_new: no such sequence");
+    auto d = std::make_unique<mdma_decoder>();
+    d->s = s;
+    d->seq = seq;
+    int st = mdma_gfx950_alloc(s->m->ctx, 16, MDMA_POOL_SCRATCH, &d->params);
+    if (st) fail(st, mdma_gfx950_last_error());
+    *out = d.release();
+  });
+}
+
+int mdma_gfx950_decoder_forward(mdma_decoder *d, uint32_t token, uint32_t pos, float *logits) {
+  return guarded([&] {
+    if (!d) shape_fail("decoder_forward: null argument");
+    mdma_session *s = d->s;
+    const uint64_t seq = d->seq;
+    // Model::validate_decode (src/model.rs:338-353).
+    if (token >= s->m->cfg.vocab || pos >= s->capacity || pos > s->len[seq])
+      shape_fail("decode requires a valid token and resumable KV prefix within capacity");
+    mdma_ctx *ctx = s->m->ctx;
+    std::lock_guard<std::recursive_mutex> lk(ctx->lock);
+    uint32_t *prm = reinterpret_cast<uint32_t *>(d->params->ptr);
+    auto step = [&]() {
+      embed_dev(s, prm, 1);
+      run_layers(s, 1, 0, seq, false, prm + 1);
+      head(s, 0, 1, seq);
+    };
+    const uint32_t vals[2] = {token, pos};
+    launch_set_u32(ctx, prm, vals, 2);
+    d->replayed = false;
+    if (d->graph) {
+      if (mdma_gfx950_graph_launch(ctx, d->graph) == 0) {
+        d->replayed = true;
+      } else {  // the context replaced a buffer the graph captured
+        mdma_gfx950_graph_destroy(d->graph);
+        d->graph = nullptr;
+      }
+    }
+    if (!d->replayed) {
+      step();  // eagerly: sizes every context buffer the step uses
+      d->graph = capture_step(ctx, step);
+    }
+    s->len[seq] = pos + 1;
+    q8_invalidate(ctx);
+    if (logits) {
+      hip_check(hipMemcpyAsync(logits, fp(s->logits) + seq * s->m->cfg.vocab, s->m->cfg.vocab * 4,
+                               hipMemcpyDeviceToHost, ctx->stream), "decoder logits");
+      hip_check(hipStreamSynchronize(ctx->stream), "decoder sync");
+    }
+  });
+}
+
+int mdma_gfx950_decoder_replayed(const mdma_decoder *d) { return d && d->replayed ? 1 : 0; }
+
+void mdma_gfx950_decoder_free(mdma_decoder *d) { delete d; }
+
 int mdma_gfx950_generate(mdma_session *s, const uint32_t *prompts, uint64_t n_prompt, uint64_t n_gen,
                          uint32_t *out_tokens, double *step_seconds) {
   return guarded([&] {
@@ -731,17 +845,58 @@ int mdma_gfx950_generate(mdma_session *s, const uint32_t *prompts, uint64_t n_pr
     }
     launch_argmax_rows(ctx, fp(s->logits), B, c.vocab, tok, flag);
     hip_check(hipEventRecord(ev[1], ctx->stream), "event");
-    // Decode: step i embeds the tokens of step i-1 straight from device memory.
-    for (uint64_t i = 1; i < n_gen; i++) {
-      const uint32_t pos = (uint32_t)(n_prompt + i - 1);
-      embed_dev(s, tok + (i - 1) * B, B);
-      if (B == 1)
-        run_layers(s, 1, pos, 0, false);
-      else
-        run_layers(s, B, pos, 0, true);
-      head(s, 0, B, 0);
-      launch_argmax_rows(ctx, fp(s->logits), B, c.vocab, tok + i * B, flag + i * B);
-      if (step_seconds) hip_check(hipEventRecord(ev[i + 1], ctx->stream), "event");
+    if (ctx->graph_decode && n_gen > 2) {
+      // Decode with one captured step, replayed (src/backend/rocm/graph.rs):
+      // the step reads the position and its tokens from device memory and
+      // ends by recording its tokens and advancing the position, so every
+      // replay is the next step. Step 1 runs eagerly (it sizes the context's
+      // buffers), then the graph runs steps 2.. (eagerly again if the step
+      // cannot be captured).
+      mdma_buf *gpb = alloc_or_throw(ctx, (2 + 2 * B) * 4, MDMA_POOL_SCRATCH, s->owned);
+      struct Release {
+        mdma_session *s;
+        mdma_buf *b;
+        ~Release() {
+          s->owned.erase(std::find(s->owned.begin(), s->owned.end(), b));
+          mdma_gfx950_free(b);
+        }
+      } release{s, gpb};
+      uint32_t *gp = reinterpret_cast<uint32_t *>(gpb->ptr), *cur = gp + 2, *cur_flag = gp + 2 + B;
+      hip_check(hipMemcpyAsync(cur, tok, B * 4, hipMemcpyDeviceToDevice, ctx->stream), "decode tokens");
+      const uint32_t start[2] = {(uint32_t)n_prompt, 1u};
+      launch_set_u32(ctx, gp, start, 2);
+      auto step = [&]() {
+        embed_dev(s, cur, B);
+        run_layers(s, B, 0, 0, B > 1, gp);
+        head(s, 0, B, 0);
+        launch_argmax_rows(ctx, fp(s->logits), B, c.vocab, cur, cur_flag);
+        launch_step_record(ctx, gp, cur, cur_flag, tok, flag, (uint32_t)B);
+      };
+      step();
+      if (step_seconds) hip_check(hipEventRecord(ev[2], ctx->stream), "event");
+      mdma_graph *g = capture_step(ctx, step);
+      for (uint64_t i = 2; i < n_gen; i++) {
+        if (!g) step();
+        else if (mdma_gfx950_graph_launch(ctx, g)) fail(MDMA_ERR_BACKEND, "decode graph launch failed");
+        if (step_seconds) hip_check(hipEventRecord(ev[i + 1], ctx->stream), "event");
+      }
+      if (g) {
+        hip_check(hipStreamSynchronize(ctx->stream), "decode graph sync");
+        mdma_gfx950_graph_destroy(g);
+      }
+    } else {
+      // Decode: step i embeds the tokens of step i-1 straight from device memory.
+      for (uint64_t i = 1; i < n_gen; i++) {
+        const uint32_t pos = (uint32_t)(n_prompt + i - 1);
+        embed_dev(s, tok + (i - 1) * B, B);
+        if (B == 1)
+          run_layers(s, 1, pos, 0, false);
+        else
+          run_layers(s, B, pos, 0, true);
+        head(s, 0, B, 0);
+        launch_argmax_rows(ctx, fp(s->logits), B, c.vocab, tok + i * B, flag + i * B);
+        if (step_seconds) hip_check(hipEventRecord(ev[i + 1], ctx->stream), "event");
+      }
     }
     for (uint64_t b = 0; b < B; b++) s->len[b] = n_prompt + n_gen - 1;
     std::vector<uint32_t> toks(n_gen * B), flags(n_gen * B);

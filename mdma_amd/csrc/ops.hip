@@ -418,6 +418,9 @@ struct AttnQ8 {
 struct AttnRope {
   const float *k, *v, *tab;
   uint32_t pos;
+  // Set in a captured decode step: the position is read from here (written
+  // before each replay), and the launch's grid is sized for the whole cache.
+  const uint32_t *pos_dev;
 };
 
 // Device-scope (all XCDs) coherent store and load of one float.
@@ -482,8 +485,24 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
   // The arguments' scalar loads in one batch (one wait, not a chain).
   sgpr_ready(q, K, V, o, part, cnt, prefix, hd, n_q_heads, n_kv_heads, scale, seq_stride, tpw);
   if constexpr (QUANT) sgpr_ready(q8.q, q8.d, q8.s16);
-  if constexpr (ROPE) sgpr_ready(rp.k, rp.v, rp.tab, rp.pos);
+  if constexpr (ROPE) sgpr_ready(rp.k, rp.v, rp.tab, rp.pos, rp.pos_dev);
   const uint32_t kvh = blockIdx.x, split = blockIdx.y, i = blockIdx.z, n_splits = gridDim.y;
+  // The new row's position and the tiles per run. From device memory in a
+  // captured step: the runs are then those the host would have chosen for
+  // this length (tiles per run ceil(tiles / n_splits); the grid's n_splits
+  // is the host's count for the whole cache, which equals the count for
+  // this length whenever the length has more tiles than runs, and otherwise
+  // gives one tile per run as the host does), so a replay computes the same
+  // partials, merged in the same order, as the eager launch.
+  uint32_t rpos = ROPE ? rp.pos : 0;
+  if constexpr (ROPE) {
+    if (rp.pos_dev) {
+      rpos = *rp.pos_dev;
+      prefix = rpos;  // one new query per sequence at rpos: visible = rpos + 1
+      const uint32_t tl = (rpos + ATT_TILE) / ATT_TILE;
+      tpw = (tl + n_splits - 1) / n_splits;
+    }
+  }
   const uint32_t visible = seq_stride ? prefix + 1 : prefix + i + 1;
   const uint32_t tiles = (visible + ATT_TILE - 1) / ATT_TILE, t0 = split * tpw;
   if (t0 >= tiles) return;  // this query's keys end before the run
@@ -505,7 +524,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
   for (int k = 0; k < QP; k++) {
     const uint32_t p = min(tid + 256 * k, n_qp - 1), h = p / hp, e = p % hp;
     qx[k] = *reinterpret_cast<const float2 *>(qv + h * hd + 2 * e);
-    if (ROPE) qcs[k] = reinterpret_cast<const float2 *>(rp.tab)[(size_t)rp.pos * hp + e];
+    if (ROPE) qcs[k] = reinterpret_cast<const float2 *>(rp.tab)[(size_t)rpos * hp + e];
   }
   // The new key (ROPE: position visible - 1) is not read from the cache: it
   // is rotated from rp.k and rounded to f16 exactly as the cache stores it
@@ -517,7 +536,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
   if (ROPE) {
     kn2 = reinterpret_cast<const float2 *>(rp.k + ((size_t)i * n_kv_heads + kvh) * hd)[en];
     vn2 = reinterpret_cast<const float2 *>(rp.v + ((size_t)i * n_kv_heads + kvh) * hd)[en];
-    cn2 = reinterpret_cast<const float2 *>(rp.tab)[(size_t)rp.pos * hp + en];
+    cn2 = reinterpret_cast<const float2 *>(rp.tab)[(size_t)rpos * hp + en];
   }
   // Ping-pong tile buffers: the loads for tile+1 go out before tile is
   // computed (clamped to the run's last tile, so every load is in bounds and
@@ -656,7 +675,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
   constexpr int NO = (G * 128 * C + 255) / 256;
   float out[NO];
   const size_t orow = ((size_t)i * n_q_heads + qh0) * hd;
-  if (n_splits == 1) {
+  if (live == 1) {  // one run (always so when the grid has one split): no partials
 #pragma unroll
     for (int k = 0; k < NO; k++) {
       const uint32_t t = tid + 256 * k;
@@ -1083,9 +1102,10 @@ bool launch_attn_q8(mdma_ctx *ctx, const float *q, const uint16_t *k, const uint
 
 bool launch_attn_rope(mdma_ctx *ctx, const float *q, const float *k, const float *v, const float *tab, uint32_t pos,
                       uint16_t *kc, uint16_t *vc, float *o, uint64_t n_q, uint64_t kv_len, uint64_t hd,
-                      uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride, bool int8_out) {
-  if (!n_q || !kv_len || pos != kv_len - 1) return false;
-  const AttnRope rp{k, v, tab, pos};
+                      uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride, bool int8_out,
+                      const uint32_t *pos_dev) {
+  if (!n_q || !kv_len || (!pos_dev && pos != kv_len - 1)) return false;
+  const AttnRope rp{k, v, tab, pos, pos_dev};
   if (!int8_out)
     return attn_impl(ctx, q, kc, vc, o, n_q, kv_len, hd, n_q_heads, n_kv_heads, seq_stride, nullptr, &rp);
   const uint64_t n_in = n_q_heads * hd;
@@ -1095,6 +1115,44 @@ bool launch_attn_rope(mdma_ctx *ctx, const float *q, const float *k, const float
   if (!attn_impl(ctx, q, kc, vc, o, n_q, kv_len, hd, n_q_heads, n_kv_heads, seq_stride, &a8, &rp)) return false;
   q8_mark(ctx, o, n_q, n_in);
   return true;
+}
+
+namespace {
+struct U32x4 {
+  uint32_t v[4];
+};
+__global__ void set_u32_kernel(uint32_t *p, U32x4 vals, int n) {
+  for (int i = 0; i < n; i++) p[i] = vals.v[i];
+}
+__global__ __launch_bounds__(1024) void step_record_kernel(uint32_t *params, const uint32_t *cur,
+                                                           const uint32_t *cur_flag, uint32_t *hist,
+                                                           uint32_t *hist_flag, uint32_t B) {
+  const uint32_t step = params[1];
+  for (uint32_t b = threadIdx.x; b < B; b += blockDim.x) {
+    hist[(size_t)step * B + b] = cur[b];
+    hist_flag[(size_t)step * B + b] = cur_flag[b];
+  }
+  __syncthreads();  // every thread has read the step before it advances
+  if (threadIdx.x == 0) {
+    params[0] += 1;
+    params[1] += 1;
+  }
+}
+}  // namespace
+
+void launch_set_u32(mdma_ctx *ctx, uint32_t *p, const uint32_t *vals, int n) {
+  if (n < 1 || n > 4) fail(MDMA_ERR_BACKEND, "set_u32: 1 to 4 values");
+  U32x4 v{};
+  for (int i = 0; i < n; i++) v.v[i] = vals[i];
+  set_u32_kernel<<<dim3(1), dim3(1), 0, ctx->stream>>>(p, v, n);
+  hip_check(hipGetLastError(), "set_u32 launch");
+}
+
+void launch_step_record(mdma_ctx *ctx, uint32_t *params, const uint32_t *cur, const uint32_t *cur_flag,
+                        uint32_t *hist, uint32_t *hist_flag, uint32_t B) {
+  step_record_kernel<<<dim3(1), dim3(B < 1024 ? (B + 63) / 64 * 64 : 1024), 0, ctx->stream>>>(
+      params, cur, cur_flag, hist, hist_flag, B);
+  hip_check(hipGetLastError(), "step_record launch");
 }
 
 void launch_argmax_rows(mdma_ctx *ctx, const float *x, uint64_t rows, uint64_t n, uint32_t *idx, uint32_t *flag) {

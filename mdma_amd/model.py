@@ -33,6 +33,8 @@ _SIGS = {
     "session_reset": ([_P], C.c_int), "prefill": ([_P, _U64, _P, _U64, C.c_uint32, _P], C.c_int),
     "forward": ([_P, _U64, C.c_uint32, C.c_uint32, _P], C.c_int),
     "generate": ([_P, _P, _U64, _U64, _P, _P], C.c_int),
+    "decoder_new": ([_P, _U64, _P], C.c_int), "decoder_forward": ([_P, C.c_uint32, C.c_uint32, _P], C.c_int),
+    "decoder_replayed": ([_P], C.c_int), "decoder_free": ([_P], None),
 }
 _bound = False
 
@@ -113,7 +115,36 @@ class Session:
                                            secs.ctypes.data))
         return out, secs
 
+    def decoder(self, seq: int = 0) -> "Decoder":
+        return Decoder(self, seq)
+
     def close(self):
         if self.handle and self.model.backend.ctx is not None:
             _lib().mdma_gfx950_session_free(self.handle)
+        self.handle = None
+
+
+class Decoder:
+    """The graph decode executor (HipDecoder, src/backend/rocm/graph.rs:
+    105-262): forward(token, pos) replays one captured decode step of the
+    session's sequence `seq`; close it before the session."""
+
+    def __init__(self, session: Session, seq: int = 0):
+        self.session = session
+        h = C.c_void_p()
+        _check(_lib().mdma_gfx950_decoder_new(session.handle, seq, C.byref(h)))
+        self.handle = h.value
+
+    def forward(self, token: int, pos: int) -> np.ndarray:
+        logits = np.empty(self.session.model.config.vocab, np.float32)
+        _check(_lib().mdma_gfx950_decoder_forward(self.handle, token, pos, logits.ctypes.data))
+        return logits
+
+    @property
+    def replayed(self) -> bool:
+        return bool(_lib().mdma_gfx950_decoder_replayed(self.handle))
+
+    def close(self):
+        if self.handle:
+            _lib().mdma_gfx950_decoder_free(self.handle)
         self.handle = None
