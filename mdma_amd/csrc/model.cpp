@@ -118,27 +118,45 @@ struct Gguf {
       std::string name = gstr();
       uint32_t nd = get<uint32_t>();
       if (nd == 0 || nd > 4) fail(MDMA_ERR_UNSUPPORTED_MODEL, "gguf: tensor rank");
+      // tensor_n_bytes (src/gguf.rs): element and byte counts without
+      // overflow, whole blocks only; errors name the tensor.
       GgufTensor t;
+      bool over = false;
       for (uint32_t d = 0; d < nd; d++) {
         uint64_t dim = get<uint64_t>();
-        if (d == 0)
+        if (d == 0) {
           t.cols = dim;  // ne0: the contiguous (column) dimension
-        else
+        } else {
+          over |= dim && t.rows > UINT64_MAX / dim;
           t.rows *= dim;
+        }
       }
       t.dtype = (int32_t)get<uint32_t>();
       t.offset = get<uint64_t>();
-      uint64_t bs = block_size(t.dtype);
+      uint64_t bs = block_size(t.dtype), ts = type_size(t.dtype);
       if (!bs || t.cols % bs) fail(MDMA_ERR_UNSUPPORTED_MODEL, "gguf: " + name + " has an unsupported dtype or width");
-      t.bytes = t.rows * (t.cols / bs) * type_size(t.dtype);
+      const uint64_t blocks = t.cols / bs;
+      over |= t.rows && blocks > UINT64_MAX / t.rows;
+      over |= !over && ts && t.rows * blocks > UINT64_MAX / ts;
+      if (over) fail(MDMA_ERR_UNSUPPORTED_MODEL, "gguf: " + name + " byte size overflows");
+      t.bytes = t.rows * blocks * ts;
       raw.push_back({name, t});
     }
     uint64_t align = num.count("general.alignment") ? (uint64_t)num["general.alignment"] : 32;
+    if (!align) fail(MDMA_ERR_UNSUPPORTED_MODEL, "gguf: zero alignment");
     long pos = ftell(f);
     uint64_t data = ((uint64_t)pos + align - 1) / align * align;
+    if (fseeko(f, 0, SEEK_END)) fail(MDMA_ERR_IO, "gguf: seek");
+    const uint64_t file_len = (uint64_t)ftello(f);
     for (auto &kv : raw) {
-      kv.second.offset += data;
-      tensors[kv.first] = kv.second;
+      // tensor_start (src/gguf.rs): data + offset + bytes within the file,
+      // without overflow.
+      GgufTensor &t = kv.second;
+      if (t.offset > UINT64_MAX - data || t.bytes > UINT64_MAX - (data + t.offset) ||
+          data + t.offset + t.bytes > file_len)
+        fail(MDMA_ERR_UNSUPPORTED_MODEL, "gguf: " + kv.first + " extends past the end of the file");
+      t.offset += data;
+      tensors[kv.first] = t;
     }
   }
   void read(const GgufTensor &t, std::vector<uint8_t> &buf) {

@@ -399,3 +399,63 @@ def test_memory_plan_and_limits(backend, tiny):
     m.close()
     with pytest.raises(MemoryBudget):
         Model(backend, tiny[1], budget_bytes=1 << 20)
+
+
+# ------------------------------------------------------------ GGUF reader ----
+
+def raw_gguf(path, tensors, data_bytes):
+    """A GGUF v3 container of llama architecture with the given tensor
+    descriptors [(name, ggml dims ne0 first, ggml type, offset)] and
+    data_bytes bytes of data after the 32-aligned header."""
+    import struct
+
+    def s(x):
+        b = x.encode()
+        return struct.pack("<Q", len(b)) + b
+    kv = s("general.architecture") + struct.pack("<I", 8) + s("llama")
+    infos = b"".join(s(n) + struct.pack("<I", len(d)) + b"".join(struct.pack("<Q", x) for x in d)
+                     + struct.pack("<IQ", t, off) for n, d, t, off in tensors)
+    head = b"GGUF" + struct.pack("<IQQ", 3, len(tensors), 1) + kv + infos
+    head += b"\0" * ((-len(head)) % 32)
+    with open(path, "wb") as f:
+        f.write(head + b"\0" * data_bytes)
+    return len(head)
+
+
+def test_gguf_reader_sizes_and_ranges(backend, tmp_path):
+    """The C++ reader's tensor_n_bytes / tensor_start (src/gguf.rs:318-345),
+    pinned on the reference's own cases (src/gguf/tests.rs:146-175): a Q4_K
+    [2, 256] tensor is 288 bytes; element or byte counts that overflow and
+    partial blocks are refused naming the tensor; a tensor's byte range must
+    end within the file. A container that passes the reader fails later, on
+    the missing model metadata."""
+    from mdma_amd.backend import UnsupportedModel
+    p = str(tmp_path / "t.gguf")
+    U64 = 2 ** 64 - 1
+
+    def load():
+        return Model(backend, p)
+
+    def reader_ok():
+        with pytest.raises(UnsupportedModel) as e:
+            load()
+        assert "missing metadata" in e.value.msg, e.value.msg
+
+    raw_gguf(p, [("w.weight", [256, 2], 12, 0)], 288)
+    reader_ok()
+    raw_gguf(p, [("w.weight", [256, 2], 12, 0)], 287)
+    with pytest.raises(UnsupportedModel, match="w.weight"):
+        load()
+    for dims, t in (([2, U64], 0), ([U64 // 4 + 1], 0), ([257], 12)):
+        raw_gguf(p, [("bad.weight", dims, t, 0)], 64)
+        with pytest.raises(UnsupportedModel, match="bad.weight"):
+            load()
+    # Offset 16, 32 bytes of F32 [8]: the data must reach 16 + 32 past its start.
+    raw_gguf(p, [("w.weight", [8], 0, 16)], 48)
+    reader_ok()
+    raw_gguf(p, [("w.weight", [8], 0, 16)], 47)
+    with pytest.raises(UnsupportedModel, match="w.weight"):
+        load()
+    raw_gguf(p, [("w.weight", [8], 0, U64 - 8)], 48)
+    with pytest.raises(UnsupportedModel, match="w.weight"):
+        load()
