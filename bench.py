@@ -175,7 +175,7 @@ def time_graphs(be, ev, graphs, steps, warmup):
     return ms
 
 
-def per_launch(be, ev, wl, mode, reps):
+def per_launch(be, ev, wl, mode, reps, graph=True, only=None):
     """Per launch kind, over every distinct weight copy, each launch as the
     step issues it (in the int8 mode the down projection quantizes its f32 x
     in its own prologue, so its time includes that quantization):
@@ -189,12 +189,16 @@ def per_launch(be, ev, wl, mode, reps):
     starts, stops = [ev.event() for _ in range(n)], [ev.event() for _ in range(n)]
     for launch in LAUNCHES:
         name = launch[0]
-        # The graph starts with the rmsnorm writing the launches' input (and
-        # its int8 form): us_graph includes a ninth of that kernel.
-        g = be.capture(lambda: [wl.prepare(be)] + [wl.launch(be, L, name) for L in wl.layers])
-        ms = time_graphs(be, ev, [g], reps, 2)
-        g.close()
-        us_graph = ms * 1e3 / n
+        if only and name != only:
+            continue
+        us_graph = float("nan")
+        if graph:
+            # The graph starts with the rmsnorm writing the launches' input (and
+            # its int8 form): us_graph includes a ninth of that kernel.
+            g = be.capture(lambda: [wl.prepare(be)] + [wl.launch(be, L, name) for L in wl.layers])
+            ms = time_graphs(be, ev, [g], reps, 2)
+            g.close()
+            us_graph = ms * 1e3 / n
         wl.prepare(be)
         for L in wl.layers:  # warm: code loaded
             wl.launch(be, L, name)
@@ -542,6 +546,14 @@ def main():
     ap.add_argument("--no-e2e", action="store_true", help="skip the Llama-3-8B end-to-end decode")
     ap.add_argument("--e2e-only", action="store_true",
                     help="only the Llama-3-8B end-to-end leg (for a profiler's kernel trace of decode steps)")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the int8 per-launch leg and the roofline object computed from it (for a profiler's "
+                         "kernel trace whose dispatches are exactly the ones the roofline averages)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the prefill GEMM leg (for profiler traces and counters of the GEMMs)")
+    ap.add_argument("--eager-decode", action="store_true",
+                    help="end-to-end decode steps launched eagerly instead of replayed from a captured HIP graph "
+                         "(the same kernels; for profilers that do not follow graph replays)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU's share of the workload; --gpus {args.gpus} is not supported "
@@ -553,10 +565,30 @@ def main():
     t0 = time.perf_counter()
     be = Gfx950Backend(0)
     init_s = time.perf_counter() - t0
+    if args.eager_decode:
+        be.set_graph_decode(False)
     if args.e2e_only:
         print(json.dumps({"e2e_llama3_8b": e2e_decode(be), "device": be.device_label()}), flush=True)
         return
     ev = HipEvents()
+    if args.prefill_only:
+        print(json.dumps({"prefill_gemm_i8": prefill_gemms(be, ev, max(2, args.reps // 4)),
+                          "device": be.device_label()}), flush=True)
+        return
+    if args.roofline_only:
+        wl = Workload(be)
+        be.reserve_scratch(64 << 20)
+        be.set_act_mode(ACT_I8)
+        # Only the gate/up, no graph replays: the kernel's dispatches are one
+        # untimed warm pass over the weight copies, then the timed launches.
+        dom = per_launch(be, ev, wl, "i8", args.reps, graph=False, only="gate_up")["gate_up"]
+        print(json.dumps({"roofline": {"kernel": "gemv_team<Q4G, int8, gated, x staged in LDS>",
+                                       "bytes_per_launch": dom["bytes_per_launch"], "us_per_launch": dom["us_kernel"],
+                                       "us_per_launch_median": dom["us_kernel_median"],
+                                       "launches_timed": dom["launches_timed"],
+                                       "frac": round(dom["GBps_kernel"] / HBM_PEAK_GBS, 4)},
+                          "device": be.device_label()}), flush=True)
+        return
     probe = copy_probe(be, ev)
     wl = Workload(be)
     be.reserve_scratch(64 << 20)
