@@ -143,6 +143,14 @@ int mdma_gfx950_set_norm_fusion(mdma_ctx *ctx, int on);
  * qmatmul_i8 (src/backend/rocm.rs:1759-1918). */
 typedef enum { MDMA_PREFILL_AUTO = 0, MDMA_PREFILL_I8 = 1 } mdma_prefill_kernel;
 int mdma_gfx950_set_prefill_kernel(mdma_ctx *ctx, int kind);
+/* Extra: the int8 mode's batched decode GEMV kernel (calls of 5 tokens or
+ * more on prepared-layout weights that the prefill GEMM does not take, up
+ * to 16 tokens per launch). AUTO (default) streams each block of
+ * the weight tile, activations and scales through a per-wave LDS ring by
+ * DMA; STAGED loads them into registers and stages the weights in LDS (for
+ * A/B measurement and the equality test: both give the same bits). */
+typedef enum { MDMA_BATCH_AUTO = 0, MDMA_BATCH_STAGED = 1 } mdma_batch_kernel;
+int mdma_gfx950_set_batch_kernel(mdma_ctx *ctx, int kind);
 /* Extra (for tests; the reference pins its int8 matrix-core fragments the
  * same way, src/backend/rocm/tests.rs:1861-1925): block-dot capture. With
  * out set (NULL: off), every later int8-mode qmatmul, qmatmul_qkv and

@@ -26,6 +26,7 @@ LAYOUT_GGUF, LAYOUT_GFX950, LAYOUT_ROCM_Q4K_V3 = 0, 1, 2
 DOMAIN_DEVICE, DOMAIN_HOST = 0, 1
 ACT_F32, ACT_I8 = 0, 1
 PREFILL_AUTO, PREFILL_I8 = 0, 1  # mdma_prefill_kernel
+BATCH_AUTO, BATCH_STAGED = 0, 1  # mdma_batch_kernel
 
 ERROR_NAMES = {1: "ContextLimit", 2: "ShapeMismatch", 3: "NotImplemented", 4: "UnsupportedModel",
                5: "MemoryBudget", 6: "BufferBudget", 7: "InsufficientMemory", 8: "OutOfMemory",
@@ -73,7 +74,7 @@ _SIGS = {
     "available_device_bytes": [_P, _P], "supports_weight_dtype": [_P, _I32], "max_head_dim": [_P],
     "kv_elem_bytes": [_P], "join_execution": [_P], "set_buffer_budget": [_P, _U64, _U64],
     "buffer_usage": [_P, C.c_int, _P, _P], "set_act_mode": [_P, C.c_int],
-    "set_norm_fusion": [_P, C.c_int], "set_prefill_kernel": [_P, C.c_int], "capture_block_dots": [_P, _P], "set_graph_decode": [_P, C.c_int], "stream": [_P],
+    "set_norm_fusion": [_P, C.c_int], "set_prefill_kernel": [_P, C.c_int], "set_batch_kernel": [_P, C.c_int], "capture_block_dots": [_P, _P], "set_graph_decode": [_P, C.c_int], "stream": [_P],
     "alloc": [_P, _U64, C.c_int, _P], "free": [_P], "buf_len": [_P], "buf_view": [_P, _U64, _U64, _P],
     "upload": [_P, _P, _U64, _P, _U64], "download": [_P, _P, _U64, _P, _U64],
     "copy": [_P, _P, _U64, _P, _U64, _U64], "upload_weight": [_P, _P, _U64, C.c_int, _P],
@@ -275,6 +276,11 @@ class Gfx950Backend:
         """PREFILL_AUTO: the f16-path GEMM for Q4_K prefill calls, the int8
         MFMA GEMM elsewhere; PREFILL_I8: the int8 MFMA GEMM for all."""
         _check(lib().mdma_gfx950_set_prefill_kernel(self.ctx, int(kind)))
+
+    def set_batch_kernel(self, kind: int):
+        """BATCH_AUTO: batched int8 GEMVs (5+ tokens) stream through the DMA
+        ring kernel; BATCH_STAGED: the register-staged kernel (same bits)."""
+        _check(lib().mdma_gfx950_set_batch_kernel(self.ctx, int(kind)))
 
     def stream(self) -> int:
         return int(lib().mdma_gfx950_stream(self.ctx) or 0)

@@ -516,6 +516,15 @@ int mdma_gfx950_set_prefill_kernel(mdma_ctx *ctx, int kind) {
   });
 }
 
+int mdma_gfx950_set_batch_kernel(mdma_ctx *ctx, int kind) {
+  return guarded([&] {
+    need(ctx, "set_batch_kernel");
+    if (kind != MDMA_BATCH_AUTO && kind != MDMA_BATCH_STAGED) shape_fail("set_batch_kernel: unknown kind");
+    std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    ctx->batch_kernel = kind;
+  });
+}
+
 int mdma_gfx950_set_norm_fusion(mdma_ctx *ctx, int on) {
   return guarded([&] {
     need(ctx, "set_norm_fusion");

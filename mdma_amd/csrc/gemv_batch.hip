@@ -123,17 +123,31 @@ struct BQ4 {
     }
   }
   static constexpr uint32_t SUBS = 8;  // capture slots per 256-column block
-  __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, float *c, const Dots &dc) {
-    const uint32_t n = l & 15, g = l >> 4;
-    const uint4 h = *reinterpret_cast<const uint4 *>(lds + 16 * RS + 16 * n);
+  // Operands of the staged kernel: the tile in the wave's LDS, x in registers.
+  struct Staged {
+    const uint8_t *lds;
+    uint32_t n, g;
+    const X &x;
+    __device__ uint4 hdr() const { return *reinterpret_cast<const uint4 *>(lds + 16 * RS + 16 * n); }
+    __device__ uint64_t w(int p) const { return *reinterpret_cast<const uint64_t *>(lds + n * RS + 32 * p + 8 * g); }
+    __device__ uint64_t xg(int j) const { return j & 1 ? x.hi[j >> 1] : x.lo[j >> 1]; }
+  };
+  // The block's contributions c[j] (before the activation scale) for row
+  // l%16 and tokens 4*(l/16)+j, from the operand source op: hdr() the row's
+  // 16-byte header, w(p) the lane's 8 quant bytes of unit p, xg(j) the
+  // lane's 8 activation bytes of the block's 32-column group j.
+  template <class Op>
+  __device__ static void compute(const Op &op, float *c, const Dots &dc, uint32_t g) {
+    const uint4 h = op.hdr();
     constexpr uint64_t M4 = 0x0F0F0F0F0F0F0F0Full;
     v4i ai = {}, dm = {};
 #pragma unroll
     for (int p = 0; p < 4; p++) {
-      const uint64_t w = *reinterpret_cast<const uint64_t *>(lds + n * RS + 32 * p + 8 * g);
+      const uint64_t w = op.w(p);
+      const uint64_t xlo = op.xg(2 * p), xhi = op.xg(2 * p + 1);
       const v4i z = {};
-      const v4i da = mma(x.lo[p], w & M4, z);
-      const v4i db = mma(x.hi[p], (w >> 4) & M4, z);
+      const v4i da = mma(xlo, w & M4, z);
+      const v4i db = mma(xhi, (w >> 4) & M4, z);
       if (dc.p)
 #pragma unroll
         for (int j = 0; j < 4; j++) dc.put(4 * g + j, 2 * p, da[j]), dc.put(4 * g + j, 2 * p + 1, db[j]);
@@ -142,12 +156,15 @@ struct BQ4 {
       // 24-bit multiplies (full rate): |isum| <= 15*127*32.
 #pragma unroll
       for (int j = 0; j < 4; j++) ai[j] += __mul24(sca, da[j]) + __mul24(scb, db[j]);
-      dm = mma(x.lo[p], bytes8(ma), dm);
-      dm = mma(x.hi[p], bytes8(mb), dm);
+      dm = mma(xlo, bytes8(ma), dm);
+      dm = mma(xhi, bytes8(mb), dm);
     }
     const float d = h2f(h.x), dmin = h2f(h.x >> 16);
 #pragma unroll
     for (int j = 0; j < 4; j++) c[j] = d * (float)ai[j] - dmin * (float)dm[j];
+  }
+  __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, float *c, const Dots &dc) {
+    compute(Staged{lds, l & 15, l >> 4, x}, c, dc, l >> 4);
   }
 };
 
@@ -212,26 +229,41 @@ struct BQ6 {
       for (int r = 0; r < 4; r++) x.q[v][r] = xr(col(4 * b + 2 * v + (g >> 1), r) + 8 * (g & 1));
   }
   static constexpr uint32_t SUBS = 16;
-  __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, float *c, const Dots &dc) {
-    const uint32_t n = l & 15, g = l >> 4;
-    const uint4 sc4 = *reinterpret_cast<const uint4 *>(lds + 16 * RS + 16 * n);
+  struct Staged {
+    const uint8_t *lds;
+    uint32_t n, g;
+    const X &x;
+    __device__ uint4 sc() const { return *reinterpret_cast<const uint4 *>(lds + 16 * RS + 16 * n); }
+    __device__ float d() const {
+      return h2f((uint16_t)*reinterpret_cast<const uint32_t *>(lds + 16 * RS + 256 + 4 * n));
+    }
+    // Plane k (A, B, high bits) of the lane's unit of pair v.
+    __device__ uint64_t w(int v, int k) const {
+      return *reinterpret_cast<const uint64_t *>(lds + n * RS + 48 * (2 * v + (g >> 1)) + 8 * (g & 1) + 16 * k);
+    }
+    __device__ uint64_t xg(int j) const { return x.q[j >> 2][j & 3]; }
+  };
+  // As BQ4::compute: sc() the row's 16 scale bytes, d() its d, w(v, k)
+  // plane k's 8 bytes of the lane's unit of pair v, xg(4v + r) the lane's
+  // activations of quarter r of pair v (the block's 32-column group 4v+r).
+  template <class Op>
+  __device__ static void compute(const Op &op, float *c, const Dots &dc, uint32_t g) {
+    const uint4 sc4 = op.sc();
     const uint32_t scw[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
     v4i ai = {};
 #pragma unroll
     for (int v = 0; v < 2; v++) {
-      const uint8_t *p = lds + n * RS + 48 * (2 * v + (g >> 1)) + 8 * (g & 1);
-      const uint64_t wa = *reinterpret_cast<const uint64_t *>(p);
-      const uint64_t wb = *reinterpret_cast<const uint64_t *>(p + 16);
-      const uint64_t wq = *reinterpret_cast<const uint64_t *>(p + 32);
+      const uint64_t wa = op.w(v, 0), wb = op.w(v, 1), wq = op.w(v, 2);
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const uint32_t lo = q6_centre4(u6((uint32_t)wa, (uint32_t)wb, (uint32_t)wq, r));
         const uint32_t hi = q6_centre4(u6((uint32_t)(wa >> 32), (uint32_t)(wb >> 32), (uint32_t)(wq >> 32), r));
         const uint64_t wv = (uint64_t)lo | ((uint64_t)hi << 32);
+        const uint64_t xq = op.xg(4 * v + r);
         // Unit 2v: lanes g < 2; unit 2v+1: lanes g >= 2.
         const v4i z = {};
-        const v4i d0 = mma(g < 2 ? x.q[v][r] : 0ull, wv, z);
-        const v4i d1 = mma(g < 2 ? 0ull : x.q[v][r], wv, z);
+        const v4i d0 = mma(g < 2 ? xq : 0ull, wv, z);
+        const v4i d1 = mma(g < 2 ? 0ull : xq, wv, z);
         // Sub-block (16 columns) of unit 4b + 2v + e, quarter r: 8v + 2r + e.
         if (dc.p)
 #pragma unroll
@@ -243,9 +275,12 @@ struct BQ6 {
         for (int j = 0; j < 4; j++) ai[j] += __mul24(s0, d0[j]) + __mul24(s1, d1[j]);
       }
     }
-    const float d = h2f((uint16_t)*reinterpret_cast<const uint32_t *>(lds + 16 * RS + 256 + 4 * n));
+    const float d = op.d();
 #pragma unroll
     for (int j = 0; j < 4; j++) c[j] = d * (float)ai[j];
+  }
+  __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, float *c, const Dots &dc) {
+    compute(Staged{lds, l & 15, l >> 4, x}, c, dc, l >> 4);
   }
 };
 
@@ -287,17 +322,27 @@ struct BQ8 {
     for (int i = 0; i < 8; i++) x.q[i] = xr(256 * b + 32 * i + 8 * g);
   }
   static constexpr uint32_t SUBS = 8;
-  __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, float *c, const Dots &dc) {
-    const uint32_t n = l & 15, g = l >> 4;
-    const uint4 d4 = *reinterpret_cast<const uint4 *>(lds + 16 * RS + 16 * n);
+  struct Staged {
+    const uint8_t *lds;
+    uint32_t n, g;
+    const X &x;
+    __device__ uint4 sc() const { return *reinterpret_cast<const uint4 *>(lds + 16 * RS + 16 * n); }
+    __device__ uint64_t w(int i) const { return *reinterpret_cast<const uint64_t *>(lds + n * RS + 32 * i + 8 * g); }
+    __device__ uint64_t xg(int i) const { return x.q[i]; }
+  };
+  // As BQ4::compute: sc() the row's eight f16 scales, w(i) the lane's 8
+  // quant bytes of block i, xg(i) the lane's activations of block i.
+  template <class Op>
+  __device__ static void compute(const Op &op, float *c, const Dots &dc, uint32_t g) {
+    const uint4 d4 = op.sc();
     const uint32_t dw[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
     for (int j = 0; j < 4; j++) c[j] = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      const uint64_t w = *reinterpret_cast<const uint64_t *>(lds + n * RS + 32 * i + 8 * g);
+      const uint64_t w = op.w(i);
       const v4i z = {};
-      const v4i dq = mma(x.q[i], w, z);
+      const v4i dq = mma(op.xg(i), w, z);
       if (dc.p)
 #pragma unroll
         for (int j = 0; j < 4; j++) dc.put(4 * g + j, i, dq[j]);
@@ -305,6 +350,9 @@ struct BQ8 {
 #pragma unroll
       for (int j = 0; j < 4; j++) c[j] = fmaf(d, (float)dq[j], c[j]);
     }
+  }
+  __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, float *c, const Dots &dc) {
+    compute(Staged{lds, l & 15, l >> 4, x}, c, dc, l >> 4);
   }
 };
 
@@ -527,7 +575,423 @@ void launch_fmt(mdma_ctx *ctx, const BatchSet &bs, uint32_t tiles, bool gated, c
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// The DMA-ring kernel (the default): gemv_batch's products and summation
+// order (its results are equal bit for bit), with every byte a block needs
+// moved by global_load_lds straight into a ring of two LDS slots per wave:
+// one pair of 256-column blocks is computed while the next pair lands. The
+// wave holds no registers for the loads in flight and waits for a pair
+// with an exact count (s_waitcnt vmcnt) rather than the compiler's, which
+// drains every load in flight. A pair makes each row's plane read a whole
+// 128-byte line: one request, where one block's 64 bytes take one each.
+//
+// A slot (the pair's 512 columns of the wave's tile):
+//   x      a 512-byte row per token (XN = 8 or 16 rows); the 16-byte chunk
+//          k of token t at position k ^ t, so 16 tokens reading the same
+//          32-column group hit distinct banks. Tokens past T repeat T-1.
+//   scale  the pair's per-256 activation scales, [block][token] (f32).
+//   w      per weight: each plane as 16 rows x RB bytes (RB: the row's
+//          plane bytes for the pair), the 16-byte chunk c of row n at
+//          position c ^ (n * RB / 256), so 16 rows reading one chunk hit
+//          distinct banks; then the per-row pieces, [row][block] 16 bytes.
+// An operand read is one XOR of the lane's base offset with 16c (weight
+// chunk c) or 32j (x group j of the pair's 16).
+
+// A plane of RB bytes per row in the slot (64 lanes x 16 bytes per DMA).
+template <uint32_t RB>
+struct Plane {
+  static constexpr uint32_t CH = RB / 16;      // 16-byte chunks per row
+  static constexpr uint32_t ROWS = 64 / CH;    // rows per DMA
+  static constexpr uint32_t NDMA = 16 / ROWS;  // DMAs per plane
+  static constexpr uint32_t BYTES = 16 * RB;
+  __device__ static uint32_t f(uint32_t n) { return (n * RB) >> 8; }
+  __device__ static uint32_t row(uint32_t L, int k) { return ROWS * k + L / CH; }
+  __device__ static uint32_t chunk(uint32_t L, int k) { return (L % CH) ^ f(row(L, k)); }
+  // Read base of lane (row n, k-group g) before the chunk's XOR.
+  __device__ static uint32_t base(uint32_t n, uint32_t g) { return RB * n + 8 * (g & 1) + 16 * f(n); }
+  template <int NP>
+  __device__ static void src(size_t rb, uint32_t row0, uint32_t n_out, uint32_t L, uint32_t (&o)[NDMA]) {
+#pragma unroll
+    for (int k = 0; k < (int)NDMA; k++) o[k] = (uint32_t)(min(row0 + row(L, k), n_out - 1) * rb) + 16 * chunk(L, k);
+  }
+  // Plane DMAs of pair s: the plane starts at pl in the row.
+  __device__ static void issue(const uint8_t *w, const uint32_t (&o)[NDMA], uint32_t pl, uint32_t s, uint8_t *dst) {
+#pragma unroll
+    for (int k = 0; k < (int)NDMA; k++) lds_dma16(w, o[k] + pl + RB * s, dst + 1024 * k);
+  }
+};
+// Source of lane L for a 16-byte-per-row-per-block piece at off in the
+// row: lanes 0..31 load rows L/2, halves L%2 (the pair's two blocks).
+__device__ __forceinline__ uint32_t pair_piece(size_t rb, uint32_t row0, uint32_t n_out, uint32_t L, uint32_t off) {
+  return (uint32_t)(min(row0 + ((L >> 1) & 15), n_out - 1) * rb) + off + 16 * (L & 1);
+}
+__device__ __forceinline__ void issue_piece(const uint8_t *w, uint32_t o, uint32_t s, uint8_t *dst, uint32_t L) {
+  if (L < 32) lds_dma16(w, o + 32 * s, dst);
+}
+
+// Q4_K: planes A | B, then the headers.
+struct RQ4 {
+  using B = BQ4;
+  using P = Plane<128>;
+  static constexpr uint32_t WB = 2 * P::BYTES + 512;
+  static constexpr int NDMA = 2 * P::NDMA + 1;
+  struct Src {
+    uint32_t pl[P::NDMA], hd, U;
+  };
+  __device__ static Src src(size_t rb, uint32_t n_in, uint32_t row0, uint32_t n_out, uint32_t L) {
+    Src s;
+    s.U = n_in / 64;
+    P::src<2>(rb, row0, n_out, L, s.pl);
+    s.hd = pair_piece(rb, row0, n_out, L, 32 * s.U);
+    return s;
+  }
+  __device__ static void issue(const uint8_t *w, const Src &s, uint32_t sp, uint8_t *slot, uint32_t L) {
+    P::issue(w, s.pl, 0, sp, slot);
+    P::issue(w, s.pl, 16 * s.U, sp, slot + P::BYTES);
+    issue_piece(w, s.hd, sp, slot + 2 * P::BYTES, L);
+  }
+  __device__ static uint32_t wofs(uint32_t n, uint32_t g) { return P::base(n, g) + P::BYTES * (g >> 1); }
+  struct Op {
+    const uint8_t *ws, *xs;
+    uint32_t wo, xo, n, bi;
+    __device__ uint4 hdr() const { return *reinterpret_cast<const uint4 *>(ws + 2 * P::BYTES + 32 * n + 16 * bi); }
+    __device__ uint64_t w(int p) const { return *reinterpret_cast<const uint64_t *>(ws + (wo ^ (16 * (4 * bi + p)))); }
+    __device__ uint64_t xg(int j) const {
+      return *reinterpret_cast<const uint64_t *>(xs + (xo ^ (32 * (8 * bi + j))));
+    }
+  };
+};
+
+// Q6_K: planes A | B | high bits, the scale bytes, then d: the word of
+// lane n (at 4n) holds row n's f16 d of the pair's two blocks.
+struct RQ6 {
+  using B = BQ6;
+  using P = Plane<128>;
+  static constexpr uint32_t WB = 3 * P::BYTES + 512 + 256;
+  static constexpr int NDMA = 3 * P::NDMA + 2;
+  struct Src {
+    uint32_t pl[P::NDMA], sc, d, U;
+  };
+  __device__ static Src src(size_t rb, uint32_t n_in, uint32_t row0, uint32_t n_out, uint32_t L) {
+    Src s;
+    s.U = n_in / 64;
+    P::src<3>(rb, row0, n_out, L, s.pl);
+    s.sc = pair_piece(rb, row0, n_out, L, 48 * s.U);
+    s.d = (uint32_t)(min(row0 + (L & 15), n_out - 1) * rb) + 52 * s.U;
+    return s;
+  }
+  __device__ static void issue(const uint8_t *w, const Src &s, uint32_t sp, uint8_t *slot, uint32_t L) {
+#pragma unroll
+    for (int k = 0; k < 3; k++) P::issue(w, s.pl, 16 * k * s.U, sp, slot + k * P::BYTES);
+    issue_piece(w, s.sc, sp, slot + 3 * P::BYTES, L);
+    lds_dma4(w, s.d + 4 * sp, slot + 3 * P::BYTES + 512);
+  }
+  // The lane's unit half g/2 is bit 0 of its chunks: folded into the base.
+  __device__ static uint32_t wofs(uint32_t n, uint32_t g) { return P::base(n, g) ^ (16 * (g >> 1)); }
+  struct Op {
+    const uint8_t *ws, *xs;
+    uint32_t wo, xo, n, bi;
+    __device__ uint4 sc() const { return *reinterpret_cast<const uint4 *>(ws + 3 * P::BYTES + 32 * n + 16 * bi); }
+    __device__ float d() const {
+      return h2f(*reinterpret_cast<const uint32_t *>(ws + 3 * P::BYTES + 512 + 4 * n) >> (16 * bi));
+    }
+    __device__ uint64_t w(int v, int k) const {
+      return *reinterpret_cast<const uint64_t *>(ws + P::BYTES * k + (wo ^ (16 * (4 * bi + 2 * v))));
+    }
+    __device__ uint64_t xg(int j) const {
+      return *reinterpret_cast<const uint64_t *>(xs + (xo ^ (32 * (8 * bi + j))));
+    }
+  };
+};
+
+// Q8_0: planes A | B (a block's eight units are 128 bytes per plane), then
+// the scales.
+struct RQ8 {
+  using B = BQ8;
+  using P = Plane<256>;
+  static constexpr uint32_t WB = 2 * P::BYTES + 512;
+  static constexpr int NDMA = 2 * P::NDMA + 1;
+  struct Src {
+    uint32_t pl[P::NDMA], hd, U;
+  };
+  __device__ static Src src(size_t rb, uint32_t n_in, uint32_t row0, uint32_t n_out, uint32_t L) {
+    Src s;
+    s.U = n_in / 32;
+    P::src<2>(rb, row0, n_out, L, s.pl);
+    s.hd = pair_piece(rb, row0, n_out, L, 32 * s.U);
+    return s;
+  }
+  __device__ static void issue(const uint8_t *w, const Src &s, uint32_t sp, uint8_t *slot, uint32_t L) {
+    P::issue(w, s.pl, 0, sp, slot);
+    P::issue(w, s.pl, 16 * s.U, sp, slot + P::BYTES);
+    issue_piece(w, s.hd, sp, slot + 2 * P::BYTES, L);
+  }
+  __device__ static uint32_t wofs(uint32_t n, uint32_t g) { return P::base(n, g) + P::BYTES * (g >> 1); }
+  struct Op {
+    const uint8_t *ws, *xs;
+    uint32_t wo, xo, n, bi;
+    __device__ uint4 sc() const { return *reinterpret_cast<const uint4 *>(ws + 2 * P::BYTES + 32 * n + 16 * bi); }
+    __device__ uint64_t w(int i) const { return *reinterpret_cast<const uint64_t *>(ws + (wo ^ (16 * (8 * bi + i)))); }
+    __device__ uint64_t xg(int i) const {
+      return *reinterpret_cast<const uint64_t *>(xs + (xo ^ (32 * (8 * bi + i))));
+    }
+  };
+};
+
+template <class R, bool GATED, int XN>
+constexpr uint32_t ring_slot() {
+  return 512 * XN + 256 + (GATED ? 2 : 1) * R::WB;
+}
+constexpr uint32_t RING_LDS_MAX = 160 * 1024;
+template <class R, int TW, bool GATED, int XN>
+constexpr bool ring_fits() {
+  return TW * 2 * ring_slot<R, GATED, XN>() <= RING_LDS_MAX;
+}
+
+// XN: token rows staged per pair (8 for T <= 8, else 16).
+template <class R, int TW, bool GATED, int XN, bool CAP = false>
+__global__ __launch_bounds__(64 * TW) void gemv_ring(BatchSet bs, const int8_t *__restrict__ qx,
+                                                     const float *__restrict__ dx, uint32_t T,
+                                                     float *__restrict__ ygated) {
+  using F = typename R::B;
+  constexpr int NR = GATED ? 2 : 1;
+  constexpr uint32_t XB = 512 * XN, SLOT = ring_slot<R, GATED, XN>();
+  constexpr int PB = XN / 2 + 1 + NR * R::NDMA;  // DMA instructions per pair
+  static_assert(PB <= 63, "wait count beyond vmcnt's range");
+  static_assert(TW == 1 || TW * 2 * SLOT >= NCHMAX * NR * 4 * 64 * sizeof(float), "chunk sums fit the ring");
+  static_assert(TW * 2 * SLOT <= RING_LDS_MAX, "ring beyond the LDS");
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[TW][2][SLOT];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t lane = threadIdx.x & 63;
+  uint32_t tile = blockIdx.x;
+  int ji = 0;
+  if (bs.n > 1 && tile >= bs.j[0].tiles) {
+    tile -= bs.j[0].tiles;
+    ji = 1;
+    if (bs.n > 2 && tile >= bs.j[1].tiles) {
+      tile -= bs.j[1].tiles;
+      ji = 2;
+    }
+  }
+  const BatchJob J = ji == 0 ? bs.j[0] : (ji == 1 ? bs.j[1] : bs.j[2]);
+  const uint32_t n_in = bs.n_in, nb = n_in / 256, n_out = J.n_out;
+  const uint32_t nch = nb < NCHMAX ? nb : NCHMAX;
+  // Lane l: weight row l%16 and token l%16 of the MFMA operands, k-group l/16.
+  const uint32_t n = lane & 15, g = lane >> 4, r_lane = tile * TROWS + n;
+  const size_t rb = F::row_bytes(n_in);
+  const uint8_t *wbase[NR];
+  wbase[0] = J.w;
+  if (GATED) wbase[NR - 1] = bs.j[1].w;
+  // DMA sources (the same rows of gate and up).
+  const typename R::Src src = R::src(rb, n_in, tile * TROWS, n_out, lane);
+  uint32_t xsrc[XN / 2];
+#pragma unroll
+  for (int i = 0; i < XN / 2; i++) {
+    const uint32_t t = 2 * i + (lane >> 5);
+    xsrc[i] = min(t, T - 1) * n_in + 16 * ((lane & 31) ^ t);
+  }
+  const uint32_t ssrc = (min(lane & 15, T - 1) * nb + ((lane >> 4) & 1)) * 4;
+  // Operand reads: x of token n (rows past the slot's tokens read its last).
+  const uint32_t tr = min(n, (uint32_t)XN - 1);
+  const uint32_t xo = 512 * tr + 8 * (g & 1) + 16 * ((g >> 1) ^ tr), wo = R::wofs(n, g);
+  auto issue = [&](int s, uint32_t sp) {
+    uint8_t *sl = ring[wave][s];
+#pragma unroll
+    for (int i = 0; i < XN / 2; i++) lds_dma16(qx, xsrc[i] + 512 * sp, sl + 1024 * i);
+    lds_dma4(dx, ssrc + 8 * sp, sl + XB);
+#pragma unroll
+    for (int r = 0; r < NR; r++) R::issue(wbase[r], src, sp, sl + XB + 256 + r * R::WB, lane);
+  };
+  constexpr int NJ = 4;
+  float acc[NR][NJ], tot[NR][NJ];
+  // Sums of this wave's finished chunks (waves > 0; wave 0 adds its own to
+  // tot as they finish).
+  constexpr int CPW = TW > 1 ? (NCHMAX + TW - 1) / TW : 1;
+  float part[CPW][NR][NJ];
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int j = 0; j < NJ; j++) acc[r][j] = tot[r][j] = 0.f;
+  const uint32_t nsub = n_in / (256 / F::SUBS);
+  int32_t *dcap[NR];
+  dcap[0] = J.dots;
+  if (GATED) dcap[NR - 1] = bs.j[1].dots;
+  const uint32_t c0 = wave * nch / TW, c1 = (wave + 1) * nch / TW;
+  const uint32_t b0 = c0 * nb / nch, b1 = c1 * nb / nch;
+  uint32_t ch = c0, ch_end = (c0 + 1) * nb / nch;
+  auto chunk_done = [&](uint32_t b) {
+    if (b + 1 == ch_end) {
+      if (wave == 0) {
+#pragma unroll
+        for (int r = 0; r < NR; r++)
+#pragma unroll
+          for (int j = 0; j < NJ; j++) tot[r][j] += acc[r][j];
+      } else {
+        const uint32_t k = ch - c0;
+#pragma unroll
+        for (int kk = 0; kk < CPW; kk++)
+          if (k == (uint32_t)kk)
+#pragma unroll
+            for (int r = 0; r < NR; r++)
+#pragma unroll
+              for (int j = 0; j < NJ; j++) part[kk][r][j] = acc[r][j];
+      }
+#pragma unroll
+      for (int r = 0; r < NR; r++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++) acc[r][j] = 0.f;
+      ch++;
+      ch_end = (ch + 1) * nb / nch;
+    }
+  };
+  // Blocks 2sp + bi of the slot that are the wave's, in order.
+  auto use = [&](int s, uint32_t sp) {
+    const uint8_t *sl = ring[wave][s];
+#pragma unroll
+    for (int bi = 0; bi < 2; bi++) {
+      const uint32_t bb = 2 * sp + bi;
+      if (bb < b0 || bb >= b1) continue;
+      const float4 sv = *reinterpret_cast<const float4 *>(sl + XB + 64 * bi + 16 * g);
+      const float sj[NJ] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+      for (int r = 0; r < NR; r++) {
+        float c[NJ];
+        Dots dc{nullptr, (size_t)n_out * nsub, T};
+        if constexpr (CAP) {
+          if (r_lane < n_out) dc.p = dcap[r] + (size_t)r_lane * nsub + F::SUBS * bb;
+        }
+        F::compute(typename R::Op{sl + XB + 256 + r * R::WB, sl, wo, xo, n, (uint32_t)bi}, c, dc, g);
+#pragma unroll
+        for (int j = 0; j < NJ; j++) acc[r][j] = fmaf(sj[j], c[j], acc[r][j]);
+      }
+      chunk_done(bb);
+    }
+  };
+  // The pairs holding the wave's blocks; a pair past its last is loaded as
+  // its last again (in bounds; every pair issues the same DMAs, so the wait
+  // count is fixed).
+  const uint32_t s0 = b0 >> 1, s1 = (b1 + 1) >> 1;
+  issue(0, s0);
+  for (uint32_t sp = s0; sp < s1; sp += 2) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const uint32_t cur = sp + i;
+      if (cur >= s1) break;
+      // The slot refilled now was read by the previous pair: its reads are
+      // complete before the DMAs overwrite it.
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      issue(i ^ 1, min(cur + 1, s1 - 1));
+      // Pair cur's DMAs done: only the pair issued after it remains.
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PB) : "memory");
+      use(i, cur);
+    }
+  }
+  lds_wait_dma();  // the repeated last pair lands before the ring is reused
+  if constexpr (TW > 1) {
+    // Chunk sums of waves > 0 through the (now idle) ring, added by wave 0
+    // in chunk order.
+    float *red = reinterpret_cast<float *>(&ring[0][0][0]);  // [chunk][r][j][lane]
+    __syncthreads();
+    if (wave > 0) {
+#pragma unroll
+      for (int kk = 0; kk < CPW; kk++)
+        if (c0 + kk < c1)
+#pragma unroll
+          for (int r = 0; r < NR; r++)
+#pragma unroll
+            for (int j = 0; j < NJ; j++) red[(((c0 + kk) * NR + r) * NJ + j) * 64 + lane] = part[kk][r][j];
+    }
+    __syncthreads();
+    if (wave > 0) return;
+    for (uint32_t k = c1; k < nch; k++)
+#pragma unroll
+      for (int r = 0; r < NR; r++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++) tot[r][j] += red[((k * NR + r) * NJ + j) * 64 + lane];
+  }
+  if (r_lane >= n_out) return;
+  const uint32_t t0 = 4 * g;
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    if (t0 + j >= T) continue;
+    if (GATED) {
+      const float gv = tot[0][j], uv = tot[NR - 1][j];
+      ygated[(size_t)(t0 + j) * n_out + r_lane] = gv / (1.0f + expf(-gv)) * uv;
+    } else {
+      J.y[(size_t)(t0 + j) * n_out + r_lane] = tot[0][j];
+    }
+  }
+}
+
+template <class R, bool GATED, int XN>
+uint32_t ring_tw(mdma_ctx *ctx, uint32_t tiles, uint32_t nch) {
+  // Waves per tile: up to 4 (at most one per chunk) while the launch keeps
+  // to about one wave per SIMD (4 per CU): more waves splitting the same
+  // tiles measured slower (896 tiles: one wave each 19.1 us, two 21.0 us;
+  // 256 tiles of 56 blocks: four waves each 18.1 us, one 40.7 us).
+  constexpr uint32_t per_wave = 2 * ring_slot<R, GATED, XN>();
+  uint32_t tw = 1;
+  while (tw < 4 && 2 * tw <= nch && (uint64_t)tiles * 2 * tw <= (uint64_t)ctx->cu_count * 4 &&
+         2 * tw * per_wave <= RING_LDS_MAX)
+    tw *= 2;
+  return tw;
+}
+
+template <class R, int TW, bool GATED, int XN>
+void ring_launch(mdma_ctx *ctx, const BatchSet &bs, uint32_t tiles, const int8_t *qx, const float *dx, uint32_t T,
+                 float *yg) {
+  hipEvent_t t0 = ctx->time_start, t1 = ctx->time_stop;
+  ctx->time_start = ctx->time_stop = nullptr;
+  const dim3 grid(tiles), block(64 * TW);
+  if (bs.j[0].dots) {
+    // ring_fmt sized TW for the 16 token rows the capture stages.
+    if constexpr (ring_fits<R, TW, GATED, 16>())
+      gemv_ring<R, TW, GATED, 16, true><<<grid, block, 0, ctx->stream>>>(bs, qx, dx, T, yg);
+  } else if (t0 || t1) {
+    hipExtLaunchKernelGGL(gemv_ring<R, TW, GATED, XN>, grid, block, 0, ctx->stream, t0, t1, 0, bs, qx, dx, T, yg);
+  } else {
+    gemv_ring<R, TW, GATED, XN><<<grid, block, 0, ctx->stream>>>(bs, qx, dx, T, yg);
+  }
+  hip_check(hipGetLastError(), "gemv ring launch");
+}
+
+template <class R, bool GATED, int XN>
+void ring_fmt(mdma_ctx *ctx, const BatchSet &bs, uint32_t tiles, const int8_t *qx, const float *dx, uint32_t T,
+              float *yg) {
+  const uint32_t nb = bs.n_in / 256, nch = nb < NCHMAX ? nb : NCHMAX;
+  // The capture instantiation stages 16 token rows (any T): size its TW for that.
+  const uint32_t tw = bs.j[0].dots ? ring_tw<R, GATED, 16>(ctx, tiles, nch) : ring_tw<R, GATED, XN>(ctx, tiles, nch);
+  // (ring_tw only picks a TW whose ring fits; the guards keep the
+  // instantiations that would not out of the build.)
+  if (tw == 4) {
+    if constexpr (ring_fits<R, 4, GATED, XN>()) return ring_launch<R, 4, GATED, XN>(ctx, bs, tiles, qx, dx, T, yg);
+  } else if (tw == 2) {
+    if constexpr (ring_fits<R, 2, GATED, XN>()) return ring_launch<R, 2, GATED, XN>(ctx, bs, tiles, qx, dx, T, yg);
+  }
+  ring_launch<R, 1, GATED, XN>(ctx, bs, tiles, qx, dx, T, yg);
+}
+
+template <class R>
+void ring_dispatch(mdma_ctx *ctx, const BatchSet &bs, uint32_t tiles, bool gated, const int8_t *qx, const float *dx,
+                   uint32_t T, float *yg) {
+  if (gated) {
+    if (T <= 8) ring_fmt<R, true, 8>(ctx, bs, tiles, qx, dx, T, yg);
+    else ring_fmt<R, true, 16>(ctx, bs, tiles, qx, dx, T, yg);
+  } else {
+    if (T <= 8) ring_fmt<R, false, 8>(ctx, bs, tiles, qx, dx, T, yg);
+    else ring_fmt<R, false, 16>(ctx, bs, tiles, qx, dx, T, yg);
+  }
+}
+
 }  // namespace
+
+// Prepared-layout row bytes (the formats' row_bytes, on the host).
+static uint64_t batch_row_bytes(int32_t dt, uint64_t n_in) {
+  if (dt == DT_Q4_K) return n_in / 256 * 144;
+  if (dt == DT_Q6_K) return (n_in / 256 * 210 + 15) / 16 * 16;
+  return (n_in / 32 * 34 + 15) / 16 * 16;
+}
 
 bool gemv_batch_ok(const GemvJob *jobs, int n_jobs, uint64_t T) {
   if (T < 2 || T > 16 || n_jobs < 1 || n_jobs > 3) return false;
@@ -561,6 +1025,17 @@ void launch_gemv_batch(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, bool gate
   if (!tiles) return;
   const uint32_t t = (uint32_t)T;
   const int32_t dt = jobs[0].dtype;
+  // The ring kernel addresses a weight with 32-bit offsets.
+  // (and pairs of 256-column blocks).
+  bool ring = ctx->batch_kernel == MDMA_BATCH_AUTO && (n_in / 256) % 2 == 0;
+  for (int i = 0; i < (gated ? 2 : n_jobs); i++)
+    ring = ring && jobs[i].n_out * batch_row_bytes(dt, n_in) < (1ull << 32);
+  if (ring) {
+    if (dt == DT_Q4_K) ring_dispatch<RQ4>(ctx, bs, tiles, gated, qx, dx, t, ygated);
+    else if (dt == DT_Q6_K) ring_dispatch<RQ6>(ctx, bs, tiles, gated, qx, dx, t, ygated);
+    else ring_dispatch<RQ8>(ctx, bs, tiles, gated, qx, dx, t, ygated);
+    return;
+  }
   if (dt == DT_Q4_K) launch_fmt<BQ4>(ctx, bs, tiles, gated, qx, dx, t, ygated);
   else if (dt == DT_Q6_K) launch_fmt<BQ6>(ctx, bs, tiles, gated, qx, dx, t, ygated);
   else launch_fmt<BQ8>(ctx, bs, tiles, gated, qx, dx, t, ygated);

@@ -96,6 +96,7 @@ struct mdma_ctx {
   uint64_t host_ids_cap = 0;
   bool capturing = false;        // stream capture in progress: no synchronizing calls
   int prefill_kernel = MDMA_PREFILL_AUTO;  // mdma_gfx950_set_prefill_kernel
+  int batch_kernel = MDMA_BATCH_AUTO;      // mdma_gfx950_set_batch_kernel
   bool graph_decode = true;                // mdma_gfx950_set_graph_decode
   // Block-dot capture (mdma_gfx950_capture_block_dots): int32 slots or null.
   int32_t *dots = nullptr;

@@ -27,6 +27,26 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Global memory straight into LDS (global_load_lds): each lane of the wave
+// moves 16 (or 4) bytes from base + off to LDS address lds + 16 (4) * lane.
+// Issued as inline assembly so that the compiler does not track it: its own
+// LDS-DMA tracking cannot tell runtime-indexed LDS buffers apart and would
+// wait for these loads before every LDS read of the other buffer. The
+// kernel waits for them itself (lds_wait_dma) before reading what they
+// wrote or publishing it at a barrier.
+__device__ __forceinline__ uint32_t lds_addr(const void *lds) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);  // the LDS offset: low bits of the address
+}
+__device__ __forceinline__ void lds_dma16(const void *base, uint32_t off, const void *lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds_addr(lds))
+               : "memory");
+}
+__device__ __forceinline__ void lds_dma4(const void *base, uint32_t off, const void *lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds_addr(lds))
+               : "memory");
+}
+__device__ __forceinline__ void lds_wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 __device__ __forceinline__ float h2f(uint32_t bits16) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits16 & 0xffff));
 }

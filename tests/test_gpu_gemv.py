@@ -217,6 +217,56 @@ def test_i8_mode_batched_llama3_8b_shapes(backend, dtype, shape, T):
     assert_parity(one[0], cpu[T - 1], exact[T - 1], 1e-3, atol=1e-5, what="single token")
 
 
+@pytest.mark.parametrize("dtype", [Q4K, Q6K, Q8])
+def test_batch_ring_equals_staged(backend, dtype):
+    """The DMA-ring batch kernel (the default) and the register-staged one
+    form the same int32 products and f32 sums in the same order, so their
+    outputs are equal bit for bit: token counts 5..15 (8 and 16 staged
+    token rows), ragged tiles (rows not a multiple of 16), 2 to 56 column
+    blocks (one to eight chunks, one to four waves per tile, chunks that
+    start inside a pair of blocks), the gated gate/up and the fused
+    three-weight call. The oracle side of this kernel is
+    test_i8_mode_batched and test_i8_mode_batched_llama3_8b_shapes."""
+    def both(fn):
+        out = []
+        for kind in (backend_mod.BATCH_AUTO, backend_mod.BATCH_STAGED):
+            backend.set_batch_kernel(kind)
+            out.append(fn())
+        backend.set_batch_kernel(backend_mod.BATCH_AUTO)
+        return out
+
+    backend.set_act_mode(backend_mod.ACT_I8)
+    try:
+        # (40, 768): an odd number of 256-column blocks, which the ring kernel
+        # (pairs of blocks) leaves to the staged one.
+        for rows, k in ((29, 1024), (80, 4096), (48, 14336), (40000, 512), (40, 768)):
+            raw = synth.weight(dtype, rows, k, 60 + rows)
+            for T in (5, 8, 9, 15):
+                x = synth.normal_f32(T * k, 61 + T)
+                a, b = both(lambda: run_qmatmul(backend, dtype, raw, rows, k, x, "i8"))
+                assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (rows, k, T)
+        rows, k, T = 96, 4096, 7
+        raws = [synth.weight(dtype, rows, k, 70 + i) for i in range(3)]
+        ws = [backend.upload_weight(r, dtype, (rows, k)) for r in raws]
+        xb = backend.f32_buf(synth.normal_f32(T * k, 71))
+
+        def gate_up():
+            g, u, y = (backend.alloc(T * rows * 4) for _ in range(3))
+            backend.ffn_gate_up(ws[0], ws[1], xb, g, u, y)
+            return backend.download_f32(y).copy()
+
+        def qkv():
+            outs = [backend.alloc(T * rows * 4) for _ in range(3)]
+            backend.qmatmul_qkv(ws[0], ws[1], ws[2], xb, *outs)
+            return np.concatenate([backend.download_f32(o) for o in outs])
+
+        for fn in (gate_up, qkv):
+            a, b = both(fn)
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), fn.__name__
+    finally:
+        backend.set_act_mode(backend_mod.ACT_F32)
+
+
 @pytest.mark.parametrize("group", [32, 256])
 def test_quantize_act_bit_exact(backend, group):
     x = synth.normal_f32(8 * 1024, 77) * 3
