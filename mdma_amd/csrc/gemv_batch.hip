@@ -652,15 +652,24 @@ struct RQ4 {
     issue_piece(w, s.hd, sp, slot + 2 * P::BYTES, L);
   }
   __device__ static uint32_t wofs(uint32_t n, uint32_t g) { return P::base(n, g) + P::BYTES * (g >> 1); }
+  // Block bi's operands of lane (row n, base wo), read from the slot
+  // ahead of its products; x: the lane's eight activation groups.
   struct Op {
-    const uint8_t *ws, *xs;
-    uint32_t wo, xo, n, bi;
-    __device__ uint4 hdr() const { return *reinterpret_cast<const uint4 *>(ws + 2 * P::BYTES + 32 * n + 16 * bi); }
-    __device__ uint64_t w(int p) const { return *reinterpret_cast<const uint64_t *>(ws + (wo ^ (16 * (4 * bi + p)))); }
-    __device__ uint64_t xg(int j) const {
-      return *reinterpret_cast<const uint64_t *>(xs + (xo ^ (32 * (8 * bi + j))));
-    }
+    uint4 h;
+    uint64_t q[4];
+    const uint64_t *x;
+    __device__ uint4 hdr() const { return h; }
+    __device__ uint64_t w(int p) const { return q[p]; }
+    __device__ uint64_t xg(int j) const { return x[j]; }
   };
+  __device__ static Op load(const uint8_t *ws, const uint64_t *x, uint32_t wo, uint32_t n, uint32_t bi) {
+    Op o;
+    o.h = *reinterpret_cast<const uint4 *>(ws + 2 * P::BYTES + 32 * n + 16 * bi);
+#pragma unroll
+    for (int p = 0; p < 4; p++) o.q[p] = *reinterpret_cast<const uint64_t *>(ws + (wo ^ (16 * (4 * bi + p))));
+    o.x = x;
+    return o;
+  }
 };
 
 // Q6_K: planes A | B | high bits, the scale bytes, then d: the word of
@@ -690,19 +699,28 @@ struct RQ6 {
   // The lane's unit half g/2 is bit 0 of its chunks: folded into the base.
   __device__ static uint32_t wofs(uint32_t n, uint32_t g) { return P::base(n, g) ^ (16 * (g >> 1)); }
   struct Op {
-    const uint8_t *ws, *xs;
-    uint32_t wo, xo, n, bi;
-    __device__ uint4 sc() const { return *reinterpret_cast<const uint4 *>(ws + 3 * P::BYTES + 32 * n + 16 * bi); }
-    __device__ float d() const {
-      return h2f(*reinterpret_cast<const uint32_t *>(ws + 3 * P::BYTES + 512 + 4 * n) >> (16 * bi));
-    }
-    __device__ uint64_t w(int v, int k) const {
-      return *reinterpret_cast<const uint64_t *>(ws + P::BYTES * k + (wo ^ (16 * (4 * bi + 2 * v))));
-    }
-    __device__ uint64_t xg(int j) const {
-      return *reinterpret_cast<const uint64_t *>(xs + (xo ^ (32 * (8 * bi + j))));
-    }
+    uint4 s;
+    uint32_t dw, dsh;
+    uint64_t q[2][3];
+    const uint64_t *x;
+    __device__ uint4 sc() const { return s; }
+    __device__ float d() const { return h2f(dw >> dsh); }
+    __device__ uint64_t w(int v, int k) const { return q[v][k]; }
+    __device__ uint64_t xg(int j) const { return x[j]; }
   };
+  __device__ static Op load(const uint8_t *ws, const uint64_t *x, uint32_t wo, uint32_t n, uint32_t bi) {
+    Op o;
+    o.s = *reinterpret_cast<const uint4 *>(ws + 3 * P::BYTES + 32 * n + 16 * bi);
+    o.dw = *reinterpret_cast<const uint32_t *>(ws + 3 * P::BYTES + 512 + 4 * n);
+    o.dsh = 16 * bi;
+#pragma unroll
+    for (int v = 0; v < 2; v++)
+#pragma unroll
+      for (int k = 0; k < 3; k++)
+        o.q[v][k] = *reinterpret_cast<const uint64_t *>(ws + P::BYTES * k + (wo ^ (16 * (4 * bi + 2 * v))));
+    o.x = x;
+    return o;
+  }
 };
 
 // Q8_0: planes A | B (a block's eight units are 128 bytes per plane), then
@@ -729,42 +747,59 @@ struct RQ8 {
   }
   __device__ static uint32_t wofs(uint32_t n, uint32_t g) { return P::base(n, g) + P::BYTES * (g >> 1); }
   struct Op {
-    const uint8_t *ws, *xs;
-    uint32_t wo, xo, n, bi;
-    __device__ uint4 sc() const { return *reinterpret_cast<const uint4 *>(ws + 2 * P::BYTES + 32 * n + 16 * bi); }
-    __device__ uint64_t w(int i) const { return *reinterpret_cast<const uint64_t *>(ws + (wo ^ (16 * (8 * bi + i)))); }
-    __device__ uint64_t xg(int i) const {
-      return *reinterpret_cast<const uint64_t *>(xs + (xo ^ (32 * (8 * bi + i))));
-    }
+    uint4 s;
+    uint64_t q[8];
+    const uint64_t *x;
+    __device__ uint4 sc() const { return s; }
+    __device__ uint64_t w(int i) const { return q[i]; }
+    __device__ uint64_t xg(int i) const { return x[i]; }
   };
+  __device__ static Op load(const uint8_t *ws, const uint64_t *x, uint32_t wo, uint32_t n, uint32_t bi) {
+    Op o;
+    o.s = *reinterpret_cast<const uint4 *>(ws + 2 * P::BYTES + 32 * n + 16 * bi);
+#pragma unroll
+    for (int i = 0; i < 8; i++) o.q[i] = *reinterpret_cast<const uint64_t *>(ws + (wo ^ (16 * (8 * bi + i))));
+    o.x = x;
+    return o;
+  }
 };
 
-template <class R, bool GATED, int XN>
+// Bytes of a slot: per wave (W == 1) or shared by W waves on W tiles.
+template <class R, bool GATED, int XN, int W = 1>
 constexpr uint32_t ring_slot() {
-  return 512 * XN + 256 + (GATED ? 2 : 1) * R::WB;
+  return 512 * XN + 256 + W * (GATED ? 2 : 1) * R::WB;
 }
 constexpr uint32_t RING_LDS_MAX = 160 * 1024;
-template <class R, int TW, bool GATED, int XN>
+template <class R, int TW, int W, bool GATED, int XN>
 constexpr bool ring_fits() {
-  return TW * 2 * ring_slot<R, GATED, XN>() <= RING_LDS_MAX;
+  return TW * 2 * ring_slot<R, GATED, XN, W>() <= RING_LDS_MAX;
 }
 
-// XN: token rows staged per pair (8 for T <= 8, else 16).
-template <class R, int TW, bool GATED, int XN, bool CAP = false>
-__global__ __launch_bounds__(64 * TW) void gemv_ring(BatchSet bs, const int8_t *__restrict__ qx,
-                                                     const float *__restrict__ dx, uint32_t T,
-                                                     float *__restrict__ ygated) {
+// XN: token rows staged per pair (8 for T <= 8, else 16). Either TW waves
+// split one tile's columns (W = 1), or W waves take W consecutive tiles in
+// lockstep (TW = 1), sharing the pair's activations and scales: one staged
+// copy per workgroup instead of one per tile.
+template <class R, int TW, int W, bool GATED, int XN, bool CAP = false>
+__global__ __launch_bounds__(64 * TW * W) void gemv_ring(BatchSet bs, const int8_t *__restrict__ qx,
+                                                         const float *__restrict__ dx, uint32_t T,
+                                                         float *__restrict__ ygated) {
+  static_assert(W == 1 || TW == 1, "waves split a tile's columns or take tiles of their own");
   using F = typename R::B;
   constexpr int NR = GATED ? 2 : 1;
-  constexpr uint32_t XB = 512 * XN, SLOT = ring_slot<R, GATED, XN>();
-  constexpr int PB = XN / 2 + 1 + NR * R::NDMA;  // DMA instructions per pair
+  constexpr uint32_t XB = 512 * XN, WS = NR * R::WB, SLOT = ring_slot<R, GATED, XN, W>();
+  constexpr int PB = XN / 2 + 1 + NR * R::NDMA;  // DMA instructions per pair (W == 1)
   static_assert(PB <= 63, "wait count beyond vmcnt's range");
   static_assert(TW == 1 || TW * 2 * SLOT >= NCHMAX * NR * 4 * 64 * sizeof(float), "chunk sums fit the ring");
   static_assert(TW * 2 * SLOT <= RING_LDS_MAX, "ring beyond the LDS");
   __shared__ __attribute__((aligned(1024))) uint8_t ring[TW][2][SLOT];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63;
-  uint32_t tile = blockIdx.x;
+  // W > 1: the last workgroup's waves past the last tile take part in the
+  // barriers on the last tile's bytes and store nothing.
+  const uint32_t all_tiles = bs.j[0].tiles + (bs.n > 1 ? bs.j[1].tiles : 0) + (bs.n > 2 ? bs.j[2].tiles : 0);
+  const uint32_t tile_w = W == 1 ? blockIdx.x : blockIdx.x * W + wave;
+  const bool live = tile_w < all_tiles;
+  uint32_t tile = live ? tile_w : all_tiles - 1;
   int ji = 0;
   if (bs.n > 1 && tile >= bs.j[0].tiles) {
     tile -= bs.j[0].tiles;
@@ -785,23 +820,28 @@ __global__ __launch_bounds__(64 * TW) void gemv_ring(BatchSet bs, const int8_t *
   if (GATED) wbase[NR - 1] = bs.j[1].w;
   // DMA sources (the same rows of gate and up).
   const typename R::Src src = R::src(rb, n_in, tile * TROWS, n_out, lane);
-  uint32_t xsrc[XN / 2];
+  // The activation DMAs this wave issues (W > 1: its share of them).
+  constexpr int XD = XN / 2 / W;
+  const int xd0 = W == 1 ? 0 : wave * XD;
+  uint32_t xsrc[XD];
 #pragma unroll
-  for (int i = 0; i < XN / 2; i++) {
-    const uint32_t t = 2 * i + (lane >> 5);
+  for (int i = 0; i < XD; i++) {
+    const uint32_t t = 2 * (xd0 + i) + (lane >> 5);
     xsrc[i] = min(t, T - 1) * n_in + 16 * ((lane & 31) ^ t);
   }
   const uint32_t ssrc = (min(lane & 15, T - 1) * nb + ((lane >> 4) & 1)) * 4;
   // Operand reads: x of token n (rows past the slot's tokens read its last).
   const uint32_t tr = min(n, (uint32_t)XN - 1);
   const uint32_t xo = 512 * tr + 8 * (g & 1) + 16 * ((g >> 1) ^ tr), wo = R::wofs(n, g);
+  const int rw = W == 1 ? wave : 0;                    // the wave's ring
+  const uint32_t wofs_w = XB + 256 + (W == 1 ? 0 : wave * WS);  // its weights in a slot
   auto issue = [&](int s, uint32_t sp) {
-    uint8_t *sl = ring[wave][s];
+    uint8_t *sl = ring[rw][s];
 #pragma unroll
-    for (int i = 0; i < XN / 2; i++) lds_dma16(qx, xsrc[i] + 512 * sp, sl + 1024 * i);
-    lds_dma4(dx, ssrc + 8 * sp, sl + XB);
+    for (int i = 0; i < XD; i++) lds_dma16(qx, xsrc[i] + 512 * sp, sl + 1024 * (xd0 + i));
+    if (W == 1 || wave == 0) lds_dma4(dx, ssrc + 8 * sp, sl + XB);
 #pragma unroll
-    for (int r = 0; r < NR; r++) R::issue(wbase[r], src, sp, sl + XB + 256 + r * R::WB, lane);
+    for (int r = 0; r < NR; r++) R::issue(wbase[r], src, sp, sl + wofs_w + r * R::WB, lane);
   };
   constexpr int NJ = 4;
   float acc[NR][NJ], tot[NR][NJ];
@@ -817,12 +857,13 @@ __global__ __launch_bounds__(64 * TW) void gemv_ring(BatchSet bs, const int8_t *
   int32_t *dcap[NR];
   dcap[0] = J.dots;
   if (GATED) dcap[NR - 1] = bs.j[1].dots;
-  const uint32_t c0 = wave * nch / TW, c1 = (wave + 1) * nch / TW;
+  const int ks = W == 1 ? wave : 0;  // the wave's share of the columns
+  const uint32_t c0 = ks * nch / TW, c1 = (ks + 1) * nch / TW;
   const uint32_t b0 = c0 * nb / nch, b1 = c1 * nb / nch;
   uint32_t ch = c0, ch_end = (c0 + 1) * nb / nch;
   auto chunk_done = [&](uint32_t b) {
     if (b + 1 == ch_end) {
-      if (wave == 0) {
+      if (ks == 0) {
 #pragma unroll
         for (int r = 0; r < NR; r++)
 #pragma unroll
@@ -845,49 +886,79 @@ __global__ __launch_bounds__(64 * TW) void gemv_ring(BatchSet bs, const int8_t *
       ch_end = (ch + 1) * nb / nch;
     }
   };
-  // Blocks 2sp + bi of the slot that are the wave's, in order.
+  // Blocks 2sp + bi of the slot that are the wave's, in order. Every
+  // operand of the pair is read first (both blocks, every weight), so the
+  // reads overlap instead of each block waiting for its own.
   auto use = [&](int s, uint32_t sp) {
-    const uint8_t *sl = ring[wave][s];
+    const uint8_t *sl = ring[rw][s];
+    uint64_t xv[2][8];
+    float4 sv[2];
+    typename R::Op op[2][NR];
+#pragma unroll
+    for (int bi = 0; bi < 2; bi++) {
+      sv[bi] = *reinterpret_cast<const float4 *>(sl + XB + 64 * bi + 16 * g);
+#pragma unroll
+      for (int j = 0; j < 8; j++) xv[bi][j] = *reinterpret_cast<const uint64_t *>(sl + (xo ^ (32 * (8 * bi + j))));
+#pragma unroll
+      for (int r = 0; r < NR; r++) op[bi][r] = R::load(sl + wofs_w + r * R::WB, xv[bi], wo, n, bi);
+    }
 #pragma unroll
     for (int bi = 0; bi < 2; bi++) {
       const uint32_t bb = 2 * sp + bi;
       if (bb < b0 || bb >= b1) continue;
-      const float4 sv = *reinterpret_cast<const float4 *>(sl + XB + 64 * bi + 16 * g);
-      const float sj[NJ] = {sv.x, sv.y, sv.z, sv.w};
+      const float sj[NJ] = {sv[bi].x, sv[bi].y, sv[bi].z, sv[bi].w};
 #pragma unroll
       for (int r = 0; r < NR; r++) {
         float c[NJ];
         Dots dc{nullptr, (size_t)n_out * nsub, T};
         if constexpr (CAP) {
-          if (r_lane < n_out) dc.p = dcap[r] + (size_t)r_lane * nsub + F::SUBS * bb;
+          if (live && r_lane < n_out) dc.p = dcap[r] + (size_t)r_lane * nsub + F::SUBS * bb;
         }
-        F::compute(typename R::Op{sl + XB + 256 + r * R::WB, sl, wo, xo, n, (uint32_t)bi}, c, dc, g);
+        F::compute(op[bi][r], c, dc, g);
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[r][j] = fmaf(sj[j], c[j], acc[r][j]);
       }
       chunk_done(bb);
     }
   };
-  // The pairs holding the wave's blocks; a pair past its last is loaded as
-  // its last again (in bounds; every pair issues the same DMAs, so the wait
-  // count is fixed).
   const uint32_t s0 = b0 >> 1, s1 = (b1 + 1) >> 1;
   issue(0, s0);
-  for (uint32_t sp = s0; sp < s1; sp += 2) {
+  if constexpr (W == 1) {
+    // The pairs holding the wave's blocks; a pair past its last is loaded
+    // as its last again (in bounds; every pair issues the same DMAs, so the
+    // wait count is fixed).
+    for (uint32_t sp = s0; sp < s1; sp += 2) {
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const uint32_t cur = sp + i;
-      if (cur >= s1) break;
-      // The slot refilled now was read by the previous pair: its reads are
-      // complete before the DMAs overwrite it.
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      issue(i ^ 1, min(cur + 1, s1 - 1));
-      // Pair cur's DMAs done: only the pair issued after it remains.
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PB) : "memory");
-      use(i, cur);
+      for (int i = 0; i < 2; i++) {
+        const uint32_t cur = sp + i;
+        if (cur >= s1) break;
+        // The slot refilled now was read by the previous pair: its reads
+        // are complete before the DMAs overwrite it.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        issue(i ^ 1, min(cur + 1, s1 - 1));
+        // Pair cur's DMAs done: only the pair issued after it remains.
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PB) : "memory");
+        use(i, cur);
+      }
+    }
+    lds_wait_dma();  // the repeated last pair lands before the ring is reused
+  } else {
+    // Lockstep over every pair (all waves run the same count): each waits
+    // for its own DMAs of pair cur, the barrier publishes them all and
+    // retires every read of the other slot, then the next pair is issued
+    // into it and pair cur computed.
+    for (uint32_t sp = s0; sp < s1; sp += 2) {
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        const uint32_t cur = sp + i;
+        if (cur >= s1) break;
+        lds_wait_dma();
+        lds_barrier();
+        if (cur + 1 < s1) issue(i ^ 1, cur + 1);
+        use(i, cur);
+      }
     }
   }
-  lds_wait_dma();  // the repeated last pair lands before the ring is reused
   if constexpr (TW > 1) {
     // Chunk sums of waves > 0 through the (now idle) ring, added by wave 0
     // in chunk order.
@@ -910,7 +981,7 @@ __global__ __launch_bounds__(64 * TW) void gemv_ring(BatchSet bs, const int8_t *
 #pragma unroll
         for (int j = 0; j < NJ; j++) tot[r][j] += red[((k * NR + r) * NJ + j) * 64 + lane];
   }
-  if (r_lane >= n_out) return;
+  if (!live || r_lane >= n_out) return;
   const uint32_t t0 = 4 * g;
 #pragma unroll
   for (int j = 0; j < NJ; j++) {
@@ -924,34 +995,43 @@ __global__ __launch_bounds__(64 * TW) void gemv_ring(BatchSet bs, const int8_t *
   }
 }
 
+struct RingShape {
+  uint32_t tw, w;
+};
 template <class R, bool GATED, int XN>
-uint32_t ring_tw(mdma_ctx *ctx, uint32_t tiles, uint32_t nch) {
-  // Waves per tile: up to 4 (at most one per chunk) while the launch keeps
-  // to about one wave per SIMD (4 per CU): more waves splitting the same
-  // tiles measured slower (896 tiles: one wave each 19.1 us, two 21.0 us;
-  // 256 tiles of 56 blocks: four waves each 18.1 us, one 40.7 us).
-  constexpr uint32_t per_wave = 2 * ring_slot<R, GATED, XN>();
+RingShape ring_shape(mdma_ctx *ctx, uint32_t tiles, uint32_t nch) {
+  // Many tiles (at least 1.5 workgroups per CU of 4): 4 tiles per
+  // workgroup share the activations (the 128256-row head: 101.7 us against
+  // 113.7 us with a tile per workgroup; 896 tiles two per workgroup measured
+  // slower than one, 24.4 us against 18.5 us: the lockstep costs more than
+  // the activations it saves there). Otherwise waves per tile: up to 4 (at
+  // most one per chunk) while the launch keeps to about one wave per SIMD
+  // (4 per CU): more waves splitting the same tiles measured slower (896
+  // tiles: one wave each 19.1 us, two 21.0 us; 256 tiles of 56 blocks: four
+  // waves each 18.1 us, one 40.7 us).
+  const uint64_t cus = ctx->cu_count;
+  if (ring_fits<R, 1, 4, GATED, XN>() && (uint64_t)tiles * 2 >= 4 * 3 * cus) return {1, 4};
   uint32_t tw = 1;
-  while (tw < 4 && 2 * tw <= nch && (uint64_t)tiles * 2 * tw <= (uint64_t)ctx->cu_count * 4 &&
-         2 * tw * per_wave <= RING_LDS_MAX)
+  while (tw < 4 && 2 * tw <= nch && (uint64_t)tiles * 2 * tw <= cus * 4 &&
+         2 * tw * 2 * ring_slot<R, GATED, XN>() <= RING_LDS_MAX)
     tw *= 2;
-  return tw;
+  return {tw, 1};
 }
 
-template <class R, int TW, bool GATED, int XN>
+template <class R, int TW, int W, bool GATED, int XN>
 void ring_launch(mdma_ctx *ctx, const BatchSet &bs, uint32_t tiles, const int8_t *qx, const float *dx, uint32_t T,
                  float *yg) {
   hipEvent_t t0 = ctx->time_start, t1 = ctx->time_stop;
   ctx->time_start = ctx->time_stop = nullptr;
-  const dim3 grid(tiles), block(64 * TW);
+  const dim3 grid((tiles + W - 1) / W), block(64 * TW * W);
   if (bs.j[0].dots) {
-    // ring_fmt sized TW for the 16 token rows the capture stages.
-    if constexpr (ring_fits<R, TW, GATED, 16>())
-      gemv_ring<R, TW, GATED, 16, true><<<grid, block, 0, ctx->stream>>>(bs, qx, dx, T, yg);
+    // ring_fmt sized the shape for the 16 token rows the capture stages.
+    if constexpr (ring_fits<R, TW, W, GATED, 16>())
+      gemv_ring<R, TW, W, GATED, 16, true><<<grid, block, 0, ctx->stream>>>(bs, qx, dx, T, yg);
   } else if (t0 || t1) {
-    hipExtLaunchKernelGGL(gemv_ring<R, TW, GATED, XN>, grid, block, 0, ctx->stream, t0, t1, 0, bs, qx, dx, T, yg);
+    hipExtLaunchKernelGGL(gemv_ring<R, TW, W, GATED, XN>, grid, block, 0, ctx->stream, t0, t1, 0, bs, qx, dx, T, yg);
   } else {
-    gemv_ring<R, TW, GATED, XN><<<grid, block, 0, ctx->stream>>>(bs, qx, dx, T, yg);
+    gemv_ring<R, TW, W, GATED, XN><<<grid, block, 0, ctx->stream>>>(bs, qx, dx, T, yg);
   }
   hip_check(hipGetLastError(), "gemv ring launch");
 }
@@ -960,16 +1040,18 @@ template <class R, bool GATED, int XN>
 void ring_fmt(mdma_ctx *ctx, const BatchSet &bs, uint32_t tiles, const int8_t *qx, const float *dx, uint32_t T,
               float *yg) {
   const uint32_t nb = bs.n_in / 256, nch = nb < NCHMAX ? nb : NCHMAX;
-  // The capture instantiation stages 16 token rows (any T): size its TW for that.
-  const uint32_t tw = bs.j[0].dots ? ring_tw<R, GATED, 16>(ctx, tiles, nch) : ring_tw<R, GATED, XN>(ctx, tiles, nch);
-  // (ring_tw only picks a TW whose ring fits; the guards keep the
+  // The capture instantiation stages 16 token rows (any T): shape it for that.
+  const RingShape sh = bs.j[0].dots ? ring_shape<R, GATED, 16>(ctx, tiles, nch) : ring_shape<R, GATED, XN>(ctx, tiles, nch);
+  // (ring_shape only picks shapes whose ring fits; the guards keep the
   // instantiations that would not out of the build.)
-  if (tw == 4) {
-    if constexpr (ring_fits<R, 4, GATED, XN>()) return ring_launch<R, 4, GATED, XN>(ctx, bs, tiles, qx, dx, T, yg);
-  } else if (tw == 2) {
-    if constexpr (ring_fits<R, 2, GATED, XN>()) return ring_launch<R, 2, GATED, XN>(ctx, bs, tiles, qx, dx, T, yg);
+  if (sh.w == 4) {
+    if constexpr (ring_fits<R, 1, 4, GATED, XN>()) return ring_launch<R, 1, 4, GATED, XN>(ctx, bs, tiles, qx, dx, T, yg);
+  } else if (sh.tw == 4) {
+    if constexpr (ring_fits<R, 4, 1, GATED, XN>()) return ring_launch<R, 4, 1, GATED, XN>(ctx, bs, tiles, qx, dx, T, yg);
+  } else if (sh.tw == 2) {
+    if constexpr (ring_fits<R, 2, 1, GATED, XN>()) return ring_launch<R, 2, 1, GATED, XN>(ctx, bs, tiles, qx, dx, T, yg);
   }
-  ring_launch<R, 1, GATED, XN>(ctx, bs, tiles, qx, dx, T, yg);
+  ring_launch<R, 1, 1, GATED, XN>(ctx, bs, tiles, qx, dx, T, yg);
 }
 
 template <class R>

@@ -223,9 +223,10 @@ def test_batch_ring_equals_staged(backend, dtype):
     form the same int32 products and f32 sums in the same order, so their
     outputs are equal bit for bit: token counts 5..15 (8 and 16 staged
     token rows), ragged tiles (rows not a multiple of 16), 2 to 56 column
-    blocks (one to eight chunks, one to four waves per tile, chunks that
-    start inside a pair of blocks), the gated gate/up and the fused
-    three-weight call. The oracle side of this kernel is
+    blocks (one to eight chunks, one to four waves splitting a tile, chunks
+    that start inside a pair of blocks), workgroups of 4 tiles sharing the
+    activations (with waves past the last tile, and tiles of two weights in
+    one workgroup), the gated gate/up and the fused three-weight call. The oracle side of this kernel is
     test_i8_mode_batched and test_i8_mode_batched_llama3_8b_shapes."""
     def both(fn):
         out = []
@@ -235,34 +236,44 @@ def test_batch_ring_equals_staged(backend, dtype):
         backend.set_batch_kernel(backend_mod.BATCH_AUTO)
         return out
 
+    def same(a, b, what):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), what
+
     backend.set_act_mode(backend_mod.ACT_I8)
     try:
         # (40, 768): an odd number of 256-column blocks, which the ring kernel
-        # (pairs of blocks) leaves to the staged one.
-        for rows, k in ((29, 1024), (80, 4096), (48, 14336), (40000, 512), (40, 768)):
+        # (pairs of blocks) leaves to the staged one. (40008, 512): 2501
+        # tiles, four per workgroup.
+        for rows, k in ((29, 1024), (80, 4096), (48, 14336), (40008, 512), (40, 768)):
             raw = synth.weight(dtype, rows, k, 60 + rows)
             for T in (5, 8, 9, 15):
                 x = synth.normal_f32(T * k, 61 + T)
                 a, b = both(lambda: run_qmatmul(backend, dtype, raw, rows, k, x, "i8"))
-                assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (rows, k, T)
-        rows, k, T = 96, 4096, 7
-        raws = [synth.weight(dtype, rows, k, 70 + i) for i in range(3)]
-        ws = [backend.upload_weight(r, dtype, (rows, k)) for r in raws]
-        xb = backend.f32_buf(synth.normal_f32(T * k, 71))
+                same(a, b, (rows, k, T))
+        # Gate/up: 96 rows (one tile per workgroup, waves split its columns)
+        # and 24592 rows (1537 tiles, four per workgroup, the last one
+        # alone). Fused QKV: 96 rows each, then 16400 + 4104 + 4088 rows
+        # (1538 tiles, four per workgroup; one workgroup holds q's last
+        # tiles and k's first).
+        for shapes, k, T in (((96, 96, 96), 4096, 7), ((24592, 24592, 24592), 512, 8), ((16400, 4104, 4088), 512, 6)):
+            raws = [synth.weight(dtype, r, k, 70 + i) for i, r in enumerate(shapes)]
+            ws = [backend.upload_weight(raw, dtype, (r, k)) for raw, r in zip(raws, shapes)]
+            xb = backend.f32_buf(synth.normal_f32(T * k, 71))
 
-        def gate_up():
-            g, u, y = (backend.alloc(T * rows * 4) for _ in range(3))
-            backend.ffn_gate_up(ws[0], ws[1], xb, g, u, y)
-            return backend.download_f32(y).copy()
+            def gate_up():
+                r = shapes[0]
+                g, u, y = (backend.alloc(T * r * 4) for _ in range(3))
+                backend.ffn_gate_up(ws[0], ws[1], xb, g, u, y)
+                return backend.download_f32(y).copy()
 
-        def qkv():
-            outs = [backend.alloc(T * rows * 4) for _ in range(3)]
-            backend.qmatmul_qkv(ws[0], ws[1], ws[2], xb, *outs)
-            return np.concatenate([backend.download_f32(o) for o in outs])
+            def qkv():
+                outs = [backend.alloc(T * r * 4) for r in shapes]
+                backend.qmatmul_qkv(ws[0], ws[1], ws[2], xb, *outs)
+                return np.concatenate([backend.download_f32(o) for o in outs])
 
-        for fn in (gate_up, qkv):
-            a, b = both(fn)
-            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), fn.__name__
+            for fn in ((gate_up, qkv) if shapes[0] == shapes[2] else (qkv,)):
+                a, b = both(fn)
+                same(a, b, (fn.__name__, shapes, k, T))
     finally:
         backend.set_act_mode(backend_mod.ACT_F32)
 
