@@ -778,15 +778,18 @@ constexpr bool ring_fits() {
 // XN: token rows staged per pair (8 for T <= 8, else 16). Either TW waves
 // split one tile's columns (W = 1), or W waves take W consecutive tiles in
 // lockstep (TW = 1), sharing the pair's activations and scales: one staged
-// copy per workgroup instead of one per tile.
-template <class R, int TW, int W, bool GATED, int XN, bool CAP = false>
+// copy per workgroup instead of one per tile. SPLIT (gated, W = 2): the two
+// waves take the same tile, one gate's rows and one up's, in lockstep on
+// the shared activations: twice the waves for the same LDS.
+template <class R, int TW, int W, bool GATED, int XN, bool CAP = false, bool SPLIT = false>
 __global__ __launch_bounds__(64 * TW * W) void gemv_ring(BatchSet bs, const int8_t *__restrict__ qx,
                                                          const float *__restrict__ dx, uint32_t T,
                                                          float *__restrict__ ygated) {
   static_assert(W == 1 || TW == 1, "waves split a tile's columns or take tiles of their own");
+  static_assert(!SPLIT || (GATED && W == 2 && TW == 1), "gate and up split over a pair of waves");
   using F = typename R::B;
-  constexpr int NR = GATED ? 2 : 1;
-  constexpr uint32_t XB = 512 * XN, WS = NR * R::WB, SLOT = ring_slot<R, GATED, XN, W>();
+  constexpr int NR = GATED && !SPLIT ? 2 : 1;  // weights per wave
+  constexpr uint32_t XB = 512 * XN, WS = NR * R::WB, SLOT = XB + 256 + W * WS;
   constexpr int PB = XN / 2 + 1 + NR * R::NDMA;  // DMA instructions per pair (W == 1)
   static_assert(PB <= 63, "wait count beyond vmcnt's range");
   static_assert(TW == 1 || TW * 2 * SLOT >= NCHMAX * NR * 4 * 64 * sizeof(float), "chunk sums fit the ring");
@@ -797,7 +800,7 @@ __global__ __launch_bounds__(64 * TW * W) void gemv_ring(BatchSet bs, const int8
   // W > 1: the last workgroup's waves past the last tile take part in the
   // barriers on the last tile's bytes and store nothing.
   const uint32_t all_tiles = bs.j[0].tiles + (bs.n > 1 ? bs.j[1].tiles : 0) + (bs.n > 2 ? bs.j[2].tiles : 0);
-  const uint32_t tile_w = W == 1 ? blockIdx.x : blockIdx.x * W + wave;
+  const uint32_t tile_w = W == 1 || SPLIT ? blockIdx.x : blockIdx.x * W + wave;
   const bool live = tile_w < all_tiles;
   uint32_t tile = live ? tile_w : all_tiles - 1;
   int ji = 0;
@@ -816,8 +819,8 @@ __global__ __launch_bounds__(64 * TW * W) void gemv_ring(BatchSet bs, const int8
   const uint32_t n = lane & 15, g = lane >> 4, r_lane = tile * TROWS + n;
   const size_t rb = F::row_bytes(n_in);
   const uint8_t *wbase[NR];
-  wbase[0] = J.w;
-  if (GATED) wbase[NR - 1] = bs.j[1].w;
+  wbase[0] = SPLIT && wave == 1 ? bs.j[1].w : J.w;
+  if (GATED && !SPLIT) wbase[NR - 1] = bs.j[1].w;
   // DMA sources (the same rows of gate and up).
   const typename R::Src src = R::src(rb, n_in, tile * TROWS, n_out, lane);
   // The activation DMAs this wave issues (W > 1: its share of them).
@@ -855,8 +858,8 @@ __global__ __launch_bounds__(64 * TW * W) void gemv_ring(BatchSet bs, const int8
     for (int j = 0; j < NJ; j++) acc[r][j] = tot[r][j] = 0.f;
   const uint32_t nsub = n_in / (256 / F::SUBS);
   int32_t *dcap[NR];
-  dcap[0] = J.dots;
-  if (GATED) dcap[NR - 1] = bs.j[1].dots;
+  dcap[0] = SPLIT && wave == 1 ? bs.j[1].dots : J.dots;
+  if (GATED && !SPLIT) dcap[NR - 1] = bs.j[1].dots;
   const int ks = W == 1 ? wave : 0;  // the wave's share of the columns
   const uint32_t c0 = ks * nch / TW, c1 = (ks + 1) * nch / TW;
   const uint32_t b0 = c0 * nb / nch, b1 = c1 * nb / nch;
@@ -981,13 +984,26 @@ __global__ __launch_bounds__(64 * TW * W) void gemv_ring(BatchSet bs, const int8
 #pragma unroll
         for (int j = 0; j < NJ; j++) tot[r][j] += red[((k * NR + r) * NJ + j) * 64 + lane];
   }
+  float uv_split[NJ] = {};
+  if constexpr (SPLIT) {
+    // Up's sums (wave 1) to gate's wave through the idle ring.
+    float *red = reinterpret_cast<float *>(&ring[0][0][0]);  // [j][lane]
+    __syncthreads();
+    if (wave == 1)
+#pragma unroll
+      for (int j = 0; j < NJ; j++) red[j * 64 + lane] = tot[0][j];
+    __syncthreads();
+    if (wave == 1) return;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) uv_split[j] = red[j * 64 + lane];
+  }
   if (!live || r_lane >= n_out) return;
   const uint32_t t0 = 4 * g;
 #pragma unroll
   for (int j = 0; j < NJ; j++) {
     if (t0 + j >= T) continue;
     if (GATED) {
-      const float gv = tot[0][j], uv = tot[NR - 1][j];
+      const float gv = tot[0][j], uv = SPLIT ? uv_split[j] : tot[NR - 1][j];
       ygated[(size_t)(t0 + j) * n_out + r_lane] = gv / (1.0f + expf(-gv)) * uv;
     } else {
       J.y[(size_t)(t0 + j) * n_out + r_lane] = tot[0][j];
@@ -1018,20 +1034,21 @@ RingShape ring_shape(mdma_ctx *ctx, uint32_t tiles, uint32_t nch) {
   return {tw, 1};
 }
 
-template <class R, int TW, int W, bool GATED, int XN>
+template <class R, int TW, int W, bool GATED, int XN, bool SPLIT = false>
 void ring_launch(mdma_ctx *ctx, const BatchSet &bs, uint32_t tiles, const int8_t *qx, const float *dx, uint32_t T,
                  float *yg) {
   hipEvent_t t0 = ctx->time_start, t1 = ctx->time_stop;
   ctx->time_start = ctx->time_stop = nullptr;
-  const dim3 grid((tiles + W - 1) / W), block(64 * TW * W);
+  const dim3 grid(SPLIT ? tiles : (tiles + W - 1) / W), block(64 * TW * W);
   if (bs.j[0].dots) {
     // ring_fmt sized the shape for the 16 token rows the capture stages.
-    if constexpr (ring_fits<R, TW, W, GATED, 16>())
-      gemv_ring<R, TW, W, GATED, 16, true><<<grid, block, 0, ctx->stream>>>(bs, qx, dx, T, yg);
+    if constexpr (SPLIT || ring_fits<R, TW, W, GATED, 16>())
+      gemv_ring<R, TW, W, GATED, 16, true, SPLIT><<<grid, block, 0, ctx->stream>>>(bs, qx, dx, T, yg);
   } else if (t0 || t1) {
-    hipExtLaunchKernelGGL(gemv_ring<R, TW, W, GATED, XN>, grid, block, 0, ctx->stream, t0, t1, 0, bs, qx, dx, T, yg);
+    hipExtLaunchKernelGGL(gemv_ring<R, TW, W, GATED, XN, false, SPLIT>, grid, block, 0, ctx->stream, t0, t1, 0, bs, qx,
+                          dx, T, yg);
   } else {
-    gemv_ring<R, TW, W, GATED, XN><<<grid, block, 0, ctx->stream>>>(bs, qx, dx, T, yg);
+    gemv_ring<R, TW, W, GATED, XN, false, SPLIT><<<grid, block, 0, ctx->stream>>>(bs, qx, dx, T, yg);
   }
   hip_check(hipGetLastError(), "gemv ring launch");
 }
@@ -1046,6 +1063,10 @@ void ring_fmt(mdma_ctx *ctx, const BatchSet &bs, uint32_t tiles, const int8_t *q
   // instantiations that would not out of the build.)
   if (sh.w == 4) {
     if constexpr (ring_fits<R, 1, 4, GATED, XN>()) return ring_launch<R, 1, 4, GATED, XN>(ctx, bs, tiles, qx, dx, T, yg);
+  } else if (GATED && sh.tw == 1) {
+    // One wave per tile would hold gate and up alone: split them over a
+    // pair (the same LDS as gate and up in one wave).
+    if constexpr (GATED) return ring_launch<R, 1, 2, GATED, XN, true>(ctx, bs, tiles, qx, dx, T, yg);
   } else if (sh.tw == 4) {
     if constexpr (ring_fits<R, 4, 1, GATED, XN>()) return ring_launch<R, 4, 1, GATED, XN>(ctx, bs, tiles, qx, dx, T, yg);
   } else if (sh.tw == 2) {
