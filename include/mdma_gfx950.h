@@ -143,7 +143,7 @@ int mdma_gfx950_set_norm_fusion(mdma_ctx *ctx, int on);
  * qmatmul_i8 (src/backend/rocm.rs:1759-1918). */
 typedef enum { MDMA_PREFILL_AUTO = 0, MDMA_PREFILL_I8 = 1 } mdma_prefill_kernel;
 int mdma_gfx950_set_prefill_kernel(mdma_ctx *ctx, int kind);
-/* Extra: the int8 mode's batched decode GEMV kernel (calls of 5 tokens or
+/* Extra: the int8 mode's batched decode GEMV kernel (calls of 3 tokens or
  * more on prepared-layout weights that the prefill GEMM does not take, up
  * to 16 tokens per launch). AUTO (default) streams each block of
  * the weight tile, activations and scales through a per-wave LDS ring by

@@ -94,7 +94,7 @@ def expected(dtype, raw, rows, k, q, T, folded=False):
 
 
 # Routes by token count: 1 (prologue-quantized x; Q8_0 a quantized buffer),
-# 2 and 3 (row teams of 2 and 4 tokens), 5, 8 and 13 (MFMA batch GEMV),
+# 2 (row teams of 2 tokens), 3, 5, 8 and 13 (MFMA batch GEMV),
 # 16 and 40 (prefill GEMM, activations per 32).
 ROUTES = [1, 2, 3, 5, 8, 13, 16, 40]
 

@@ -35,11 +35,12 @@ def both(be, w, x_h, rows):
 
 
 def test_noalloc_equals_allocating_entry_two_calls(backend):
-    # Call 1: Q4_K 4096x4096, 3 tokens (row teams over int8 x in the array).
+    # Call 1: Q4_K 4096x4096, 3 tokens (the matrix-core batch GEMV over int8 x
+    # in the array).
     w1 = backend.upload_weight(synth.weight(Q4K, 4096, 4096, 1), Q4K, (4096, 4096))
     a, b = both(backend, w1, synth.normal_f32(3 * 4096, 2), 4096)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
-    # Call 2, smaller: Q6_K 1024x4096, 2 tokens.
+    # Call 2, smaller: Q6_K 1024x4096, 2 tokens (row teams).
     w2 = backend.upload_weight(synth.weight(Q6K, 1024, 4096, 3), Q6K, (1024, 4096))
     a, b = both(backend, w2, synth.normal_f32(2 * 4096, 4), 1024)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
@@ -48,7 +49,7 @@ def test_noalloc_equals_allocating_entry_two_calls(backend):
 @pytest.mark.parametrize("dtype,rows,k,T", [(Q8, 300, 1024, 1), (Q4K, 640, 4096, 8), (Q6K, 4096, 14336, 5)])
 def test_noalloc_routes_bit_exact(backend, dtype, rows, k, T):
     """One token (Q8_0: x quantized separately; K-quants quantize in the
-    kernel's prologue) and the batch GEMV (5..16 tokens, matrix cores) give
+    kernel's prologue) and the batch GEMV (3..16 tokens, matrix cores) give
     the allocating entry point's bits."""
     raw = synth.weight(dtype, rows, k, 10 + T)
     w = backend.upload_weight(raw, dtype, (rows, k))
