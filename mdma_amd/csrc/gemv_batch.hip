@@ -279,6 +279,50 @@ struct BQ6 {
 #pragma unroll
     for (int j = 0; j < 4; j++) c[j] = d * (float)ai[j];
   }
+  // compute for at most 8 tokens, with half the MFMAs and scale products:
+  // token slots 8..15 of the MFMA carry tokens 0..7 again, so one MFMA forms
+  // both sub-blocks of a 32-column group. Lane l supplies x of slot n = l%16
+  // at k-group g = l/16, kept where the slot's half matches the k-group's
+  // unit (slots 0..7: unit 2v, k-groups 0, 1; slots 8..15: unit 2v+1,
+  // k-groups 2, 3) and zero elsewhere. Results: lanes with g < 2 hold unit
+  // 2v's dots of tokens 4g+j, lanes with g >= 2 unit 2v+1's of tokens
+  // 4(g-2)+j; each lane scales by its own sub-block's scale, and the two
+  // halves' int32 sums meet across lanes l and l^32 once per block: c[j] is
+  // compute's integer total, so the results are the same bits.
+  template <class Op>
+  __device__ static void compute_paired(const Op &op, float *c, const Dots &dc, uint32_t g, uint32_t n) {
+    const uint4 sc4 = op.sc();
+    const bool hi = g >= 2;
+    const uint32_t scl[2] = {hi ? sc4.y : sc4.x, hi ? sc4.w : sc4.z};
+    const bool keep = (n >= 8) == hi;
+    v4i ai = {};
+#pragma unroll
+    for (int v = 0; v < 2; v++) {
+      const uint64_t wa = op.w(v, 0), wb = op.w(v, 1), wq = op.w(v, 2);
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const uint32_t lo = q6_centre4(u6((uint32_t)wa, (uint32_t)wb, (uint32_t)wq, r));
+        const uint32_t hw = q6_centre4(u6((uint32_t)(wa >> 32), (uint32_t)(wb >> 32), (uint32_t)(wq >> 32), r));
+        const uint64_t wv = (uint64_t)lo | ((uint64_t)hw << 32);
+        const v4i z = {};
+        const v4i dd = mma(keep ? op.xg(4 * v + r) : 0ull, wv, z);
+        if (dc.p)
+#pragma unroll
+          for (int j = 0; j < 4; j++) dc.put(4 * (g & 1) + j, 8 * v + 2 * r + (g >> 1), dd[j]);
+        const int s = (int)(int8_t)((scl[v] >> (8 * r)) & 0xff);
+#pragma unroll
+        for (int j = 0; j < 4; j++) ai[j] += __mul24(s, dd[j]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const auto p = __builtin_amdgcn_permlane32_swap(ai[j], ai[j], false, false);
+      ai[j] = (int)(p[0] + p[1]);
+    }
+    const float d = op.d();
+#pragma unroll
+    for (int j = 0; j < 4; j++) c[j] = d * (float)ai[j];
+  }
   __device__ static void compute(const uint8_t *lds, const X &x, uint32_t l, float *c, const Dots &dc) {
     compute(Staged{lds, l & 15, l >> 4, x}, c, dc, l >> 4);
   }
@@ -633,6 +677,7 @@ __device__ __forceinline__ void issue_piece(const uint8_t *w, uint32_t o, uint32
 // Q4_K: planes A | B, then the headers.
 struct RQ4 {
   using B = BQ4;
+  static constexpr bool PAIRED = false;  // B::compute_paired (at most 8 tokens)
   using P = Plane<128>;
   static constexpr uint32_t WB = 2 * P::BYTES + 512;
   static constexpr int NDMA = 2 * P::NDMA + 1;
@@ -676,6 +721,7 @@ struct RQ4 {
 // lane n (at 4n) holds row n's f16 d of the pair's two blocks.
 struct RQ6 {
   using B = BQ6;
+  static constexpr bool PAIRED = true;
   using P = Plane<128>;
   static constexpr uint32_t WB = 3 * P::BYTES + 512 + 256;
   static constexpr int NDMA = 3 * P::NDMA + 2;
@@ -727,6 +773,7 @@ struct RQ6 {
 // the scales.
 struct RQ8 {
   using B = BQ8;
+  static constexpr bool PAIRED = false;
   using P = Plane<256>;
   static constexpr uint32_t WB = 2 * P::BYTES + 512;
   static constexpr int NDMA = 2 * P::NDMA + 1;
@@ -834,7 +881,9 @@ __global__ __launch_bounds__(64 * TW * W) void gemv_ring(BatchSet bs, const int8
   }
   const uint32_t ssrc = (min(lane & 15, T - 1) * nb + ((lane >> 4) & 1)) * 4;
   // Operand reads: x of token n (rows past the slot's tokens read its last).
-  const uint32_t tr = min(n, (uint32_t)XN - 1);
+  // Paired formats at most 8 tokens: slots 8..15 read tokens 0..7 again.
+  constexpr bool PAIR = R::PAIRED && XN == 8;
+  const uint32_t tr = PAIR ? (n & 7) : min(n, (uint32_t)XN - 1);
   const uint32_t xo = 512 * tr + 8 * (g & 1) + 16 * ((g >> 1) ^ tr), wo = R::wofs(n, g);
   const int rw = W == 1 ? wave : 0;                    // the wave's ring
   const uint32_t wofs_w = XB + 256 + (W == 1 ? 0 : wave * WS);  // its weights in a slot
@@ -917,7 +966,10 @@ __global__ __launch_bounds__(64 * TW * W) void gemv_ring(BatchSet bs, const int8
         if constexpr (CAP) {
           if (live && r_lane < n_out) dc.p = dcap[r] + (size_t)r_lane * nsub + F::SUBS * bb;
         }
-        F::compute(op[bi][r], c, dc, g);
+        if constexpr (PAIR)
+          F::compute_paired(op[bi][r], c, dc, g, n);
+        else
+          F::compute(op[bi][r], c, dc, g);
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[r][j] = fmaf(sj[j], c[j], acc[r][j]);
       }
@@ -929,7 +981,9 @@ __global__ __launch_bounds__(64 * TW * W) void gemv_ring(BatchSet bs, const int8
   if constexpr (W == 1) {
     // The pairs holding the wave's blocks; a pair past its last is loaded
     // as its last again (in bounds; every pair issues the same DMAs, so the
-    // wait count is fixed).
+    // wait count is fixed). (A third slot, two pairs in flight, measured
+    // slower at every shape: the 4096x14336 Q6_K at 8 tokens 15.2 -> 16.2
+    // us.)
     for (uint32_t sp = s0; sp < s1; sp += 2) {
 #pragma unroll
       for (int i = 0; i < 2; i++) {
