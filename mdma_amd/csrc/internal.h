@@ -287,8 +287,14 @@ void gemm_i8_split_need(const mdma_ctx *ctx, const GemvJob &w, uint64_t M, uint6
                         uint64_t *counters);
 void launch_gemm_i8(mdma_ctx *ctx, const GemvJob &w, const int8_t *qx, const float *sx, const int32_t *s16,
                     uint64_t M, float *y, double *part, uint64_t part_doubles, uint32_t *cnt, uint64_t counters);
-// Token count from which the int8 mode runs the MFMA GEMM instead of the GEMV.
-constexpr uint64_t GEMM_MIN_TOKENS = 16;
+// Token count from which the int8 mode runs the MFMA GEMM instead of the
+// GEMV (activations per 32 instead of per 256). Below it the batch GEMV takes
+// up to 16 tokens per launch: on the MI355X at Llama-3-8B shapes the GEMMs
+// cost about the same at 16 as at 64 tokens (gate/up 170 us, 14336x4096
+// Q4_K 86 us, 4096x14336 Q6_K 60 us) against 18.5, 12.0 and 18.3 us for 16
+// tokens of the batch GEMV; at 64 tokens the four batch launches of the
+// 4096x14336 Q6_K match its GEMM.
+constexpr uint64_t GEMM_MIN_TOKENS = 64;
 // Prefill GEMM on the f16 matrix path (gemm_f16.hip): the same per-32 int8
 // activations, carried as exact f16 integers with the Q4_K weights' 6-bit
 // sub-scales folded into the weight operand. Whether it covers (dtype,

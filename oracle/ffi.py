@@ -216,6 +216,12 @@ class _M(C.Structure):
                 ("act_i8", C.c_int)]
 
 
+# Token count from which the device's int8 mode runs its prefill GEMM
+# (activations per 32); fewer tokens take a GEMV (per 256). Mirrors
+# ORC_GEMM_MIN_TOKENS in oracle.h.
+GEMM_MIN_TOKENS = 64
+
+
 def i8_group(dtype: int, n_out: int, n_in: int, T: int) -> int:
     """Activation group (32, 256, or 0 for f32) of the int8 mode's GEMV."""
     return int(lib().orc_i8_group(dtype, n_out, n_in, T))

@@ -586,7 +586,7 @@ typedef struct {
 } orc_ws;
 
 /* Activation group of the device's int8 mode for one GEMV of T tokens: 32
- * where it runs the prefill GEMM (T >= 16 on Q8_0 rows of whole 128-column
+ * where it runs the prefill GEMM (T >= 64 on Q8_0 rows of whole 128-column
  * tiles or Q4_K / Q6_K rows of whole 256-column blocks, weights below 4 GiB),
  * 256 where it runs a decode GEMV (quantized weights, whole 256-column
  * groups), 0 where it keeps f32 activations (float weights, other widths). */
@@ -597,7 +597,7 @@ size_t orc_i8_group(int dtype, size_t n_out, size_t n_in, size_t T) {
     size_t bs = orc_block_size(dtype), ts = orc_type_size(dtype);
     size_t row = (n_in / bs * ts + 15) / 16 * 16; /* prepared row bytes */
     int gemm_w = dtype == ORC_Q8_0 ? n_in % 128 == 0 : n_in % 256 == 0;
-    if (T >= 16 && gemm_w && (unsigned long long)n_out * row < (1ull << 32))
+    if (T >= ORC_GEMM_MIN_TOKENS && gemm_w && (unsigned long long)n_out * row < (1ull << 32))
         return 32;
     return n_in % 256 == 0 ? 256 : 0;
 }

@@ -80,6 +80,9 @@ typedef struct {
 /* orc_model.act_i8 bits: which GEMVs of the int8 mode requantize x. */
 enum { ORC_I8_QKV = 1, ORC_I8_O = 2, ORC_I8_GATE_UP = 4, ORC_I8_DOWN = 8, ORC_I8_HEAD = 16, ORC_I8_ALL = 31 };
 
+/* Token count from which the device's int8 mode runs its prefill GEMM
+ * (activations per 32) rather than a GEMV (per 256). */
+enum { ORC_GEMM_MIN_TOKENS = 64 };
 size_t orc_i8_group(int dtype, size_t n_out, size_t n_in, size_t T);
 int orc_llama_run(const orc_model *m, const uint32_t *prompt, size_t n_prompt, size_t n_gen,
                   const uint32_t *forced, uint32_t *out_tokens, float *step_logits);

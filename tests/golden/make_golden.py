@@ -11,7 +11,7 @@
 - config5_steps.json (`config5` argument; about a minute of CPU): the
   Llama-3-8B geometry with the Q4_K_M mix (random init, written by
   mdma_amd.llama_synth with fast=True and CONFIG5_SEED), f32 activations,
-  f16-rounded KV. A 16-token prompt (the prefill GEMM route in the int8
+  f16-rounded KV. A 64-token prompt (the prefill GEMM route in the int8
   mode), then 15 teacher-forced random tokens: every step's greedy token,
   top-2 margin, largest |logit| and top-8 (token, logit) pairs, in the f32
   mode and in the int8 mode (x requantized before every GEMV).
@@ -35,7 +35,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 
 
 CONFIG5_SEED = 20261202
-CONFIG5_PROMPT, CONFIG5_STEPS = 16, 16
+CONFIG5_PROMPT, CONFIG5_STEPS = 64, 16
 
 
 def config5(path="/tmp/mdma_config5.gguf"):

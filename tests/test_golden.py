@@ -67,7 +67,7 @@ def test_config5_fixture_inputs_regenerate_from_its_seed():
     """The config-5 fixture's prompt and forced tokens are the seeded
     generator's (the GPU test rebuilds the model from the same seed)."""
     fx = json.load(open(os.path.join(G, "config5_steps.json")))
-    assert fx["prompt"] == synth.tokens(16, 128256, fx["seed"] + 1).tolist()
+    assert fx["prompt"] == synth.tokens(64, 128256, fx["seed"] + 1).tolist()
     assert fx["forced"] == synth.tokens(15, 128256, fx["seed"] + 2).tolist()
     for mode in ("f32", "i8"):
         assert len(fx[mode]) == 16

@@ -48,7 +48,7 @@ def extreme_x(T, k, seed):
     product's rounding decides them, see tests/ties.py); token 1 at +1
     everywhere (every int8 value 127); token 2 alternating +-1 (+-127); the
     rest normal."""
-    group = 32 if T >= 16 else 256
+    group = 32 if T >= ffi.GEMM_MIN_TOKENS else 256
     x = synth.normal_f32(T * k, seed).reshape(T, k)
     x[0] = near_tie_x(k // group, group, seed)
     if T > 1:
@@ -94,9 +94,10 @@ def expected(dtype, raw, rows, k, q, T, folded=False):
 
 
 # Routes by token count: 1 (prologue-quantized x; Q8_0 a quantized buffer),
-# 2 (row teams of 2 tokens), 3, 5, 8 and 13 (MFMA batch GEMV),
-# 16 and 40 (prefill GEMM, activations per 32).
-ROUTES = [1, 2, 3, 5, 8, 13, 16, 40]
+# 2 (row teams of 2 tokens), 3, 5, 8, 13 and 16 (MFMA batch GEMV), 40 (batch
+# GEMV launches of 16, 16 and 8 tokens), 64 and 80 (prefill GEMM,
+# activations per 32).
+ROUTES = [1, 2, 3, 5, 8, 13, 16, 40, 64, 80]
 
 
 @pytest.mark.parametrize("k", [1024, 14336])
@@ -110,12 +111,12 @@ def test_qmatmul_block_dots_every_route(backend, dtype, k):
         for T in ROUTES:
             x = extreme_x(T, k, 901 + T)
             xb, yb = backend.f32_buf(x), backend.alloc(T * rows * 4)
-            kinds = [bm.PREFILL_AUTO] if T < 16 or dtype != Q4K else [bm.PREFILL_AUTO, bm.PREFILL_I8]
+            kinds = [bm.PREFILL_AUTO] if T < ffi.GEMM_MIN_TOKENS or dtype != Q4K else [bm.PREFILL_AUTO, bm.PREFILL_I8]
             for kind in kinds:
                 backend.set_prefill_kernel(kind)
                 got = capture(backend, lambda: backend.qmatmul(w, xb, yb), T * rows * subs(dtype, k))
-                group = 32 if T >= 16 else 256
-                folded = dtype == Q4K and T >= 16 and kind == bm.PREFILL_AUTO
+                group = 32 if T >= ffi.GEMM_MIN_TOKENS else 256
+                folded = dtype == Q4K and T >= ffi.GEMM_MIN_TOKENS and kind == bm.PREFILL_AUTO
                 want = expected(dtype, raw, rows, k, q_of(x, T, k, group), T, folded)
                 g = got.reshape(want.shape)
                 bad = np.argwhere(g != want)
@@ -138,7 +139,7 @@ def test_gate_up_block_dots(backend, dtype):
     ws = [backend.upload_weight(r, dtype, (rows, k)) for r in raws]
     backend.set_act_mode(bm.ACT_I8)
     try:
-        for T, cached in ((1, False), (1, True), (5, False), (16, False)):
+        for T, cached in ((1, False), (1, True), (5, False), (16, False), (64, False)):
             x = extreme_x(T, k, 920 + T)
             if cached:
                 xr = backend.f32_buf(x)
@@ -150,9 +151,9 @@ def test_gate_up_block_dots(backend, dtype):
             g, u, y = (backend.alloc(T * rows * 4) for _ in range(3))
             n = T * rows * subs(dtype, k)
             got = capture(backend, lambda: backend.ffn_gate_up(ws[0], ws[1], xb, g, u, y), 2 * n)
-            group = 32 if T >= 16 else 256
+            group = 32 if T >= ffi.GEMM_MIN_TOKENS else 256
             q = q_of(x, T, k, group)
-            folded = dtype == Q4K and T >= 16
+            folded = dtype == Q4K and T >= ffi.GEMM_MIN_TOKENS
             for i in range(2):
                 want = expected(dtype, raws[i], rows, k, q, T, folded)
                 assert np.array_equal(got[i * n:(i + 1) * n].reshape(want.shape), want), (dtype, T, cached, i)

@@ -3,14 +3,14 @@
 init written as GGUF with the fixture's seed), against the CPU oracle's run
 of the same model committed in tests/golden/config5_steps.json.
 
-A 16-token prompt, then 15 teacher-forced random tokens (a random model left
+A 64-token prompt, then 15 teacher-forced random tokens (a random model left
 to itself repeats one token; forcing makes every step a new context). In
 both modes every step's logits at the oracle's top-8 tokens must agree, and
 the greedy token must be the oracle's where its top-2 margin is clear:
   - f32 activations: within F32_LOGIT_RTOL of max|logit| (both sides round
     K/V to f16 through 32 layers; a value an ulp apart may round to the
     neighbouring half, a 2^-11 step);
-  - int8 activations (the production path; the 16-token prompt takes the
+  - int8 activations (the production path; the 64-token prompt takes the
     prefill GEMM): within I8_LOGIT_RTOL, the activation-flip scale measured
     on the small models (tests/test_gpu_model.py).
 Batched decode of 8 sequences must give each sequence's single-sequence

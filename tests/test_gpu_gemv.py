@@ -181,21 +181,23 @@ def test_i8_mode_llama3_8b_shapes(backend, dtype, shape):
     assert rel_rms < 0.03, rel_rms
 
 
-@pytest.mark.parametrize("T", [2, 5, 8, 11, 16, 17, 35])
+@pytest.mark.parametrize("T", [2, 5, 8, 11, 16, 17, 35, 64, 70])
 def test_i8_mode_batched(backend, T):
     rows, k = 29, 2048
     for dtype in (Q4K, Q6K, Q8):
         raw = synth.weight(dtype, rows, k, T)
         x = synth.normal_f32(T * k, 50 + T)
         got = run_qmatmul(backend, dtype, raw, rows, k, x, "i8")
-        # From 16 tokens the prepared weights go to the prefill GEMM, whose
-        # activations are quantized per 32.
-        g = 32 if T >= 16 else 256
+        # From ffi.GEMM_MIN_TOKENS tokens the prepared weights go to the
+        # prefill GEMM, whose activations are quantized per 32 (below: the
+        # batch GEMV, 16 tokens per launch, per 256).
+        gemm = T >= ffi.GEMM_MIN_TOKENS
+        g = 32 if gemm else 256
         q = np.concatenate([ffi.quantize_act(x[t * k:(t + 1) * k], g)[0] for t in range(T)])
         d = np.concatenate([ffi.quantize_act(x[t * k:(t + 1) * k], g)[1] for t in range(T)])
         xq = ffi.dequantize_act(q, d, g)
         cpu, exact = oracle_f32(dtype, raw, rows, k, xq)
-        absum = abs_dot(npq.dequantize(dtype, raw, rows, k), xq) if T >= 16 else None
+        absum = abs_dot(npq.dequantize(dtype, raw, rows, k), xq) if gemm else None
         assert_parity(got, cpu, exact, 1e-3, abs_sum=absum, what=f"i8 batched {dtype} T={T}")
 
 
@@ -417,9 +419,10 @@ def test_i8_activation_cache_reuses_and_invalidates(backend):
     assert np.array_equal(backend.download_f32(y), backend.download_f32(want))
 
 
-@pytest.mark.parametrize("T", [1, 3, 15, 16])
+@pytest.mark.parametrize("T", [1, 3, 16, 63, 64])
 def test_rmsnorm_int8_activations_bit_exact(backend, T):
-    # In the int8 mode an rmsnorm of fewer than 16 rows also leaves the int8
+    # In the int8 mode an rmsnorm of fewer than 64 rows (ffi.GEMM_MIN_TOKENS,
+    # from which the prefill GEMM quantizes per 32 itself) also leaves the int8
     # form of its output in the activation cache; a qmatmul reading y must
     # give the bits of one reading an identical copy of y quantized afresh.
     k, rows = 4096, 40
@@ -709,7 +712,7 @@ def test_packed_upload_rejects_wrong_sizes(backend):
 
 
 # ------------------------------------------------------- prefill GEMM ----
-# int8 mode with T >= 16 tokens on prepared Q8_0 / Q4_K / Q6_K weights runs a
+# int8 mode with T >= 64 tokens on prepared Q8_0 / Q4_K / Q6_K weights runs a
 # prefill GEMM on activations quantized per 32 with an f32 scale: the
 # f16-path GEMM for Q4_K (default), the int8 MFMA GEMM otherwise or when
 # asked. Oracle: the reference's "requantize, then CPU qmatmul"
@@ -741,7 +744,7 @@ def gemm_cases(f):
     return f
 
 
-@pytest.mark.parametrize("shape", [(16, 256, 64), (37, 512, 200), (130, 1024, 257), (64, 4096, 384),
+@pytest.mark.parametrize("shape", [(64, 256, 64), (97, 512, 200), (130, 1024, 257), (64, 4096, 384),
                                    (300, 768, 130)])
 @gemm_cases
 def test_prefill_gemm_i8(backend, dtype, prefill_kernel, shape):
@@ -761,7 +764,7 @@ def test_prefill_gemm_activation_ranges(backend, dtype, prefill_kernel):
     block of equal values, all at 127) and mixed block magnitudes within a
     row: the f16-path GEMM rescales each row's block sums by a power of two
     to keep them in f16 range, and must agree with the oracle throughout."""
-    T, k, rows = 40, 512, 136
+    T, k, rows = 72, 512, 136
     raw = synth.weight(dtype, rows, k, 320)
     x = synth.normal_f32(T * k, 321).reshape(T, k)
     for t in range(24):
@@ -807,7 +810,7 @@ def test_prefill_gemm_config4_shapes_sampled_rows(backend, dtype, prefill_kernel
 def test_prefill_gemm_fused_calls(backend, dtype):
     backend.set_act_mode(1)
     try:
-        T, k, n = 24, 512, 160
+        T, k, n = 64, 512, 160
         raws = [synth.weight(dtype, n, k, 500 + i) for i in range(3)]
         ws = [backend.upload_weight(r, dtype, (n, k)) for r in raws]
         x = synth.normal_f32(T * k, 510)

@@ -217,11 +217,12 @@ def step_rel_err(got, want):
     return np.max(np.abs(got.astype(np.float64) - want), axis=1) / np.max(np.abs(want), axis=1)
 
 
-@pytest.mark.parametrize("which,n_prompt", [("tiny", 8), ("gqa", 8), ("gqa", 20)])
+@pytest.mark.parametrize("which,n_prompt", [("tiny", 8), ("gqa", 8), ("gqa", 20), ("gqa", 70)])
 def test_int8_mode_decode_matches_int8_oracle(backend, tiny, gqa, which, n_prompt):
     """Per-step logits of the int8 decode path (norm-fused QKV, the one-token
     gated gate/up, the residual-storing down projection, the int8 Q6_K head;
-    a 20-token prompt takes the per-32 prefill GEMM) against the oracle's
+    a 20-token prompt the batch GEMV, a 70-token one the per-32 prefill
+    GEMM) against the oracle's
     int8 mode. Greedy tokens must agree wherever the oracle's top-2 margin
     exceeds I8_TOKEN_MARGIN."""
     path = tiny[1] if which == "tiny" else gqa

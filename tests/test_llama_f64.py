@@ -142,18 +142,21 @@ def test_int8_mode_oracle_routing_and_quantization_error(models):
     256-column groups. Its logits differ from the f32 mode's by the
     quantization error only (the reference bounds rel-RMS by 0.03,
     src/backend/rocm/tests.rs:306-376)."""
+    assert ffi.GEMM_MIN_TOKENS == 64
     assert ffi.i8_group(12, 4096, 4096, 1) == 256
     assert ffi.i8_group(14, 128256, 4096, 8) == 256
-    assert ffi.i8_group(12, 14336, 4096, 16) == 32
+    assert ffi.i8_group(12, 14336, 4096, 16) == 256  # batch GEMV
+    assert ffi.i8_group(12, 14336, 4096, 63) == 256
+    assert ffi.i8_group(12, 14336, 4096, 64) == 32   # prefill GEMM
     assert ffi.i8_group(8, 768, 288, 1) == 0       # 288 is not whole 256-groups
-    assert ffi.i8_group(8, 288, 768, 15) == 256
-    assert ffi.i8_group(8, 288, 768, 16) == 32     # Q8_0 GEMM: whole 128-column tiles
-    assert ffi.i8_group(8, 768, 384, 16) == 32
-    assert ffi.i8_group(8, 768, 384, 15) == 0
+    assert ffi.i8_group(8, 288, 768, 63) == 256
+    assert ffi.i8_group(8, 288, 768, 64) == 32     # Q8_0 GEMM: whole 128-column tiles
+    assert ffi.i8_group(8, 768, 384, 64) == 32
+    assert ffi.i8_group(8, 768, 384, 63) == 0
     assert ffi.i8_group(0, 64, 256, 1) == 0
     path, vocab = models["gqa"]
     r = gguf.Reader(path)
-    prompt = synth.tokens(20, vocab, 77)  # 20 rows: the prefill GEMVs take the per-32 route
+    prompt = synth.tokens(70, vocab, 77)  # 70 rows: the prefill GEMVs take the per-32 route
     t32, l32 = ffi.llama_run(r, prompt, 4, kv_f16=True)
     t8, l8 = ffi.llama_run(r, prompt, 4, forced=t32, kv_f16=True, act_i8=True)
     rel_rms = np.sqrt(np.mean((l8 - l32) ** 2, axis=1) / np.mean(l32 ** 2, axis=1))

@@ -59,10 +59,10 @@ def test_noalloc_routes_bit_exact(backend, dtype, rows, k, T):
 
 @pytest.mark.parametrize("dtype", [Q8, Q4K, Q6K])
 def test_noalloc_prefill_gemm_matches_oracle(backend, dtype):
-    """24 tokens: the prefill GEMM route, unsplit here (its split-K partials
+    """64 tokens: the prefill GEMM route, unsplit here (its split-K partials
     would need scratch), against the oracle's per-32 requantized qmatmul at
     the int8 bar, and against the allocating entry point's result."""
-    T, k, rows = 24, 1024, 384
+    T, k, rows = 64, 1024, 384
     raw = synth.weight(dtype, rows, k, 20)
     x = synth.normal_f32(T * k, 21)
     w = backend.upload_weight(raw, dtype, (rows, k))
