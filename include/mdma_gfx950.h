@@ -151,6 +151,15 @@ int mdma_gfx950_set_prefill_kernel(mdma_ctx *ctx, int kind);
  * A/B measurement and the equality test: both give the same bits). */
 typedef enum { MDMA_BATCH_AUTO = 0, MDMA_BATCH_STAGED = 1 } mdma_batch_kernel;
 int mdma_gfx950_set_batch_kernel(mdma_ctx *ctx, int kind);
+/* Extra (no counterpart in the reference): with on != 0, the AUTO batch
+ * kernel reads a second, tile-major copy of each prepared Q6_K weight (its
+ * size again in device memory, charged to the device budget), made at the
+ * weight's first batch call outside graph capture; each 16-row tile's bytes
+ * for a 512-column pair are then one contiguous stream instead of 128-byte
+ * pieces of 16 rows. Same bits as without. Rewriting the weight's bytes
+ * (upload, or an op's output over them) frees the copy. Off by default; the
+ * Llama driver turns it on for sessions of 3 sequences or more. */
+int mdma_gfx950_set_batch_layout(mdma_ctx *ctx, int on);
 /* Extra (for tests; the reference pins its int8 matrix-core fragments the
  * same way, src/backend/rocm/tests.rs:1861-1925): block-dot capture. With
  * out set (NULL: off), every later int8-mode qmatmul, qmatmul_qkv and

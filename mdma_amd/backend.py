@@ -74,7 +74,7 @@ _SIGS = {
     "available_device_bytes": [_P, _P], "supports_weight_dtype": [_P, _I32], "max_head_dim": [_P],
     "kv_elem_bytes": [_P], "join_execution": [_P], "set_buffer_budget": [_P, _U64, _U64],
     "buffer_usage": [_P, C.c_int, _P, _P], "set_act_mode": [_P, C.c_int],
-    "set_norm_fusion": [_P, C.c_int], "set_prefill_kernel": [_P, C.c_int], "set_batch_kernel": [_P, C.c_int], "capture_block_dots": [_P, _P], "set_graph_decode": [_P, C.c_int], "stream": [_P],
+    "set_norm_fusion": [_P, C.c_int], "set_prefill_kernel": [_P, C.c_int], "set_batch_kernel": [_P, C.c_int], "set_batch_layout": [_P, C.c_int], "capture_block_dots": [_P, _P], "set_graph_decode": [_P, C.c_int], "stream": [_P],
     "alloc": [_P, _U64, C.c_int, _P], "free": [_P], "buf_len": [_P], "buf_view": [_P, _U64, _U64, _P],
     "upload": [_P, _P, _U64, _P, _U64], "download": [_P, _P, _U64, _P, _U64],
     "copy": [_P, _P, _U64, _P, _U64, _U64], "upload_weight": [_P, _P, _U64, C.c_int, _P],
@@ -278,9 +278,15 @@ class Gfx950Backend:
         _check(lib().mdma_gfx950_set_prefill_kernel(self.ctx, int(kind)))
 
     def set_batch_kernel(self, kind: int):
-        """BATCH_AUTO: batched int8 GEMVs (5+ tokens) stream through the DMA
-        ring kernel; BATCH_STAGED: the register-staged kernel (same bits)."""
+        """BATCH_AUTO: batched int8 GEMVs (3 to 63 tokens) stream through the
+        DMA ring kernel; BATCH_STAGED: the register-staged kernel (same bits)."""
         _check(lib().mdma_gfx950_set_batch_kernel(self.ctx, int(kind)))
+
+    def set_batch_layout(self, on: bool):
+        """On: the ring kernel reads a tile-major copy of each Q6_K weight,
+        made at its first batched call (device memory of the weight's size
+        again; same bits)."""
+        _check(lib().mdma_gfx950_set_batch_layout(self.ctx, int(bool(on))))
 
     def stream(self) -> int:
         return int(lib().mdma_gfx950_stream(self.ctx) or 0)

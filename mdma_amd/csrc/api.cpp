@@ -4,6 +4,7 @@
 // rejected on the host and never reaches a kernel.
 #include <cmath>
 #include <cstdarg>
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <new>
@@ -105,8 +106,10 @@ uint64_t matmul_tokens(const mdma_qweight *w, const mdma_buf *x, const mdma_buf 
 }
 
 GemvJob job_of(const mdma_qweight *w, mdma_buf *y) {
-  return GemvJob{w->dtype, reinterpret_cast<const uint8_t *>(w->buf->ptr), w->rows, w->cols,
-                 reinterpret_cast<float *>(y->ptr), w->buf->layout};
+  GemvJob j{w->dtype, reinterpret_cast<const uint8_t *>(w->buf->ptr), w->rows, w->cols,
+            reinterpret_cast<float *>(y->ptr), w->buf->layout};
+  j.src = const_cast<mdma_buf *>(w->buf);  // the weight itself is not written; its tile images may be made
+  return j;
 }
 
 // Block-dot capture: the jobs' slots, one region after another.
@@ -214,6 +217,66 @@ void prepare_weight(mdma_ctx *ctx, const mdma_qweight *w) {
   p->repack_pending = false;
   int st = mdma_gfx950_free(p);
   if (st) fail(st, g_last_error);
+}
+
+const uint8_t *batch_tile(mdma_ctx *ctx, const GemvJob &j) {
+  mdma_buf *b = j.src;
+  if (!b || !b->owner || b->ctx != ctx || b->ptr != reinterpret_cast<const char *>(j.w) ||
+      j.layout != MDMA_LAYOUT_GFX950)
+    return nullptr;
+  if (b->tile && b->tile_stale && !ctx->capturing && !ctx->fixed_scratch) free_tile(ctx, b);
+  if (b->tile) return b->tile_stale ? nullptr : reinterpret_cast<const uint8_t *>(b->tile);
+  // Made outside capture and outside allocation-free calls only; without
+  // room in the budget or on the device the row planes serve.
+  if (!ctx->batch_layout || ctx->capturing || ctx->fixed_scratch) return nullptr;
+  const uint64_t n = batch_tile_bytes(j.dtype, j.n_out, j.n_in);
+  if (!n || b->len < j.n_out * gfx950_row_bytes(j.dtype, j.n_in)) return nullptr;
+  Ledger &l = ctx->budget[MDMA_DOMAIN_DEVICE];
+  if (l.used + n < l.used || l.used + n > l.limit) return nullptr;
+  void *d = nullptr;
+  if (hipMalloc(&d, n) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  l.used += n;
+  try {
+    launch_tile_repack(ctx, j.dtype, j.n_out, j.n_in, j.w, static_cast<uint8_t *>(d));
+  } catch (...) {
+    (void)hipFree(d);
+    l.used -= n;
+    throw;
+  }
+  b->tile = static_cast<char *>(d);
+  b->tile_charged = n;
+  ctx->tiled.push_back(b);
+  return reinterpret_cast<const uint8_t *>(b->tile);
+}
+
+// Throws nothing (it runs where outputs are retired): a failed free keeps
+// the charge, as a failed buffer free does.
+void free_tile(mdma_ctx *ctx, mdma_buf *b) {
+  if (!b->tile) return;
+  (void)hipStreamSynchronize(ctx->stream);
+  if (hipFree(b->tile) == hipSuccess) budget_refund(ctx, MDMA_DOMAIN_DEVICE, b->tile_charged);
+  else (void)hipGetLastError();
+  b->tile = nullptr;
+  b->tile_charged = 0;
+  b->tile_stale = false;
+  auto &v = ctx->tiled;
+  v.erase(std::remove(v.begin(), v.end(), b), v.end());
+  ctx->buf_epoch++;  // a captured graph may read the images
+}
+
+void drop_tiles(mdma_ctx *ctx, const void *p, uint64_t bytes) {
+  const char *a = static_cast<const char *>(p);
+  for (size_t i = ctx->tiled.size(); i-- > 0;) {
+    mdma_buf *b = ctx->tiled[i];
+    if (!(a < b->ptr + b->len && b->ptr < a + bytes)) continue;
+    // Under capture (or in an allocation-free call) nothing is freed: the
+    // images are set aside and freed by the next call that may.
+    if (ctx->capturing || ctx->fixed_scratch) b->tile_stale = true;
+    else free_tile(ctx, b);
+  }
 }
 
 void fail(int code, const std::string &msg) { throw Error{code, msg}; }
@@ -328,6 +391,7 @@ uint32_t *gemm_counters(mdma_ctx *ctx, uint64_t n) {
 }
 
 void q8_invalidate_range(mdma_ctx *ctx, const void *p, uint64_t bytes) {
+  if (!ctx->tiled.empty()) drop_tiles(ctx, p, bytes);  // an op output over a weight's bytes
   if (!ctx->q8_valid) return;
   const char *a = static_cast<const char *>(p), *x = reinterpret_cast<const char *>(ctx->q8_x);
   if (a < x + ctx->q8_n * 4 && x < a + bytes) ctx->q8_valid = false;
@@ -406,6 +470,10 @@ void mdma_gfx950_destroy(mdma_ctx *ctx) {
   if (!ctx) return;
   (void)hipSetDevice(ctx->device);
   (void)hipStreamSynchronize(ctx->stream);
+  for (mdma_buf *b : ctx->tiled) {  // buffers the caller did not free
+    (void)hipFree(b->tile);
+    b->tile = nullptr;
+  }
   if (ctx->scratch) (void)hipFree(ctx->scratch);
   if (ctx->q8) (void)hipFree(ctx->q8);
   if (ctx->argmax_part) (void)hipFree(ctx->argmax_part);
@@ -525,6 +593,14 @@ int mdma_gfx950_set_batch_kernel(mdma_ctx *ctx, int kind) {
   });
 }
 
+int mdma_gfx950_set_batch_layout(mdma_ctx *ctx, int on) {
+  return guarded([&] {
+    need(ctx, "set_batch_layout");
+    std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    ctx->batch_layout = on != 0;
+  });
+}
+
 int mdma_gfx950_set_norm_fusion(mdma_ctx *ctx, int on) {
   return guarded([&] {
     need(ctx, "set_norm_fusion");
@@ -580,6 +656,7 @@ int mdma_gfx950_free(mdma_buf *buf) {
     no_capture(ctx, "free");
     // Kernels queued on the stream may still read the buffer.
     hip_check(hipStreamSynchronize(ctx->stream), "free: stream sync");
+    free_tile(ctx, buf);
     if (buf->ptr) {
       hipError_t e = hipFree(buf->ptr);
       if (e != hipSuccess) {
@@ -625,6 +702,7 @@ int mdma_gfx950_upload(mdma_ctx *ctx, mdma_buf *dst, uint64_t offset, const void
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
     q8_invalidate(ctx);
     no_capture(ctx, "upload");
+    drop_tiles(ctx, dst->ptr + offset, len);
     hip_check(hipMemcpyAsync(dst->ptr + offset, src, len, hipMemcpyHostToDevice, ctx->stream), "upload");
     hip_check(hipStreamSynchronize(ctx->stream), "upload sync");
   });

@@ -836,12 +836,11 @@ void quantize_into_scratch(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n
 }
 
 
-// Tokens from which int8-mode GEMVs of prepared rows go to the matrix-core
-// batch kernel (below: the row-team kernels, which keep each token's
-// activations in registers). At Llama-3-8B shapes the batch kernel's ring
-// is faster from 3 tokens on every weight (gate/up 16.2 us against 28.9
-// us at 3 tokens); at 2 the row teams still win on the Q6_K down and head.
-constexpr uint64_t BATCH_MIN_TOKENS = 3;
+// BATCH_MIN_TOKENS: below it int8-mode GEMVs of prepared rows run the
+// row-team kernels, which keep each token's activations in registers. At
+// Llama-3-8B shapes the batch kernel's ring is faster from 3 tokens on every
+// weight (gate/up 16.2 us against 28.9 us at 3 tokens); at 2 the row teams
+// still win on the Q6_K down and head.
 
 // Prepared-layout jobs go to the row-team kernels; a mix of layouts or
 // dtypes runs job by job; raw GGUF jobs use the kernels above.

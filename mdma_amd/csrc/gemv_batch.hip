@@ -402,6 +402,7 @@ struct BQ8 {
 
 struct BatchJob {
   const uint8_t *w;
+  const uint8_t *wt;  // the weight's tile image (tile_repack_q6) or null
   float *y;
   uint32_t n_out, tiles;
   int32_t *dots;  // block-dot capture or null
@@ -678,9 +679,14 @@ __device__ __forceinline__ void issue_piece(const uint8_t *w, uint32_t o, uint32
 struct RQ4 {
   using B = BQ4;
   static constexpr bool PAIRED = false;  // B::compute_paired (at most 8 tokens)
+  // A tile image (issue_tile) measured no faster than the row planes for
+  // Q4_K (gate/up at 8 tokens 16.6 against 16.1-16.6 us).
+  static constexpr bool TILED = false;
   using P = Plane<128>;
   static constexpr uint32_t WB = 2 * P::BYTES + 512;
   static constexpr int NDMA = 2 * P::NDMA + 1;
+  static constexpr int NDMA_T = NDMA;
+  static constexpr uint32_t IMG = 0;
   struct Src {
     uint32_t pl[P::NDMA], hd, U;
   };
@@ -722,9 +728,22 @@ struct RQ4 {
 struct RQ6 {
   using B = BQ6;
   static constexpr bool PAIRED = true;
+  static constexpr bool TILED = true;
   using P = Plane<128>;
   static constexpr uint32_t WB = 3 * P::BYTES + 512 + 256;
   static constexpr int NDMA = 3 * P::NDMA + 2;
+  // The tile image of a (tile, pair): the slot's weight bytes as issue()
+  // leaves them (planes A, B, high bits, the scale bytes, then the 16 rows'
+  // d words), IMG bytes in a row: six 1 KiB DMAs and one of 36 lanes.
+  static constexpr uint32_t IMG = 3 * P::BYTES + 512 + 64;
+  static constexpr int NDMA_T = (IMG + 1023) / 1024;
+  static_assert(IMG % 16 == 0 && IMG <= WB, "the image fits the slot");
+  // o: the pair's image offset in the tile's images plus 16 * L.
+  __device__ static void issue_tile(const uint8_t *wt, uint32_t o, uint8_t *slot, uint32_t L) {
+#pragma unroll
+    for (int i = 0; i < NDMA_T - 1; i++) lds_dma16(wt, o + 1024 * i, slot + 1024 * i);
+    if (L < (IMG - 1024 * (NDMA_T - 1)) / 16) lds_dma16(wt, o + 1024 * (NDMA_T - 1), slot + 1024 * (NDMA_T - 1));
+  }
   struct Src {
     uint32_t pl[P::NDMA], sc, d, U;
   };
@@ -774,9 +793,12 @@ struct RQ6 {
 struct RQ8 {
   using B = BQ8;
   static constexpr bool PAIRED = false;
+  static constexpr bool TILED = false;
   using P = Plane<256>;
   static constexpr uint32_t WB = 2 * P::BYTES + 512;
   static constexpr int NDMA = 2 * P::NDMA + 1;
+  static constexpr int NDMA_T = NDMA;
+  static constexpr uint32_t IMG = 0;
   struct Src {
     uint32_t pl[P::NDMA], hd, U;
   };
@@ -828,7 +850,7 @@ constexpr bool ring_fits() {
 // copy per workgroup instead of one per tile. SPLIT (gated, W = 2): the two
 // waves take the same tile, one gate's rows and one up's, in lockstep on
 // the shared activations: twice the waves for the same LDS.
-template <class R, int TW, int W, bool GATED, int XN, bool CAP = false, bool SPLIT = false>
+template <class R, int TW, int W, bool GATED, int XN, bool CAP = false, bool SPLIT = false, bool TL = false>
 __global__ __launch_bounds__(64 * TW * W) void gemv_ring(BatchSet bs, const int8_t *__restrict__ qx,
                                                          const float *__restrict__ dx, uint32_t T,
                                                          float *__restrict__ ygated) {
@@ -837,7 +859,8 @@ __global__ __launch_bounds__(64 * TW * W) void gemv_ring(BatchSet bs, const int8
   using F = typename R::B;
   constexpr int NR = GATED && !SPLIT ? 2 : 1;  // weights per wave
   constexpr uint32_t XB = 512 * XN, WS = NR * R::WB, SLOT = XB + 256 + W * WS;
-  constexpr int PB = XN / 2 + 1 + NR * R::NDMA;  // DMA instructions per pair (W == 1)
+  static_assert(!TL || (R::TILED && !CAP), "tile images: the formats that have them, no capture");
+  constexpr int PB = XN / 2 + 1 + NR * (TL ? R::NDMA_T : R::NDMA);  // DMA instructions per pair (W == 1)
   static_assert(PB <= 63, "wait count beyond vmcnt's range");
   static_assert(TW == 1 || TW * 2 * SLOT >= NCHMAX * NR * 4 * 64 * sizeof(float), "chunk sums fit the ring");
   static_assert(TW * 2 * SLOT <= RING_LDS_MAX, "ring beyond the LDS");
@@ -870,6 +893,14 @@ __global__ __launch_bounds__(64 * TW * W) void gemv_ring(BatchSet bs, const int8
   if (GATED && !SPLIT) wbase[NR - 1] = bs.j[1].w;
   // DMA sources (the same rows of gate and up).
   const typename R::Src src = R::src(rb, n_in, tile * TROWS, n_out, lane);
+  // TL: the tile's images instead, IMG bytes per pair (the same tile of
+  // gate and up).
+  const uint8_t *tbase[NR];
+  if constexpr (TL) {
+    const size_t timg = (size_t)tile * (nb / 2) * R::IMG;
+    tbase[0] = (SPLIT && wave == 1 ? bs.j[1].wt : J.wt) + timg;
+    if (GATED && !SPLIT) tbase[NR - 1] = bs.j[1].wt + timg;
+  }
   // The activation DMAs this wave issues (W > 1: its share of them).
   constexpr int XD = XN / 2 / W;
   const int xd0 = W == 1 ? 0 : wave * XD;
@@ -893,7 +924,12 @@ __global__ __launch_bounds__(64 * TW * W) void gemv_ring(BatchSet bs, const int8
     for (int i = 0; i < XD; i++) lds_dma16(qx, xsrc[i] + 512 * sp, sl + 1024 * (xd0 + i));
     if (W == 1 || wave == 0) lds_dma4(dx, ssrc + 8 * sp, sl + XB);
 #pragma unroll
-    for (int r = 0; r < NR; r++) R::issue(wbase[r], src, sp, sl + wofs_w + r * R::WB, lane);
+    for (int r = 0; r < NR; r++) {
+      if constexpr (TL)
+        R::issue_tile(tbase[r], sp * R::IMG + 16 * lane, sl + wofs_w + r * R::WB, lane);
+      else
+        R::issue(wbase[r], src, sp, sl + wofs_w + r * R::WB, lane);
+    }
   };
   constexpr int NJ = 4;
   float acc[NR][NJ], tot[NR][NJ];
@@ -1088,7 +1124,7 @@ RingShape ring_shape(mdma_ctx *ctx, uint32_t tiles, uint32_t nch) {
   return {tw, 1};
 }
 
-template <class R, int TW, int W, bool GATED, int XN, bool SPLIT = false>
+template <class R, int TW, int W, bool GATED, int XN, bool SPLIT = false, bool TL = false>
 void ring_launch(mdma_ctx *ctx, const BatchSet &bs, uint32_t tiles, const int8_t *qx, const float *dx, uint32_t T,
                  float *yg) {
   hipEvent_t t0 = ctx->time_start, t1 = ctx->time_stop;
@@ -1099,15 +1135,15 @@ void ring_launch(mdma_ctx *ctx, const BatchSet &bs, uint32_t tiles, const int8_t
     if constexpr (SPLIT || ring_fits<R, TW, W, GATED, 16>())
       gemv_ring<R, TW, W, GATED, 16, true, SPLIT><<<grid, block, 0, ctx->stream>>>(bs, qx, dx, T, yg);
   } else if (t0 || t1) {
-    hipExtLaunchKernelGGL(gemv_ring<R, TW, W, GATED, XN, false, SPLIT>, grid, block, 0, ctx->stream, t0, t1, 0, bs, qx,
-                          dx, T, yg);
+    hipExtLaunchKernelGGL(gemv_ring<R, TW, W, GATED, XN, false, SPLIT, TL>, grid, block, 0, ctx->stream, t0, t1, 0, bs,
+                          qx, dx, T, yg);
   } else {
-    gemv_ring<R, TW, W, GATED, XN, false, SPLIT><<<grid, block, 0, ctx->stream>>>(bs, qx, dx, T, yg);
+    gemv_ring<R, TW, W, GATED, XN, false, SPLIT, TL><<<grid, block, 0, ctx->stream>>>(bs, qx, dx, T, yg);
   }
   hip_check(hipGetLastError(), "gemv ring launch");
 }
 
-template <class R, bool GATED, int XN>
+template <class R, bool GATED, int XN, bool TL>
 void ring_fmt(mdma_ctx *ctx, const BatchSet &bs, uint32_t tiles, const int8_t *qx, const float *dx, uint32_t T,
               float *yg) {
   const uint32_t nb = bs.n_in / 256, nch = nb < NCHMAX ? nb : NCHMAX;
@@ -1116,32 +1152,90 @@ void ring_fmt(mdma_ctx *ctx, const BatchSet &bs, uint32_t tiles, const int8_t *q
   // (ring_shape only picks shapes whose ring fits; the guards keep the
   // instantiations that would not out of the build.)
   if (sh.w == 4) {
-    if constexpr (ring_fits<R, 1, 4, GATED, XN>()) return ring_launch<R, 1, 4, GATED, XN>(ctx, bs, tiles, qx, dx, T, yg);
+    if constexpr (ring_fits<R, 1, 4, GATED, XN>()) return ring_launch<R, 1, 4, GATED, XN, false, TL>(ctx, bs, tiles, qx, dx, T, yg);
   } else if (GATED && sh.tw == 1) {
     // One wave per tile would hold gate and up alone: split them over a
     // pair (the same LDS as gate and up in one wave).
-    if constexpr (GATED) return ring_launch<R, 1, 2, GATED, XN, true>(ctx, bs, tiles, qx, dx, T, yg);
+    if constexpr (GATED) return ring_launch<R, 1, 2, GATED, XN, true, TL>(ctx, bs, tiles, qx, dx, T, yg);
   } else if (sh.tw == 4) {
-    if constexpr (ring_fits<R, 4, 1, GATED, XN>()) return ring_launch<R, 4, 1, GATED, XN>(ctx, bs, tiles, qx, dx, T, yg);
+    if constexpr (ring_fits<R, 4, 1, GATED, XN>()) return ring_launch<R, 4, 1, GATED, XN, false, TL>(ctx, bs, tiles, qx, dx, T, yg);
   } else if (sh.tw == 2) {
-    if constexpr (ring_fits<R, 2, 1, GATED, XN>()) return ring_launch<R, 2, 1, GATED, XN>(ctx, bs, tiles, qx, dx, T, yg);
+    if constexpr (ring_fits<R, 2, 1, GATED, XN>()) return ring_launch<R, 2, 1, GATED, XN, false, TL>(ctx, bs, tiles, qx, dx, T, yg);
   }
-  ring_launch<R, 1, 1, GATED, XN>(ctx, bs, tiles, qx, dx, T, yg);
+  ring_launch<R, 1, 1, GATED, XN, false, TL>(ctx, bs, tiles, qx, dx, T, yg);
 }
 
-template <class R>
-void ring_dispatch(mdma_ctx *ctx, const BatchSet &bs, uint32_t tiles, bool gated, const int8_t *qx, const float *dx,
-                   uint32_t T, float *yg) {
+template <class R, bool TL>
+void ring_dispatch_tl(mdma_ctx *ctx, const BatchSet &bs, uint32_t tiles, bool gated, const int8_t *qx, const float *dx,
+                      uint32_t T, float *yg) {
   if (gated) {
-    if (T <= 8) ring_fmt<R, true, 8>(ctx, bs, tiles, qx, dx, T, yg);
-    else ring_fmt<R, true, 16>(ctx, bs, tiles, qx, dx, T, yg);
+    if (T <= 8) ring_fmt<R, true, 8, TL>(ctx, bs, tiles, qx, dx, T, yg);
+    else ring_fmt<R, true, 16, TL>(ctx, bs, tiles, qx, dx, T, yg);
   } else {
-    if (T <= 8) ring_fmt<R, false, 8>(ctx, bs, tiles, qx, dx, T, yg);
-    else ring_fmt<R, false, 16>(ctx, bs, tiles, qx, dx, T, yg);
+    if (T <= 8) ring_fmt<R, false, 8, TL>(ctx, bs, tiles, qx, dx, T, yg);
+    else ring_fmt<R, false, 16, TL>(ctx, bs, tiles, qx, dx, T, yg);
   }
+}
+// tl: every job's tile image is there (formats that have one).
+template <class R>
+void ring_dispatch(mdma_ctx *ctx, const BatchSet &bs, uint32_t tiles, bool gated, bool tl, const int8_t *qx,
+                   const float *dx, uint32_t T, float *yg) {
+  if constexpr (R::TILED) {
+    if (tl && !bs.j[0].dots) return ring_dispatch_tl<R, true>(ctx, bs, tiles, gated, qx, dx, T, yg);
+  }
+  ring_dispatch_tl<R, false>(ctx, bs, tiles, gated, qx, dx, T, yg);
+}
+
+// The Q6_K tile images of a prepared weight: for tile t (rows 16t..16t+15,
+// rows past the last repeating it, as the ring's clamped row-plane DMAs
+// read them) and block pair s, RQ6::IMG bytes at (t * pairs + s) * IMG
+// holding what RQ6::issue places in a slot: per plane (A, B, high bits)
+// byte 1024k + 16L is chunk ((L % 8) ^ (r / 2)) of row r = 8k + L / 8's 128
+// bytes of the pair, then byte 16L (L < 32) of the scale piece is row L / 2's
+// 16 scale bytes of block 2s + L % 2, then row n's d word (the f16 d of
+// blocks 2s and 2s + 1) at 4n. One thread per 16 bytes of image.
+__global__ __launch_bounds__(256) void tile_repack_q6_kernel(const uint8_t *__restrict__ w, uint8_t *__restrict__ out,
+                                                             uint32_t n_out, uint32_t n_in, uint64_t chunks) {
+  constexpr uint32_t CPI = RQ6::IMG / 16;  // 16-byte chunks per image
+  const uint64_t idx = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= chunks) return;
+  const uint32_t pairs = n_in / 512, U = n_in / 64, c = (uint32_t)(idx % CPI);
+  const uint64_t img = idx / CPI;
+  const uint32_t t = (uint32_t)(img / pairs), sp = (uint32_t)(img % pairs);
+  const size_t rb = BQ6::row_bytes(n_in);
+  auto row = [&](uint32_t r) { return w + (size_t)min(16 * t + r, n_out - 1) * rb; };
+  uint4 v;
+  if (c < 3 * 128) {
+    const uint32_t pl = c / 128, k = (c % 128) / 64, L = c % 64, r = 8 * k + L / 8;
+    v = *reinterpret_cast<const uint4 *>(row(r) + 16 * U * pl + 128 * sp + 16 * ((L % 8) ^ (r / 2)));
+  } else if (c < 3 * 128 + 32) {
+    const uint32_t L = c - 3 * 128;
+    v = *reinterpret_cast<const uint4 *>(row(L >> 1) + 48 * U + 32 * sp + 16 * (L & 1));
+  } else {
+    const uint32_t j = c - (3 * 128 + 32);  // rows 4j..4j+3
+    uint32_t d[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) d[q] = *reinterpret_cast<const uint32_t *>(row(4 * j + q) + 52 * U + 4 * sp);
+    v = make_uint4(d[0], d[1], d[2], d[3]);
+  }
+  *reinterpret_cast<uint4 *>(out + 16 * idx) = v;
 }
 
 }  // namespace
+
+uint64_t batch_tile_bytes(int32_t dtype, uint64_t n_out, uint64_t n_in) {
+  if (dtype != DT_Q6_K || !n_out || !n_in || n_in % 512) return 0;
+  return (n_out + TROWS - 1) / TROWS * (n_in / 512) * RQ6::IMG;
+}
+
+void launch_tile_repack(mdma_ctx *ctx, int32_t dtype, uint64_t n_out, uint64_t n_in, const uint8_t *w,
+                        uint8_t *out) {
+  const uint64_t chunks = batch_tile_bytes(dtype, n_out, n_in) / 16;
+  if (!chunks) return;
+  tile_repack_q6_kernel<<<dim3((uint32_t)((chunks + 255) / 256)), dim3(256), 0, ctx->stream>>>(
+      w, out, (uint32_t)n_out, (uint32_t)n_in, chunks);
+  hip_check(hipGetLastError(), "tile repack launch");
+}
 
 // Prepared-layout row bytes (the formats' row_bytes, on the host).
 static uint64_t batch_row_bytes(int32_t dt, uint64_t n_in) {
@@ -1173,6 +1267,7 @@ void launch_gemv_batch(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, bool gate
   uint32_t tiles = 0;
   for (int i = 0; i < (gated ? 2 : n_jobs); i++) {
     bs.j[i].w = jobs[i].w;
+    bs.j[i].wt = nullptr;
     bs.j[i].y = jobs[i].y;
     bs.j[i].dots = jobs[i].dots;
     bs.j[i].n_out = (uint32_t)jobs[i].n_out;
@@ -1188,9 +1283,17 @@ void launch_gemv_batch(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, bool gate
   for (int i = 0; i < (gated ? 2 : n_jobs); i++)
     ring = ring && jobs[i].n_out * batch_row_bytes(dt, n_in) < (1ull << 32);
   if (ring) {
-    if (dt == DT_Q4_K) ring_dispatch<RQ4>(ctx, bs, tiles, gated, qx, dx, t, ygated);
-    else if (dt == DT_Q6_K) ring_dispatch<RQ6>(ctx, bs, tiles, gated, qx, dx, t, ygated);
-    else ring_dispatch<RQ8>(ctx, bs, tiles, gated, qx, dx, t, ygated);
+    // Q6_K weights' tile images (made here at a weight's first such call
+    // when the context asks for them): contiguous DMA per pair instead of
+    // 128-byte row pieces (the 4096x14336 Q6_K at 8 tokens 15.3 -> 12.6 us).
+    bool tl = dt == DT_Q6_K && !jobs[0].dots;
+    for (int i = 0; tl && i < (gated ? 2 : n_jobs); i++) {
+      bs.j[i].wt = batch_tile(ctx, jobs[i]);
+      tl = bs.j[i].wt != nullptr;
+    }
+    if (dt == DT_Q4_K) ring_dispatch<RQ4>(ctx, bs, tiles, gated, false, qx, dx, t, ygated);
+    else if (dt == DT_Q6_K) ring_dispatch<RQ6>(ctx, bs, tiles, gated, tl, qx, dx, t, ygated);
+    else ring_dispatch<RQ8>(ctx, bs, tiles, gated, false, qx, dx, t, ygated);
     return;
   }
   if (dt == DT_Q4_K) launch_fmt<BQ4>(ctx, bs, tiles, gated, qx, dx, t, ygated);

@@ -66,6 +66,12 @@ struct mdma_buf {
   // dtype and shape the first op that reads them supplies; that op repacks
   // them into the prepared layout (see prepare_weight).
   bool repack_pending = false;
+  // A Q6_K weight's tile images for the batch GEMV (gemv_batch.hip), made
+  // at its first batch call when the context's batch layout is on; freed
+  // with the buffer or when its bytes are written again.
+  char *tile = nullptr;
+  uint64_t tile_charged = 0;
+  bool tile_stale = false;  // its bytes were written since (set aside under capture)
 };
 
 struct mdma_ctx {
@@ -75,6 +81,8 @@ struct mdma_ctx {
   mdma::Ledger budget[2];  // MDMA_DOMAIN_DEVICE, MDMA_DOMAIN_HOST
   int act_mode = MDMA_ACT_F32;
   bool norm_fusion = true;  // one-token int8 decode: attention rmsnorm fused into the GEMVs around it
+  bool batch_layout = false;  // mdma_gfx950_set_batch_layout
+  std::vector<mdma_buf *> tiled;  // buffers holding tile images
   std::string label;
   uint64_t total_bytes = 0;
   int cu_count = 0;
@@ -200,6 +208,8 @@ struct GemvJob {
   // n_in / 32 otherwise); the f16-path GEMM stores its block dot times the
   // Q4_K sub-block scale, the integer it forms.
   int32_t *dots = nullptr;
+  // The weight's buffer (for its batch tile images), or null.
+  mdma_buf *src = nullptr;
 };
 // Sub-blocks per row in the block-dot capture layout.
 inline uint64_t dot_subs(int32_t dtype, uint64_t n_in) { return dtype == DT_Q6_K ? n_in / 16 : n_in / 32; }
@@ -236,6 +246,18 @@ bool launch_gemv_i8_x(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, bool gated
 bool gemv_batch_ok(const GemvJob *jobs, int n_jobs, uint64_t T);
 void launch_gemv_batch(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, bool gated, const float *x, uint64_t T,
                        float *ygated);
+// Tokens from which int8-mode GEMVs of prepared rows go to the batch kernel.
+constexpr uint64_t BATCH_MIN_TOKENS = 3;
+// The batch kernel's tile images of a prepared weight (Q6_K, rows of whole
+// 512-column pairs; 0 bytes otherwise), the kernel that writes them, and
+// the job's images (made now when the context's batch layout is on and the
+// call may allocate; null if the job has none).
+uint64_t batch_tile_bytes(int32_t dtype, uint64_t n_out, uint64_t n_in);
+void launch_tile_repack(mdma_ctx *ctx, int32_t dtype, uint64_t n_out, uint64_t n_in, const uint8_t *w, uint8_t *out);
+const uint8_t *batch_tile(mdma_ctx *ctx, const GemvJob &job);
+// Frees the tile images of every buffer whose bytes overlap [p, p + bytes).
+void drop_tiles(mdma_ctx *ctx, const void *p, uint64_t bytes);
+void free_tile(mdma_ctx *ctx, mdma_buf *b);
 // pro: one token in the int8 mode, x quantized by the GEMV's prologue.
 // The rmsnorm of a Llama layer's residual stream fused into the GEMVs on
 // either side of it (one token, int8 mode): res/ssq for the GEMV that

@@ -183,7 +183,9 @@ struct Weight {
   uint64_t rows = 0, cols = 0;
   mdma_buf *buf = nullptr;
   GemvJob job(float *y) const {
-    return GemvJob{dtype, reinterpret_cast<const uint8_t *>(buf->ptr), rows, cols, y, buf->layout};
+    GemvJob j{dtype, reinterpret_cast<const uint8_t *>(buf->ptr), rows, cols, y, buf->layout};
+    j.src = buf;
+    return j;
   }
 };
 
@@ -204,6 +206,11 @@ struct mdma_model {
   mdma_buf *output_norm = nullptr;
   std::vector<Layer> layers;
   uint64_t weight_bytes = 0;
+  // The batch GEMV's tile images of the Q6_K matrices (made at their first
+  // batched call once a session of BATCH_MIN_TOKENS sequences or more
+  // turns the context's batch layout on); reserved by that session.
+  uint64_t tile_bytes = 0;
+  bool tiles_reserved = false;
   uint64_t budget = 0;  // 0 = unlimited (NativeMemoryBudget limit)
   uint64_t reserved = 0;
   std::vector<mdma_buf *> owned;
@@ -565,6 +572,7 @@ int mdma_gfx950_model_load(mdma_ctx *ctx, const char *path, uint64_t budget_byte
       const GgufTensor &t = kv.second;
       const uint64_t n = gfx950_layout_dtype(t.dtype) ? t.rows * gfx950_row_bytes(t.dtype, t.cols) : t.bytes;
       m->weight_bytes += (n + 255) / 256 * 256;
+      if (kv.first != "token_embd.weight") m->tile_bytes += batch_tile_bytes(t.dtype, t.rows, t.cols);
     }
     reserve(m.get(), m->weight_bytes);  // Model::load_reserved: before any upload
     std::vector<uint8_t> tmp;
@@ -609,7 +617,7 @@ int mdma_gfx950_model_plan(const mdma_model *m, uint64_t capacity, uint64_t batc
     if (!m || !out) shape_fail("model_plan: null argument");
     if (!batch) batch = 1;
     mdma_memory_plan p{};
-    p.weight_bytes = m->weight_bytes;
+    p.weight_bytes = m->weight_bytes + (batch >= BATCH_MIN_TOKENS ? m->tile_bytes : 0);
     p.kv_bytes = kv_bytes(m->cfg, capacity, batch);
     p.workspace_bytes = workspace_bytes(m->cfg, tokens > batch ? tokens : batch, batch, capacity * batch);
     p.headroom_bytes = DEVICE_HEADROOM;
@@ -645,9 +653,16 @@ int mdma_gfx950_session_new(mdma_model *m, uint64_t capacity, uint64_t batch, ui
     const mdma_model_config &c = m->cfg;
     const uint64_t n_ids = capacity * batch;
     const uint64_t bytes = kv_bytes(c, capacity, batch) + workspace_bytes(c, s->rows, batch, n_ids);
+    // Batched sessions read the Q6_K matrices' tile images (reserved once
+    // for the model; the images themselves follow at their first use).
+    const uint64_t tiles = batch >= BATCH_MIN_TOKENS && !m->tiles_reserved ? m->tile_bytes : 0;
     std::lock_guard<std::recursive_mutex> lk(m->ctx->lock);
-    reserve(m, bytes);
+    reserve(m, bytes + tiles);
     s->reserved = bytes;
+    if (batch >= BATCH_MIN_TOKENS) {
+      m->tiles_reserved = true;
+      m->ctx->batch_layout = true;
+    }
     const uint64_t kvw = c.n_kv_heads * c.head_dim;
     for (uint64_t i = 0; i < c.n_layers; i++) {
       s->kc.push_back(alloc_or_throw(m->ctx, batch * capacity * kvw * 2, MDMA_POOL_KV, s->owned));

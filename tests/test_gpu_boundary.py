@@ -157,6 +157,37 @@ def test_budget_charges_context_scratch_growth():
             be.close()
 
 
+def test_budget_refusing_tile_images_keeps_row_planes():
+    """With the batch layout on, a Q6_K weight's tile images are charged to
+    the device budget at its first batched call: a quota one byte short of
+    them leaves the call on the row planes (same bits, no error, nothing
+    charged for them); a quota that holds them shows their bytes."""
+    rows, k, T = 64, 2048, 8
+    raw = synth.weight(Q6K, rows, k, 740)
+    x = synth.normal_f32(T * k, 741)
+    tile = len(raw)  # 16-row tiles of 512-column pairs: the GGUF bytes
+    out, grow = [], None
+    for extra in (None, -1, 0):
+        be = fresh()
+        try:
+            if extra is not None:
+                be.set_buffer_budget(device=held + grow + tile + extra)
+            w = be.upload_weight(raw, Q6K, (rows, k))
+            xb, yb = be.f32_buf(x), be.alloc(T * rows * 4)
+            held = be.buffer_usage(DOMAIN_DEVICE)[0]
+            be.set_batch_layout(extra is not None)
+            be.qmatmul_i8(w, xb, yb)
+            used = be.buffer_usage(DOMAIN_DEVICE)[0] - held
+            if extra is None:
+                grow = used  # the int8 activation buffer's growth alone
+            else:
+                assert used == grow + (tile if extra == 0 else 0), (extra, used, grow)
+            out.append(be.download_f32(yb).copy())
+        finally:
+            be.close()
+    assert all(np.array_equal(o.view(np.uint32), out[0].view(np.uint32)) for o in out)
+
+
 def test_insufficient_memory_before_any_allocation(backend, tmp_path):
     p = str(tmp_path / "tiny.gguf")
     llama_synth.write(p, llama_synth.TINYSTORIES, llama_synth.Q8_ALL, 1)

@@ -15,6 +15,7 @@ from conftest import abs_dot, assert_parity, f32_exact
 from ties import near_tie_x
 from mdma_amd import synth
 from mdma_amd import backend as backend_mod
+from mdma_amd.backend import DOMAIN_DEVICE
 from mdma_amd.backend import LAYOUT_GFX950, POOL_WEIGHTS, QWeight, ShapeMismatch, pack_weight
 from oracle import ffi
 
@@ -228,18 +229,25 @@ def test_batch_ring_equals_staged(backend, dtype):
     blocks (one to eight chunks, one to four waves splitting a tile, chunks
     that start inside a pair of blocks), workgroups of 4 tiles sharing the
     activations (with waves past the last tile, and tiles of two weights in
-    one workgroup), the gated gate/up and the fused three-weight call. The oracle side of this kernel is
-    test_i8_mode_batched and test_i8_mode_batched_llama3_8b_shapes."""
+    one workgroup), the gated gate/up and the fused three-weight call. The
+    ring runs twice: on the row planes and, with the batch layout on, on the
+    Q6_K weights' tile images (made at each weight's first call here). The
+    oracle side of this kernel is test_i8_mode_batched and
+    test_i8_mode_batched_llama3_8b_shapes."""
     def both(fn):
         out = []
-        for kind in (backend_mod.BATCH_AUTO, backend_mod.BATCH_STAGED):
+        for kind, tiles in ((backend_mod.BATCH_AUTO, True), (backend_mod.BATCH_AUTO, False),
+                            (backend_mod.BATCH_STAGED, False)):
             backend.set_batch_kernel(kind)
+            backend.set_batch_layout(tiles)
             out.append(fn())
         backend.set_batch_kernel(backend_mod.BATCH_AUTO)
+        backend.set_batch_layout(False)
         return out
 
-    def same(a, b, what):
-        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), what
+    def same(a, b, c, what):
+        assert np.array_equal(a.view(np.uint32), c.view(np.uint32)), ("tile images", what)
+        assert np.array_equal(b.view(np.uint32), c.view(np.uint32)), ("row planes", what)
 
     backend.set_act_mode(backend_mod.ACT_I8)
     try:
@@ -250,8 +258,8 @@ def test_batch_ring_equals_staged(backend, dtype):
             raw = synth.weight(dtype, rows, k, 60 + rows)
             for T in (5, 8, 9, 15):
                 x = synth.normal_f32(T * k, 61 + T)
-                a, b = both(lambda: run_qmatmul(backend, dtype, raw, rows, k, x, "i8"))
-                same(a, b, (rows, k, T))
+                a, b, c = both(lambda: run_qmatmul(backend, dtype, raw, rows, k, x, "i8"))
+                same(a, b, c, (rows, k, T))
         # Gate/up: 96 rows (one tile per workgroup, waves split its columns)
         # and 24592 rows (1537 tiles, four per workgroup, the last one
         # alone). Fused QKV: 96 rows each, then 16400 + 4104 + 4088 rows
@@ -274,10 +282,39 @@ def test_batch_ring_equals_staged(backend, dtype):
                 return np.concatenate([backend.download_f32(o) for o in outs])
 
             for fn in ((gate_up, qkv) if shapes[0] == shapes[2] else (qkv,)):
-                a, b = both(fn)
-                same(a, b, (fn.__name__, shapes, k, T))
+                a, b, c = both(fn)
+                same(a, b, c, (fn.__name__, shapes, k, T))
     finally:
         backend.set_act_mode(backend_mod.ACT_F32)
+
+
+def test_batch_tile_images_follow_rewrites(backend):
+    """A Q6_K weight's tile images are made at its first batched call (with
+    the batch layout on) and charged to the device ledger by exactly the
+    weight's GGUF bytes (16-row tiles of 512-column pairs, rows a multiple of
+    16); rewriting the weight's bytes frees them, and the next call reads
+    the new bytes (made again from them)."""
+    rows, k, T = 64, 2048, 8
+    raws = [synth.weight(Q6K, rows, k, 880 + i) for i in range(2)]
+    x = synth.normal_f32(T * k, 882)
+    want = [run_qmatmul(backend, Q6K, r, rows, k, x, "i8") for r in raws]  # row planes (layout off)
+    w = backend.upload_weight(raws[0], Q6K, (rows, k))
+    xb, yb = backend.f32_buf(x), backend.alloc(T * rows * 4)
+    backend.set_batch_layout(True)
+    try:
+        before = backend.buffer_usage(DOMAIN_DEVICE)[0]
+        backend.qmatmul_i8(w, xb, yb)
+        assert backend.buffer_usage(DOMAIN_DEVICE)[0] - before == len(raws[0])
+        assert np.array_equal(backend.download_f32(yb).reshape(T, rows), want[0])
+        # The prepared bytes of the second weight, written over the first.
+        backend.upload(w.buf, 0, backend_mod.pack_weight(raws[1], Q6K, (rows, k)))
+        assert backend.buffer_usage(DOMAIN_DEVICE)[0] == before
+        backend.qmatmul_i8(w, xb, yb)
+        assert np.array_equal(backend.download_f32(yb).reshape(T, rows), want[1])
+        w.buf.close()
+        assert backend.buffer_usage(DOMAIN_DEVICE)[0] < before
+    finally:
+        backend.set_batch_layout(False)
 
 
 @pytest.mark.parametrize("group", [32, 256])
