@@ -135,7 +135,7 @@ int mdma_gfx950_set_act_mode(mdma_ctx *ctx, int mode);
  * Default on; off runs the separate norm kernel (for A/B measurement and
  * the parity test of the fused path). */
 int mdma_gfx950_set_norm_fusion(mdma_ctx *ctx, int on);
-/* Extra: the int8 mode's prefill GEMM kernel (calls of 16 or more tokens).
+/* Extra: the int8 mode's prefill GEMM kernel (calls of 64 or more tokens).
  * AUTO (default) takes the f16-path GEMM where it covers the weight (Q4_K
  * rows of whole 256-column blocks) and the int8 MFMA GEMM elsewhere; I8
  * forces the int8 MFMA GEMM (for A/B measurement and parity of both).
@@ -144,8 +144,8 @@ int mdma_gfx950_set_norm_fusion(mdma_ctx *ctx, int on);
 typedef enum { MDMA_PREFILL_AUTO = 0, MDMA_PREFILL_I8 = 1 } mdma_prefill_kernel;
 int mdma_gfx950_set_prefill_kernel(mdma_ctx *ctx, int kind);
 /* Extra: the int8 mode's batched decode GEMV kernel (calls of 3 tokens or
- * more on prepared-layout weights that the prefill GEMM does not take, up
- * to 16 tokens per launch). AUTO (default) streams each block of
+ * more on prepared-layout weights that the prefill GEMM does not take (3 to
+ * 63 tokens), up to 16 tokens per launch). AUTO (default) streams each block of
  * the weight tile, activations and scales through a per-wave LDS ring by
  * DMA; STAGED loads them into registers and stages the weights in LDS (for
  * A/B measurement and the equality test: both give the same bits). */
