@@ -686,7 +686,6 @@ struct RQ4 {
   static constexpr uint32_t WB = 2 * P::BYTES + 512;
   static constexpr int NDMA = 2 * P::NDMA + 1;
   static constexpr int NDMA_T = NDMA;
-  static constexpr uint32_t IMG = 0;
   struct Src {
     uint32_t pl[P::NDMA], hd, U;
   };
@@ -798,7 +797,6 @@ struct RQ8 {
   static constexpr uint32_t WB = 2 * P::BYTES + 512;
   static constexpr int NDMA = 2 * P::NDMA + 1;
   static constexpr int NDMA_T = NDMA;
-  static constexpr uint32_t IMG = 0;
   struct Src {
     uint32_t pl[P::NDMA], hd, U;
   };
