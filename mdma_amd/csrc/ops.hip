@@ -466,7 +466,11 @@ __device__ __forceinline__ void attn_load(AttnTile<C> &t, const uint16_t *__rest
   }
 }
 
-template <int G, int C, bool QUANT, bool ROPE>
+// ONE: every run is one tile (the host's choice whenever the runs cover the
+// keys a tile each): no second tile buffer, 92 VGPRs instead of 181 at G = 4,
+// so five workgroups fit a CU instead of two (batch-8 decode at 768-key
+// caches: 640 workgroups in one wave of the chip).
+template <int G, int C, bool QUANT, bool ROPE, bool ONE = false>
 __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict__ q, uint16_t *__restrict__ K,
                                                          uint16_t *__restrict__ V, float *__restrict__ o,
                                                          float *__restrict__ part, uint32_t *__restrict__ cnt,
@@ -651,9 +655,9 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
     }
     lds_barrier();  // sc is rewritten by the next tile
   };
-  if (t1 - t0 == 1) {
+  if (ONE || t1 - t0 == 1) {
     process(ta, t0);
-  } else {
+  } else if constexpr (!ONE) {
     for (uint32_t tile = t0; tile < t1; tile += 2) {
       attn_load<C>(tb, K, V, min(tile + 1, t1 - 1), visible, kv_row, hd, lane, wave);
       process(ta, tile);
@@ -1051,10 +1055,15 @@ bool attn_impl(mdma_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t
     const AttnQ8 a8 = q8 ? *q8 : AttnQ8{nullptr, nullptr, nullptr};
     const AttnRope ar = rope ? *rope : AttnRope{nullptr, nullptr, nullptr, 0};
     const dim3 grid((uint32_t)n_kv_heads, (uint32_t)n_splits, (uint32_t)n_q);
-#define MDMA_ATT_GO(GG, CC, QQ, RR)                                                                            \
-  attn_split_kernel<GG, CC, QQ, RR><<<grid, dim3(256), 0, ctx->stream>>>(                                      \
+#define MDMA_ATT_GO1(GG, CC, QQ, RR, OO)                                                                       \
+  attn_split_kernel<GG, CC, QQ, RR, OO><<<grid, dim3(256), 0, ctx->stream>>>(                                  \
       q, k, v, o, part, cnt, prefix, (uint32_t)hd, (uint32_t)n_q_heads, (uint32_t)n_kv_heads, scale, seq_stride, \
       (uint32_t)tpw, a8, ar)
+#define MDMA_ATT_GO(GG, CC, QQ, RR)          \
+  do {                                       \
+    if (tpw == 1) MDMA_ATT_GO1(GG, CC, QQ, RR, true);  \
+    else MDMA_ATT_GO1(GG, CC, QQ, RR, false); \
+  } while (0)
 #define MDMA_ATT(GG, CC)                                \
   do {                                                  \
     if (q8 && rope) MDMA_ATT_GO(GG, CC, true, true);    \
@@ -1074,6 +1083,7 @@ bool attn_impl(mdma_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t
     }
 #undef MDMA_ATT
 #undef MDMA_ATT_GO
+#undef MDMA_ATT_GO1
     hip_check(hipGetLastError(), "attn launch");
     return true;
   }
