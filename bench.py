@@ -253,10 +253,13 @@ Q6_SHAPES = {"q6k_head": (128256, 4096), "q6k_down": (4096, 14336)}
 def q6k_gemvs(be, ev, reps):
     """Kernel-only rates (dispatch timestamps) of the Q6_K GEMVs, weights
     rotated over >= 1 GiB of copies; int8 mode at T = 1, 4, 8 and the f32
-    mode at T = 1. Bytes: weights + activations + outputs, each once."""
+    mode at T = 1. Bytes: weights + activations + outputs, each once. The
+    batched calls read the weights' tile images, as batched decode sessions
+    do (made at each copy's first batched call, before the timed ones)."""
     from mdma_amd import synth
     from mdma_amd.backend import ACT_F32, ACT_I8
 
+    be.set_batch_layout(True)
     out = {}
     for name, (rows, k) in Q6_SHAPES.items():
         raw = synth.weight(Q6K, rows, k, SEED + 7)
@@ -287,6 +290,7 @@ def q6k_gemvs(be, ev, reps):
         for w in ws:
             w.buf.close()
     be.set_act_mode(ACT_I8)
+    be.set_batch_layout(False)
     return out
 
 
@@ -551,6 +555,8 @@ def main():
                          "kernel trace whose dispatches are exactly the ones the roofline averages)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the prefill GEMM leg (for profiler traces and counters of the GEMMs)")
+    ap.add_argument("--q6-only", action="store_true",
+                    help="only the Q6_K GEMV leg (head and down at 1, 4 and 8 tokens; for profiler traces)")
     ap.add_argument("--eager-decode", action="store_true",
                     help="end-to-end decode steps launched eagerly instead of replayed from a captured HIP graph "
                          "(the same kernels; for profilers that do not follow graph replays)")
@@ -571,6 +577,10 @@ def main():
         print(json.dumps({"e2e_llama3_8b": e2e_decode(be), "device": be.device_label()}), flush=True)
         return
     ev = HipEvents()
+    if args.q6_only:
+        print(json.dumps({"q6k_gemv": q6k_gemvs(be, ev, max(2, args.reps // 4)), "device": be.device_label()}),
+              flush=True)
+        return
     if args.prefill_only:
         print(json.dumps({"prefill_gemm_i8": prefill_gemms(be, ev, max(2, args.reps // 4)),
                           "device": be.device_label()}), flush=True)
