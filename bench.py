@@ -488,14 +488,16 @@ def cpu_e2e(path_8b, cores):
     return out
 
 
-def mdma_bench(be, path, init_seconds, prompt_len=512, steps=256, repetitions=2):
+def mdma_bench(be, path, init_seconds, prompt_len=512, steps=256, repetitions=2, execution="eager"):
     """The reference's mdma-bench protocol (src/bin/mdma-bench.rs:19-116) on
     the same model: load with a memory budget, then one untimed warmup trial
     and `repetitions` timed trials, each on a fresh KV cache: a prefill of
     prompt_len tokens, then `steps` decode steps, each downloading the
-    logits and taking the host's greedy argmax (the eager decoder), in the
-    int8 mode. Its JSON fields; the prompt is seeded token ids (no
-    tokenizer)."""
+    logits and taking the host's greedy argmax, in the int8 mode. Its
+    MDMA_BENCH_DECODER choices (:23-25, :72-90): "eager" steps
+    Model::forward; "executor" steps the backend's decoder (here the graph
+    decode executor), made outside the timer. Its JSON fields; the prompt is
+    seeded token ids (no tokenizer)."""
     from mdma_amd import synth
     from mdma_amd.backend import ACT_I8
     from mdma_amd.model import Model
@@ -514,17 +516,25 @@ def mdma_bench(be, path, init_seconds, prompt_len=512, steps=256, repetitions=2)
         a = time.perf_counter()
         logits = s.prefill(tokens, 0)
         pre = time.perf_counter() - a
-        a = time.perf_counter()
-        for i in range(steps):
-            logits = s.forward(int(np.argmax(logits)), prompt_len + i)
-        dec = time.perf_counter() - a
+        if execution == "executor":
+            d = s.decoder()
+            a = time.perf_counter()
+            for i in range(steps):
+                logits = d.forward(int(np.argmax(logits)), prompt_len + i)
+            dec = time.perf_counter() - a
+            d.close()
+        else:
+            a = time.perf_counter()
+            for i in range(steps):
+                logits = s.forward(int(np.argmax(logits)), prompt_len + i)
+            dec = time.perf_counter() - a
         assert np.all(np.isfinite(logits))
         s.close()
         if trial > 0:
             trials.append({"prefill_seconds": round(pre, 5), "decode_seconds": round(dec, 5),
                            "prefill_tokens_per_second": round(prompt_len / pre, 1),
                            "decode_tokens_per_second": round(steps / dec, 1)})
-    out = {"backend": "gfx950", "architecture": "llama", "model": os.path.basename(path), "execution": "eager",
+    out = {"backend": "gfx950", "architecture": "llama", "model": os.path.basename(path), "execution": execution,
            "artifact_bytes": os.path.getsize(path), "backend_init_seconds": round(init_seconds, 4),
            "load_seconds": round(load_s, 3), "prompt_tokens": prompt_len, "decode_steps": steps,
            "context_capacity": cap, "kv_element_bytes": be.kv_elem_bytes(),
@@ -535,7 +545,7 @@ def mdma_bench(be, path, init_seconds, prompt_len=512, steps=256, repetitions=2)
                                            max(plan_p.workspace_bytes, plan_d.workspace_bytes)),
            "warmup_trials": 1, "trials": trials}
     m.close()
-    print(f"[bench] mdma-bench: {trials}", file=sys.stderr, flush=True)
+    print(f"[bench] mdma-bench ({execution}): {trials}", file=sys.stderr, flush=True)
     return out
 
 
@@ -640,6 +650,7 @@ def main():
             w.buf.close()
     e2e = None if args.no_e2e else e2e_decode(be)
     protocol = None if args.no_e2e else mdma_bench(be, E2E_PATH, init_s)
+    protocol_x = None if args.no_e2e else mdma_bench(be, E2E_PATH, init_s, execution="executor")
     cpu = None if args.no_cpu else cpu_baseline(wl.raws, args.cpu_seconds)
     if cpu is not None and not args.no_e2e:
         cpu["e2e"] = cpu_e2e(E2E_PATH, cpu["cores"])
@@ -664,6 +675,7 @@ def main():
         "prefill_gemm_i8": gemm,
         "e2e_llama3_8b": e2e,
         "mdma_bench": protocol,
+        "mdma_bench_executor": protocol_x,
         "copy_probe": probe,
         "device": be.device_label(),
     }
