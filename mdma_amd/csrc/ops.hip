@@ -490,7 +490,10 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
   sgpr_ready(q, K, V, o, part, cnt, prefix, hd, n_q_heads, n_kv_heads, scale, seq_stride, tpw);
   if constexpr (QUANT) sgpr_ready(q8.q, q8.d, q8.s16);
   if constexpr (ROPE) sgpr_ready(rp.k, rp.v, rp.tab, rp.pos, rp.pos_dev);
-  const uint32_t kvh = blockIdx.x, split = blockIdx.y, i = blockIdx.z, n_splits = gridDim.y;
+  // sub workgroups per KV head (the grid's x is n_kv_heads * sub), each with
+  // G of the head's query heads: the first query head is blockIdx.x * G.
+  const uint32_t sub = gridDim.x / n_kv_heads, kvh = blockIdx.x / sub;
+  const uint32_t split = blockIdx.y, i = blockIdx.z, n_splits = gridDim.y;
   // The new row's position and the tiles per run. From device memory in a
   // captured step: the runs are then those the host would have chosen for
   // this length (tiles per run ceil(tiles / n_splits); the grid's n_splits
@@ -511,7 +514,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
   const uint32_t tiles = (visible + ATT_TILE - 1) / ATT_TILE, t0 = split * tpw;
   if (t0 >= tiles) return;  // this query's keys end before the run
   const uint32_t t1 = min(t0 + tpw, tiles), live = (tiles + tpw - 1) / tpw;
-  const uint32_t kv_row = n_kv_heads * hd, qh0 = kvh * G;
+  const uint32_t kv_row = n_kv_heads * hd, qh0 = blockIdx.x * G;
   const uint32_t tid = threadIdx.x, lane = tid & 63, l4 = lane & 3;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   K += (size_t)i * seq_stride + (size_t)kvh * hd;
@@ -567,7 +570,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
     const uint32_t vw = (uint32_t)f2h(vn2.x) | ((uint32_t)f2h(vn2.y) << 16);
     knew[tid] = kw;
     vnew[tid] = vw;
-    if (jn / ATT_TILE >= t0 && jn / ATT_TILE < t1) {
+    if (jn / ATT_TILE >= t0 && jn / ATT_TILE < t1 && blockIdx.x % sub == 0) {
       *reinterpret_cast<uint32_t *>(K + (size_t)jn * kv_row + 2 * tid) = kw;
       *reinterpret_cast<uint32_t *>(V + (size_t)jn * kv_row + 2 * tid) = vw;
     }
@@ -713,7 +716,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (tid == 0) {
-      uint32_t *c = cnt + ((size_t)i * n_kv_heads + kvh) * CNT_STRIDE;
+      uint32_t *c = cnt + ((size_t)i * gridDim.x + blockIdx.x) * CNT_STRIDE;
       const uint32_t prev = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       last = prev == live - 1;
       // every run of this (query, KV head) has arrived: ready for the next call
@@ -1033,7 +1036,7 @@ bool attn_impl(mdma_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t
   uint16_t *k = const_cast<uint16_t *>(kc), *v = const_cast<uint16_t *>(vc);
   const float scale = 1.0f / sqrtf((float)hd);
   const uint32_t prefix = (uint32_t)(seq_stride ? kv_len - 1 : kv_len - n_q);
-  const uint64_t G = n_kv_heads ? n_q_heads / n_kv_heads : 0, C = (hd + 127) / 128;
+  const uint64_t GQ = n_kv_heads ? n_q_heads / n_kv_heads : 0, C = (hd + 127) / 128;
   // Runs of tiles per (query, KV head): enough workgroups to cover the chip
   // (about MDMA_ATT_WG_TARGET), at least one tile and at most ATT_MAX_RUNS
   // runs each; long prompts use one run per query.
@@ -1044,6 +1047,20 @@ bool attn_impl(mdma_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t
   if (!n_splits) n_splits = 1;
   const uint64_t tpw = (tiles + n_splits - 1) / n_splits;
   n_splits = tiles ? (tiles + tpw - 1) / tpw : 1;
+  // Few workgroups (short contexts, few queries): a KV head's query heads
+  // split over MDMA_ATT_SUB workgroups, each reading the same K/V tiles with
+  // a share of the heads (less work per workgroup on the critical path).
+#ifndef MDMA_ATT_SUB
+#define MDMA_ATT_SUB 2
+#endif
+#ifndef MDMA_ATT_SUB_WG_PER_CU
+#define MDMA_ATT_SUB_WG_PER_CU 2
+#endif
+  uint64_t sub = 1;
+  if (MDMA_ATT_SUB > 1 && GQ % MDMA_ATT_SUB == 0 && (!q8 || (GQ / MDMA_ATT_SUB * hd) % 256 == 0) &&
+      pairs * n_splits * MDMA_ATT_SUB <= MDMA_ATT_SUB_WG_PER_CU * (uint64_t)ctx->cu_count)
+    sub = MDMA_ATT_SUB;
+  const uint64_t G = GQ / sub;
   const uint64_t part_bytes = n_splits > 1 ? n_q * n_q_heads * n_splits * (hd + 2) * 4 : 0;
   const bool split_ok = hd % 8 == 0 && hd <= 256 && (G == 1 || G == 2 || G == 4 || G == 8) && G * C <= 8 &&
                         n_splits < 65536 && n_q < 65536 && part_bytes <= (256ull << 20);
@@ -1051,10 +1068,12 @@ bool attn_impl(mdma_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t
   if (rope && !(split_ok && n_q && kv_len && hd % 8 == 0 && (seq_stride || n_q == 1))) return false;
   if (split_ok && n_q && kv_len) {
     float *part = part_bytes ? reinterpret_cast<float *>(scratch(ctx, part_bytes)) : nullptr;
-    uint32_t *cnt = part_bytes ? attn_counters(ctx, n_q * n_kv_heads) : nullptr;
+    // Counters for the most sub-groups any launch of this shape may take (a
+    // captured step and the eager one may choose differently).
+    uint32_t *cnt = part_bytes ? attn_counters(ctx, n_q * n_kv_heads * MDMA_ATT_SUB) : nullptr;
     const AttnQ8 a8 = q8 ? *q8 : AttnQ8{nullptr, nullptr, nullptr};
     const AttnRope ar = rope ? *rope : AttnRope{nullptr, nullptr, nullptr, 0};
-    const dim3 grid((uint32_t)n_kv_heads, (uint32_t)n_splits, (uint32_t)n_q);
+    const dim3 grid((uint32_t)(n_kv_heads * sub), (uint32_t)n_splits, (uint32_t)n_q);
 #define MDMA_ATT_GO1(GG, CC, QQ, RR, OO)                                                                       \
   attn_split_kernel<GG, CC, QQ, RR, OO><<<grid, dim3(256), 0, ctx->stream>>>(                                  \
       q, k, v, o, part, cnt, prefix, (uint32_t)hd, (uint32_t)n_q_heads, (uint32_t)n_kv_heads, scale, seq_stride, \
