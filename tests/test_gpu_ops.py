@@ -138,6 +138,34 @@ def test_attention_over_f16_cache(backend, hd, nq, nkv, n_q, kv_len):
     np.testing.assert_allclose(got[:q.size], want, rtol=2e-5, atol=2e-6)
 
 
+@pytest.mark.parametrize("hd,G", [(64, 2), (128, 4)])
+def test_attention_head_split_same_bits(backend, hd, G):
+    """A launch with few workgroups splits each KV head's query heads over
+    two workgroups; one with many does not. The same heads' outputs must be
+    the same bits either way: 2 KV heads (split) against 200 KV heads whose
+    first 2 hold the same q, K and V (not split), one 64-key tile per run in
+    both (384 keys: 6 runs)."""
+    kv_len, small, big = 384, 2, 200
+    q_b = synth.normal_f32(big * G * hd, 11)
+    k_b = f16r(synth.normal_f32(kv_len * big * hd, 12)).reshape(kv_len, big * hd)
+    v_b = f16r(synth.normal_f32(kv_len * big * hd, 13)).reshape(kv_len, big * hd)
+    outs = []
+    for nkv in (small, big):
+        q = q_b[:nkv * G * hd]
+        k = np.ascontiguousarray(k_b[:, :nkv * hd]).reshape(-1)
+        v = np.ascontiguousarray(v_b[:, :nkv * hd]).reshape(-1)
+        kb, vb = backend.alloc(k.size * 2), backend.alloc(v.size * 2)
+        backend.upload(kb, 0, k.astype(np.float16))
+        backend.upload(vb, 0, v.astype(np.float16))
+        o = backend.alloc(q.size * 4)
+        backend.attn(backend.f32_buf(q), KvView(kb, vb, kv_len), AttnSpec(hd, nkv * G, nkv), o)
+        outs.append(backend.download_f32(o))
+    assert np.array_equal(outs[0], outs[1][:small * G * hd])
+    want = ffi.attention(q_b[:small * G * hd], np.ascontiguousarray(k_b[:, :small * hd]).reshape(-1),
+                         np.ascontiguousarray(v_b[:, :small * hd]).reshape(-1), kv_len, hd, small * G, small)
+    np.testing.assert_allclose(outs[0], want, rtol=2e-5, atol=2e-6)
+
+
 def test_attention_hand_computed(backend):
     # src/backend/cpu/tests.rs:186-214 (values exact in f16).
     kb, vb = backend.alloc(8), backend.alloc(8)
