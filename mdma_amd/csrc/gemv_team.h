@@ -562,6 +562,16 @@ __global__ __launch_bounds__(team_wg(PRO, TW)) void gemv_team(TeamSet ts, const 
     }
   };
   double ssq_lane = 0.0;  // residual mode: this lane's stored rows' squares
+  // Multi-wave teams, one token, residual mode: the residual value of the row
+  // this lane of wave 0 stores at the end (row r_begin + lane), loaded now so
+  // its latency is not at the kernel's tail. Unconditional and clamped (a load
+  // under a branch waits for every load in flight); without res the output
+  // itself is read and the value unused.
+  float res_pre = 0.f;
+  if constexpr (TW > 1 && !GATED && TT == 1 && !F32) {
+    const float *rp = ts.res ? ts.res : J.y;
+    res_pre = rp[min(r_begin + (uint32_t)lane, r_last)];
+  }
   auto consume = [&](const typename F::W(&w)[PL][NR], int it) {
     const uint32_t r0 = r_begin + it * R;
     Acc s[NR][TT];
@@ -816,7 +826,8 @@ __global__ __launch_bounds__(team_wg(PRO, TW)) void gemv_team(TeamSet ts, const 
         } else {
           float yv = (float)g;
           if (ts.res) {  // uniform; one token
-            yv = ts.res[row] + yv;
+            // i == lane here (ITERS * R <= 64 rows per team at one token)
+            yv = ((TT == 1 && !F32 && ITERS * R <= 64) ? res_pre : ts.res[row]) + yv;
             ssq_lane += (double)(yv * yv);
           }
           J.y[(size_t)t * n_out + row] = yv;
