@@ -819,7 +819,9 @@ __device__ __forceinline__ int32_t total_key(float f) {
 // logits of each row to (key, index, non-finite flag), argmax_final_kernel
 // the chunks of a row; ties go to the larger index (max_by keeps the last
 // maximum, src/sampler.rs:64-74) at both levels.
-constexpr uint32_t ARGMAX_CHUNK = 4096;
+// Chunks of 1024 logits: four per thread, loaded together (a latency-bound
+// pass: the chain per thread is what it costs).
+constexpr uint32_t ARGMAX_CHUNK = 1024;
 struct ArgPart {
   int32_t key;
   uint32_t idx, bad;
@@ -833,10 +835,16 @@ __global__ __launch_bounds__(256) void argmax_part_kernel(const float *__restric
   int32_t bk = INT32_MIN;
   uint32_t bi = 0, bad = 0;
   bool have = false;
-  for (uint64_t i = c0 + threadIdx.x; i < c1; i += 256) {
-    const float v = xr[i];
-    bad |= !isfinite(v);
-    const int32_t k = total_key(v);
+  constexpr int PER = ARGMAX_CHUNK / 256;
+  float v[PER];
+#pragma unroll
+  for (int j = 0; j < PER; j++) v[j] = xr[min(c0 + threadIdx.x + 256 * j, n - 1)];  // clamped, unconditional
+#pragma unroll
+  for (int j = 0; j < PER; j++) {  // increasing index: ties go to the later one
+    const uint64_t i = c0 + threadIdx.x + 256 * j;
+    if (i >= c1) break;
+    bad |= !isfinite(v[j]);
+    const int32_t k = total_key(v[j]);
     if (!have || k >= bk) {
       bk = k;
       bi = (uint32_t)i;
