@@ -393,6 +393,53 @@ def e2e_decode(be, n_prompt=512, n_gen=256, batches=(1, 8), path=E2E_PATH):
     return out
 
 
+CONFIG1_SEED, CONFIG1_PROMPT_SEED = 1, 1001
+
+
+def config1_model(path):
+    """Config 1: TinyStories-15M geometry, every linear Q8_0, random init
+    (seed CONFIG1_SEED) written as GGUF; the CPU leg writes the same file."""
+    from mdma_amd import llama_synth
+
+    llama_synth.write(path, llama_synth.TINYSTORIES, llama_synth.Q8_ALL, CONFIG1_SEED)
+
+
+def e2e_config1(be, n_gen=64):
+    """Config 1 on the GPU: the seeded 8-token prompt, 64 greedy tokens, in
+    the f32-activation mode (whose tokens must be the CPU backend's) and the
+    int8 mode; decode replays the captured step. Tokens are returned for the
+    comparison with the CPU leg."""
+    import tempfile
+
+    from mdma_amd import synth
+    from mdma_amd.backend import ACT_F32, ACT_I8
+    from mdma_amd.model import Model
+
+    out, toks = {}, {}
+    prompt = synth.tokens(8, 32000, CONFIG1_PROMPT_SEED)
+    with tempfile.TemporaryDirectory() as d:
+        p = os.path.join(d, "tiny.gguf")
+        config1_model(p)
+        for mode, name in ((ACT_F32, "f32"), (ACT_I8, "i8")):
+            be.set_act_mode(mode)
+            m = Model(be, p)
+            s = m.session(8 + n_gen, 1, 8)
+            s.generate(prompt[None, :], 4)  # warm
+            s.reset()
+            t, secs = s.generate(prompt[None, :], n_gen)
+            dec = secs[1:]
+            out[name] = {"prompt_tokens": 8, "decode_tokens": len(dec), "prefill_ms": round(secs[0] * 1e3, 3),
+                         "decode_tok_s": round(len(dec) / dec.sum(), 1),
+                         "decode_ms_per_step_p50": round(float(np.median(dec)) * 1e3, 4),
+                         "tokens_sha1": hashlib.sha1(np.ascontiguousarray(t[0]).tobytes()).hexdigest()[:16]}
+            toks[name] = t[0].astype(np.uint32)
+            s.close()
+            m.close()
+    be.set_act_mode(ACT_I8)
+    print(f"[bench] config 1 on the GPU: {out}", file=sys.stderr, flush=True)
+    return out, toks
+
+
 def copy_probe(be, ev, nbytes=1 << 30, reps=10):
     """Device-to-device copy rate (bytes read + bytes written per second) of
     hipMemcpyAsync on the library's stream: the achievable-bandwidth
@@ -470,14 +517,15 @@ def cpu_e2e(path_8b, cores):
     out = {"cores": cores, "cpu": cpu_model(), "kind": "port"}
     with tempfile.TemporaryDirectory() as d:
         p1 = os.path.join(d, "tiny.gguf")
-        llama_synth.write(p1, llama_synth.TINYSTORIES, llama_synth.Q8_ALL, 1)
+        config1_model(p1)
         r = gguf.Reader(p1)
-        ffi.llama_timed(r, synth.tokens(8, 32000, 1001), 4, threads=cores)  # warm
-        _, secs = ffi.llama_timed(r, synth.tokens(8, 32000, 1001), 64, threads=cores)
+        ffi.llama_timed(r, synth.tokens(8, 32000, CONFIG1_PROMPT_SEED), 4, threads=cores)  # warm
+        toks, secs = ffi.llama_timed(r, synth.tokens(8, 32000, CONFIG1_PROMPT_SEED), 64, threads=cores)
         dec = secs[1:]
         out["config1"] = {"prompt_tokens": 8, "decode_tokens": 63, "prefill_ms": round(secs[0] * 1e3, 2),
                           "decode_tok_s": round(len(dec) / dec.sum(), 1),
-                          "decode_ms_per_step_p50": round(float(np.median(dec)) * 1e3, 2)}
+                          "decode_ms_per_step_p50": round(float(np.median(dec)) * 1e3, 2),
+                          "tokens": np.asarray(toks, dtype=np.uint32)}
     r = gguf.Reader(path_8b)
     _, secs = ffi.llama_timed(r, synth.tokens(16, 128256, SEED + 60), 4, threads=cores)
     dec = secs[1:]
@@ -649,11 +697,16 @@ def main():
         for w in L.values():
             w.buf.close()
     e2e = None if args.no_e2e else e2e_decode(be)
+    c1, c1_toks = (None, None) if args.no_e2e else e2e_config1(be)
     protocol = None if args.no_e2e else mdma_bench(be, E2E_PATH, init_s)
     protocol_x = None if args.no_e2e else mdma_bench(be, E2E_PATH, init_s, execution="executor")
     cpu = None if args.no_cpu else cpu_baseline(wl.raws, args.cpu_seconds)
     if cpu is not None and not args.no_e2e:
         cpu["e2e"] = cpu_e2e(E2E_PATH, cpu["cores"])
+        # Greedy tokens of the same model and prompt: the GPU's f32 mode
+        # against the CPU backend's (BASELINE's exact-match requirement).
+        cpu_toks = cpu["e2e"]["config1"].pop("tokens")
+        c1["f32_tokens_equal_cpu"] = bool(np.array_equal(c1_toks["f32"], cpu_toks))
     f = results["f32"]
     line = {
         "metric": "Q4_K GEMV HBM GB/s (% of peak) @8B shapes; decode tok/s, 1 MI355X",
@@ -674,6 +727,7 @@ def main():
         "q6k_gemv": q6,
         "prefill_gemm_i8": gemm,
         "e2e_llama3_8b": e2e,
+        "e2e_config1": c1,
         "mdma_bench": protocol,
         "mdma_bench_executor": protocol_x,
         "copy_probe": probe,
