@@ -495,11 +495,24 @@ def cpu_baseline(raws, budget_s):
         el = time.perf_counter() - t0
         if el >= budget_s:
             break
+    # Prefill on the CPU (CpuBackend::qmatmul over 64 token rows, each weight
+    # row dequantized once and dotted with every token): a bounded sample of
+    # the first prefill GEMM shape, 64 of its 512 tokens, f32 activations.
+    pm, pk, pn = 64, 4096, 14336
+    xp = rng.standard_normal(pm * pk).astype(np.float32)
+    t0 = time.perf_counter()
+    reps = 0
+    while reps < 2 or time.perf_counter() - t0 < 2.0:
+        ffi.qmatmul(Q4K, raws["gate"], pn, pk, xp, threads=cores)
+        reps += 1
+    pel = (time.perf_counter() - t0) / reps
     return {"value": round(gemv_bytes * n / el / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
             "cpu": cpu_model(),
             "sample": f"{n} full Q4_K layer steps (the same 7 GEMV shapes, f32 activations), {el:.1f} s, "
                       "oracle/oracle.c restating CpuBackend::qmatmul (row-parallel, sequential f32 dot)",
-            "ms_per_step": round(el * 1e3 / n, 2)}
+            "ms_per_step": round(el * 1e3 / n, 2),
+            "prefill": {"GOPS": round(2.0 * pm * pk * pn / pel / 1e9, 2), "ms": round(pel * 1e3, 2),
+                        "sample": f"Q4_K {pn}x{pk} over {pm} token rows (f32 activations), {reps} calls"}}
 
 
 def cpu_e2e(path_8b, cores):
