@@ -119,31 +119,31 @@ def test_gqa_q4km_greedy_and_batched_decode_match_oracle(backend, gqa):
     m.close()
 
 
-# 1230 prompt tokens: the decode at position 1230 sees 20 tiles of 64 keys,
-# split into runs of two tiles, so the new key sits in the second tile of the
+# Long prompts. At 1230 tokens the decode at position 1230 sees 20 tiles of 64
+# keys split into runs of two, so the new key sits in the second tile of the
 # last run (the fused RoPE attention's ping-pong loop substitutes it there).
-LONG_PROMPT = 1230
-
-
+# At 2150 it sees 34 tiles in runs of three, the last run a single tile
+# holding the new key.
 @pytest.fixture(scope="module")
 def gqa_long(tmp_path_factory):
     p = str(tmp_path_factory.mktemp("gguf") / "gqa_long.gguf")
-    llama_synth.write(p, dict(GQA_SMALL, n_ctx=2048), llama_synth.Q4_K_M, 5)
+    llama_synth.write(p, dict(GQA_SMALL, n_ctx=4096), llama_synth.Q4_K_M, 5)
     return p
 
 
-def test_long_context_decode_matches_oracle(backend, gqa_long):
+@pytest.mark.parametrize("long_prompt", [1230, 2150])
+def test_long_context_decode_matches_oracle(backend, gqa_long, long_prompt):
     backend.set_act_mode(ACT_F32)
     r = gguf.Reader(gqa_long)
-    p = synth.tokens(LONG_PROMPT, 2048, 2200)
+    p = synth.tokens(long_prompt, 2048, 2200)
     m = Model(backend, gqa_long)
-    s = m.session(LONG_PROMPT + 4, 1, LONG_PROMPT)
+    s = m.session(long_prompt + 4, 1, long_prompt)
     logits = s.prefill(p, 0)
     _, want = ffi.llama_generate(r, p, 1, kv_f16=True)
     np.testing.assert_allclose(logits, want, rtol=2e-3, atol=5e-4)  # f16 cache resolution, as above
     tok = int(np.argmax(logits))
     assert tok == int(np.argmax(want))
-    nxt = s.forward(tok, LONG_PROMPT)
+    nxt = s.forward(tok, long_prompt)
     _, want2 = ffi.llama_generate(r, p, 2, kv_f16=True)
     np.testing.assert_allclose(nxt, want2, rtol=2e-3, atol=5e-4)
     assert int(np.argmax(nxt)) == int(np.argmax(want2))
