@@ -815,8 +815,8 @@ __device__ __forceinline__ int32_t total_key(float f) {
   return b ^ (int32_t)(((uint32_t)(b >> 31)) >> 1);
 }
 
-// Greedy argmax in two passes: argmax_part_kernel reduces chunks of 4096
-// logits of each row to (key, index, non-finite flag), argmax_final_kernel
+// Greedy argmax in two passes: argmax_part_kernel reduces chunks of
+// ARGMAX_CHUNK logits of each row to (key, index, non-finite flag), argmax_final_kernel
 // the chunks of a row; ties go to the larger index (max_by keeps the last
 // maximum, src/sampler.rs:64-74) at both levels.
 // Chunks of 1024 logits: four per thread, loaded together (a latency-bound
