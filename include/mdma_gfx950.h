@@ -58,10 +58,21 @@ typedef enum { MDMA_LAYOUT_GGUF = 0, MDMA_LAYOUT_GFX950 = 1, MDMA_LAYOUT_ROCM_Q4
 /* MemoryDomain (src/memory/buffers.rs:5-10): the two ledgers of a BufferBudget. */
 typedef enum { MDMA_DOMAIN_DEVICE = 0, MDMA_DOMAIN_HOST = 1 } mdma_memory_domain;
 
-/* Activation mode of the decode GEMV: f32 activations (exact parity mode) or
- * int8 activations quantized per 256 with an f32 scale. The reference's
- * counterpart is the MDMA_HIP_F32 switch (src/backend/select.rs:49). */
-typedef enum { MDMA_ACT_F32 = 0, MDMA_ACT_I8 = 1 } mdma_act_mode;
+/* Activation mode of the quantized matmuls and the ops around them:
+ *  - MDMA_ACT_F32: f32 activations; every output the dot product rounded once
+ *    to f32 (closer to exact than the CPU's sequential sum);
+ *  - MDMA_ACT_I8: int8 activations quantized per 256 (decode) or per 32
+ *    (prefill GEMM) with an f32 scale;
+ *  - MDMA_ACT_F32_CPU: f32 activations in the CPU backend's arithmetic
+ *    order, bit-identical to it: each qmatmul output the sequential f32 sum,
+ *    from -0.0, of f32-rounded products of the dequantized row
+ *    (CpuBackend::qmatmul, src/backend/cpu.rs:46-48,335-368), and rmsnorm,
+ *    add_rmsnorm, silu_mul, ffn_gate_up and attn in the CPU's order with the
+ *    C library's expf (cpu.rs:50-60,388-402,447-458,530-590). A parity mode:
+ *    its sums are sequential chains, one lane per output row.
+ * The reference's counterpart is the MDMA_HIP_F32 switch
+ * (src/backend/select.rs:49). */
+typedef enum { MDMA_ACT_F32 = 0, MDMA_ACT_I8 = 1, MDMA_ACT_F32_CPU = 2 } mdma_act_mode;
 
 typedef struct mdma_ctx mdma_ctx;
 typedef struct mdma_buf mdma_buf;
@@ -307,6 +318,22 @@ int mdma_gfx950_graph_launch(mdma_ctx *ctx, mdma_graph *graph);
 void mdma_gfx950_graph_destroy(mdma_graph *graph);
 /* Pre-size the context scratch and int8-activation buffers so a later capture needs no growth. */
 int mdma_gfx950_reserve_scratch(mdma_ctx *ctx, uint64_t bytes);
+/* Graph replay parameters (ReplayParams, src/backend/rocm/graph.rs:12-15,
+ * read by the reference's *_graph kernels, src/backend/rocm/kernels/
+ * kernels.hip:385-410,620-640 and attention.hip:70-74): with params set (a
+ * device buffer of two uint32: token, position) the trait-level ops whose
+ * arguments change from one decode step to the next read them from device
+ * memory when they run, so one captured forward_device replays every step:
+ *  - embed reads its single token id from params[0] (n_ids must be 1; the
+ *    host ids are not read);
+ *  - rope, rope_kv_write and kv_write rotate at position params[1] and write
+ *    the cache rows at element params[1] * row width (the pos and
+ *    elem_offset arguments are not read; n_tokens must be 1);
+ *  - attn attends to params[1] + 1 keys (kv->len is not read; its launch is
+ *    sized for `capacity` keys, which the caches must hold, and n_q must be 1).
+ * Set while capturing a decode step, then cleared (params NULL); a graph
+ * launch replays the step for the values params holds at that time. */
+int mdma_gfx950_set_replay_params(mdma_ctx *ctx, const mdma_buf *params, uint64_t capacity);
 /* Extra (no counterpart in the reference; for benchmarks and profiling):
  * the next GEMV kernel this context launches on prepared weights is
  * dispatched with these hipEvent_t handles (either may be NULL), which its

@@ -24,7 +24,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmdma_gfx
 POOL_WEIGHTS, POOL_KV, POOL_SCRATCH = 0, 1, 2
 LAYOUT_GGUF, LAYOUT_GFX950, LAYOUT_ROCM_Q4K_V3 = 0, 1, 2
 DOMAIN_DEVICE, DOMAIN_HOST = 0, 1
-ACT_F32, ACT_I8 = 0, 1
+ACT_F32, ACT_I8, ACT_F32_CPU = 0, 1, 2  # mdma_act_mode
 PREFILL_AUTO, PREFILL_I8 = 0, 1  # mdma_prefill_kernel
 BATCH_AUTO, BATCH_STAGED = 0, 1  # mdma_batch_kernel
 
@@ -89,7 +89,7 @@ _SIGS = {
     "attn": [_P, _P, _P, _P, _P], "greedy": [_P, _P, _U64, _U64, _P],
     "quantize_act": [_P, _P, _U64, _P, _P, _P], "block_dot_i32": [_P, _P, _P, _P],
     "graph_begin": [_P], "graph_end": [_P, _P], "graph_launch": [_P, _P], "graph_destroy": [_P],
-    "reserve_scratch": [_P, _U64],
+    "reserve_scratch": [_P, _U64], "set_replay_params": [_P, _P, _U64],
     "time_next_gemv": [_P, _P, _P],
     "prepared_bytes": [_I32, _U64, _U64],
     "pack_weight": [_I32, _U64, _U64, _P, _U64, _P, _U64],
@@ -425,6 +425,14 @@ class Gfx950Backend:
 
     def reserve_scratch(self, nbytes: int):
         _check(lib().mdma_gfx950_reserve_scratch(self.ctx, nbytes))
+
+    def set_replay_params(self, params: "Buf | None", capacity: int = 0):
+        """ReplayParams (src/backend/rocm/graph.rs:12-15): with params (a
+        device buffer of two uint32, token and position) set, embed, rope,
+        rope_kv_write, kv_write and attn read them from device memory when
+        they run; None clears it."""
+        _check(lib().mdma_gfx950_set_replay_params(self.ctx, params.handle if params is not None else None,
+                                                   capacity))
 
     def capture(self, fn) -> "Graph":
         """Record the launches fn() makes into a replayable HIP graph."""

@@ -127,6 +127,8 @@ void attach_dots(mdma_ctx *ctx, GemvJob *jobs, int n, uint64_t T) {
 void run_gemv(mdma_ctx *ctx, int mode, const GemvJob *jobs, int n, const float *x, uint64_t T) {
   if (mode == MDMA_ACT_I8)
     launch_gemv_i8(ctx, jobs, n, x, T);
+  else if (mode == MDMA_ACT_F32_CPU)
+    for (int i = 0; i < n; i++) launch_gemv_seq(ctx, jobs[i], x, T);
   else
     launch_gemv_f32(ctx, jobs, n, x, T);
 }
@@ -150,6 +152,24 @@ void fill_rope(float *tab, uint64_t p0, uint64_t p1, uint64_t hd, float theta) {
       tab[(p * half + i) * 2 + 0] = cosf(a);
       tab[(p * half + i) * 2 + 1] = sinf(a);
     }
+}
+
+// A setting that selects kernels: a graph captured under the old value
+// would replay the old kernels, so a change bumps the buffer epoch and such
+// graphs refuse to replay (a decoder then captures again).
+template <class T>
+void set_kernel_choice(mdma_ctx *ctx, T &field, T value) {
+  if (field == value) return;
+  field = value;
+  ctx->buf_epoch++;
+}
+
+// The device position of a replayed decode step (params[1]), or null outside
+// replay; a replayed step has one token.
+const uint32_t *replay_pos(const mdma_ctx *ctx, uint64_t n_tokens, const char *op) {
+  if (!ctx->replay) return nullptr;
+  if (n_tokens != 1) shape_fail(fmt("%s: a replayed decode step has one token", op));
+  return ctx->replay + 1;
 }
 
 void check_rope(const mdma_rope_spec *spec, uint64_t qe, uint64_t ke, uint64_t n_tokens,
@@ -548,9 +568,10 @@ int mdma_gfx950_buffer_usage(mdma_ctx *ctx, int domain, uint64_t *used, uint64_t
 int mdma_gfx950_set_act_mode(mdma_ctx *ctx, int mode) {
   return guarded([&] {
     need(ctx, "set_act_mode");
-    if (mode != MDMA_ACT_F32 && mode != MDMA_ACT_I8) shape_fail("set_act_mode: unknown mode");
+    if (mode != MDMA_ACT_F32 && mode != MDMA_ACT_I8 && mode != MDMA_ACT_F32_CPU)
+      shape_fail("set_act_mode: unknown mode");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
-    ctx->act_mode = mode;
+    set_kernel_choice(ctx, ctx->act_mode, mode);
   });
 }
 
@@ -580,7 +601,7 @@ int mdma_gfx950_set_prefill_kernel(mdma_ctx *ctx, int kind) {
     need(ctx, "set_prefill_kernel");
     if (kind != MDMA_PREFILL_AUTO && kind != MDMA_PREFILL_I8) shape_fail("set_prefill_kernel: unknown kind");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
-    ctx->prefill_kernel = kind;
+    set_kernel_choice(ctx, ctx->prefill_kernel, kind);
   });
 }
 
@@ -589,7 +610,7 @@ int mdma_gfx950_set_batch_kernel(mdma_ctx *ctx, int kind) {
     need(ctx, "set_batch_kernel");
     if (kind != MDMA_BATCH_AUTO && kind != MDMA_BATCH_STAGED) shape_fail("set_batch_kernel: unknown kind");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
-    ctx->batch_kernel = kind;
+    set_kernel_choice(ctx, ctx->batch_kernel, kind);
   });
 }
 
@@ -597,7 +618,7 @@ int mdma_gfx950_set_batch_layout(mdma_ctx *ctx, int on) {
   return guarded([&] {
     need(ctx, "set_batch_layout");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
-    ctx->batch_layout = on != 0;
+    set_kernel_choice(ctx, ctx->batch_layout, on != 0);
   });
 }
 
@@ -605,7 +626,7 @@ int mdma_gfx950_set_norm_fusion(mdma_ctx *ctx, int on) {
   return guarded([&] {
     need(ctx, "set_norm_fusion");
     std::lock_guard<std::recursive_mutex> g(ctx->lock);
-    ctx->norm_fusion = on != 0;
+    set_kernel_choice(ctx, ctx->norm_fusion, on != 0);
   });
 }
 
@@ -687,6 +708,9 @@ int mdma_gfx950_buf_view(mdma_buf *parent, uint64_t offset, uint64_t len, mdma_b
     b->layout = parent->layout;
     b->owner = false;
     b->repack_pending = false;  // a window of raw bytes is read by the raw kernels
+    // The view points into the parent's raw bytes: the parent stays raw (its
+    // repack would free them under the view) and the raw kernels read it.
+    parent->repack_pending = false;
     *out = b;
   });
 }
@@ -885,13 +909,18 @@ int mdma_gfx950_ffn_gate_up(mdma_ctx *ctx, const mdma_qweight *gate, const mdma_
     // as the trait allows. When the scratch is larger than T*n_out (the
     // default impl would then run silu_mul over the whole scratch length),
     // fall back to that exact sequence so the contract holds bit for bit.
+    // The CPU-order mode runs that sequence too (its SiLU is the CPU's).
     uint64_t gse = f32_elems("ffn_gate_up", gate_scratch), use = f32_elems("ffn_gate_up", up_scratch);
-    if (gse != T * gate->rows || use != gse) {
+    if (gse != T * gate->rows || use != gse || ctx->act_mode == MDMA_ACT_F32_CPU) {
       if (use != gse) shape_fail("silu_mul: input lengths differ");
       run_gemv(ctx, ctx->act_mode, &gj, 1, xp, T);
       run_gemv(ctx, ctx->act_mode, &uj, 1, xp, T);
-      launch_silu_mul(ctx, reinterpret_cast<const float *>(gate_scratch->ptr),
-                      reinterpret_cast<const float *>(up_scratch->ptr), yp, gse);
+      const float *gp = reinterpret_cast<const float *>(gate_scratch->ptr),
+                  *up_p = reinterpret_cast<const float *>(up_scratch->ptr);
+      if (ctx->act_mode == MDMA_ACT_F32_CPU)
+        launch_silu_mul_seq(ctx, gp, up_p, yp, gse);
+      else
+        launch_silu_mul(ctx, gp, up_p, yp, gse);
       return;
     }
     if (ctx->act_mode == MDMA_ACT_I8)
@@ -912,16 +941,24 @@ int mdma_gfx950_embed(mdma_ctx *ctx, const mdma_qweight *table, const uint32_t *
     uint64_t oe = f32_elems("embed", out);
     // shape::embed (shape.rs:92-110).
     if (!n_ids) shape_fail("embed: no tokens");
-    need(ids, "embed");
     if (oe < n_ids * table->cols)
       shape_fail(fmt("embed: out has %llu elems, needs %llu", (unsigned long long)oe,
                      (unsigned long long)(n_ids * table->cols)));
+    same_ctx(ctx, table->buf, "embed");
+    same_ctx(ctx, out, "embed");
+    if (ctx->replay) {
+      // Graph replay: the token id is read from params[0] when the kernel
+      // runs (embed_gather_graph, src/backend/rocm/kernels/kernels.hip:385).
+      if (n_ids != 1) shape_fail("embed: a replayed decode step embeds one token");
+      launch_embed(ctx, table->dtype, table->buf->layout, reinterpret_cast<const uint8_t *>(table->buf->ptr),
+                   table->cols, ctx->replay, 1, reinterpret_cast<float *>(out->ptr));
+      return;
+    }
+    need(ids, "embed");
     for (uint64_t i = 0; i < n_ids; i++)
       if (ids[i] >= table->rows)
         shape_fail(fmt("embed: token_id %u out of range (vocab %llu)", ids[i],
                        (unsigned long long)table->rows));
-    same_ctx(ctx, table->buf, "embed");
-    same_ctx(ctx, out, "embed");
     no_capture(ctx, "embed");
     uint32_t *dev_ids = reinterpret_cast<uint32_t *>(scratch(ctx, n_ids * 4));
     hip_check(hipMemcpyAsync(dev_ids, ids, n_ids * 4, hipMemcpyHostToDevice, ctx->stream), "embed ids");
@@ -937,6 +974,7 @@ int mdma_gfx950_embed(mdma_ctx *ctx, const mdma_qweight *table, const uint32_t *
 // (the same values bit for bit as quantizing y there).
 static void rmsnorm_rows(mdma_ctx *ctx, const float *w, uint64_t dim, const float *a, const float *b, float *sum,
                          float *y, uint64_t rows, float eps) {
+  if (ctx->act_mode == MDMA_ACT_F32_CPU) return launch_rmsnorm_seq(ctx, w, dim, a, b, sum, y, rows, eps);
   if (ctx->act_mode == MDMA_ACT_I8 && rows < GEMM_MIN_TOKENS && launch_rmsnorm_q8(ctx, w, dim, a, b, sum, y, rows, eps))
     return;
   launch_rmsnorm(ctx, w, dim, a, b, sum, y, rows, eps);
@@ -976,9 +1014,13 @@ int mdma_gfx950_add_rmsnorm(mdma_ctx *ctx, const mdma_buf *w, const mdma_buf *a,
       // exact behaviour when sum is longer than a + b.
       launch_add(ctx, reinterpret_cast<const float *>(a->ptr), reinterpret_cast<const float *>(b->ptr),
                  reinterpret_cast<float *>(sum->ptr), ae);
-      launch_rmsnorm(ctx, reinterpret_cast<const float *>(w->ptr), dim,
-                     reinterpret_cast<const float *>(sum->ptr), nullptr, nullptr,
-                     reinterpret_cast<float *>(y->ptr), se / dim, eps);
+      if (ctx->act_mode == MDMA_ACT_F32_CPU)
+        launch_rmsnorm_seq(ctx, reinterpret_cast<const float *>(w->ptr), dim, reinterpret_cast<const float *>(sum->ptr),
+                           nullptr, nullptr, reinterpret_cast<float *>(y->ptr), se / dim, eps);
+      else
+        launch_rmsnorm(ctx, reinterpret_cast<const float *>(w->ptr), dim,
+                       reinterpret_cast<const float *>(sum->ptr), nullptr, nullptr,
+                       reinterpret_cast<float *>(y->ptr), se / dim, eps);
       return;
     }
     rmsnorm_rows(ctx, reinterpret_cast<const float *>(w->ptr), dim, reinterpret_cast<const float *>(a->ptr),
@@ -1008,8 +1050,12 @@ int mdma_gfx950_silu_mul(mdma_ctx *ctx, const mdma_buf *gate, const mdma_buf *up
     uint64_t ge = f32_elems("silu_mul", gate), ue = f32_elems("silu_mul", up), ye = f32_elems("silu_mul", y);
     if (ge != ue) shape_fail("silu_mul: input lengths differ");
     if (ye < ge) shape_fail("silu_mul: output too small");
-    launch_silu_mul(ctx, reinterpret_cast<const float *>(gate->ptr), reinterpret_cast<const float *>(up->ptr),
-                    reinterpret_cast<float *>(y->ptr), ge);
+    if (ctx->act_mode == MDMA_ACT_F32_CPU)
+      launch_silu_mul_seq(ctx, reinterpret_cast<const float *>(gate->ptr), reinterpret_cast<const float *>(up->ptr),
+                          reinterpret_cast<float *>(y->ptr), ge);
+    else
+      launch_silu_mul(ctx, reinterpret_cast<const float *>(gate->ptr), reinterpret_cast<const float *>(up->ptr),
+                      reinterpret_cast<float *>(y->ptr), ge);
   });
 }
 
@@ -1021,9 +1067,11 @@ int mdma_gfx950_rope(mdma_ctx *ctx, mdma_buf *q, mdma_buf *k, uint32_t pos, uint
     q8_invalidate(ctx);
     uint64_t qh, kh;
     check_rope(spec, f32_elems("rope", q), f32_elems("rope", k), n_tokens, &qh, &kh);
-    const float *tab = rope_table(ctx, pos + n_tokens - 1, spec->head_dim, spec->theta);
-    launch_rope(ctx, reinterpret_cast<float *>(q->ptr), n_tokens, qh, spec->head_dim, tab, pos);
-    launch_rope(ctx, reinterpret_cast<float *>(k->ptr), n_tokens, kh, spec->head_dim, tab, pos);
+    // Graph replay: position params[1], the table covering the capacity.
+    const uint32_t *pd = replay_pos(ctx, n_tokens, "rope");
+    const float *tab = rope_table(ctx, pd ? ctx->replay_cap - 1 : pos + n_tokens - 1, spec->head_dim, spec->theta);
+    launch_rope(ctx, reinterpret_cast<float *>(q->ptr), n_tokens, qh, spec->head_dim, tab, pos, pd);
+    launch_rope(ctx, reinterpret_cast<float *>(k->ptr), n_tokens, kh, spec->head_dim, tab, pos, pd);
   });
 }
 
@@ -1039,6 +1087,17 @@ int mdma_gfx950_kv_write(mdma_ctx *ctx, const mdma_buf *k, const mdma_buf *v, md
     range("kv_write", 0, n_elems * 4, f32_elems("kv_write", v) * 4);
     need(dst_k, "kv_write");
     need(dst_v, "kv_write");
+    if (ctx->replay) {
+      // Graph replay (kv_write_graph, src/backend/rocm/kernels/kernels.hip:404):
+      // the row at element params[1] * n_elems; the caches hold the capacity.
+      range("kv_write", 0, n_elems * 2 * ctx->replay_cap, dst_k->len);
+      range("kv_write", 0, n_elems * 2 * ctx->replay_cap, dst_v->len);
+      if (!n_elems) return;
+      launch_kv_write(ctx, reinterpret_cast<const float *>(k->ptr), reinterpret_cast<const float *>(v->ptr),
+                      reinterpret_cast<uint16_t *>(dst_k->ptr), reinterpret_cast<uint16_t *>(dst_v->ptr), n_elems,
+                      ctx->replay + 1);
+      return;
+    }
     range("kv_write", elem_offset * 2, n_elems * 2, dst_k->len);
     range("kv_write", elem_offset * 2, n_elems * 2, dst_v->len);
     if (!n_elems) return;
@@ -1061,6 +1120,22 @@ int mdma_gfx950_rope_kv_write(mdma_ctx *ctx, mdma_buf *q, mdma_buf *k, const mdm
     range("kv_write", 0, n_elems * 4, f32_elems("rope_kv_write", v) * 4);
     need(dst_k, "rope_kv_write");
     need(dst_v, "rope_kv_write");
+    const uint32_t *pd = replay_pos(ctx, n_tokens, "rope_kv_write");
+    if (pd) {
+      // Graph replay (rope_kv_graph, src/backend/rocm/kernels/kernels.hip:620):
+      // position params[1], rows at element params[1] * k's width; the
+      // caches hold the capacity.
+      if (n_elems != ke || f32_elems("rope_kv_write", v) != ke)
+        shape_fail("rope_kv_write: a replayed decode step writes k and v whole");
+      range("kv_write", 0, n_elems * 2 * ctx->replay_cap, dst_k->len);
+      range("kv_write", 0, n_elems * 2 * ctx->replay_cap, dst_v->len);
+      const float *tab = rope_table(ctx, ctx->replay_cap - 1, spec->head_dim, spec->theta);
+      launch_rope_kv_write(ctx, reinterpret_cast<float *>(q->ptr), qh, reinterpret_cast<const float *>(k->ptr),
+                           reinterpret_cast<const float *>(v->ptr), kh, spec->head_dim, 1, tab, 0,
+                           reinterpret_cast<uint16_t *>(dst_k->ptr), reinterpret_cast<uint16_t *>(dst_v->ptr), 0, 1,
+                           pd);
+      return;
+    }
     range("kv_write", elem_offset * 2, n_elems * 2, dst_k->len);
     range("kv_write", elem_offset * 2, n_elems * 2, dst_v->len);
     const float *tab = rope_table(ctx, pos + n_tokens - 1, spec->head_dim, spec->theta);
@@ -1099,19 +1174,27 @@ int mdma_gfx950_attn(mdma_ctx *ctx, const mdma_buf *q, const mdma_kv_view *kv, c
       shape_fail("attn: q heads are not a multiple of KV heads");
     if (spec->head_dim > 256) shape_fail("attn: head_dim above max_head_dim 256");
     uint64_t n_q = qe / per;
-    if (n_q > kv->len) shape_fail("attn: n_q exceeds kv.len");
-    uint64_t need_e = kv->len * spec->n_kv_heads * spec->head_dim;
+    // Graph replay (attn_decode_graph, src/backend/rocm/kernels/kernels.hip:695):
+    // params[1] + 1 keys, the launch sized for the capacity.
+    const uint32_t *pd = replay_pos(ctx, n_q, "attn");
+    const uint64_t len = pd ? ctx->replay_cap : kv->len;
+    if (n_q > len) shape_fail("attn: n_q exceeds kv.len");
+    uint64_t need_e = len * spec->n_kv_heads * spec->head_dim;
     if (kv->k->len / 2 < need_e || kv->v->len / 2 < need_e) shape_fail("attn: K/V too short for kv.len");
     if (oe < qe) shape_fail("attn: o too small");
     const float *qp = reinterpret_cast<const float *>(q->ptr);
     const uint16_t *kp = reinterpret_cast<const uint16_t *>(kv->k->ptr), *vp = reinterpret_cast<const uint16_t *>(kv->v->ptr);
     float *op = reinterpret_cast<float *>(o->ptr);
+    if (ctx->act_mode == MDMA_ACT_F32_CPU) {
+      launch_attn_seq(ctx, qp, kp, vp, op, n_q, len, spec->head_dim, spec->n_q_heads, spec->n_kv_heads, 0, pd);
+      return;
+    }
     // In the int8 mode, decode-sized outputs also leave their int8 form in
     // the activation cache for a qmatmul that reads o next.
     if (ctx->act_mode == MDMA_ACT_I8 && n_q < GEMM_MIN_TOKENS &&
-        launch_attn_q8(ctx, qp, kp, vp, op, n_q, kv->len, spec->head_dim, spec->n_q_heads, spec->n_kv_heads))
+        launch_attn_q8(ctx, qp, kp, vp, op, n_q, len, spec->head_dim, spec->n_q_heads, spec->n_kv_heads, 0, pd))
       return;
-    launch_attn(ctx, qp, kp, vp, op, n_q, kv->len, spec->head_dim, spec->n_q_heads, spec->n_kv_heads);
+    launch_attn(ctx, qp, kp, vp, op, n_q, len, spec->head_dim, spec->n_q_heads, spec->n_kv_heads, 0, pd);
   });
 }
 
@@ -1284,6 +1367,24 @@ int mdma_gfx950_time_next_gemv(mdma_ctx *ctx, void *start_event, void *stop_even
     no_capture(ctx, "time_next_gemv");
     ctx->time_start = static_cast<hipEvent_t>(start_event);
     ctx->time_stop = static_cast<hipEvent_t>(stop_event);
+  });
+}
+
+int mdma_gfx950_set_replay_params(mdma_ctx *ctx, const mdma_buf *params, uint64_t capacity) {
+  return guarded([&] {
+    need(ctx, "set_replay_params");
+    std::lock_guard<std::recursive_mutex> g(ctx->lock);
+    if (!params) {
+      ctx->replay = nullptr;
+      ctx->replay_cap = 0;
+      return;
+    }
+    same_ctx(ctx, params, "set_replay_params");
+    if (params->len < 8) shape_fail("set_replay_params: params must hold two uint32 (token, position)");
+    if (reinterpret_cast<uintptr_t>(params->ptr) % 4) shape_fail("set_replay_params: params must be 4-byte aligned");
+    if (!capacity || capacity > 0xffffffffull) shape_fail("set_replay_params: capacity out of range");
+    ctx->replay = reinterpret_cast<const uint32_t *>(params->ptr);
+    ctx->replay_cap = capacity;
   });
 }
 

@@ -11,7 +11,7 @@
 // is every Q4_K weight value q * sc (q <= 15, sc <= 63: at most 945): each
 // product of the f16 MFMA is exact and each 32-column block's dot product,
 // at most 2^23 in magnitude, is summed exactly in its f32 accumulator. So
-// v_mfma_f32_32x32x16_f16 computes the same integer block dots as an int8
+// v_mfma_f32_16x16x32_f16 computes the same integer block dots as an int8
 // MFMA, but hands them over as exact f32 with the 6-bit sub-scale already
 // applied: the float epilogue is one FMA per output and block,
 //   part += s_x[m, b] * C_b[n, m]
@@ -35,7 +35,8 @@
 // (u = 2^-24) of the exact product of the quantized operands.
 //
 // Tiling: a 256-thread workgroup computes 128 weight rows x 128 tokens; each
-// of its 4 waves 64 x 64 (2 x 2 MFMA tiles of 32 x 32). The weight rows are
+// of its 4 waves 64 x 64 (4 x 4 MFMA tiles of 16 x 16, one 16x16x32 MFMA per
+// tile and 32-column block). The weight rows are
 // the MFMA's first operand, so each lane holds one token's column of a tile:
 // the activation scale s_x is a per-lane scalar, and each output of a lane
 // is one weight row. K advances 64 columns (one Q4_K sub-block pair) per

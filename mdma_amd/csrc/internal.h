@@ -125,6 +125,11 @@ struct mdma_ctx {
   // freed or replaced (scratch, int8 activations, counters, partials, RoPE
   // table); a graph captured under another epoch refuses to replay.
   uint64_t buf_epoch = 0;
+  // Graph replay parameters (mdma_gfx950_set_replay_params): device words
+  // [token, position] the trait-level decode ops read, and the KV capacity
+  // their launches are sized for; null when not set.
+  const uint32_t *replay = nullptr;
+  uint64_t replay_cap = 0;
   // This device's copy of the library's static scratch array (noalloc.hip),
   // from hipGetSymbolAddress at create.
   char *static_scratch = nullptr;
@@ -342,29 +347,50 @@ bool launch_rmsnorm_q8(mdma_ctx *ctx, const float *w, uint64_t dim, const float 
                        float *y, uint64_t rows, float eps);
 void launch_add(mdma_ctx *ctx, const float *a, const float *b, float *y, uint64_t n);
 void launch_silu_mul(mdma_ctx *ctx, const float *g, const float *u, float *y, uint64_t n);
+// pos_dev (a captured decode step, one position): the position is read from
+// device memory when the kernel runs, pos is not used, and kv_write's and
+// rope_kv_write's rows go to that position's row of dk / dv (which then
+// point at the cache's position 0).
 void launch_rope(mdma_ctx *ctx, float *x, uint64_t n_tokens, uint64_t heads, uint64_t hd,
-                 const float *tab, uint32_t pos);
+                 const float *tab, uint32_t pos, const uint32_t *pos_dev = nullptr);
 void launch_kv_write(mdma_ctx *ctx, const float *k, const float *v, uint16_t *dk, uint16_t *dv,
-                     uint64_t n);
+                     uint64_t n, const uint32_t *pos_dev = nullptr);
 // kv_stride: elements between consecutive tokens' cache rows (0 = kv_heads*hd,
 // contiguous); pos_step: position increment per token (1 in a sequence, 0
 // across the sequences of a decode batch).
 void launch_rope_kv_write(mdma_ctx *ctx, float *q, uint64_t q_heads, const float *k,
                           const float *v, uint64_t kv_heads, uint64_t hd, uint64_t n_tokens,
                           const float *tab, uint32_t pos, uint16_t *dk, uint16_t *dv,
-                          uint64_t kv_stride = 0, uint32_t pos_step = 1);
+                          uint64_t kv_stride = 0, uint32_t pos_step = 1, const uint32_t *pos_dev = nullptr);
 // seq_stride 0: causal over one sequence. Otherwise query i is sequence i's
 // single decode query over its own cache at k + i*seq_stride, kv_len keys.
+// pos_dev (a captured decode step, one query per sequence): the position is
+// read from device memory when the kernel runs and kv_len is the cache
+// capacity the launch is sized for; the results equal a launch with that
+// position as the last key, bit for bit.
 void launch_attn(mdma_ctx *ctx, const float *q, const uint16_t *k, const uint16_t *v, float *o,
                  uint64_t n_q, uint64_t kv_len, uint64_t hd, uint64_t n_q_heads,
-                 uint64_t n_kv_heads, uint64_t seq_stride = 0);
+                 uint64_t n_kv_heads, uint64_t seq_stride = 0, const uint32_t *pos_dev = nullptr);
+// The CPU-order mode (cpu_order.hip): the CPU backend's arithmetic order,
+// bit for bit. qmatmul of one job (any layout of Q4_K / Q6_K / Q8_0, or F32
+// / F16 rows); rmsnorm with the optional residual add (b, sum nullable);
+// silu_mul; causal GQA attention (seq_stride and pos_dev as launch_attn /
+// launch_attn_rope; kv_len is then the cache capacity).
+void launch_gemv_seq(mdma_ctx *ctx, const GemvJob &j, const float *x, uint64_t T);
+void launch_rmsnorm_seq(mdma_ctx *ctx, const float *w, uint64_t dim, const float *a, const float *b, float *sum,
+                        float *y, uint64_t rows, float eps);
+void launch_silu_mul_seq(mdma_ctx *ctx, const float *g, const float *u, float *y, uint64_t n);
+void launch_attn_seq(mdma_ctx *ctx, const float *q, const uint16_t *k, const uint16_t *v, float *o, uint64_t n_q,
+                     uint64_t kv_len, uint64_t hd, uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride = 0,
+                     const uint32_t *pos_dev = nullptr);
 // Greedy argmax of each row of x [rows, n] into idx[row]; flag[row] = any non-finite.
 // launch_attn that also leaves the int8 form of o (per 256) in the
 // int8-activation buffer, marked as holding o. False, launching nothing, when
 // the shape has no such variant (needs hd % 8 == 0, hd <= 256, a power-of-two
 // group of at most 8 query heads per KV head, group outputs whole 256s).
 bool launch_attn_q8(mdma_ctx *ctx, const float *q, const uint16_t *k, const uint16_t *v, float *o, uint64_t n_q,
-                    uint64_t kv_len, uint64_t hd, uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride = 0);
+                    uint64_t kv_len, uint64_t hd, uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride = 0,
+                    const uint32_t *pos_dev = nullptr);
 // Decode attention with launch_rope_kv_write folded in: q, k, v are the
 // unrotated projections of n_q queries, each the single new token of its
 // sequence (seq_stride apart in kc / vc; or one query over one sequence,

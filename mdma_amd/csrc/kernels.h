@@ -39,11 +39,11 @@ __device__ __forceinline__ uint32_t lds_addr(const void *lds) {
 }
 __device__ __forceinline__ void lds_dma16(const void *base, uint32_t off, const void *lds) {
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds_addr(lds))
-               : "memory");
+               : "memory", "m0");
 }
 __device__ __forceinline__ void lds_dma4(const void *base, uint32_t off, const void *lds) {
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds_addr(lds))
-               : "memory");
+               : "memory", "m0");
 }
 __device__ __forceinline__ void lds_wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 

@@ -372,17 +372,34 @@ void gemv(mdma_ctx *ctx, const GemvJob *jobs, int n, const float *x, uint64_t T,
   if (!fresh) q8_invalidate(ctx);
   if (ctx->act_mode == MDMA_ACT_I8)
     launch_gemv_i8(ctx, jobs, n, x, T);
+  else if (ctx->act_mode == MDMA_ACT_F32_CPU)
+    for (int i = 0; i < n; i++) launch_gemv_seq(ctx, jobs[i], x, T);
   else
     launch_gemv_f32(ctx, jobs, n, x, T);
 }
 
+// The CPU-order mode runs the trait's default ffn_gate_up (backend.rs:472-489):
+// gate and up into their buffers, then silu_mul.
 void gemv_gated(mdma_ctx *ctx, const GemvJob &g, const GemvJob &u, const float *x, uint64_t T, float *y,
                 bool fresh = false) {
   if (!fresh) q8_invalidate(ctx);
-  if (ctx->act_mode == MDMA_ACT_I8)
+  if (ctx->act_mode == MDMA_ACT_I8) {
     launch_gemv_i8_gated(ctx, g, u, x, T, y);
-  else
+  } else if (ctx->act_mode == MDMA_ACT_F32_CPU) {
+    launch_gemv_seq(ctx, g, x, T);
+    launch_gemv_seq(ctx, u, x, T);
+    launch_silu_mul_seq(ctx, g.y, u.y, y, T * g.n_out);
+  } else {
     launch_gemv_f32_gated(ctx, g, u, x, T, y);
+  }
+}
+
+void rmsnorm(mdma_ctx *ctx, const float *w, uint64_t dim, const float *a, const float *b, float *sum, float *y,
+             uint64_t rows, float eps) {
+  if (ctx->act_mode == MDMA_ACT_F32_CPU)
+    launch_rmsnorm_seq(ctx, w, dim, a, b, sum, y, rows, eps);
+  else
+    launch_rmsnorm(ctx, w, dim, a, b, sum, y, rows, eps);
 }
 
 // Llama::run_layers (src/model/arch/llama.rs:158-246) for T token rows in
@@ -410,7 +427,7 @@ void run_layers(mdma_session *s, uint64_t T, uint32_t pos, uint64_t seq, bool ba
   auto norm = [&](const mdma_buf *w, const float *a, const float *b, float *sum) {
     q8_invalidate(ctx);
     if (fuse_q8 && launch_rmsnorm_q8(ctx, fp(w), E, a, b, sum, fp(s->normed), T, c.rms_eps)) return true;
-    launch_rmsnorm(ctx, fp(w), E, a, b, sum, fp(s->normed), T, c.rms_eps);
+    rmsnorm(ctx, fp(w), E, a, b, sum, fp(s->normed), T, c.rms_eps);
     return false;
   };
   bool fresh = false;
@@ -442,6 +459,7 @@ void run_layers(mdma_session *s, uint64_t T, uint32_t pos, uint64_t seq, bool ba
   // per-workgroup sums of squares; the QKV GEMV normalizes x in its prologue.
   // n_part > 0: x already holds the residual stream and the partials wait.
   const bool fuse_norm = ctx->norm_fusion && fuse_q8 && T == 1 && !batched;
+  const bool cpu_order = ctx->act_mode == MDMA_ACT_F32_CPU;
   uint32_t n_part = 0;
   for (uint64_t i = 0; i < c.n_layers; i++) {
     const Layer &L = m->layers[i];
@@ -460,7 +478,16 @@ void run_layers(mdma_session *s, uint64_t T, uint32_t pos, uint64_t seq, bool ba
     if (!qkv_done) gemv(ctx, qkv, 3, fp(s->normed), T, fresh);
     // KvCache::rope_write (src/kv_cache.rs:212-244): rotate q, store rotated k and v.
     uint16_t *kb = reinterpret_cast<uint16_t *>(s->kc[i]->ptr), *vb = reinterpret_cast<uint16_t *>(s->vc[i]->ptr);
-    if ((batched || T == 1) && decode_attend(batched ? kb : kb + seq * cache_stride,
+    if (cpu_order) {
+      // The CPU's order: RoPE and the cache write, then attention; a
+      // captured step reads the position from device memory in both.
+      uint16_t *ks = batched ? kb : kb + seq * cache_stride, *vs = batched ? vb : vb + seq * cache_stride;
+      const uint64_t at = pos_dev ? 0 : (uint64_t)pos * kvw;
+      launch_rope_kv_write(ctx, fp(s->q), c.n_heads, fp(s->k), fp(s->v), c.n_kv_heads, hd, T, tab, pos, ks + at,
+                           vs + at, batched ? cache_stride : 0, batched ? 0 : 1, pos_dev);
+      launch_attn_seq(ctx, fp(s->q), ks, vs, fp(s->attn_out), T, pos_dev ? s->capacity : pos + (batched ? 1 : T), hd,
+                      c.n_heads, c.n_kv_heads, batched ? cache_stride : 0, pos_dev);
+    } else if ((batched || T == 1) && decode_attend(batched ? kb : kb + seq * cache_stride,
                                              batched ? vb : vb + seq * cache_stride, batched ? cache_stride : 0)) {
       // RoPE, the cache write and attention in one launch.
     } else if (batched) {
@@ -495,7 +522,7 @@ void run_layers(mdma_session *s, uint64_t T, uint32_t pos, uint64_t seq, bool ba
   if (n_part) {
     launch_rmsnorm(ctx, fp(m->output_norm), E, fp(x), nullptr, nullptr, fp(s->normed), T, c.rms_eps);
   } else {
-    launch_rmsnorm(ctx, fp(m->output_norm), E, fp(x), fp(s->proj), fp(x_alt), fp(s->normed), T, c.rms_eps);
+    rmsnorm(ctx, fp(m->output_norm), E, fp(x), fp(s->proj), fp(x_alt), fp(s->normed), T, c.rms_eps);
     std::swap(x, x_alt);
   }
   // Keep s->x as the buffer holding the residual stream.

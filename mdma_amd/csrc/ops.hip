@@ -4,6 +4,8 @@
 // cache, and greedy argmax. Semantics follow the reference CPU backend
 // (/root/reference/src/backend/cpu.rs) op for op; these are simple, correct
 // kernels, not the hot path.
+#include <algorithm>
+
 #include "internal.h"
 #include "kernels.h"
 
@@ -249,10 +251,12 @@ __device__ __forceinline__ void rot(float &x0, float &x1, float c, float s) {
   x1 = cc + d;
 }
 
-// x: [n_tokens, heads, hd]; tab: [pos][hd/2] (cos, sin).
+// x: [n_tokens, heads, hd]; tab: [pos][hd/2] (cos, sin). pos_dev (a
+// captured decode step): the position is read from there.
 __global__ void rope_kernel(float *__restrict__ x, uint32_t heads, uint32_t hd, uint64_t pairs,
-                            const float *__restrict__ tab, uint32_t pos) {
+                            const float *__restrict__ tab, uint32_t pos, const uint32_t *__restrict__ pos_dev) {
   const uint32_t half = hd / 2;
+  if (pos_dev) pos = *pos_dev;
   for (uint64_t p = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; p < pairs; p += (uint64_t)gridDim.x * blockDim.x) {
     const uint64_t t = p / ((uint64_t)heads * half);
     const uint32_t i = p % half;
@@ -264,8 +268,14 @@ __global__ void rope_kernel(float *__restrict__ x, uint32_t heads, uint32_t hd, 
   }
 }
 
+// pos_dev (a captured decode step): the rows start *pos_dev * n elements
+// after dk / dv.
 __global__ void kv_write_kernel(const float *__restrict__ k, const float *__restrict__ v, uint16_t *__restrict__ dk,
-                                uint16_t *__restrict__ dv, size_t n) {
+                                uint16_t *__restrict__ dv, size_t n, const uint32_t *__restrict__ pos_dev) {
+  if (pos_dev) {
+    dk += (size_t)*pos_dev * n;
+    dv += (size_t)*pos_dev * n;
+  }
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
     dk[i] = f2h(k[i]);
     dv[i] = f2h(v[i]);
@@ -276,12 +286,20 @@ __global__ void kv_write_kernel(const float *__restrict__ k, const float *__rest
 // stored with v as f16 rows. Token t sits at position pos + t*pos_step and
 // its cache row starts kv_stride elements after token t-1's (kv_stride =
 // the row width for one sequence; a cache-to-cache stride when each token
-// is a different sequence of a batch, with pos_step 0).
+// is a different sequence of a batch, with pos_step 0). pos_dev (a captured
+// decode step): the position is read from there, and the rows of position
+// p start p * pos_row elements after dk / dv.
 __global__ void rope_kv_kernel(float *__restrict__ q, uint64_t q_pairs, uint32_t q_heads, const float *__restrict__ k,
                                const float *__restrict__ v, uint64_t k_pairs, uint32_t kv_heads, uint32_t hd,
                                const float *__restrict__ tab, uint32_t pos, uint32_t pos_step, uint64_t kv_stride,
-                               uint16_t *__restrict__ dk, uint16_t *__restrict__ dv) {
+                               uint16_t *__restrict__ dk, uint16_t *__restrict__ dv,
+                               const uint32_t *__restrict__ pos_dev, uint64_t pos_row) {
   const uint32_t half = hd / 2;
+  if (pos_dev) {
+    pos = *pos_dev;
+    dk += (size_t)pos * pos_row;
+    dv += (size_t)pos * pos_row;
+  }
   for (uint64_t p = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; p < q_pairs + k_pairs;
        p += (uint64_t)gridDim.x * blockDim.x) {
     if (p < q_pairs) {
@@ -337,11 +355,13 @@ __device__ float block_sumf(float v, float *sh) {
 __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q, const uint16_t *__restrict__ K,
                                                    const uint16_t *__restrict__ V, float *__restrict__ o,
                                                    uint32_t prefix, uint32_t hd, uint32_t n_q_heads,
-                                                   uint32_t n_kv_heads, float scale, uint64_t seq_stride) {
+                                                   uint32_t n_kv_heads, float scale, uint64_t seq_stride,
+                                                   const uint32_t *__restrict__ pos_dev) {
   __shared__ float qs[256];
   __shared__ float sc[ATT_CHUNK];
   __shared__ float red[4];
   const uint32_t qh = blockIdx.x, i = blockIdx.y;
+  if (pos_dev) prefix = *pos_dev;  // a captured decode step: one query per sequence at *pos_dev
   const uint32_t kvh = qh / (n_q_heads / n_kv_heads), kv_row = n_kv_heads * hd;
   const uint32_t visible = seq_stride ? prefix + 1 : prefix + i + 1;
   K += (size_t)i * seq_stride;
@@ -421,6 +441,11 @@ struct AttnRope {
   // Set in a captured decode step: the position is read from here (written
   // before each replay), and the launch's grid is sized for the whole cache.
   const uint32_t *pos_dev;
+  // With pos_dev: the host's run count before it meets the key count,
+  // min(ceil(MDMA_ATT_WG_TARGET / pairs), ATT_MAX_RUNS); the kernel splits
+  // the live keys as the host would (runs min(runs0, tiles), each
+  // ceil(tiles / runs) tiles).
+  uint32_t runs0;
 };
 
 // Device-scope (all XCDs) coherent store and load of one float.
@@ -495,20 +520,17 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
   const uint32_t sub = gridDim.x / n_kv_heads, kvh = blockIdx.x / sub;
   const uint32_t split = blockIdx.y, i = blockIdx.z, n_splits = gridDim.y;
   // The new row's position and the tiles per run. From device memory in a
-  // captured step: the runs are then those the host would have chosen for
-  // this length (tiles per run ceil(tiles / n_splits); the grid's n_splits
-  // is the host's count for the whole cache, which equals the count for
-  // this length whenever the length has more tiles than runs, and otherwise
-  // gives one tile per run as the host does), so a replay computes the same
-  // partials, merged in the same order, as the eager launch.
+  // captured step: the runs are those the host chooses for this length
+  // (attn_impl: min(runs0, tiles) runs of ceil(tiles / runs) tiles each),
+  // so a replay computes the same partials, merged in the same order, as
+  // the eager launch. The grid's n_splits, min(runs0, tiles of the whole
+  // cache), is at least that many runs.
   uint32_t rpos = ROPE ? rp.pos : 0;
-  if constexpr (ROPE) {
-    if (rp.pos_dev) {
-      rpos = *rp.pos_dev;
-      prefix = rpos;  // one new query per sequence at rpos: visible = rpos + 1
-      const uint32_t tl = (rpos + ATT_TILE) / ATT_TILE;
-      tpw = (tl + n_splits - 1) / n_splits;
-    }
+  if (rp.pos_dev) {
+    rpos = *rp.pos_dev;
+    prefix = rpos;  // one new query per sequence at rpos: visible = rpos + 1
+    const uint32_t tl = (rpos + ATT_TILE) / ATT_TILE, runs = min(rp.runs0, tl);
+    tpw = (tl + runs - 1) / runs;
   }
   const uint32_t visible = seq_stride ? prefix + 1 : prefix + i + 1;
   const uint32_t tiles = (visible + ATT_TILE - 1) / ATT_TILE, t0 = split * tpw;
@@ -1011,50 +1033,58 @@ void launch_silu_mul(mdma_ctx *ctx, const float *g, const float *u, float *y, ui
 }
 
 void launch_rope(mdma_ctx *ctx, float *x, uint64_t n_tokens, uint64_t heads, uint64_t hd, const float *tab,
-                 uint32_t pos) {
+                 uint32_t pos, const uint32_t *pos_dev) {
   const uint64_t pairs = n_tokens * heads * (hd / 2);
   if (!pairs) return;
-  rope_kernel<<<dim3(grid1d(pairs)), dim3(256), 0, ctx->stream>>>(x, (uint32_t)heads, (uint32_t)hd, pairs, tab, pos);
+  rope_kernel<<<dim3(grid1d(pairs)), dim3(256), 0, ctx->stream>>>(x, (uint32_t)heads, (uint32_t)hd, pairs, tab, pos,
+                                                                  pos_dev);
   hip_check(hipGetLastError(), "rope launch");
 }
 
-void launch_kv_write(mdma_ctx *ctx, const float *k, const float *v, uint16_t *dk, uint16_t *dv, uint64_t n) {
-  kv_write_kernel<<<dim3(grid1d(n)), dim3(256), 0, ctx->stream>>>(k, v, dk, dv, n);
+void launch_kv_write(mdma_ctx *ctx, const float *k, const float *v, uint16_t *dk, uint16_t *dv, uint64_t n,
+                     const uint32_t *pos_dev) {
+  kv_write_kernel<<<dim3(grid1d(n)), dim3(256), 0, ctx->stream>>>(k, v, dk, dv, n, pos_dev);
   hip_check(hipGetLastError(), "kv_write launch");
 }
 
 void launch_rope_kv_write(mdma_ctx *ctx, float *q, uint64_t q_heads, const float *k, const float *v,
                           uint64_t kv_heads, uint64_t hd, uint64_t n_tokens, const float *tab, uint32_t pos,
-                          uint16_t *dk, uint16_t *dv, uint64_t kv_stride, uint32_t pos_step) {
+                          uint16_t *dk, uint16_t *dv, uint64_t kv_stride, uint32_t pos_step, const uint32_t *pos_dev) {
   const uint64_t qp = n_tokens * q_heads * (hd / 2), kp = n_tokens * kv_heads * (hd / 2);
   if (!qp && !kp) return;
   if (!kv_stride) kv_stride = kv_heads * hd;
   rope_kv_kernel<<<dim3(grid1d(qp + kp)), dim3(256), 0, ctx->stream>>>(
-      q, qp, (uint32_t)q_heads, k, v, kp, (uint32_t)kv_heads, (uint32_t)hd, tab, pos, pos_step, kv_stride, dk, dv);
+      q, qp, (uint32_t)q_heads, k, v, kp, (uint32_t)kv_heads, (uint32_t)hd, tab, pos, pos_step, kv_stride, dk, dv,
+      pos_dev, kv_heads * hd);
   hip_check(hipGetLastError(), "rope_kv_write launch");
 }
 
 namespace {
 // rope: RoPE and the new key's cache write folded in (decode only); the
-// cache is written only then. False, launching nothing, when q8 or rope is
-// asked for a shape without that variant.
+// cache is written only then. A rope with no k only carries pos_dev (a
+// captured decode step reading its position from device memory, kv_len the
+// cache capacity): attention alone. False, launching nothing, when q8 or
+// rope is asked for a shape without that variant.
 bool attn_impl(mdma_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t *vc, float *o, uint64_t n_q,
                uint64_t kv_len, uint64_t hd, uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride,
-               const AttnQ8 *q8, const AttnRope *rope = nullptr) {
+               const AttnQ8 *q8, const AttnRope *rope_in = nullptr) {
   uint16_t *k = const_cast<uint16_t *>(kc), *v = const_cast<uint16_t *>(vc);
+  const uint32_t *pos_dev = rope_in ? rope_in->pos_dev : nullptr;
+  const AttnRope *rope = rope_in && rope_in->k ? rope_in : nullptr;
+  if (pos_dev && !(seq_stride || n_q == 1)) return false;
   const float scale = 1.0f / sqrtf((float)hd);
   const uint32_t prefix = (uint32_t)(seq_stride ? kv_len - 1 : kv_len - n_q);
   const uint64_t GQ = n_kv_heads ? n_q_heads / n_kv_heads : 0, C = (hd + 127) / 128;
   // Runs of tiles per (query, KV head): enough workgroups to cover the chip
   // (about MDMA_ATT_WG_TARGET), at least one tile and at most ATT_MAX_RUNS
   // runs each; long prompts use one run per query.
+  // A captured step (rope->pos_dev) sizes the grid for the whole cache and
+  // the kernel recomputes the runs for the live length with these rules.
   const uint64_t tiles = (kv_len + ATT_TILE - 1) / ATT_TILE, pairs = n_q * n_kv_heads;
-  uint64_t n_splits = pairs ? (MDMA_ATT_WG_TARGET + pairs - 1) / pairs : 1;
-  if (n_splits > ATT_MAX_RUNS) n_splits = ATT_MAX_RUNS;
-  if (n_splits > tiles) n_splits = tiles;
-  if (!n_splits) n_splits = 1;
+  const uint64_t runs0 = std::min<uint64_t>(pairs ? (MDMA_ATT_WG_TARGET + pairs - 1) / pairs : 1, ATT_MAX_RUNS);
+  uint64_t n_splits = std::max<uint64_t>(std::min(runs0, tiles), 1);
   const uint64_t tpw = (tiles + n_splits - 1) / n_splits;
-  n_splits = tiles ? (tiles + tpw - 1) / tpw : 1;
+  if (!pos_dev) n_splits = tiles ? (tiles + tpw - 1) / tpw : 1;
   // Few workgroups (short contexts, few queries): a KV head's query heads
   // split over MDMA_ATT_SUB workgroups, each reading the same K/V tiles with
   // a share of the heads (less work per workgroup on the critical path).
@@ -1080,7 +1110,8 @@ bool attn_impl(mdma_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t
     // captured step and the eager one may choose differently).
     uint32_t *cnt = part_bytes ? attn_counters(ctx, n_q * n_kv_heads * MDMA_ATT_SUB) : nullptr;
     const AttnQ8 a8 = q8 ? *q8 : AttnQ8{nullptr, nullptr, nullptr};
-    const AttnRope ar = rope ? *rope : AttnRope{nullptr, nullptr, nullptr, 0};
+    AttnRope ar = rope ? *rope : AttnRope{nullptr, nullptr, nullptr, 0, pos_dev, 0};
+    ar.runs0 = (uint32_t)runs0;
     const dim3 grid((uint32_t)(n_kv_heads * sub), (uint32_t)n_splits, (uint32_t)n_q);
 #define MDMA_ATT_GO1(GG, CC, QQ, RR, OO)                                                                       \
   attn_split_kernel<GG, CC, QQ, RR, OO><<<grid, dim3(256), 0, ctx->stream>>>(                                  \
@@ -1115,24 +1146,31 @@ bool attn_impl(mdma_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t
     return true;
   }
   attn_kernel<<<dim3((uint32_t)n_q_heads, (uint32_t)n_q), dim3(256), 0, ctx->stream>>>(
-      q, k, v, o, prefix, (uint32_t)hd, (uint32_t)n_q_heads, (uint32_t)n_kv_heads, scale, seq_stride);
+      q, k, v, o, prefix, (uint32_t)hd, (uint32_t)n_q_heads, (uint32_t)n_kv_heads, scale, seq_stride, pos_dev);
   hip_check(hipGetLastError(), "attn launch");
   return true;
 }
 }  // namespace
 
 void launch_attn(mdma_ctx *ctx, const float *q, const uint16_t *k, const uint16_t *v, float *o, uint64_t n_q,
-                 uint64_t kv_len, uint64_t hd, uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride) {
-  attn_impl(ctx, q, k, v, o, n_q, kv_len, hd, n_q_heads, n_kv_heads, seq_stride, nullptr);
+                 uint64_t kv_len, uint64_t hd, uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride,
+                 const uint32_t *pos_dev) {
+  const AttnRope pd{nullptr, nullptr, nullptr, 0, pos_dev, 0};
+  if (!attn_impl(ctx, q, k, v, o, n_q, kv_len, hd, n_q_heads, n_kv_heads, seq_stride, nullptr,
+                 pos_dev ? &pd : nullptr))
+    fail(MDMA_ERR_BACKEND, "attn: no launch reads the position from device memory for this shape");
 }
 
 bool launch_attn_q8(mdma_ctx *ctx, const float *q, const uint16_t *k, const uint16_t *v, float *o, uint64_t n_q,
-                    uint64_t kv_len, uint64_t hd, uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride) {
+                    uint64_t kv_len, uint64_t hd, uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride,
+                    const uint32_t *pos_dev) {
   const uint64_t n_in = n_q_heads * hd;
   if (!n_q || !kv_len || n_in % 256) return false;
   AttnQ8 a8;
   q8_slots(ctx, n_q, n_in, &a8.q, &a8.d, &a8.s16);
-  if (!attn_impl(ctx, q, k, v, o, n_q, kv_len, hd, n_q_heads, n_kv_heads, seq_stride, &a8)) return false;
+  const AttnRope pd{nullptr, nullptr, nullptr, 0, pos_dev, 0};
+  if (!attn_impl(ctx, q, k, v, o, n_q, kv_len, hd, n_q_heads, n_kv_heads, seq_stride, &a8, pos_dev ? &pd : nullptr))
+    return false;
   q8_mark(ctx, o, n_q, n_in);
   return true;
 }
@@ -1142,7 +1180,7 @@ bool launch_attn_rope(mdma_ctx *ctx, const float *q, const float *k, const float
                       uint64_t n_q_heads, uint64_t n_kv_heads, uint64_t seq_stride, bool int8_out,
                       const uint32_t *pos_dev) {
   if (!n_q || !kv_len || (!pos_dev && pos != kv_len - 1)) return false;
-  const AttnRope rp{k, v, tab, pos, pos_dev};
+  const AttnRope rp{k, v, tab, pos, pos_dev, 0};
   if (!int8_out)
     return attn_impl(ctx, q, kc, vc, o, n_q, kv_len, hd, n_q_heads, n_kv_heads, seq_stride, nullptr, &rp);
   const uint64_t n_in = n_q_heads * hd;

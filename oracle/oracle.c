@@ -250,22 +250,53 @@ typedef struct {
     int status;
 } qm_job;
 
+/* Eight tokens' dots with one row at once: lane k of the vectors is token
+ * k's own sequential sum (from -0.0, each product rounded, no FMA), so every
+ * output equals dot(row, x_k, n) bit for bit; the eight independent chains
+ * only run side by side. xt holds the eight tokens interleaved, [n][8]. */
+typedef float orc_v8 __attribute__((vector_size(32)));
+
+static void dot8(const float *row, const orc_v8 *xt, size_t n, float *out) {
+    orc_v8 s = {-0.0f, -0.0f, -0.0f, -0.0f, -0.0f, -0.0f, -0.0f, -0.0f};
+    for (size_t i = 0; i < n; i++) {
+        orc_v8 p = row[i] * xt[i];
+        s = s + p;
+    }
+    for (int k = 0; k < 8; k++)
+        out[k] = s[k];
+}
+
 static void *qm_worker(void *arg) {
     qm_job *j = (qm_job *)arg;
+    size_t T8 = j->n_tokens / 8;
     float *row = (float *)malloc(j->n_in * sizeof(float));
-    if (!row) {
+    orc_v8 *xt = T8 ? (orc_v8 *)aligned_alloc(32, T8 * j->n_in * sizeof(orc_v8)) : NULL;
+    if (!row || (T8 && !xt)) {
+        free(row);
+        free(xt);
         j->status = SHAPE;
         return NULL;
     }
+    for (size_t g = 0; g < T8; g++)
+        for (size_t i = 0; i < j->n_in; i++)
+            for (int k = 0; k < 8; k++)
+                xt[g * j->n_in + i][k] = j->x[(8 * g + (size_t)k) * j->n_in + i];
     for (size_t r = j->r0; r < j->r1; r++) {
         if (orc_dequantize_row(j->dtype, j->w + r * j->row_bytes, j->row_bytes, row, j->n_in)) {
             j->status = SHAPE;
             break;
         }
-        for (size_t t = 0; t < j->n_tokens; t++)
+        for (size_t g = 0; g < T8; g++) {
+            float o[8];
+            dot8(row, xt + g * j->n_in, j->n_in, o);
+            for (int k = 0; k < 8; k++)
+                j->y[(8 * g + (size_t)k) * j->n_out + r] = o[k];
+        }
+        for (size_t t = 8 * T8; t < j->n_tokens; t++)
             j->y[t * j->n_out + r] = dot(row, j->x + t * j->n_in, j->n_in);
     }
     free(row);
+    free(xt);
     return NULL;
 }
 

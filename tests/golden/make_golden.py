@@ -8,6 +8,8 @@
   /root/reference/src/backend/rocm/decode/tests.rs:81-96), each output checked
   here against an f64 dot product of the dequantized rows before it is written.
 - int8_small.npz: activations, their int8 quantization and block dots.
+- config5_greedy.json (`config5_greedy [seq ...]` argument): the configured
+  config-5 workload, free-running (see config5_greedy).
 - config5_steps.json (`config5` argument; about a minute of CPU): the
   Llama-3-8B geometry with the Q4_K_M mix (random init, written by
   mdma_amd.llama_synth with fast=True and CONFIG5_SEED), f32 activations,
@@ -36,6 +38,58 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 
 CONFIG5_SEED = 20261202
 CONFIG5_PROMPT, CONFIG5_STEPS = 64, 16
+# The configured workload: a 512-token prompt, then 256 greedy tokens; the
+# batch-8 prompts are sequences 0..7 of config5_prompts (sequence 0 is the
+# batch-1 prompt).
+GREEDY_PROMPT, GREEDY_GEN, GREEDY_BATCH = 512, 256, 8
+
+
+def config5_prompts(seed=CONFIG5_SEED, n=GREEDY_PROMPT, batch=GREEDY_BATCH):
+    V = llama_synth.LLAMA3_8B["vocab"]
+    return np.stack([synth.tokens(n, V, seed + 100 + b) for b in range(batch)])
+
+
+def logits_sha1(v):
+    import hashlib
+    return hashlib.sha1(np.ascontiguousarray(v, dtype="<f4").tobytes()).hexdigest()
+
+
+def step_record(lg, tok):
+    order = np.argsort(lg)[::-1][:4]
+    assert int(order[0]) == int(tok) or lg[order[0]] == lg[tok]
+    return {"greedy": int(tok), "margin": float(lg[order[0]] - lg[order[1]]), "max_abs": float(np.max(np.abs(lg))),
+            "top4": [[int(t), float(lg[t])] for t in order], "sha1": logits_sha1(lg)}
+
+
+def config5_greedy(path="/tmp/mdma_config5.gguf", seqs=(0,)):
+    """config5_greedy.json: the oracle's free-running greedy decode of the
+    configured workload (512-token prompt, 256 tokens, f16-rounded KV) in
+    the f32 mode and the int8 mode, for the prompts `seqs` of
+    config5_prompts; per step the greedy token, top-2 margin, largest
+    |logit|, top-4 (token, logit) and the sha1 of the logits' f32 bytes."""
+    import time
+    if not os.path.exists(path):
+        llama_synth.write(path, llama_synth.LLAMA3_8B, llama_synth.Q4_K_M, CONFIG5_SEED, fast=True)
+    r = gguf.Reader(path)
+    prompts = config5_prompts()
+    out = {"seed": CONFIG5_SEED, "n_prompt": GREEDY_PROMPT, "n_gen": GREEDY_GEN,
+           "prompts_sha1": hashlib_sha1(prompts), "seqs": {}}
+    for b in seqs:
+        rec = {}
+        for mode, act_i8 in (("f32", False), ("i8", True)):
+            t0 = time.time()
+            toks, logits = ffi.llama_run(r, prompts[b], GREEDY_GEN, kv_f16=True, act_i8=act_i8)
+            rec[mode] = [step_record(logits[i], toks[i]) for i in range(GREEDY_GEN)]
+            rec[mode + "_cpu_seconds"] = round(time.time() - t0, 1)
+            print(f"config5 greedy seq {b} {mode}: {time.time() - t0:.0f} s; tokens {toks[:16].tolist()}...", flush=True)
+        out["seqs"][str(b)] = rec
+        with open(os.path.join(HERE, "config5_greedy.json"), "w") as f:
+            json.dump(out, f)
+
+
+def hashlib_sha1(a):
+    import hashlib
+    return hashlib.sha1(np.ascontiguousarray(a, dtype="<u4").tobytes()).hexdigest()
 
 
 def config5(path="/tmp/mdma_config5.gguf"):
@@ -108,5 +162,7 @@ def main():
 if __name__ == "__main__":
     if len(sys.argv) > 1 and sys.argv[1] == "config5":
         config5()
+    elif len(sys.argv) > 1 and sys.argv[1] == "config5_greedy":
+        config5_greedy(seqs=tuple(int(b) for b in sys.argv[2:]) or (0,))
     else:
         main()

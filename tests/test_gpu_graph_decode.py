@@ -95,3 +95,63 @@ def test_generate_graph_equals_eager(backend, model_path, mode, batch):
         backend.set_graph_decode(True)
         m.close()
         backend.set_act_mode(ACT_F32)
+
+
+GQA_LONG = dict(GQA_SMALL, n_ctx=2048)
+
+
+@pytest.mark.parametrize("mode", [ACT_F32, ACT_I8])
+def test_graph_decoder_split_runs_match_eager_at_long_capacity(backend, tmp_path, mode):
+    # A captured step sizes its attention grid for the whole cache and splits
+    # the live keys into runs on the device. At capacity 1280 (20 tiles of 64
+    # keys) the runs for the whole cache (10 of 2 tiles) are fewer than the
+    # run limit for live lengths of 10 to 16 tiles, where the eager launch
+    # takes one tile per run: positions 640-1023 are where a device rule that
+    # started from the grid's run count instead of the host's would merge
+    # different partials.
+    p = str(tmp_path / "gqa_long.gguf")
+    llama_synth.write(p, GQA_LONG, llama_synth.Q4_K_M, 21)
+    backend.set_act_mode(mode)
+    m = Model(backend, p)
+    s = m.session(1280, batch=2, max_tokens=640)
+    d = s.decoder(0)
+    try:
+        rng = np.random.default_rng(3)
+        prompt = rng.integers(0, m.config.vocab, size=640).astype(np.uint32)
+        s.prefill(prompt, 0, seq=0)
+        s.prefill(prompt, 0, seq=1)
+        replays = 0
+        for pos in range(640, 1024):
+            token = (pos * 37) % m.config.vocab
+            want = s.forward(token, pos, seq=1)
+            got = d.forward(token, pos)
+            replays += d.replayed
+            assert np.array_equal(bits(got), bits(want)), f"graph logits at position {pos}"
+        assert replays >= 380, replays
+    finally:
+        d.close()
+        s.close(), m.close()
+        backend.set_act_mode(ACT_F32)
+
+
+def test_decoder_recaptures_after_a_mode_change(backend, model_path):
+    # A kernel-selecting setting changes what a capture would record: the
+    # graph captured before it refuses to replay and the decoder captures
+    # again, so its logits stay equal to forward's in the new mode.
+    backend.set_act_mode(ACT_F32)
+    m = Model(backend, model_path)
+    s = m.session(64, batch=2, max_tokens=8)
+    d = s.decoder(0)
+    try:
+        for pos in range(12):
+            mode = ACT_I8 if pos >= 6 else ACT_F32
+            backend.set_act_mode(mode)
+            want = s.forward(pos + 5, pos, seq=1)
+            got = d.forward(pos + 5, pos)
+            assert np.array_equal(bits(got), bits(want)), pos
+            if pos == 6:
+                assert not d.replayed  # recaptured under the new mode
+    finally:
+        d.close()
+        s.close(), m.close()
+        backend.set_act_mode(ACT_F32)

@@ -207,12 +207,22 @@ def test_qmatmul_is_sequential_f32_without_fma():
 
 
 def test_qmatmul_batched_equals_sequential_and_threads_do_not_matter():
+    # 19 tokens: two groups of eight run side by side, then three alone.
     w = synth.weight(Q4K, 33, 512, 5)
-    x = synth.normal_f32(5 * 512, 6)
+    x = synth.normal_f32(19 * 512, 6)
     full = ffi.qmatmul(Q4K, w, 33, 512, x, threads=7)
-    for t in range(5):
+    for t in range(19):
         one = ffi.qmatmul(Q4K, w, 33, 512, x[t * 512:(t + 1) * 512], threads=1)
         assert np.array_equal(full[t], one[0])
+
+
+def test_qmatmul_token_groups_keep_each_tokens_sequential_sum():
+    # The cancellation case of the test above in every lane of an eight-token
+    # group, with the tokens scaled apart: each lane keeps its own order.
+    w = f32w([1e8, 1.0, -1e8, 1.0])
+    x = np.concatenate([np.float32(2.0 ** k) * np.ones(4, np.float32) for k in range(9)])
+    got = ffi.qmatmul(F32, w, 1, 4, x)[:, 0]
+    assert list(got) == [np.float32(2.0 ** k) for k in range(9)]
 
 
 @pytest.mark.parametrize("dtype", [Q8, Q4K, Q6K])
