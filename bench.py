@@ -175,7 +175,7 @@ def time_graphs(be, ev, graphs, steps, warmup):
     return ms
 
 
-def per_launch(be, ev, wl, mode, reps, graph=True, only=None):
+def per_launch(be, ev, wl, mode, reps, graph=True, only=None, durations=None):
     """Per launch kind, over every distinct weight copy, each launch as the
     step issues it (in the int8 mode the down projection quantizes its f32 x
     in its own prologue, so its time includes that quantization):
@@ -187,6 +187,7 @@ def per_launch(be, ev, wl, mode, reps, graph=True, only=None):
     out = {}
     n = reps * len(wl.layers)
     starts, stops = [ev.event() for _ in range(n)], [ev.event() for _ in range(n)]
+    all_durs = {}
     for launch in LAUNCHES:
         name = launch[0]
         if only and name != only:
@@ -211,14 +212,19 @@ def per_launch(be, ev, wl, mode, reps, graph=True, only=None):
                 i += 1
         be.join_execution()
         durs = [ev.elapsed_ms(starts[k], stops[k]) * 1e3 for k in range(n)]
+        all_durs[name] = durs
         us = sum(durs) / n
         b = launch_bytes(launch, mode)
+        pct = np.percentile(durs, [10, 50, 90])
         out[name] = {"us_kernel": round(us, 3), "us_kernel_median": round(float(np.median(durs)), 3),
+                     "us_kernel_p10_p50_p90_max": [round(float(v), 3) for v in pct] + [round(max(durs), 3)],
                      "GBps_kernel": round(b / us / 1e3, 1),
                      "us_graph": round(us_graph, 3), "GBps_graph": round(b / us_graph / 1e3, 1),
                      "bytes_per_launch": b, "launches_timed": n}
     for e in starts + stops:
         ev.destroy(e)
+    if durations is not None:
+        durations.update(all_durs)
     return out
 
 
@@ -254,18 +260,20 @@ def q6k_gemvs(be, ev, reps):
     """Kernel-only rates (dispatch timestamps) of the Q6_K GEMVs, weights
     rotated over >= 1 GiB of copies; int8 mode at T = 1, 4, 8 and the f32
     mode at T = 1. Bytes: weights + activations + outputs, each once. The
-    batched calls read the weights' tile images, as batched decode sessions
-    do (made at each copy's first batched call, before the timed ones)."""
+    batched calls run twice: reading the weights' row planes (`_rows`), then
+    their tile images, as batched decode sessions do (made at each copy's
+    first batched call with the batch layout on, before the timed ones)."""
     from mdma_amd import synth
     from mdma_amd.backend import ACT_F32, ACT_I8
 
-    be.set_batch_layout(True)
     out = {}
     for name, (rows, k) in Q6_SHAPES.items():
         raw = synth.weight(Q6K, rows, k, SEED + 7)
         copies = max(2, -(-MALL_DEFEAT_BYTES // len(raw)))
         ws = [be.upload_weight(raw, Q6K, (rows, k)) for _ in range(copies)]
-        for T, mode in ((1, "i8"), (4, "i8"), (8, "i8"), (1, "f32")):
+        for T, mode, tiles in ((1, "i8", False), (4, "i8", False), (8, "i8", False), (4, "i8", True),
+                               (8, "i8", True), (1, "f32", False)):
+            be.set_batch_layout(tiles)
             be.set_act_mode(ACT_I8 if mode == "i8" else ACT_F32)
             x = be.f32_buf(synth.normal_f32(T * k, SEED + 8))
             y = be.alloc(T * rows * 4)
@@ -282,7 +290,7 @@ def q6k_gemvs(be, ev, reps):
             for e in st + sp:
                 ev.destroy(e)
             b = len(raw) + T * (x_bytes(k, mode)) + T * rows * 4
-            out[f"{name}_T{T}_{mode}"] = {"us_kernel": round(us, 3), "GBps_kernel": round(b / us / 1e3, 1),
+            out[f"{name}_T{T}_{mode}" + ("_rows" if T > 1 and not tiles else "")] = {"us_kernel": round(us, 3), "GBps_kernel": round(b / us / 1e3, 1),
                                           "pct_of_hbm_peak": round(100 * b / us / 1e3 / HBM_PEAK_GBS, 1),
                                           "bytes_per_launch": b, "launches_timed": n}
             x.close()
@@ -351,13 +359,14 @@ def prefill_gemms(be, ev, reps):
 E2E_PATH = "/tmp/mdma_bench_llama3_8b_q4km.gguf"
 
 
-def e2e_decode(be, n_prompt=512, n_gen=256, batches=(1, 8), path=E2E_PATH):
+def e2e_decode(be, n_prompt=512, n_gen=256, batches=(1, 8), path=E2E_PATH, capacity=4096):
     """Llama-3-8B geometry, Q4_K_M mix (attention and down Q6_K, gate/up and
     token_embd Q4_K, head Q6_K), random init written as GGUF; a 512-token
     random prompt prefill, then greedy decode at batch 1 and 8, int8
-    activations, f16 KV. Step times come from HIP events recorded on the
-    stream between steps (the whole generation is queued on the device;
-    tokens feed back through device memory)."""
+    activations, f16 KV caches of config 5's context (4096 positions per
+    sequence). Step times come from HIP events recorded on the stream between
+    steps (the whole generation is queued on the device; tokens feed back
+    through device memory)."""
     from mdma_amd import llama_synth
     from mdma_amd.backend import ACT_I8
     from mdma_amd.model import Model
@@ -371,10 +380,11 @@ def e2e_decode(be, n_prompt=512, n_gen=256, batches=(1, 8), path=E2E_PATH):
     m = Model(be, path)
     load_s = time.perf_counter() - t0
     out = {"model": "Llama-3-8B geometry, Q4_K_M mix, random init", "weight_bytes": int(m.plan(1).weight_bytes),
-           "load_seconds": round(load_s, 2), "prompt_tokens": n_prompt, "decode_tokens": n_gen}
+           "load_seconds": round(load_s, 2), "prompt_tokens": n_prompt, "decode_tokens": n_gen,
+           "kv_capacity": capacity}
     from mdma_amd import synth
     for B in batches:
-        s = m.session(n_prompt + n_gen, B, n_prompt)
+        s = m.session(capacity, B, n_prompt)
         prompts = np.stack([synth.tokens(n_prompt, 128256, SEED + 50 + b) for b in range(B)])
         s.generate(prompts, 4)  # warm: code paths, activation buffers, RoPE table
         s.reset()
@@ -662,11 +672,14 @@ def main():
         be.set_act_mode(ACT_I8)
         # Only the gate/up, no graph replays: the kernel's dispatches are one
         # untimed warm pass over the weight copies, then the timed launches.
-        dom = per_launch(be, ev, wl, "i8", args.reps, graph=False, only="gate_up")["gate_up"]
+        durs = {}
+        dom = per_launch(be, ev, wl, "i8", args.reps, graph=False, only="gate_up", durations=durs)["gate_up"]
         print(json.dumps({"roofline": {"kernel": "gemv_team<Q4G, int8, gated, x staged in LDS>",
                                        "bytes_per_launch": dom["bytes_per_launch"], "us_per_launch": dom["us_kernel"],
                                        "us_per_launch_median": dom["us_kernel_median"],
+                                       "us_p10_p50_p90_max": dom["us_kernel_p10_p50_p90_max"],
                                        "launches_timed": dom["launches_timed"],
+                                       "us_each": [round(v, 3) for v in durs["gate_up"]],
                                        "frac": round(dom["GBps_kernel"] / HBM_PEAK_GBS, 4)},
                           "device": be.device_label()}), flush=True)
         return
@@ -699,6 +712,7 @@ def main():
                       "x's int8 form from the fused rmsnorm)",
             "bytes_per_launch": dom["bytes_per_launch"], "us_per_launch": dom["us_kernel"],
             "us_per_launch_median": dom["us_kernel_median"],
+            "us_p10_p50_p90_max": dom["us_kernel_p10_p50_p90_max"],
             "timing": (f"achieved = bytes_per_launch / us_per_launch, us_per_launch the mean of "
                        f"{dom['launches_timed']} kernel-only durations from the dispatches' own start/end "
                        "timestamps (the statistic rocprofv3 --stats reports as its average)"),

@@ -297,8 +297,11 @@ int mdma_gfx950_qmatmul_i8(mdma_ctx *ctx, const mdma_qweight *w, const mdma_buf 
  * per GPU instead of the context's buffers. It calls no hipMalloc or
  * hipFree; an x needing more than 8 MiB of scratch (about 6.1 million
  * values) fails with MDMA_ERR_BUFFER_BUDGET before anything runs. Calls
- * through one context run in its stream's order; calls from two contexts on
- * one GPU share the array and race. */
+ * through one context run in its stream's order; calls from several
+ * contexts on one GPU share the array and are ordered by an event per GPU
+ * (each call's stream waits for the previous call's kernels), except under
+ * stream capture, where a captured call races with other contexts' calls
+ * that run while its graph replays. */
 int mdma_gfx950_qmatmul_i8_noalloc(mdma_ctx *ctx, const mdma_qweight *w, const mdma_buf *x, mdma_buf *y);
 
 /* Stream capture into a replayable HIP graph (the reference's graph decode

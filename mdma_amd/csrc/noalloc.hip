@@ -14,8 +14,14 @@
 //
 // Every call on one GPU shares that GPU's array and each call overwrites
 // what it reads before reading it (nothing in it needs to start at zero).
-// Calls through one context run in its stream's order; calls from two
-// contexts on one GPU run on different streams and would race on the array.
+// Calls through one context run in its stream's order. Calls from several
+// contexts on one GPU are ordered too: each GPU has one event, created at
+// set-up with the array's address, that every call's stream waits for
+// before its launches and records after them, under a host lock per GPU,
+// so the calls' kernels run one call after another. Under stream capture
+// the event is not used (a captured graph cannot wait for work outside
+// it): a graph that holds this call races with calls from other contexts
+// replayed or run at the same time on that GPU.
 #include <algorithm>
 #include <cstdio>
 #include <mutex>
@@ -30,9 +36,12 @@ static __device__ __align__(256) uint8_t scratch[STATIC_SCRATCH_BYTES];
 
 namespace {
 
-// This device's address of `scratch`, per device ordinal, resolved once.
+// This device's address of `scratch`, per device ordinal, resolved once,
+// and the device's ordering event and host lock (the calls' order).
 std::mutex g_setup_lock;
 char *g_device_scratch[256] = {};
+hipEvent_t g_order_event[256] = {};
+std::mutex g_order_lock[256];
 
 char *device_scratch(int device) {
   std::lock_guard<std::mutex> lk(g_setup_lock);
@@ -43,6 +52,9 @@ char *device_scratch(int device) {
     hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(::scratch));
     mdma::hip_check(e, "hipGetSymbolAddress(static scratch)");
     if (!ptr) mdma::fail(MDMA_ERR_BACKEND, "hipGetSymbolAddress(static scratch) returned null");
+    hipEvent_t ev = nullptr;
+    mdma::hip_check(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "allocation-free scratch: order event");
+    g_order_event[device] = ev;
     g_device_scratch[device] = static_cast<char *>(ptr);
   }
   return g_device_scratch[device];
@@ -100,8 +112,16 @@ extern "C" int mdma_gfx950_qmatmul_i8_noalloc(mdma_ctx *ctx, const mdma_qweight 
                     (unsigned long long)n, (unsigned long long)need, (unsigned long long)STATIC_SCRATCH_BYTES);
       mdma::fail(MDMA_ERR_BUFFER_BUDGET, m);
     }
-    FixedScratch fs(ctx, ctx->static_scratch, STATIC_SCRATCH_BYTES, y);
-    mdma::qmatmul_run(ctx, w, x, y, MDMA_ACT_I8);
+    // Calls from other contexts on this GPU: their kernels first (not under
+    // capture, see above).
+    std::lock_guard<std::mutex> order(g_order_lock[ctx->device]);
+    const hipEvent_t ev = g_order_event[ctx->device];
+    if (!ctx->capturing) mdma::hip_check(hipStreamWaitEvent(ctx->stream, ev, 0), "qmatmul_i8_noalloc: order wait");
+    {
+      FixedScratch fs(ctx, ctx->static_scratch, STATIC_SCRATCH_BYTES, y);
+      mdma::qmatmul_run(ctx, w, x, y, MDMA_ACT_I8);
+    }
+    if (!ctx->capturing) mdma::hip_check(hipEventRecord(ev, ctx->stream), "qmatmul_i8_noalloc: order record");
     return MDMA_OK;
   } catch (const mdma::Error &e) {
     mdma::set_last_error(e.msg);

@@ -491,10 +491,12 @@ __device__ __forceinline__ void attn_load(AttnTile<C> &t, const uint16_t *__rest
   }
 }
 
-// ONE: every run is one tile (the host's choice whenever the runs cover the
-// keys a tile each): no second tile buffer, 92 VGPRs instead of 181 at G = 4,
+// ONE: one tile buffer, each tile of a run loaded after the previous one is
+// computed (the host's choice whenever every run is one tile, or the grid
+// has more workgroups than two per CU): 92 VGPRs instead of 181 at G = 4,
 // so five workgroups fit a CU instead of two (batch-8 decode at 768-key
-// caches: 640 workgroups in one wave of the chip).
+// caches: 640 workgroups in one wave of the chip). The same tiles in the
+// same order as the two-buffer loop: the same bits.
 template <int G, int C, bool QUANT, bool ROPE, bool ONE = false>
 __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict__ q, uint16_t *__restrict__ K,
                                                          uint16_t *__restrict__ V, float *__restrict__ o,
@@ -680,9 +682,16 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
     }
     lds_barrier();  // sc is rewritten by the next tile
   };
-  if (ONE || t1 - t0 == 1) {
+  if (ONE) {
+    // One tile buffer: a run of several tiles loads each after the previous
+    // one is computed (no prefetch, half the registers).
+    for (uint32_t tile = t0; tile < t1; tile++) {
+      if (tile > t0) attn_load<C>(ta, K, V, tile, visible, kv_row, hd, lane, wave);
+      process(ta, tile);
+    }
+  } else if (t1 - t0 == 1) {
     process(ta, t0);
-  } else if constexpr (!ONE) {
+  } else {
     for (uint32_t tile = t0; tile < t1; tile += 2) {
       attn_load<C>(tb, K, V, min(tile + 1, t1 - 1), visible, kv_row, hd, lane, wave);
       process(ta, tile);
@@ -1113,13 +1122,18 @@ bool attn_impl(mdma_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t
     AttnRope ar = rope ? *rope : AttnRope{nullptr, nullptr, nullptr, 0, pos_dev, 0};
     ar.runs0 = (uint32_t)runs0;
     const dim3 grid((uint32_t)(n_kv_heads * sub), (uint32_t)n_splits, (uint32_t)n_q);
+    // One tile buffer when every run is one tile, or when more workgroups
+    // than the two-buffer kernel keeps resident (two per CU) share the chip:
+    // a captured step sized for a long cache runs one-tile runs at short
+    // lengths, and there occupancy counts more than the prefetch.
+    const bool one = tpw == 1 || (uint64_t)grid.x * grid.y * grid.z > 2 * (uint64_t)ctx->cu_count;
 #define MDMA_ATT_GO1(GG, CC, QQ, RR, OO)                                                                       \
   attn_split_kernel<GG, CC, QQ, RR, OO><<<grid, dim3(256), 0, ctx->stream>>>(                                  \
       q, k, v, o, part, cnt, prefix, (uint32_t)hd, (uint32_t)n_q_heads, (uint32_t)n_kv_heads, scale, seq_stride, \
       (uint32_t)tpw, a8, ar)
 #define MDMA_ATT_GO(GG, CC, QQ, RR)          \
   do {                                       \
-    if (tpw == 1) MDMA_ATT_GO1(GG, CC, QQ, RR, true);  \
+    if (one) MDMA_ATT_GO1(GG, CC, QQ, RR, true);  \
     else MDMA_ATT_GO1(GG, CC, QQ, RR, false); \
   } while (0)
 #define MDMA_ATT(GG, CC)                                \

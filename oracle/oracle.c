@@ -250,53 +250,71 @@ typedef struct {
     int status;
 } qm_job;
 
-/* Eight tokens' dots with one row at once: lane k of the vectors is token
- * k's own sequential sum (from -0.0, each product rounded, no FMA), so every
- * output equals dot(row, x_k, n) bit for bit; the eight independent chains
- * only run side by side. xt holds the eight tokens interleaved, [n][8]. */
+/* Eight rows' dots with one token at once: lane k of the vectors is row k's
+ * own sequential sum (from -0.0, each product rounded, no FMA), so every
+ * output equals dot(row_k, x, n) bit for bit; the independent chains only
+ * run side by side (eight rows per vector, four tokens per pass), which
+ * also reads x once per eight rows instead of once per row. wt holds the
+ * eight dequantized rows interleaved, [n][8]. */
 typedef float orc_v8 __attribute__((vector_size(32)));
 
-static void dot8(const float *row, const orc_v8 *xt, size_t n, float *out) {
-    orc_v8 s = {-0.0f, -0.0f, -0.0f, -0.0f, -0.0f, -0.0f, -0.0f, -0.0f};
-    for (size_t i = 0; i < n; i++) {
-        orc_v8 p = row[i] * xt[i];
-        s = s + p;
+static void dots_8rows(const orc_v8 *wt, size_t n, const float *const *x, int nt, orc_v8 *out) {
+    const orc_v8 z = {-0.0f, -0.0f, -0.0f, -0.0f, -0.0f, -0.0f, -0.0f, -0.0f};
+    orc_v8 s0 = z, s1 = z, s2 = z, s3 = z;
+    if (nt == 4) {
+        for (size_t i = 0; i < n; i++) {
+            orc_v8 p0 = wt[i] * x[0][i], p1 = wt[i] * x[1][i], p2 = wt[i] * x[2][i], p3 = wt[i] * x[3][i];
+            s0 = s0 + p0;
+            s1 = s1 + p1;
+            s2 = s2 + p2;
+            s3 = s3 + p3;
+        }
+    } else {
+        for (size_t i = 0; i < n; i++) {
+            orc_v8 p0 = wt[i] * x[0][i];
+            s0 = s0 + p0;
+        }
     }
-    for (int k = 0; k < 8; k++)
-        out[k] = s[k];
+    out[0] = s0, out[1] = s1, out[2] = s2, out[3] = s3;
 }
 
 static void *qm_worker(void *arg) {
     qm_job *j = (qm_job *)arg;
-    size_t T8 = j->n_tokens / 8;
     float *row = (float *)malloc(j->n_in * sizeof(float));
-    orc_v8 *xt = T8 ? (orc_v8 *)aligned_alloc(32, T8 * j->n_in * sizeof(orc_v8)) : NULL;
-    if (!row || (T8 && !xt)) {
+    orc_v8 *wt = (orc_v8 *)aligned_alloc(32, j->n_in * sizeof(orc_v8));
+    if (!row || !wt) {
         free(row);
-        free(xt);
+        free(wt);
         j->status = SHAPE;
         return NULL;
     }
-    for (size_t g = 0; g < T8; g++)
-        for (size_t i = 0; i < j->n_in; i++)
-            for (int k = 0; k < 8; k++)
-                xt[g * j->n_in + i][k] = j->x[(8 * g + (size_t)k) * j->n_in + i];
-    for (size_t r = j->r0; r < j->r1; r++) {
-        if (orc_dequantize_row(j->dtype, j->w + r * j->row_bytes, j->row_bytes, row, j->n_in)) {
-            j->status = SHAPE;
-            break;
+    for (size_t r0 = j->r0; r0 < j->r1; r0 += 8) {
+        size_t nr = j->r1 - r0 < 8 ? j->r1 - r0 : 8;
+        for (size_t k = 0; k < 8; k++) { /* rows past the block's end repeat its last row */
+            size_t r = r0 + (k < nr ? k : nr - 1);
+            if (orc_dequantize_row(j->dtype, j->w + r * j->row_bytes, j->row_bytes, row, j->n_in)) {
+                j->status = SHAPE;
+                goto done;
+            }
+            for (size_t i = 0; i < j->n_in; i++)
+                wt[i][k] = row[i];
         }
-        for (size_t g = 0; g < T8; g++) {
-            float o[8];
-            dot8(row, xt + g * j->n_in, j->n_in, o);
-            for (int k = 0; k < 8; k++)
-                j->y[(8 * g + (size_t)k) * j->n_out + r] = o[k];
+        for (size_t t = 0; t < j->n_tokens;) {
+            int nt = j->n_tokens - t >= 4 ? 4 : 1;
+            const float *xs[4];
+            for (int q = 0; q < 4; q++)
+                xs[q] = j->x + (t + (size_t)(q < nt ? q : 0)) * j->n_in;
+            orc_v8 o[4];
+            dots_8rows(wt, j->n_in, xs, nt, o);
+            for (int q = 0; q < nt; q++)
+                for (size_t k = 0; k < nr; k++)
+                    j->y[(t + (size_t)q) * j->n_out + r0 + k] = o[q][k];
+            t += (size_t)nt;
         }
-        for (size_t t = 8 * T8; t < j->n_tokens; t++)
-            j->y[t * j->n_out + r] = dot(row, j->x + t * j->n_in, j->n_in);
     }
+done:
     free(row);
-    free(xt);
+    free(wt);
     return NULL;
 }
 
@@ -318,6 +336,7 @@ int orc_qmatmul(int dtype, const uint8_t *w, size_t w_bytes, size_t n_out, size_
     qm_job *jobs = (qm_job *)calloc((size_t)n_threads, sizeof(qm_job));
     pthread_t *th = (pthread_t *)calloc((size_t)n_threads, sizeof(pthread_t));
     size_t per = (n_out + (size_t)n_threads - 1) / (size_t)n_threads;
+    per = (per + 7) / 8 * 8; /* whole blocks of eight rows per thread */
     for (int i = 0; i < n_threads; i++) {
         qm_job *j = &jobs[i];
         j->dtype = dtype;

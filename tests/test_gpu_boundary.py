@@ -56,6 +56,30 @@ def test_trait_upload_repacks_on_first_use(backend, dtype, rows, k):
         assert np.array_equal(backend.download_f32(yb), backend.download_f32(y2))
 
 
+def test_view_of_trait_upload_keeps_the_weight_raw(backend):
+    # A view into a weight's raw bytes taken before its first use: the weight
+    # stays raw (a repack would free the bytes under the view), the view
+    # downloads the uploaded bytes, and ops through the parent and the view
+    # both read them.
+    rows, k = 96, 1024
+    raw = synth.weight(Q4K, rows, k, 711)
+    x = synth.normal_f32(2 * k, 712)
+    buf = backend.upload_weight_bytes(raw, LAYOUT_GGUF)
+    view = backend.view(buf, 0, buf.len)
+    xb = backend.f32_buf(x)
+    y_parent, y_view = backend.alloc(2 * rows * 4), backend.alloc(2 * rows * 4)
+    backend.qmatmul_f32(QWeight(Q4K, (rows, k), buf), xb, y_parent)
+    assert backend.buf_layout(buf) == LAYOUT_GGUF and buf.len == raw.nbytes
+    assert np.array_equal(backend.download(view, 0, view.len), raw.view(np.uint8))
+    backend.qmatmul_f32(QWeight(Q4K, (rows, k), view), xb, y_view)
+    a, b = backend.download_f32(y_parent), backend.download_f32(y_view)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    cpu = ffi.qmatmul(Q4K, raw, rows, k, x)
+    assert_parity(a, cpu, f32_exact(npq.dequantize(Q4K, raw, rows, k), x), rtol=1e-5, what="view of raw weight",
+                  correctly_rounded=True)
+    view.close()
+
+
 def test_trait_upload_layouts(backend):
     raw = synth.weight(Q4K, 8, 256, 710)
     with pytest.raises(bm.NotImplemented):

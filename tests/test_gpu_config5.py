@@ -24,7 +24,7 @@ import numpy as np
 import pytest
 
 from mdma_amd import llama_synth, synth
-from mdma_amd.backend import ACT_F32, ACT_I8
+from mdma_amd.backend import ACT_F32, ACT_F32_CPU, ACT_I8
 from mdma_amd.model import Model
 
 pytestmark = pytest.mark.gpu
@@ -95,3 +95,138 @@ def test_config5_batched_decode_equals_single_sequences(backend, config5):
         assert np.array_equal(one[0], batched[b]), b
     s.close()
     m.close()
+
+
+# ---- the configured workload, free-running: 512-token prompt, 256 greedy tokens, ctx 4096 ----
+GREEDY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "config5_greedy.json")
+N_PROMPT, N_GEN, CAPACITY = 512, 256, 4096
+
+
+def config5_prompts(seed, batch=8):
+    # tests/golden/make_golden.py config5_prompts: sequence b from seed + 100 + b.
+    return np.stack([synth.tokens(N_PROMPT, 128256, seed + 100 + b) for b in range(batch)])
+
+
+def greedy_last(v):
+    return int(v.size - 1 - np.argmax(v[::-1]))  # sampler::greedy: ties to the last index
+
+
+def free_run(backend, path, prompt):
+    """Prefill, then greedy decode through Model::forward steps on a cache of
+    config 5's context: (tokens [N_GEN], logits [N_GEN, vocab])."""
+    m = Model(backend, path)
+    s = m.session(CAPACITY, 1, N_PROMPT)
+    lg = s.prefill(prompt, 0)
+    toks, logits = [], []
+    for i in range(N_GEN):
+        logits.append(lg)
+        toks.append(greedy_last(lg))
+        if i + 1 < N_GEN:
+            lg = s.forward(toks[-1], N_PROMPT + i)
+    s.reset()
+    gen, _ = s.generate(prompt[None, :], N_GEN)  # the captured, replayed decode loop
+    s.close()
+    m.close()
+    return np.array(toks), np.stack(logits), gen[0]
+
+
+def sha1(v):
+    import hashlib
+    return hashlib.sha1(np.ascontiguousarray(v, dtype="<f4").tobytes()).hexdigest()
+
+
+@pytest.fixture(scope="module")
+def greedy_fx(config5):
+    fx = json.load(open(GREEDY))
+    assert fx["seed"] == config5[1]["seed"] and fx["n_prompt"] == N_PROMPT and fx["n_gen"] == N_GEN
+    prompts = config5_prompts(fx["seed"])
+    import hashlib
+    assert hashlib.sha1(np.ascontiguousarray(prompts, dtype="<u4").tobytes()).hexdigest() == fx["prompts_sha1"]
+    return fx, prompts
+
+
+def test_config5_cpu_order_greedy_bit_identical(backend, config5, greedy_fx):
+    """The CPU-order mode: every one of the 256 steps' logits has the oracle's
+    bytes (sha1 of the f32 logits), so all 256 greedy tokens are the CPU
+    backend's, near-ties included; generate's replayed loop gives the same
+    tokens."""
+    path = config5[0]
+    fx, prompts = greedy_fx
+    steps = fx["seqs"]["0"]["f32"]
+    backend.set_act_mode(ACT_F32_CPU)
+    try:
+        toks, logits, gen = free_run(backend, path, prompts[0])
+    finally:
+        backend.set_act_mode(ACT_F32)
+    bad = [i for i in range(N_GEN) if sha1(logits[i]) != steps[i]["sha1"]]
+    assert not bad, f"logits differ from the oracle's at steps {bad[:8]}"
+    assert toks.tolist() == [st["greedy"] for st in steps]
+    assert np.array_equal(gen, toks)
+    print(f"config5 cpu-order: 256 steps bit-identical; smallest top-2 margin / max|logit| "
+          f"{min(st['margin'] / st['max_abs'] for st in steps):.2e}")
+
+
+@pytest.mark.parametrize("mode", ["f32", "i8"])
+def test_config5_greedy_tokens_match_oracle_until_first_near_tie(backend, config5, greedy_fx, mode):
+    """The fast f32 mode and the int8 mode (the benchmarked path): the greedy
+    tokens equal the oracle's at every step up to the first one whose top-2
+    margin is within the measured logit error (the fast modes' sums round
+    differently from the CPU's, a near-tie may flip), which the test names;
+    until then the top-4 logits agree within the same bars as the
+    teacher-forced test. generate's replayed loop gives the eager tokens."""
+    path = config5[0]
+    fx, prompts = greedy_fx
+    steps = fx["seqs"]["0"][mode]
+    backend.set_act_mode(ACT_F32 if mode == "f32" else ACT_I8)
+    try:
+        toks, logits, gen = free_run(backend, path, prompts[0])
+    finally:
+        backend.set_act_mode(ACT_F32)
+    rtol = F32_LOGIT_RTOL if mode == "f32" else I8_LOGIT_RTOL
+    margin = 2 * F32_LOGIT_RTOL if mode == "f32" else I8_TOKEN_MARGIN
+    assert np.array_equal(gen, toks)
+    stop = next((i for i, st in enumerate(steps) if st["margin"] / st["max_abs"] <= margin), N_GEN)
+    for i in range(stop):
+        st = steps[i]
+        t = np.array([t for t, _ in st["top4"]])
+        want = np.array([v for _, v in st["top4"]])
+        err = float(np.max(np.abs(logits[i, t] - want)) / st["max_abs"])
+        assert err <= rtol, (mode, i, err)
+        assert toks[i] == st["greedy"], (mode, i)
+    print(f"config5 {mode}: greedy tokens equal the oracle's for steps 0..{stop - 1}"
+          + (f"; step {stop} is a near-tie (margin / max|logit| {steps[stop]['margin'] / steps[stop]['max_abs']:.2e})"
+             if stop < N_GEN else " (all 256)"))
+    assert stop >= 64, f"near-tie at step {stop}: too early for the gate to mean anything"
+
+
+def test_config5_int8_batch8_decode(backend, config5, greedy_fx):
+    """int8 batch-8 decode at Llama-3-8B geometry (the ring GEMVs over the Q6_K
+    tile images, the benchmarked batch path): sequence 0 follows the oracle's
+    int8 tokens up to the oracle's first near-tie, and every sequence follows
+    its own single-sequence decode up to that decode's first near-tie
+    (batched and single GEMVs sum blocks in different orders)."""
+    path = config5[0]
+    fx, prompts = greedy_fx
+    backend.set_act_mode(ACT_I8)
+    try:
+        m = Model(backend, path)
+        s = m.session(CAPACITY, 8, N_PROMPT)
+        batched, _ = s.generate(prompts, N_GEN)
+        s.close()
+        m.close()
+        singles = [free_run(backend, path, prompts[b]) for b in range(8)]
+    finally:
+        backend.set_act_mode(ACT_F32)
+    steps = fx["seqs"]["0"]["i8"]
+    stop0 = next((i for i, st in enumerate(steps) if st["margin"] / st["max_abs"] <= I8_TOKEN_MARGIN), N_GEN)
+    assert batched[0][:stop0].tolist() == [st["greedy"] for st in steps[:stop0]]
+    report = []
+    for b in range(8):
+        toks, logits, _ = singles[b]
+        srt = np.sort(logits, axis=1)
+        rel = (srt[:, -1] - srt[:, -2]) / np.max(np.abs(logits), axis=1)
+        stop = next((i for i in range(N_GEN) if rel[i] <= I8_TOKEN_MARGIN), N_GEN)
+        assert np.array_equal(batched[b][:stop], toks[:stop]), b
+        report.append(stop)
+    print(f"config5 int8 batch 8: sequence 0 equals the oracle for {stop0} steps; each sequence equals its "
+          f"single-sequence decode up to its first near-tie, steps {report}")

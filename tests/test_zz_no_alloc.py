@@ -97,3 +97,27 @@ def test_noalloc_rejects_oversize_and_keeps_cached_activations(backend):
         assert np.array_equal(backend.download_f32(y1), backend.download_f32(y2))
     finally:
         backend.set_act_mode(backend_mod.ACT_F32)
+
+
+def test_noalloc_calls_from_two_contexts_on_one_gpu(backend):
+    """Two contexts share the GPU's static array: their calls, issued back to
+    back without waiting for each other, are ordered by the per-GPU event,
+    so each output equals its allocating counterpart's."""
+    other = backend_mod.Gfx950Backend(0)
+    try:
+        k, rows = 4096, 2048
+        raw = synth.weight(Q4K, rows, k, 41)
+        wa, wb = backend.upload_weight(raw, Q4K, (rows, k)), other.upload_weight(raw, Q4K, (rows, k))
+        xs = [synth.normal_f32(5 * k, 50 + i) for i in range(6)]
+        outs = []
+        for i, x in enumerate(xs):
+            be, w = (backend, wa) if i % 2 == 0 else (other, wb)
+            xb, yb = be.f32_buf(x), be.alloc(5 * rows * 4)
+            be.qmatmul_i8_noalloc(w, xb, yb)
+            outs.append((be, w, x, xb, yb))
+        for be, w, x, xb, yb in outs:
+            want = be.alloc(5 * rows * 4)
+            be.qmatmul_i8(w, be.f32_buf(x), want)
+            assert np.array_equal(be.download_f32(yb).view(np.uint32), be.download_f32(want).view(np.uint32))
+    finally:
+        other.close()
