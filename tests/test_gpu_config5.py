@@ -137,6 +137,8 @@ def sha1(v):
 
 @pytest.fixture(scope="module")
 def greedy_fx(config5):
+    if not os.path.exists(GREEDY):
+        pytest.skip("tests/golden/config5_greedy.json not generated yet (make_golden.py config5_greedy)")
     fx = json.load(open(GREEDY))
     assert fx["seed"] == config5[1]["seed"] and fx["n_prompt"] == N_PROMPT and fx["n_gen"] == N_GEN
     prompts = config5_prompts(fx["seed"])
