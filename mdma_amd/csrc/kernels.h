@@ -34,16 +34,22 @@ __device__ __forceinline__ void lds_barrier() {
 // wait for these loads before every LDS read of the other buffer. The
 // kernel waits for them itself (lds_wait_dma) before reading what they
 // wrote or publishing it at a barrier.
+// The statement sets M0, a register the compiler reserves: clang does not
+// honour M0 in a clobber list, so nothing here tells it that M0 changed.
+// That is safe only while the kernels that use these helpers contain no
+// other M0 use; tests/test_m0_usage.py compiles them and checks that every
+// M0 write is one of these statements, directly followed by its DMA, and
+// that no other instruction reads or writes M0.
 __device__ __forceinline__ uint32_t lds_addr(const void *lds) {
   return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);  // the LDS offset: low bits of the address
 }
 __device__ __forceinline__ void lds_dma16(const void *base, uint32_t off, const void *lds) {
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds_addr(lds))
-               : "memory", "m0");
+               : "memory");
 }
 __device__ __forceinline__ void lds_dma4(const void *base, uint32_t off, const void *lds) {
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds_addr(lds))
-               : "memory", "m0");
+               : "memory");
 }
 __device__ __forceinline__ void lds_wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 

@@ -167,22 +167,23 @@ static void deq_q6_k(const uint8_t *b, float *y) {
     const uint8_t *ql = b, *qh = b + 128;
     const int8_t *sc = (const int8_t *)(b + 192);
     float d = ld_f16(b + 208);
-    for (int n = 0; n < 2; n++) {
-        const uint8_t *l8 = ql + 64 * n, *h8 = qh + 32 * n;
-        const int8_t *s8 = sc + 8 * n;
-        float *yy = y + 128 * n;
-        for (int l = 0; l < 32; l++) {
-            int is = l / 16;
-            int q1 = (int)((l8[l] & 0xF) | (((h8[l] >> 0) & 3) << 4)) - 32;
-            int q2 = (int)((l8[l + 32] & 0xF) | (((h8[l] >> 2) & 3) << 4)) - 32;
-            int q3 = (int)((l8[l] >> 4) | (((h8[l] >> 4) & 3) << 4)) - 32;
-            int q4 = (int)((l8[l + 32] >> 4) | (((h8[l] >> 6) & 3) << 4)) - 32;
-            yy[l] = d * (float)s8[is] * (float)q1;
-            yy[l + 32] = d * (float)s8[is + 2] * (float)q2;
-            yy[l + 64] = d * (float)s8[is + 4] * (float)q3;
-            yy[l + 96] = d * (float)s8[is + 6] * (float)q4;
+    /* Column 128n + 32r + l: quarter r of half n takes the low (r < 2) or high
+     * nibble of ql[64n + 32(r & 1) + l], bits 2r..2r+1 of qh[32n + l], and the
+     * scale sc[8n + 2r + l/16]. Written quarter by quarter, 16 columns of one
+     * scale at a time, so the compiler vectorizes the inner loop. */
+    for (int n = 0; n < 2; n++)
+        for (int r = 0; r < 4; r++) {
+            const uint8_t *l8 = ql + 64 * n + 32 * (r & 1), *h8 = qh + 32 * n;
+            const int sl = 4 * (r >> 1), sh = 2 * r;
+            for (int h = 0; h < 2; h++) {
+                float ds = d * (float)sc[8 * n + 2 * r + h];
+                float *yy = y + 128 * n + 32 * r + 16 * h;
+                for (int l = 0; l < 16; l++) {
+                    int q = (int)(((l8[16 * h + l] >> sl) & 0xF) | (((h8[16 * h + l] >> sh) & 3) << 4)) - 32;
+                    yy[l] = ds * (float)q;
+                }
+            }
         }
-    }
 }
 
 /* dequantize_row: src/backend/cpu/dequant.rs:13-58 (whole blocks only). */
