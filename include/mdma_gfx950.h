@@ -138,7 +138,11 @@ int mdma_gfx950_join_execution(mdma_ctx *ctx);
 int mdma_gfx950_set_buffer_budget(mdma_ctx *ctx, uint64_t device_bytes, uint64_t host_bytes);
 /* BufferBudget::used / limit of one domain (mdma_memory_domain). */
 int mdma_gfx950_buffer_usage(mdma_ctx *ctx, int domain, uint64_t *used, uint64_t *limit);
-/* Extra: select the decode GEMV activation mode (default MDMA_ACT_F32). */
+/* Extra: select the arithmetic of the GEMVs, GEMMs and per-token ops that
+ * follow (a mdma_act_mode; default MDMA_ACT_F32). MDMA_ACT_F32_CPU also switches
+ * rmsnorm, silu_mul and attention to the CPU backend's evaluation order. After a
+ * mode change, graphs captured before it refuse to launch (mdma_gfx950_graph_launch
+ * fails; the library's decoder recaptures its step). */
 int mdma_gfx950_set_act_mode(mdma_ctx *ctx, int mode);
 /* Extra: in the int8 mode's one-token decode, fuse each layer's attention
  * RMSNorm into the GEMVs around it (the down projection stores the residual
