@@ -16,6 +16,16 @@ the greedy token must be the oracle's where its top-2 margin is clear:
 Batched decode of 8 sequences must give each sequence's single-sequence
 tokens (f32 mode: every GEMV is the correctly rounded dot product, whatever
 the batch).
+
+Then the configured workload itself, free running (tests/golden/
+config5_greedy.json, written by make_golden.py config5_greedy): a 512-token
+prompt, 256 greedy tokens, a session of 4096 positions, against the
+oracle's own free-running decode (f16-rounded KV) in the f32 and int8 modes:
+  - the CPU-order mode's logits equal the oracle's bytes at all 256 steps;
+  - the f32 and int8 modes keep the top-4 logits within the bars above and
+    give the oracle's 256 greedy tokens;
+  - int8 batch-8 decode gives the oracle's tokens for sequence 0 and every
+    sequence's single-sequence tokens.
 """
 import json
 import os
@@ -137,14 +147,31 @@ def sha1(v):
 
 @pytest.fixture(scope="module")
 def greedy_fx(config5):
-    if not os.path.exists(GREEDY):
-        pytest.skip("tests/golden/config5_greedy.json not generated yet (make_golden.py config5_greedy)")
     fx = json.load(open(GREEDY))
     assert fx["seed"] == config5[1]["seed"] and fx["n_prompt"] == N_PROMPT and fx["n_gen"] == N_GEN
     prompts = config5_prompts(fx["seed"])
     import hashlib
     assert hashlib.sha1(np.ascontiguousarray(prompts, dtype="<u4").tobytes()).hexdigest() == fx["prompts_sha1"]
     return fx, prompts
+
+
+def top4_error(logits, steps):
+    """Per step: max over the oracle's top-4 tokens of |gpu - oracle| / max|logit|."""
+    err = np.zeros(len(steps))
+    for i, st in enumerate(steps):
+        t = np.array([t for t, _ in st["top4"]])
+        want = np.array([v for _, v in st["top4"]])
+        err[i] = np.max(np.abs(logits[i, t] - want)) / st["max_abs"]
+    return err
+
+
+def first_token_mismatch(toks, steps):
+    bad = [i for i, st in enumerate(steps) if int(toks[i]) != st["greedy"]]
+    if not bad:
+        return None
+    i = bad[0]
+    return f"step {i}: gpu {int(toks[i])}, oracle {steps[i]['greedy']} (oracle top-2 margin / max|logit| " \
+           f"{steps[i]['margin'] / steps[i]['max_abs']:.2e}); {len(bad)} steps differ"
 
 
 def test_config5_cpu_order_greedy_bit_identical(backend, config5, greedy_fx):
@@ -169,13 +196,17 @@ def test_config5_cpu_order_greedy_bit_identical(backend, config5, greedy_fx):
 
 
 @pytest.mark.parametrize("mode", ["f32", "i8"])
-def test_config5_greedy_tokens_match_oracle_until_first_near_tie(backend, config5, greedy_fx, mode):
-    """The fast f32 mode and the int8 mode (the benchmarked path): the greedy
-    tokens equal the oracle's at every step up to the first one whose top-2
-    margin is within the measured logit error (the fast modes' sums round
-    differently from the CPU's, a near-tie may flip), which the test names;
-    until then the top-4 logits agree within the same bars as the
-    teacher-forced test. generate's replayed loop gives the eager tokens."""
+def test_config5_greedy_tokens_match_oracle(backend, config5, greedy_fx, mode):
+    """The fast f32 mode and the int8 mode (the benchmarked path), free
+    running at the configured workload: every step's top-4 logits agree with
+    the oracle's within the teacher-forced test's bars, and all 256 greedy
+    tokens are the oracle's. Their sums round differently from the CPU's, so
+    a step whose top-2 margin falls within that error could flip; none of
+    the fixture's does today, and a change that flips one fails here with
+    the step and its margin. (The random-init model keeps choosing one
+    token, whatever the context; the logits differ at every step, which is
+    what the top-4 check and the CPU-order test's sha1s follow.)
+    generate's replayed loop gives the eager tokens."""
     path = config5[0]
     fx, prompts = greedy_fx
     steps = fx["seqs"]["0"][mode]
@@ -185,28 +216,26 @@ def test_config5_greedy_tokens_match_oracle_until_first_near_tie(backend, config
     finally:
         backend.set_act_mode(ACT_F32)
     rtol = F32_LOGIT_RTOL if mode == "f32" else I8_LOGIT_RTOL
-    margin = 2 * F32_LOGIT_RTOL if mode == "f32" else I8_TOKEN_MARGIN
+    err = top4_error(logits, steps)
+    assert np.all(err <= rtol), (mode, int(np.argmax(err)), float(err.max()))
+    mism = first_token_mismatch(toks, steps)
+    assert mism is None, f"{mode}: {mism}"
     assert np.array_equal(gen, toks)
-    stop = next((i for i, st in enumerate(steps) if st["margin"] / st["max_abs"] <= margin), N_GEN)
-    for i in range(stop):
-        st = steps[i]
-        t = np.array([t for t, _ in st["top4"]])
-        want = np.array([v for _, v in st["top4"]])
-        err = float(np.max(np.abs(logits[i, t] - want)) / st["max_abs"])
-        assert err <= rtol, (mode, i, err)
-        assert toks[i] == st["greedy"], (mode, i)
-    print(f"config5 {mode}: greedy tokens equal the oracle's for steps 0..{stop - 1}"
-          + (f"; step {stop} is a near-tie (margin / max|logit| {steps[stop]['margin'] / steps[stop]['max_abs']:.2e})"
-             if stop < N_GEN else " (all 256)"))
-    assert stop >= 64, f"near-tie at step {stop}: too early for the gate to mean anything"
+    print(f"config5 {mode}: 256 greedy tokens equal the oracle's; worst top-4 |dlogit|/max|logit| {err.max():.2e}, "
+          f"smallest oracle margin {min(st['margin'] / st['max_abs'] for st in steps):.2e}")
 
 
 def test_config5_int8_batch8_decode(backend, config5, greedy_fx):
-    """int8 batch-8 decode at Llama-3-8B geometry (the ring GEMVs over the Q6_K
-    tile images, the benchmarked batch path): sequence 0 follows the oracle's
-    int8 tokens up to the oracle's first near-tie, and every sequence follows
-    its own single-sequence decode up to that decode's first near-tie
-    (batched and single GEMVs sum blocks in different orders)."""
+    """int8 batch-8 decode at Llama-3-8B geometry on a 4096-position cache
+    (the ring GEMVs over the Q6_K tile images, the benchmarked batch path):
+    sequence 0's 256 tokens are the oracle's int8 tokens, and every
+    sequence's tokens are its single-sequence decode's until a step where
+    they part. Batched and single GEMVs sum blocks in different orders, so
+    an activation can quantize to the neighbouring int8 value and the logits
+    differ by up to the int8 bar (I8_LOGIT_RTOL of max|logit|, the error
+    measured against the oracle); a parting step must therefore be a
+    near-tie of the single run (top-2 margin within twice that bar), never a
+    clear choice."""
     path = config5[0]
     fx, prompts = greedy_fx
     backend.set_act_mode(ACT_I8)
@@ -220,15 +249,19 @@ def test_config5_int8_batch8_decode(backend, config5, greedy_fx):
     finally:
         backend.set_act_mode(ACT_F32)
     steps = fx["seqs"]["0"]["i8"]
-    stop0 = next((i for i, st in enumerate(steps) if st["margin"] / st["max_abs"] <= I8_TOKEN_MARGIN), N_GEN)
-    assert batched[0][:stop0].tolist() == [st["greedy"] for st in steps[:stop0]]
+    mism = first_token_mismatch(batched[0], steps)
+    assert mism is None, f"batch 8, sequence 0 against the oracle: {mism}"
     report = []
     for b in range(8):
         toks, logits, _ = singles[b]
-        srt = np.sort(logits, axis=1)
-        rel = (srt[:, -1] - srt[:, -2]) / np.max(np.abs(logits), axis=1)
-        stop = next((i for i in range(N_GEN) if rel[i] <= I8_TOKEN_MARGIN), N_GEN)
-        assert np.array_equal(batched[b][:stop], toks[:stop]), b
-        report.append(stop)
-    print(f"config5 int8 batch 8: sequence 0 equals the oracle for {stop0} steps; each sequence equals its "
-          f"single-sequence decode up to its first near-tie, steps {report}")
+        diff = np.nonzero(batched[b] != toks)[0]
+        if not diff.size:
+            report.append("all 256")
+            continue
+        i = int(diff[0])
+        srt = np.sort(logits[i])
+        rel = float((srt[-1] - srt[-2]) / np.max(np.abs(logits[i])))
+        assert rel <= 2 * I8_LOGIT_RTOL, (b, i, rel)
+        report.append(f"{i} (near-tie, margin {rel:.1e})")
+    print(f"config5 int8 batch 8: sequence 0 equals the oracle for 256 steps; each sequence equals its "
+          f"single-sequence decode up to step: {report}")

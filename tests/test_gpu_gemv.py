@@ -843,6 +843,42 @@ def test_prefill_gemm_config4_shapes_sampled_rows(backend, dtype, prefill_kernel
         w.buf.close(), xb.close(), yb.close()
 
 
+def q6k_full_scale_range(raw, rows, k, seed):
+    """Q6_K blocks whose sub-block scales span the whole int8 range, as real
+    Q6_K files have (the quantizer sets a scale of -128 in every super-block):
+    each block gets -128 and 127 and random scales in [-128, 127]."""
+    rng = np.random.default_rng(seed)
+    b = np.frombuffer(raw, np.uint8).copy().reshape(rows * (k // 256), 210)
+    n = b.shape[0]
+    sc = rng.integers(-128, 128, size=(n, 16)).astype(np.int8)
+    lo = rng.integers(0, 16, size=n)
+    sc[np.arange(n), lo] = -128
+    sc[np.arange(n), (lo + rng.integers(1, 16, size=n)) % 16] = 127
+    b[:, 192:208] = sc.view(np.uint8)
+    return b.reshape(-1)
+
+
+def test_prefill_gemm_q6k_full_scale_range(backend):
+    """Q6_K sub-block scales over all of [-128, 127] (the benchmark
+    distribution keeps them in [-64, 63]; weight values sc * q then reach
+    4096), at a config-4 shape and a small one."""
+    for T, k, rows in ((64, 512, 96), (512, 4096, 14336)):
+        raw = q6k_full_scale_range(synth.weight(Q6K, rows, k, 600 + T), rows, k, 601)
+        x = synth.normal_f32(T * k, 602 + T)
+        w = backend.upload_weight(raw, Q6K, (rows, k))
+        xb, yb = backend.f32_buf(x), backend.alloc(T * rows * 4)
+        backend.qmatmul_i8(w, xb, yb)
+        y = backend.download_f32(yb).reshape(T, rows)
+        rb = len(raw) // rows
+        for r0 in sorted({0, rows // 2 + 13, rows - 16}):
+            sl = raw[r0 * rb:(r0 + 16) * rb]
+            tok = np.unique(np.r_[0:8, min(130, T - 3):min(133, T), T - 8:T])
+            cpu, exact, absum = oracle_i8_32(Q6K, sl, 16, k, x.reshape(T, k)[tok].reshape(-1))
+            assert_parity(y[tok, r0:r0 + 16].reshape(-1), cpu, exact, 1e-3, abs_sum=absum,
+                          what=f"gemm q6k full scales T={T} rows {r0}..")
+        w.buf.close(), xb.close(), yb.close()
+
+
 @pytest.mark.parametrize("dtype", [Q8, Q4K, Q6K])
 def test_prefill_gemm_fused_calls(backend, dtype):
     backend.set_act_mode(1)
