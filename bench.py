@@ -403,6 +403,37 @@ def e2e_decode(be, n_prompt=512, n_gen=256, batches=(1, 8), path=E2E_PATH, capac
     return out
 
 
+def e2e_cpu_order(be, n_prompt=512, n_gen=32, path=E2E_PATH, capacity=4096):
+    """The CPU-order mode (MDMA_ACT_F32_CPU: every output in the CPU
+    backend's rounding order, logits bit-identical to it) on the config-5
+    model: a 512-token prompt, then n_gen greedy steps at batch 1, decode
+    replaying the captured step. A parity mode, not a throughput one: each
+    output row is one lane's sequential chain of n_in additions."""
+    from mdma_amd import llama_synth, synth
+    from mdma_amd.backend import ACT_F32, ACT_F32_CPU
+    from mdma_amd.model import Model
+
+    if not os.path.exists(path):
+        llama_synth.write(path, llama_synth.LLAMA3_8B, llama_synth.Q4_K_M, SEED, fast=True)
+    be.set_act_mode(ACT_F32_CPU)
+    try:
+        m = Model(be, path)
+        s = m.session(capacity, 1, n_prompt)
+        prompt = synth.tokens(n_prompt, 128256, SEED + 50)[None, :]
+        s.generate(prompt, 2)  # warm
+        s.reset()
+        toks, secs = s.generate(prompt, n_gen)
+        s.close()
+        m.close()
+    finally:
+        be.set_act_mode(ACT_F32)
+    dec = secs[1:]
+    return {"prompt_tokens": n_prompt, "decode_tokens": n_gen, "kv_capacity": capacity,
+            "prefill_and_first_token_ms": round(secs[0] * 1e3, 1), "decode_tok_s": round(len(dec) / dec.sum(), 2),
+            "decode_ms_per_step_p50": round(float(np.median(dec)) * 1e3, 2),
+            "tokens_sha1": hashlib.sha1(np.ascontiguousarray(toks).tobytes()).hexdigest()[:16]}
+
+
 CONFIG1_SEED, CONFIG1_PROMPT_SEED = 1, 1001
 
 
@@ -638,6 +669,8 @@ def main():
                     help="only the prefill GEMM leg (for profiler traces and counters of the GEMMs)")
     ap.add_argument("--q6-only", action="store_true",
                     help="only the Q6_K GEMV leg (head and down at 1, 4 and 8 tokens; for profiler traces)")
+    ap.add_argument("--cpu-order-only", action="store_true",
+                    help="only the CPU-order mode's end-to-end decode (parity mode: the CPU backend's rounding order)")
     ap.add_argument("--eager-decode", action="store_true",
                     help="end-to-end decode steps launched eagerly instead of replayed from a captured HIP graph "
                          "(the same kernels; for profilers that do not follow graph replays)")
@@ -654,6 +687,9 @@ def main():
     init_s = time.perf_counter() - t0
     if args.eager_decode:
         be.set_graph_decode(False)
+    if args.cpu_order_only:
+        print(json.dumps({"e2e_cpu_order": e2e_cpu_order(be), "device": be.device_label()}), flush=True)
+        return
     if args.e2e_only:
         print(json.dumps({"e2e_llama3_8b": e2e_decode(be), "device": be.device_label()}), flush=True)
         return
