@@ -405,6 +405,228 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q, 
   if (threadIdx.x < hd) o[((size_t)i * n_q_heads + qh) * hd + threadIdx.x] = acc / l;
 }
 
+// Causal GQA attention for a prompt (one sequence, seq_stride 0: query i
+// sees keys [0, prefix + i]; at least ATT_PREFILL_MIN queries) on the matrix
+// cores, flash-attention style. A workgroup takes 64 rows, 64/G queries
+// times the G query heads of one KV head; wave w owns rows 16w..16w+15.
+// Per tile of 64 keys:
+//   S = Q K^T on v_mfma_f32_16x16x32_f16. The f16 keys are exact operands;
+//     q is split exactly into three f16 parts (hi = f16(q), mid = f16(q -
+//     hi), lo = q - hi - mid: 11 + 11 + 2 of its 24 bits), three MFMAs of
+//     exact products added in f32, as the f32 kernels' dot products are;
+//   an online softmax per row: the row's 64 scores sit on the 16 lanes of
+//     one DPP row (4 per lane, one per 16-key block), max and sum by DPP;
+//   O += P V on the same MFMA, P (f32, through a per-wave LDS tile of rows x
+//     keys) split into f16 hi and lo as it is read; V goes to LDS
+//     transposed (dims x keys), so an operand's 8 keys are one 16-byte read.
+// s = (q.k) * scale and p = expf(s - m) in f32, the output O / l.
+constexpr uint32_t ATT_PREFILL_MIN = 64;
+
+typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_row_op_max(float v) {
+  return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, -INFINITY),
+                                                                         __builtin_bit_cast(int, v), CTRL, 0xF, 0xF,
+                                                                         false)));
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_row_op_sum(float v) {
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF,
+                                                                    false));
+}
+// Max / sum over the 16 lanes of this lane's DPP row, in every lane of it.
+__device__ __forceinline__ float row16_max(float v) {
+  v = dpp_row_op_max<0xB1>(v);
+  v = dpp_row_op_max<0x4E>(v);
+  v = dpp_row_op_max<0x141>(v);
+  return dpp_row_op_max<0x140>(v);
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v = dpp_row_op_sum<0xB1>(v);
+  v = dpp_row_op_sum<0x4E>(v);
+  v = dpp_row_op_sum<0x141>(v);
+  return dpp_row_op_sum<0x140>(v);
+}
+
+template <int G, int HD>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restrict__ q, const uint16_t *__restrict__ K,
+                                                           const uint16_t *__restrict__ V, float *__restrict__ o,
+                                                           uint32_t n_q, uint32_t prefix, uint32_t n_q_heads,
+                                                           uint32_t n_kv_heads, float scale) {
+  constexpr int QT = 64 / G;             // queries per workgroup
+  constexpr int NC = HD / 32;            // 32-dim K steps of S
+  constexpr int ND = HD / 16;            // 16-dim blocks of O
+  constexpr int KCH = HD / 8;            // 16-byte chunks of a key row
+  constexpr int LPT = 64 * KCH / 256;    // chunks of K (and of V) per thread per tile
+  constexpr int VP = 64 + 8;             // padded row of the transposed V tile (f16)
+  constexpr int PP = 64 + 4;             // padded row of the P tiles (f32)
+  __shared__ __attribute__((aligned(16))) uint16_t ks[64 * HD];        // keys x dims, chunks swizzled
+  __shared__ __attribute__((aligned(16))) uint16_t vt[HD * VP];        // dims x keys
+  __shared__ __attribute__((aligned(16))) float pw[4][16 * PP];         // per wave: P, rows x keys
+  sgpr_ready(q, K, V, o, n_q, prefix, n_q_heads, n_kv_heads, scale);
+  const uint32_t kvh = blockIdx.x, q0 = blockIdx.y * QT;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, lq = lane >> 4;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t kv_row = n_kv_heads * HD, kv_last = prefix + n_q - 1;
+  const uint16_t *Kh = K + (size_t)kvh * HD, *Vh = V + (size_t)kvh * HD;
+
+  // Tile t's K and V chunks into registers (rows clamped to the cache).
+  // Item i of a thread: keys 2 kp, 2 kp + 1 (kp = lane % 32) of chunk
+  // lane / 32 + 2 (wave + 4 i): the two keys' V values pair up into 32-bit
+  // words of the transposed tile, and a wave's 32-bit writes for one dim
+  // fall on 64 different banks (lanes 32..63 write the rows 8 dims on).
+  constexpr int IT = LPT / 2;  // items per thread
+  uint4 kr[IT][2], vr[IT][2];
+  auto item_ch = [&](int i) { return (lane >> 5) + 2 * (wave + 4 * i); };
+  const uint32_t kp = lane & 31;
+  auto gload = [&](uint32_t t) {
+#pragma unroll
+    for (int i = 0; i < IT; i++) {
+      const uint32_t ch = item_ch(i);
+#pragma unroll
+      for (int e = 0; e < 2; e++) {
+        const size_t row = (size_t)min(64 * t + 2 * kp + e, kv_last) * kv_row + 8 * ch;
+        kr[i][e] = *reinterpret_cast<const uint4 *>(Kh + row);
+        vr[i][e] = *reinterpret_cast<const uint4 *>(Vh + row);
+      }
+    }
+  };
+  gload(0);
+
+  // This lane's Q operand row (16 wave + l16) as f16 hi + mid + lo, dims
+  // 32c + 8lq (each remainder is exact in f32).
+  v8h_t qhi[NC], qmid[NC], qlo[NC];
+  {
+    const uint32_t r = 16 * wave + l16, qi = min(q0 + r / G, n_q - 1), h = kvh * G + r % G;
+    const float *qr = q + ((size_t)qi * n_q_heads + h) * HD + 8 * lq;
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      const float4 a = *reinterpret_cast<const float4 *>(qr + 32 * c);
+      const float4 b = *reinterpret_cast<const float4 *>(qr + 32 * c + 4);
+      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const _Float16 hi = (_Float16)x[e];
+        const float r1 = x[e] - (float)hi;
+        const _Float16 mid = (_Float16)r1;
+        qhi[c][e] = hi;
+        qmid[c][e] = mid;
+        qlo[c][e] = (_Float16)(r1 - (float)mid);
+      }
+    }
+  }
+  // Output rows of this lane: 16 wave + 4 lq + j; the last key each sees.
+  uint32_t vis[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) vis[j] = prefix + q0 + (16 * wave + 4 * lq + j) / G;
+  float m[4], l[4];
+  v4f_t O[ND];
+#pragma unroll
+  for (int j = 0; j < 4; j++) m[j] = -INFINITY, l[j] = 0.f;
+#pragma unroll
+  for (int n = 0; n < ND; n++) O[n] = v4f_t{0.f, 0.f, 0.f, 0.f};
+  const uint32_t n_tiles = (prefix + min(q0 + QT, n_q) - 1) / 64 + 1;
+  float *pwf = pw[wave];
+
+  for (uint32_t t = 0; t < n_tiles; t++) {
+    lds_barrier();  // the previous tile's reads of ks and vt are done
+#pragma unroll
+    for (int i = 0; i < IT; i++) {
+      const uint32_t ch = item_ch(i);
+#pragma unroll
+      for (int e = 0; e < 2; e++) {
+        const uint32_t key = 2 * kp + e;
+        *reinterpret_cast<uint4 *>(&ks[key * HD + 8 * (ch ^ (key & (KCH - 1)))]) = kr[i][e];
+      }
+      const uint32_t a[4] = {vr[i][0].x, vr[i][0].y, vr[i][0].z, vr[i][0].w};
+      const uint32_t b[4] = {vr[i][1].x, vr[i][1].y, vr[i][1].z, vr[i][1].w};
+#pragma unroll
+      for (int d = 0; d < 8; d++) {
+        // dim 8 ch + d of keys 2 kp (low half) and 2 kp + 1 (high half)
+        const uint32_t w = __builtin_amdgcn_perm(b[d >> 1], a[d >> 1], (d & 1) ? 0x07060302u : 0x05040100u);
+        *reinterpret_cast<uint32_t *>(&vt[(8 * ch + d) * VP + 2 * kp]) = w;
+      }
+    }
+    lds_barrier();
+    if (t + 1 < n_tiles) gload(t + 1);  // in flight over this tile's arithmetic
+
+    // ---- S = Q K^T: 16 rows x 64 keys per wave ----
+    v4f_t S[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; kb++) S[kb] = v4f_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      v8h_t B[4];
+#pragma unroll
+      for (int kb = 0; kb < 4; kb++) {
+        const uint32_t key = 16 * kb + l16;
+        B[kb] = *reinterpret_cast<const v8h_t *>(&ks[key * HD + 8 * ((4 * c + lq) ^ (key & (KCH - 1)))]);
+      }
+#pragma unroll
+      for (int kb = 0; kb < 4; kb++) S[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qlo[c], B[kb], S[kb], 0, 0, 0);
+#pragma unroll
+      for (int kb = 0; kb < 4; kb++) S[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qmid[c], B[kb], S[kb], 0, 0, 0);
+#pragma unroll
+      for (int kb = 0; kb < 4; kb++) S[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qhi[c], B[kb], S[kb], 0, 0, 0);
+    }
+    // ---- online softmax; P to this wave's LDS tile ----
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      float s[4], mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 4; kb++) {
+        const uint32_t key = 64 * t + 16 * kb + l16;
+        s[kb] = key <= vis[j] ? S[kb][j] * scale : -INFINITY;
+        mx = fmaxf(mx, s[kb]);
+      }
+      const float mn = fmaxf(m[j], row16_max(mx));  // finite: key 0 is every row's
+      const float alpha = expf(m[j] - mn);          // 0 on the first tile (m = -inf)
+      float ps = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 4; kb++) {
+        const float p = expf(s[kb] - mn);  // 0 for masked keys
+        ps += p;
+        pwf[(4 * lq + j) * PP + 16 * kb + l16] = p;
+      }
+      l[j] = l[j] * alpha + row16_sum(ps);
+      m[j] = mn;
+#pragma unroll
+      for (int n = 0; n < ND; n++) O[n][j] *= alpha;
+    }
+    // ---- O += P V (the wave reads back only its own P tile) ----
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const float4 p0 = *reinterpret_cast<const float4 *>(&pwf[l16 * PP + 32 * c + 8 * lq]);
+      const float4 p1 = *reinterpret_cast<const float4 *>(&pwf[l16 * PP + 32 * c + 8 * lq + 4]);
+      const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+      v8h_t Ah, Al;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const _Float16 hi = (_Float16)pv[e];
+        Ah[e] = hi;
+        Al[e] = (_Float16)(pv[e] - (float)hi);
+      }
+      v8h_t B[ND];
+#pragma unroll
+      for (int n = 0; n < ND; n++) B[n] = *reinterpret_cast<const v8h_t *>(&vt[(16 * n + l16) * VP + 32 * c + 8 * lq]);
+#pragma unroll
+      for (int n = 0; n < ND; n++) O[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ah, B[n], O[n], 0, 0, 0);
+#pragma unroll
+      for (int n = 0; n < ND; n++) O[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, B[n], O[n], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint32_t r = 16 * wave + 4 * lq + j, qi = q0 + r / G, h = kvh * G + r % G;
+    if (qi >= n_q) continue;
+    float *orow = o + ((size_t)qi * n_q_heads + h) * HD + l16;
+#pragma unroll
+    for (int n = 0; n < ND; n++) orow[16 * n] = O[n][j] / l[j];
+  }
+}
+
 // Split-key attention (flash-decoding). A workgroup takes one query, one KV
 // head with all G query heads of its group (each f16 K/V row is read once
 // for the group) and a run of `tpw` tiles of ATT_TILE keys, with an online
@@ -1079,6 +1301,32 @@ bool attn_impl(mdma_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t
                const AttnQ8 *q8, const AttnRope *rope_in = nullptr) {
   uint16_t *k = const_cast<uint16_t *>(kc), *v = const_cast<uint16_t *>(vc);
   const uint32_t *pos_dev = rope_in ? rope_in->pos_dev : nullptr;
+  const uint64_t GP = n_kv_heads ? n_q_heads / n_kv_heads : 0;
+  if (!rope_in && !q8 && !seq_stride && n_q >= ATT_PREFILL_MIN && kv_len >= n_q && (hd == 64 || hd == 128) &&
+      n_kv_heads && GP * n_kv_heads == n_q_heads && (GP == 1 || GP == 2 || GP == 4 || GP == 8) &&
+      kv_len * n_kv_heads * hd < (1ull << 32) && n_kv_heads < 65536) {
+    // A prompt's causal attention on the matrix cores (attn_prefill_kernel).
+    const dim3 grid((uint32_t)n_kv_heads, (uint32_t)((n_q + 64 / GP - 1) / (64 / GP)));
+    const float sc = 1.0f / sqrtf((float)hd);
+    const uint32_t pre = (uint32_t)(kv_len - n_q);
+#define MDMA_ATTP(GG, HH)                                                                                          \
+  attn_prefill_kernel<GG, HH><<<grid, dim3(256), 0, ctx->stream>>>(q, k, v, o, (uint32_t)n_q, pre, (uint32_t)n_q_heads, \
+                                                                   (uint32_t)n_kv_heads, sc)
+    if (hd == 128) {
+      if (GP == 1) MDMA_ATTP(1, 128);
+      else if (GP == 2) MDMA_ATTP(2, 128);
+      else if (GP == 4) MDMA_ATTP(4, 128);
+      else MDMA_ATTP(8, 128);
+    } else {
+      if (GP == 1) MDMA_ATTP(1, 64);
+      else if (GP == 2) MDMA_ATTP(2, 64);
+      else if (GP == 4) MDMA_ATTP(4, 64);
+      else MDMA_ATTP(8, 64);
+    }
+#undef MDMA_ATTP
+    hip_check(hipGetLastError(), "attn prefill launch");
+    return true;
+  }
   const AttnRope *rope = rope_in && rope_in->k ? rope_in : nullptr;
   if (pos_dev && !(seq_stride || n_q == 1)) return false;
   const float scale = 1.0f / sqrtf((float)hd);

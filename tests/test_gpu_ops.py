@@ -122,7 +122,12 @@ def test_kv_write_and_fused_rope_kv_write(backend):
                                                   (128, 32, 8, 1, 700), (128, 32, 8, 4, 2500), (64, 4, 1, 5, 5),
                                                   (128, 32, 8, 1, 64), (128, 32, 8, 1, 65), (128, 32, 8, 70, 70),
                                                   (128, 16, 2, 3, 300), (256, 8, 2, 2, 130), (96, 6, 3, 1, 200),
-                                                  (64, 12, 4, 2, 129), (128, 32, 8, 8, 2500)])
+                                                  (64, 12, 4, 2, 129), (128, 32, 8, 8, 2500),
+                                                  # prompts of 64 queries and more (the matrix-core kernel):
+                                                  # G = 4, 1, 8, 2, hd 128 and 64, with and without a prefix
+                                                  (128, 32, 8, 64, 64), (128, 32, 8, 512, 512),
+                                                  (128, 32, 8, 200, 300), (64, 8, 8, 128, 128),
+                                                  (128, 16, 2, 96, 100), (64, 8, 4, 65, 65)])
 def test_attention_over_f16_cache(backend, hd, nq, nkv, n_q, kv_len):
     q = synth.normal_f32(n_q * nq * hd, 1)
     k = f16r(synth.normal_f32(kv_len * nkv * hd, 2))
