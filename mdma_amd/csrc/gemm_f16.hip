@@ -46,6 +46,8 @@
 // per CU.
 #include <hip/hip_ext.h>
 
+#include <algorithm>
+
 #include <type_traits>
 
 #include "kernels.h"
@@ -145,7 +147,32 @@ struct F16Args {
   uint32_t M, N, K;
   uint64_t row_bytes;
   int32_t *dots;       // block-dot capture [M, N, K/32] (sc * block dot) or null
+  // Split K (gridDim.z splits of sb_split super-blocks each): f32 partial
+  // tiles [tile][split][TM * TN] and one zeroed arrival counter per tile.
+  float *part;
+  uint32_t *cnt;
+  uint32_t sb_split;
+  // Up to 3 weights sharing x in one launch (fused QKV): weight j takes the
+  // column tiles from jt[j]; w, y and N above are replaced by its own.
+  uint32_t n_jobs;
+  const uint8_t *jw[3];
+  float *jy[3];
+  uint32_t jn[3], jt[3];
 };
+
+// The workgroup's weight of a fused launch (static indices: the values
+// stay uniform, in SGPRs) and its first weight row.
+struct F16Job {
+  const uint8_t *w;
+  float *y;
+  uint32_t N, bn;
+};
+__device__ __forceinline__ F16Job f16_job(const F16Args &a) {
+  const uint32_t bx = blockIdx.x;
+  if (a.n_jobs > 2 && bx >= a.jt[2]) return F16Job{a.jw[2], a.jy[2], a.jn[2], (bx - a.jt[2]) * TN};
+  if (a.n_jobs > 1 && bx >= a.jt[1]) return F16Job{a.jw[1], a.jy[1], a.jn[1], (bx - a.jt[1]) * TN};
+  return F16Job{a.w, a.y, a.N, bx * TN};
+}
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
@@ -173,6 +200,50 @@ __device__ __forceinline__ void q4_f16(uint32_t q, h2 sa, h2 na, h2 sb, h2 nb_, 
   hi[1] = f(__builtin_amdgcn_perm(c, u, 0x04030402u), sb, nb_);
 }
 
+// Split K: every split stores its f32 partial tile; the split that arrives
+// last adds them in split order (the same sums whatever the arrival order)
+// into acc and goes on to store Y; the others return false. A tile's
+// partial is [value k of a thread][thread], so each store and load of a
+// wave covers 256 consecutive bytes. Partials move between workgroups
+// (possibly on different XCDs, whose L2s are not coherent with each other)
+// only through device-scope stores and loads; each wave waits for its
+// stores before the barrier that precedes the counter's device-scope add.
+__device__ bool f16_split_merge(float (&acc)[4][4][4], const F16Args &a) {
+  __shared__ uint32_t last;
+  const uint32_t tile = blockIdx.y * gridDim.x + blockIdx.x, S = gridDim.z, z = blockIdx.z, tid = threadIdx.x;
+  float *pt = a.part + (size_t)tile * S * (TM * TN) + tid;
+#pragma unroll
+  for (int k = 0; k < 64; k++)
+    __hip_atomic_store(pt + (size_t)z * (TM * TN) + 256 * k, acc[k >> 4][(k >> 2) & 3][k & 3], __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(a.cnt + tile * CNT_STRIDE, 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    last = prev == S - 1;
+    if (last) __hip_atomic_store(a.cnt + tile * CNT_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last) return false;
+  // Split by split, a split's 64 loads in flight together. The f32 sums in
+  // split order round as often as the unsplit kernel's chain over the same
+  // super-blocks does (one addition per super-block).
+  float sum[64];
+#pragma unroll
+  for (int k = 0; k < 64; k++) sum[k] = 0.f;
+  for (uint32_t y = 0; y < S; y++) {
+    const float *py = pt + (size_t)y * (TM * TN);
+#pragma unroll
+    for (int k = 0; k < 64; k++)
+      sum[k] += y == z ? acc[k >> 4][(k >> 2) & 3][k & 3]
+                       : __hip_atomic_load(py + 256 * k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+#pragma unroll
+  for (int k = 0; k < 64; k++) acc[k >> 4][(k >> 2) & 3][k & 3] = sum[k];
+  return true;
+}
+
 // CAP: the block-dot capture instantiation (F16Args::dots set).
 template <int DT, bool CAP = false>
 __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
@@ -187,7 +258,8 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
   __shared__ float invs[TM];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t bn = blockIdx.x * TN, bm = blockIdx.y * TM;
+  const F16Job J = f16_job(a);
+  const uint32_t bn = J.bn, bm = blockIdx.y * TM;
   const int wn = (wave & 1) * 64, wm = (wave >> 1) * 64;
   // 16 x 16 MFMA tiles: lane l holds column l % 16 (a token) and K chunk
   // l / 16 of its operands, and rows 4 (l / 16) .. + 3 of its result.
@@ -210,11 +282,11 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
   const uint32_t s_row = min(bm + s_tok, a.M - 1);
   const uint32_t so = 4 * (s_row * nb + s_blk), po = 2 * (s_row * nb + (s_blk ? a.p_lo : 0));
   const int w_row = tid >> 1, w_plane = tid & 1;
-  const uint32_t wrow = min(bn + w_row, a.N - 1) * rb;
+  const uint32_t wrow = min(bn + w_row, J.N - 1) * rb;
   const uint32_t wo = wrow + 16 * (w_plane ? U : 0);
   // Headers: lanes 0..31 of wave w load rows 32 w + lane (the rows of the
   // wave's own threads).
-  const uint32_t ho = min(bn + 32 * wave + (lane & 31), a.N - 1) * rb + 32 * U;
+  const uint32_t ho = min(bn + 32 * wave + (lane & 31), J.N - 1) * rb + 32 * U;
   if (tid < TM) invs[tid] = a.inv[min(bm + tid, a.M - 1)];
 
   // Stage st's operands into LDS: X into xs[st & 1], s_x into sxs[st & 1],
@@ -223,8 +295,8 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
 #pragma unroll
     for (int i = 0; i < 4; i++) lds_dma16(a.xh, xo[i] + 128 * st, &xs[st & 1][32 * wave + 8 * i][0]);
     lds_dma4(a.sx, so + 8 * st, &sxs[st & 1][0][64 * wave]);
-    lds_dma16(a.w, wo + 16 * st, &wraw[32 * wave][0]);
-    if (st % 4 == 0 && lane < 32) lds_dma16(a.w, ho + 4 * st, &whd[32 * wave][0]);
+    lds_dma16(J.w, wo + 16 * st, &wraw[32 * wave][0]);
+    if (st % 4 == 0 && lane < 32) lds_dma16(J.w, ho + 4 * st, &whd[32 * wave][0]);
   };
   // P of super-block sb into xmin (its previous contents, the last
   // super-block's, are read by that super-block's epilogue: issued after it).
@@ -278,19 +350,21 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
 #pragma unroll
       for (int r = 0; r < 4; r++) acc[i][j][r] = 0.f, part[i][j][r] = 0.f;
 
-  gload(0);
-  pload(0);
+  // This split's stages (whole super-blocks).
+  const uint32_t st0 = blockIdx.z * a.sb_split * 4, st1 = min(st0 + a.sb_split * 4, nst);
+  gload(st0);
+  pload(st0 / 4);
   lds_wait_dma();
-  wstore(0);
+  wstore(st0);
   hstore();
   lds_barrier();
-  for (uint32_t st = 0; st < nst; st++) {
+  for (uint32_t st = st0; st < st1; st++) {
     // Stage st + 1's loads in flight over this stage's MFMAs, into the other
     // buffers (last read by stage st - 1, before the barrier). A
     // super-block's P goes in at its second stage, after the previous
     // super-block's epilogue.
-    if (st + 1 < nst) gload(st + 1);
-    if (st % 4 == 0 && st > 0) pload(st / 4);
+    if (st + 1 < st1) gload(st + 1);
+    if (st % 4 == 0 && st > st0) pload(st / 4);
     const int buf = st & 1;
     // One block (h) of the stage: one 16x16x32 MFMA per tile, then
     // part += s_x * dot. FIRST (a super-block's first block): part = s_x * dot.
@@ -324,7 +398,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
 #pragma unroll
           for (int r = 0; r < 4; r++) {
             const uint32_t n = bn + wn + 16 * i + 4 * lq + r;
-            if (m < a.M && n < a.N) a.dots[((size_t)m * a.N + n) * nb + 2 * st + h] = (int)c[t % 3][r];
+            if (m < a.M && n < J.N) a.dots[((size_t)m * J.N + n) * nb + 2 * st + h] = (int)c[t % 3][r];
           }
         }
 #pragma unroll
@@ -360,14 +434,15 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
       }
     }
     lds_wait_dma();
-    if (st + 1 < nst) wstore(st + 1);
+    if (st + 1 < st1) wstore(st + 1);
     // A super-block's epilogue operands go to LDS once the previous
     // super-block's epilogue (stage st - 1) has passed the barrier.
-    if (st % 4 == 0 && st > 0) hstore();
+    if (st % 4 == 0 && st > st0) hstore();
     lds_barrier();
   }
+  if (gridDim.z > 1 && !f16_split_merge(acc, a)) return;
   // ---- store: lane = token; a tile's 4 outputs are 4 consecutive rows ----
-  const bool vec = (a.N & 3) == 0;
+  const bool vec = (J.N & 3) == 0;
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     const uint32_t m = bm + wm + 16 * j + l16;
@@ -375,13 +450,219 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const uint32_t n = bn + wn + 16 * i + 4 * lq;
-      float *yp = a.y + (size_t)m * a.N + n;
-      if (vec && n + 3 < a.N) {
+      float *yp = J.y + (size_t)m * J.N + n;
+      if (vec && n + 3 < J.N) {
         *reinterpret_cast<float4 *>(yp) = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
       } else {
 #pragma unroll
         for (int t = 0; t < 4; t++)
-          if (n + t < a.N) yp[t] = acc[i][j][t];
+          if (n + t < J.N) yp[t] = acc[i][j][t];
+      }
+    }
+  }
+}
+
+// Q6_K on the f16 path (same tiling and stages as gemm_f16_kernel). The
+// weight value w = sc * q (sc in [-128, 127], q in [-32, 31]) passes 2048,
+// past which f16 holds only even integers, so the operand is split exactly:
+// A1 = f16(w), the f16 product of the exact f16 operands q and sc, rounded
+// once, and A2 = w - A1 in {-1, 0, 1}, a fused multiply-add of the same
+// operands (exact). |A1| <= 4096 and |A2| <= 1, so a block's partial sums
+// stay below 32 * 127 * 4097 < 2^24 and the MFMA adds them exactly: the
+// f32 block dot is the integer sum_k q_x * sc * q. A stage whose A2 is zero
+// across the workgroup (no |sc| above 64 meets an odd product past 2048)
+// skips the A2 MFMAs. d multiplies each super-block's part as Q4_K's does;
+// Q6_K has no min term.
+// Stage st is columns [64 st, 64 st + 64) = quarters 2 qp and 2 qp + 1 (qp =
+// st % 2, blocks 0 and 1) of half n = st / 2 % 2 of super-block st / 4: the
+// prepared units 2 (st / 2) + h' (h' = 0, 1) hold columns [16 h', 16 h' + 16)
+// of every quarter (planes A, B: ql of quarters 0/2 and 1/3; Q: qh).
+// The converted operands are single-buffered (a second barrier per stage)
+// so that two workgroups fit a CU's LDS.
+__device__ __forceinline__ void q6_pair_f16(uint32_t v, h2 sc2, uint32_t &a1, uint32_t &a2, int k) {
+  const h2 off = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+  const h2 q = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, v, k ? 0x04030402u : 0x04010400u)) + off;
+  const h2 p = q * sc2;
+  a1 = __builtin_bit_cast(uint32_t, p);
+  a2 = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, sc2, -p));
+}
+
+__global__ __launch_bounds__(256, 2) void gemm_f16_q6_kernel(F16Args a) {
+  __shared__ __attribute__((aligned(16))) _Float16 ws[TN][SK];      // A1
+  __shared__ __attribute__((aligned(16))) _Float16 ws2[TN][SK];     // A2
+  __shared__ __attribute__((aligned(16))) _Float16 xs[2][TM][SK];   // activations, f16 int8 values
+  __shared__ __attribute__((aligned(16))) uint8_t wraw[3][256][16];  // planes A, B, Q of thread (row, h')
+  __shared__ __attribute__((aligned(16))) uint32_t wsc[256];        // the unit's 4 scales
+  __shared__ __attribute__((aligned(16))) uint32_t dvr[TN];         // the dword holding d, then d (f32)
+  __shared__ __attribute__((aligned(16))) float sxs[2][2][TM];
+  __shared__ uint32_t need2[2];  // per stage parity: some A2 of the stage is not zero
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const F16Job J = f16_job(a);
+  const uint32_t bn = J.bn, bm = blockIdx.y * TM;
+  const int wn = (wave & 1) * 64, wm = (wave >> 1) * 64;
+  const int l16 = lane & 15, lq = lane >> 4;
+  const uint32_t K = a.K, nb = K / 32, nst = K / SK, U = K / 64, rb = (uint32_t)a.row_bytes;
+
+  uint32_t xo[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int row = 32 * wave + 8 * i + (lane >> 3);
+    xo[i] = 2 * (min(bm + row, a.M - 1) * K + 8 * swz(row, lane & 7));
+  }
+  const int s_tok = tid & 127, s_blk = tid >> 7;
+  const uint32_t so = 4 * (min(bm + s_tok, a.M - 1) * nb + s_blk);
+  // Quant planes: thread = (row tid / 2, unit h' = tid % 2).
+  const int w_row = tid >> 1, w_h = tid & 1;
+  const uint32_t wrow = min(bn + w_row, J.N - 1) * rb;
+  // d: lanes 0..31 of wave w take rows 32 w + lane.
+  const uint32_t drow = min(bn + 32 * wave + (lane & 31), J.N - 1) * rb + 52 * U;
+
+  auto gload = [&](uint32_t st) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) lds_dma16(a.xh, xo[i] + 128 * st, &xs[st & 1][32 * wave + 8 * i][0]);
+    lds_dma4(a.sx, so + 8 * st, &sxs[st & 1][0][64 * wave]);
+    if (st % 2 == 0) {  // the half super-block's planes serve both its stages
+      const uint32_t u = 2 * (st / 2) + w_h;
+#pragma unroll
+      for (int p = 0; p < 3; p++) lds_dma16(J.w, wrow + 16 * (p * U + u), &wraw[p][64 * wave][0]);
+      lds_dma4(J.w, wrow + 48 * U + 4 * u, &wsc[64 * wave]);
+    }
+    // A super-block's d goes in with its second stage (the previous
+    // super-block's epilogue, at its last stage, has read dvr by then).
+    if (st % 4 == 1 && lane < 32) lds_dma4(J.w, (drow + 2 * (st / 4)) & ~3u, &dvr[32 * wave]);
+  };
+  // Stage st's operands: this thread's 16 columns of each of the two blocks.
+  auto wstore = [&](uint32_t st) {
+    const uint4 A = *reinterpret_cast<const uint4 *>(&wraw[0][tid][0]);
+    const uint4 B = *reinterpret_cast<const uint4 *>(&wraw[1][tid][0]);
+    const uint4 Q = *reinterpret_cast<const uint4 *>(&wraw[2][tid][0]);
+    const uint32_t sc4 = wsc[tid];
+    const int qp = st & 1;
+    const uint32_t av[4] = {A.x, A.y, A.z, A.w}, bv[4] = {B.x, B.y, B.z, B.w}, hv[4] = {Q.x, Q.y, Q.z, Q.w};
+    uint32_t any = 0;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int qq = 2 * qp + h;
+      const _Float16 fs = (_Float16)(float)(int8_t)(sc4 >> (8 * qq));
+      const h2 sc2 = {fs, fs};
+      const int c0 = 4 * h + 2 * w_h;
+#pragma unroll
+      for (int d = 0; d < 4; d++) {  // columns 4d..4d+3 of the thread's 16: half of chunk c0 + d / 2
+        const uint32_t nd = h ? bv[d] : av[d];
+        const uint32_t nib = qp ? (nd >> 4) & 0x0F0F0F0Fu : nd & 0x0F0F0F0Fu;
+        const uint32_t v = nib | (((hv[d] >> (2 * qq)) & 0x03030303u) << 4);
+        uint32_t a1[2], a2[2];
+        q6_pair_f16(v, sc2, a1[0], a2[0], 0);
+        q6_pair_f16(v, sc2, a1[1], a2[1], 1);
+        any |= (a2[0] | a2[1]) & 0x7FFF7FFFu;
+        const int col = 8 * swz(w_row, c0 + (d >> 1)) + 4 * (d & 1);
+        *reinterpret_cast<uint2 *>(&ws[w_row][col]) = make_uint2(a1[0], a1[1]);
+        *reinterpret_cast<uint2 *>(&ws2[w_row][col]) = make_uint2(a2[0], a2[1]);
+      }
+    }
+    if (__builtin_amdgcn_ballot_w64(any != 0) != 0 && lane == 0) atomicOr(&need2[st & 1], 1u);
+  };
+  // Super-block sb's d (the half of the aligned dword holding it) as f32,
+  // in place, rows 0..127.
+  auto hstore = [&](uint32_t sb) {
+    if (tid < TN) {
+      const uint32_t w = dvr[tid];
+      dvr[tid] = __builtin_bit_cast(uint32_t, h2f(sb & 1 ? w >> 16 : w));
+    }
+  };
+
+  float acc[4][4][4], part[4][4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) acc[i][j][r] = 0.f, part[i][j][r] = 0.f;
+
+  if (tid < 2) need2[tid] = 0u;
+  lds_barrier();
+  const uint32_t st0 = blockIdx.z * a.sb_split * 4, st1 = min(st0 + a.sb_split * 4, nst);
+  gload(st0);
+  lds_wait_dma();
+  lds_barrier();
+  wstore(st0);
+  lds_barrier();
+  for (uint32_t st = st0; st < st1; st++) {
+    if (st + 1 < st1) gload(st + 1);
+    const int buf = st & 1;
+    const bool n2 = need2[buf] != 0u;
+    auto block = [&](int h, auto first) {
+      v8h A[4], A2[4], B[4];
+      float s[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int r = wn + 16 * i + l16;
+        A[i] = *reinterpret_cast<const v8h *>(&ws[r][8 * swz(r, 4 * h + lq)]);
+        if (n2) A2[i] = *reinterpret_cast<const v8h *>(&ws2[r][8 * swz(r, 4 * h + lq)]);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int r = wm + 16 * j + l16;
+        B[j] = *reinterpret_cast<const v8h *>(&xs[buf][r][8 * swz(r, 4 * h + lq)]);
+        s[j] = sxs[buf][h][r];
+      }
+      auto dot = [&](int t) {
+        v4f c = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[t >> 2], B[t & 3], v4f{}, 0, 0, 0);
+        if (n2) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(A2[t >> 2], B[t & 3], c, 0, 0, 0);
+        return c;
+      };
+      v4f c[3];
+      c[0] = dot(0);
+      c[1] = dot(1);
+#pragma unroll
+      for (int t = 0; t < 16; t++) {
+        if (t + 2 < 16) c[(t + 2) % 3] = dot(t + 2);
+        const int i = t >> 2, j = t & 3;
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          part[i][j][r] = first ? s[j] * c[t % 3][r] : fmaf(s[j], c[t % 3][r], part[i][j][r]);
+      }
+    };
+    if (st % 4 == 0) block(0, std::true_type{});
+    else block(0, std::false_type{});
+    block(1, std::false_type{});
+    if (st % 4 == 3) {  // the super-block's last stage: acc += d * part
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float4 d4 = *reinterpret_cast<const float4 *>(&dvr[wn + 16 * i + 4 * lq]);
+        const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) acc[i][j][r] = fmaf(dv[r], part[i][j][r], acc[i][j][r]);
+      }
+    }
+    lds_wait_dma();
+    lds_barrier();  // every wave is done with the stage's operands and flag
+    if (tid == 0) need2[buf] = 0u;  // next written by the stage after next
+    if (st + 1 < st1) {
+      wstore(st + 1);
+      if ((st + 1) % 4 == 1) hstore((st + 1) / 4);
+    }
+    lds_barrier();
+  }
+  if (gridDim.z > 1 && !f16_split_merge(acc, a)) return;
+  const bool vec = (J.N & 3) == 0;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint32_t m = bm + wm + 16 * j + l16;
+    if (m >= a.M) continue;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t n = bn + wn + 16 * i + 4 * lq;
+      float *yp = J.y + (size_t)m * J.N + n;
+      if (vec && n + 3 < J.N) {
+        *reinterpret_cast<float4 *>(yp) = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+          if (n + t < J.N) yp[t] = acc[i][j][t];
       }
     }
   }
@@ -390,7 +671,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
 }  // namespace
 
 bool gemm_f16_supported(int32_t dtype, int layout, uint64_t n_in, uint64_t n_out) {
-  if (layout != MDMA_LAYOUT_GFX950 || dtype != DT_Q4_K) return false;
+  if (layout != MDMA_LAYOUT_GFX950 || (dtype != DT_Q4_K && dtype != DT_Q6_K)) return false;
   if (n_in % 256 || n_in > 32 * (uint64_t)MAX_BLOCKS) return false;
   // Weight offsets are 32-bit inside the kernel.
   return n_out * gfx950_row_bytes(dtype, n_in) < (1ull << 32);
@@ -404,7 +685,56 @@ uint64_t gemm_f16_input_bytes(uint64_t M, uint64_t K) {
   return r256(M * K * 2) + r256(M * (K / 32) * 4) + 2 * r256(M * (K / 32) * 2) + r256(M * 4);
 }
 
-void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t M, char *s) {
+namespace {
+// Splits of K for a launch of few output tiles (few weight rows): enough
+// workgroups for two per CU, whole super-blocks, at least two per split.
+struct F16Split {
+  uint32_t S, sbs;
+};
+F16Split f16_plan(const mdma_ctx *ctx, uint64_t tiles, uint64_t K) {
+  const uint64_t cus = ctx->cu_count ? ctx->cu_count : 256, nsb = K / 256;
+  if (tiles >= cus || nsb < 4) return F16Split{1, (uint32_t)nsb};
+  const uint64_t S = std::min<uint64_t>(std::min<uint64_t>((2 * cus + tiles - 1) / tiles, nsb / 2), 16);
+  const uint64_t sbs = (nsb + S - 1) / S;
+  return F16Split{(uint32_t)((nsb + sbs - 1) / sbs), (uint32_t)sbs};
+}
+uint64_t rows_per_launch(uint64_t K) { return ((1ull << 31) / K) / TM * TM; }
+}  // namespace
+
+namespace {
+// One launch's weights: the jobs fused into it (same type and shape of x, no
+// block-dot capture), or the one job.
+bool f16_fusable(const GemvJob *jobs, int n_jobs) {
+  if (n_jobs < 2 || n_jobs > 3) return false;
+  for (int i = 0; i < n_jobs; i++)
+    if (jobs[i].dtype != jobs[0].dtype || jobs[i].n_in != jobs[0].n_in || jobs[i].dots) return false;
+  return true;
+}
+uint64_t col_tiles(const GemvJob *jobs, int n) {
+  uint64_t t = 0;
+  for (int i = 0; i < n; i++) t += (jobs[i].n_out + TN - 1) / TN;
+  return t;
+}
+}  // namespace
+
+uint64_t gemm_f16_split_bytes(const mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, uint64_t M, uint64_t *tiles) {
+  const uint64_t K = jobs[0].n_in, Mc = std::min(M, rows_per_launch(K)), mt = (Mc + TM - 1) / TM;
+  const int groups = f16_fusable(jobs, n_jobs) ? 1 : n_jobs;
+  uint64_t bytes = 0;
+  *tiles = 0;
+  for (int g = 0; g < groups; g++) {
+    const uint64_t t = (groups == 1 ? col_tiles(jobs, n_jobs) : col_tiles(jobs + g, 1)) * mt;
+    const F16Split sp = f16_plan(ctx, t, K);
+    if (sp.S > 1) {
+      bytes = std::max(bytes, t * sp.S * (uint64_t)(TM * TN) * 4);
+      *tiles = std::max(*tiles, t);
+    }
+  }
+  return bytes;
+}
+
+void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t M, char *s,
+                     float *part, uint64_t part_bytes, uint32_t *cnt, uint64_t counters) {
   const uint64_t K = jobs[0].n_in, nb = K / 32;
   _Float16 *xh = reinterpret_cast<_Float16 *>(s);
   s += r256(M * K * 2);
@@ -418,20 +748,43 @@ void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float
   gemm_act_kernel<<<dim3((uint32_t)M), dim3(256), 0, ctx->stream>>>(x, (uint32_t)K, xh, sx, ph, pl, inv);
   hip_check(hipGetLastError(), "gemm activation launch");
   // Token rows per launch: activation offsets are 32-bit inside the kernel.
-  const uint64_t rows = ((1ull << 31) / K) / TM * TM;
+  const uint64_t rows = rows_per_launch(K);
   hipEvent_t t0 = ctx->time_start, t1 = ctx->time_stop;
   ctx->time_start = ctx->time_stop = nullptr;
-  for (int i = 0; i < n_jobs; i++) {
-    const GemvJob &w = jobs[i];
+  const bool fused = f16_fusable(jobs, n_jobs);
+  const int groups = fused ? 1 : n_jobs;
+  for (int g = 0; g < groups; g++) {
+    const GemvJob *gj = fused ? jobs : jobs + g;
+    const int nj = fused ? n_jobs : 1;
+    const GemvJob &w = gj[0];
     for (uint64_t m0 = 0; m0 < M; m0 += rows) {
       const uint64_t Mc = M - m0 < rows ? M - m0 : rows;
+      // Split K when the launch has few tiles and the partials fit (not for
+      // the block-dot capture, whose dots are stored by the one split).
+      const uint64_t ct = col_tiles(gj, nj), tiles = ct * ((Mc + TM - 1) / TM);
+      F16Split sp = f16_plan(ctx, tiles, K);
+      if (sp.S > 1 && (w.dots || !part || !cnt || tiles > counters ||
+                       tiles * sp.S * (uint64_t)(TM * TN) * 4 > part_bytes))
+        sp = F16Split{1, (uint32_t)(K / 256)};
       F16Args a{xh + m0 * K, sx + m0 * nb, ph + m0 * nb, (uint32_t)(pl - ph), inv + m0, w.w, w.y + m0 * w.n_out,
                 (uint32_t)Mc, (uint32_t)w.n_out, (uint32_t)K, gfx950_row_bytes(w.dtype, K),
-                w.dots ? w.dots + m0 * w.n_out * (K / 32) : nullptr};
-      const dim3 grid((uint32_t)((w.n_out + TN - 1) / TN), (uint32_t)((Mc + TM - 1) / TM)), block(256);
+                w.dots ? w.dots + m0 * w.n_out * (K / 32) : nullptr, sp.S > 1 ? part : nullptr,
+                sp.S > 1 ? cnt : nullptr, sp.sbs, (uint32_t)nj, {}, {}, {}, {}};
+      uint32_t first = 0;
+      for (int j = 0; j < nj; j++) {
+        a.jw[j] = gj[j].w;
+        a.jy[j] = gj[j].y + m0 * gj[j].n_out;
+        a.jn[j] = (uint32_t)gj[j].n_out;
+        a.jt[j] = first;
+        first += (uint32_t)((gj[j].n_out + TN - 1) / TN);
+      }
+      const dim3 grid((uint32_t)ct, (uint32_t)((Mc + TM - 1) / TM), sp.S), block(256);
       // Timing events bracket the calls' GEMM launches (not the prologue).
-      const hipEvent_t e0 = i == 0 && m0 == 0 ? t0 : nullptr, e1 = i == n_jobs - 1 && m0 + Mc >= M ? t1 : nullptr;
-      if (a.dots) gemm_f16_kernel<DT_Q4_K, true><<<grid, block, 0, ctx->stream>>>(a);
+      const hipEvent_t e0 = g == 0 && m0 == 0 ? t0 : nullptr, e1 = g == groups - 1 && m0 + Mc >= M ? t1 : nullptr;
+      if (w.dtype == DT_Q6_K) {
+        if (e0 || e1) hipExtLaunchKernelGGL(gemm_f16_q6_kernel, grid, block, 0, ctx->stream, e0, e1, 0, a);
+        else gemm_f16_q6_kernel<<<grid, block, 0, ctx->stream>>>(a);
+      } else if (a.dots) gemm_f16_kernel<DT_Q4_K, true><<<grid, block, 0, ctx->stream>>>(a);
       else if (e0 || e1) hipExtLaunchKernelGGL(gemm_f16_kernel<DT_Q4_K>, grid, block, 0, ctx->stream, e0, e1, 0, a);
       else gemm_f16_kernel<DT_Q4_K><<<grid, block, 0, ctx->stream>>>(a);
       hip_check(hipGetLastError(), "gemm f16 launch");

@@ -22,6 +22,8 @@
 //  - Fused QKV: up to three jobs (same dtype) in one launch; waves are dealt
 //    out to jobs in order. Gated: the wave computes R rows of gate AND up,
 //    then writes silu(g) * u.
+#include <algorithm>
+
 #include "kernels.h"
 
 namespace mdma {
@@ -887,28 +889,34 @@ void launch_gemv_f32_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up
   });
 }
 
-// Prefill-sized int8 calls (T >= GEMM_MIN_TOKENS) on prepared Q8_0 / Q4_K
-// weights run the MFMA GEMM with activations quantized per 32 (quantized
-// once for every job sharing x). Returns false when a job is not covered.
-// Q4_K jobs take the f16-path GEMM unless the context asks for the int8
-// one, or its inputs do not fit where they must go (a capture's fixed-size
-// scratch, an allocation-free call's buffer).
+// Prefill-sized int8 calls (T >= GEMM_MIN_TOKENS) on prepared Q8_0 / Q4_K /
+// Q6_K weights run an MFMA GEMM with activations quantized per 32
+// (quantized once for every job sharing x). Returns false when a job is not
+// covered. Q4_K and Q6_K jobs take the f16-path GEMM unless the context asks
+// for the int8 one, or its inputs do not fit where they must go (a
+// capture's fixed-size scratch, an allocation-free call's buffer).
 static bool try_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t T) {
   if (ctx->prefill_kernel != MDMA_PREFILL_AUTO) return false;
   for (int i = 0; i < n_jobs; i++)
     if (!gemm_f16_supported(jobs[i].dtype, jobs[i].layout, jobs[i].n_in, jobs[i].n_out) ||
-        jobs[i].n_in != jobs[0].n_in)
-      return false;
-  const uint64_t need = gemm_f16_input_bytes(T, jobs[0].n_in);
+        jobs[i].n_in != jobs[0].n_in || (jobs[i].dtype == DT_Q6_K && jobs[i].dots))
+      return false;  // (Q6_K block-dot capture: the int8 GEMM's per-16 dots)
+  const uint64_t need = (gemm_f16_input_bytes(T, jobs[0].n_in) + 255) / 256 * 256;
+  // Split-K partials (launches run one after another and share them).
+  uint64_t nc = 0, pb = gemm_f16_split_bytes(ctx, jobs, n_jobs, T, &nc);
   char *s;
-  if (ctx->fixed_scratch) {
+  if (ctx->fixed_scratch) {  // an allocation-free call: unsplit, inputs in its fixed buffer
     if (need > ctx->fixed_cap) return false;
     s = ctx->fixed_scratch;
+    pb = 0;
   } else {
     if (ctx->capturing && need > ctx->scratch_cap) return false;
-    s = scratch(ctx, need);
+    if (ctx->capturing && need + pb > ctx->scratch_cap) pb = 0;  // under capture the scratch cannot grow
+    s = scratch(ctx, need + pb);
   }
-  launch_gemm_f16(ctx, jobs, n_jobs, x, T, s);
+  uint32_t *cnt = pb && nc ? gemm_counters(ctx, nc) : nullptr;
+  launch_gemm_f16(ctx, jobs, n_jobs, x, T, s, cnt ? reinterpret_cast<float *>(s + need) : nullptr, cnt ? pb : 0, cnt,
+                  cnt ? nc : 0);
   return true;
 }
 

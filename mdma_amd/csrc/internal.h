@@ -329,7 +329,11 @@ constexpr uint64_t GEMM_MIN_TOKENS = 64;
 // launch (quantization prologue, then each job's GEMM) with that scratch.
 bool gemm_f16_supported(int32_t dtype, int layout, uint64_t n_in, uint64_t n_out);
 uint64_t gemm_f16_input_bytes(uint64_t M, uint64_t K);
-void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t M, char *scratch);
+// Split-K partials the f16-path launches of these jobs over M tokens take
+// (bytes; 0 = unsplit) and the arrival counters they need (*tiles).
+uint64_t gemm_f16_split_bytes(const mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, uint64_t M, uint64_t *tiles);
+void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t M, char *scratch,
+                     float *part, uint64_t part_bytes, uint32_t *cnt, uint64_t counters);
 void launch_quantize_act(mdma_ctx *ctx, const float *x, uint64_t n, uint64_t group, int8_t *q,
                          float *d, int32_t *sum16);
 void launch_block_dot(mdma_ctx *ctx, const GemvJob &w, const int8_t *qx, uint64_t T, int32_t *out);

@@ -751,7 +751,7 @@ def test_packed_upload_rejects_wrong_sizes(backend):
 # ------------------------------------------------------- prefill GEMM ----
 # int8 mode with T >= 64 tokens on prepared Q8_0 / Q4_K / Q6_K weights runs a
 # prefill GEMM on activations quantized per 32 with an f32 scale: the
-# f16-path GEMM for Q4_K (default), the int8 MFMA GEMM otherwise or when
+# f16-path GEMM for Q4_K and Q6_K (default), the int8 MFMA GEMM otherwise or when
 # asked. Oracle: the reference's "requantize, then CPU qmatmul"
 # (src/backend/rocm/decode/tests.rs:68-130).
 
@@ -763,10 +763,10 @@ def oracle_i8_32(dtype, raw, rows, k, x):
     return cpu, exact, abs_dot(npq.dequantize(dtype, raw, rows, k), xq)
 
 
-# (dtype, prefill kernel): both kernels for Q4_K, the int8 one elsewhere.
+# (dtype, prefill kernel): both kernels for Q4_K and Q6_K, the int8 one for Q8_0.
 GEMM_CASES = [(Q8, backend_mod.PREFILL_I8), (Q4K, backend_mod.PREFILL_AUTO), (Q4K, backend_mod.PREFILL_I8),
-              (Q6K, backend_mod.PREFILL_I8)]
-GEMM_IDS = ["q8-i8", "q4k-f16", "q4k-i8", "q6k-i8"]
+              (Q6K, backend_mod.PREFILL_AUTO), (Q6K, backend_mod.PREFILL_I8)]
+GEMM_IDS = ["q8-i8", "q4k-f16", "q4k-i8", "q6k-f16", "q6k-i8"]
 
 
 @pytest.fixture
@@ -858,10 +858,20 @@ def q6k_full_scale_range(raw, rows, k, seed):
     return b.reshape(-1)
 
 
-def test_prefill_gemm_q6k_full_scale_range(backend):
+@pytest.mark.parametrize("kind", [backend_mod.PREFILL_AUTO, backend_mod.PREFILL_I8], ids=["f16", "i8"])
+def test_prefill_gemm_q6k_full_scale_range(backend, kind):
     """Q6_K sub-block scales over all of [-128, 127] (the benchmark
     distribution keeps them in [-64, 63]; weight values sc * q then reach
-    4096), at a config-4 shape and a small one."""
+    4096, past f16's consecutive integers: the f16 path carries them as the
+    exact split A1 + A2), at a config-4 shape and a small one."""
+    backend.set_prefill_kernel(kind)
+    try:
+        q6k_full_scale_cases(backend, kind)
+    finally:
+        backend.set_prefill_kernel(backend_mod.PREFILL_AUTO)
+
+
+def q6k_full_scale_cases(backend, kind):
     for T, k, rows in ((64, 512, 96), (512, 4096, 14336)):
         raw = q6k_full_scale_range(synth.weight(Q6K, rows, k, 600 + T), rows, k, 601)
         x = synth.normal_f32(T * k, 602 + T)
@@ -875,7 +885,7 @@ def test_prefill_gemm_q6k_full_scale_range(backend):
             tok = np.unique(np.r_[0:8, min(130, T - 3):min(133, T), T - 8:T])
             cpu, exact, absum = oracle_i8_32(Q6K, sl, 16, k, x.reshape(T, k)[tok].reshape(-1))
             assert_parity(y[tok, r0:r0 + 16].reshape(-1), cpu, exact, 1e-3, abs_sum=absum,
-                          what=f"gemm q6k full scales T={T} rows {r0}..")
+                          what=f"gemm q6k full scales kind={kind} T={T} rows {r0}..")
         w.buf.close(), xb.close(), yb.close()
 
 
