@@ -308,9 +308,9 @@ GEMM_SHAPES = [(512, 4096, 14336), (2048, 14336, 4096)]  # (M tokens, K, N)
 
 
 def prefill_gemms(be, ev, reps):
-    """Prefill GEMMs at the two prefill shapes: Q4_K weights on the f16-path
-    GEMM (the default for Q4_K) and on the int8 MFMA GEMM, Q8_0 and Q6_K (the
-    Q4_K_M mix's attention and down type) on the int8 MFMA GEMM.
+    """Prefill GEMMs at the two prefill shapes: Q4_K and Q6_K (the Q4_K_M
+    mix's attention and down type) weights on the f16-path GEMM (their
+    default) and on the int8 MFMA GEMM, Q8_0 on the int8 MFMA GEMM.
     Kernel-only GEMM duration (dispatch timestamps) and the whole qmatmul
     call (per-32 activation quantization + GEMM) timed by events on the
     stream. TOPS = 2*M*N*K / time, against the int8 and the f16 dense peaks."""
@@ -323,7 +323,7 @@ def prefill_gemms(be, ev, reps):
         x = be.f32_buf(synth.normal_f32(M * K, SEED + 20))
         y = be.alloc(M * N * 4)
         for dt, name, kind in ((12, "q4k_f16path", PREFILL_AUTO), (12, "q4k_i8", PREFILL_I8), (8, "q8_0", PREFILL_I8),
-                               (14, "q6k", PREFILL_I8)):
+                               (14, "q6k_f16path", PREFILL_AUTO), (14, "q6k_i8", PREFILL_I8)):
             be.set_prefill_kernel(kind)
             raw = synth.weight(dt, N, K, SEED + 21)
             w = be.upload_weight(raw, dt, (N, K))
