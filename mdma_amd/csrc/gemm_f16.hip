@@ -42,7 +42,7 @@
 // is one weight row. K advances 64 columns (one Q4_K sub-block pair) per
 // stage through two LDS buffers: while a stage computes from one, the next
 // is converted into the other and the one after is in flight from global
-// memory, with one barrier per stage. About 76 KB of LDS: two workgroups
+// memory, with one barrier per stage. About 80 KB of LDS: two workgroups
 // per CU.
 #include <hip/hip_ext.h>
 
