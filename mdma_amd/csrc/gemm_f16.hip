@@ -158,6 +158,9 @@ struct F16Args {
   const uint8_t *jw[3];
   float *jy[3];
   uint32_t jn[3], jt[3];
+  // Gated launch (gemm_f16_kernel's GLU instantiation): jw[0] gate, jw[1]
+  // up, both N rows; glu_y [M, N] receives silu(gate) * up.
+  float *glu_y;
 };
 
 // The workgroup's weight of a fused launch (static indices: the values
@@ -245,7 +248,13 @@ __device__ bool f16_split_merge(float (&acc)[4][4][4], const F16Args &a) {
 }
 
 // CAP: the block-dot capture instantiation (F16Args::dots set).
-template <int DT, bool CAP = false>
+// GLU: the gated instantiation. A workgroup takes 64 rows of gate and the
+// same 64 rows of up (tile rows 32 w .. 32 w + 31 of wave w: gate for even
+// w, up for odd, rows bn + 32 (w / 2) + ..), so each lane holds a gate
+// output and its up output in acc[i] and acc[i + 2], and the epilogue
+// writes silu(gate) * up: the same per-output arithmetic as two separate
+// tiles, the same bits as the elementwise silu_mul of their outputs.
+template <int DT, bool CAP = false, bool GLU = false>
 __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
   __shared__ __attribute__((aligned(16))) _Float16 ws[2][TN][SK];  // weights, f16 q * sc
   __shared__ __attribute__((aligned(16))) _Float16 xs[2][TM][SK];  // activations, f16 int8 values
@@ -259,12 +268,22 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const F16Job J = f16_job(a);
-  const uint32_t bn = J.bn, bm = blockIdx.y * TM;
+  const uint32_t bn = GLU ? blockIdx.x * (TN / 2) : J.bn, bm = blockIdx.y * TM, N = GLU ? a.N : J.N;
   const int wn = (wave & 1) * 64, wm = (wave >> 1) * 64;
   // 16 x 16 MFMA tiles: lane l holds column l % 16 (a token) and K chunk
   // l / 16 of its operands, and rows 4 (l / 16) .. + 3 of its result.
   const int l16 = lane & 15, lq = lane >> 4;
   const uint32_t K = a.K, nb = K / 32, nst = K / SK, U = K / 64, rb = (uint32_t)a.row_bytes;
+  // Weight row of tile row r, and the weight this wave's loads read (its
+  // tile rows are 32 wave .. 32 wave + 31).
+  auto trow = [&](uint32_t r) { return GLU ? bn + 32 * (r >> 6) + (r & 31) : bn + r; };
+  const uint8_t *wsrc = J.w;
+  if constexpr (GLU) {
+    // The wave index made uniform first, so the choice is a scalar select
+    // of two kernel arguments (no per-lane pointer to rebuild).
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    wsrc = (wv & 1) ? a.jw[1] : a.jw[0];
+  }
 
   // Byte offsets of each lane's DMA sources (32-bit: the launcher keeps the
   // activations below 2^31 elements and the weights below 2^32 bytes).
@@ -282,11 +301,11 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
   const uint32_t s_row = min(bm + s_tok, a.M - 1);
   const uint32_t so = 4 * (s_row * nb + s_blk), po = 2 * (s_row * nb + (s_blk ? a.p_lo : 0));
   const int w_row = tid >> 1, w_plane = tid & 1;
-  const uint32_t wrow = min(bn + w_row, J.N - 1) * rb;
+  const uint32_t wrow = min(trow(w_row), N - 1) * rb;
   const uint32_t wo = wrow + 16 * (w_plane ? U : 0);
   // Headers: lanes 0..31 of wave w load rows 32 w + lane (the rows of the
   // wave's own threads).
-  const uint32_t ho = min(bn + 32 * wave + (lane & 31), J.N - 1) * rb + 32 * U;
+  const uint32_t ho = min(trow(32 * wave + (lane & 31)), N - 1) * rb + 32 * U;
   if (tid < TM) invs[tid] = a.inv[min(bm + tid, a.M - 1)];
 
   // Stage st's operands into LDS: X into xs[st & 1], s_x into sxs[st & 1],
@@ -295,8 +314,8 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
 #pragma unroll
     for (int i = 0; i < 4; i++) lds_dma16(a.xh, xo[i] + 128 * st, &xs[st & 1][32 * wave + 8 * i][0]);
     lds_dma4(a.sx, so + 8 * st, &sxs[st & 1][0][64 * wave]);
-    lds_dma16(J.w, wo + 16 * st, &wraw[32 * wave][0]);
-    if (st % 4 == 0 && lane < 32) lds_dma16(J.w, ho + 4 * st, &whd[32 * wave][0]);
+    lds_dma16(wsrc, wo + 16 * st, &wraw[32 * wave][0]);
+    if (st % 4 == 0 && lane < 32) lds_dma16(wsrc, ho + 4 * st, &whd[32 * wave][0]);
   };
   // P of super-block sb into xmin (its previous contents, the last
   // super-block's, are read by that super-block's epilogue: issued after it).
@@ -441,6 +460,22 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
     lds_barrier();
   }
   if (gridDim.z > 1 && !f16_split_merge(acc, a)) return;
+  if constexpr (GLU) {  // silu(gate) * up; the launcher keeps N a multiple of 128
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t m = bm + wm + 16 * j + l16;
+      if (m >= a.M) continue;
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        const uint32_t n = bn + (wn >> 1) + 16 * i + 4 * lq;
+        float h[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) h[r] = silu_mul1(acc[i][j][r], acc[i + 2][j][r]);
+        *reinterpret_cast<float4 *>(a.glu_y + (size_t)m * N + n) = make_float4(h[0], h[1], h[2], h[3]);
+      }
+    }
+    return;
+  }
   // ---- store: lane = token; a tile's 4 outputs are 4 consecutive rows ----
   const bool vec = (J.N & 3) == 0;
 #pragma unroll
@@ -733,8 +768,14 @@ uint64_t gemm_f16_split_bytes(const mdma_ctx *ctx, const GemvJob *jobs, int n_jo
   return bytes;
 }
 
+bool gemm_f16_glu_ok(const GemvJob &gate, const GemvJob &up) {
+  const GemvJob gu[2] = {gate, up};
+  return gate.dtype == DT_Q4_K && up.dtype == DT_Q4_K && gate.n_out == up.n_out && gate.n_out % TN == 0 &&
+         f16_fusable(gu, 2);
+}
+
 void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t M, char *s,
-                     float *part, uint64_t part_bytes, uint32_t *cnt, uint64_t counters) {
+                     float *part, uint64_t part_bytes, uint32_t *cnt, uint64_t counters, float *glu_y) {
   const uint64_t K = jobs[0].n_in, nb = K / 32;
   _Float16 *xh = reinterpret_cast<_Float16 *>(s);
   s += r256(M * K * 2);
@@ -753,6 +794,8 @@ void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float
   ctx->time_start = ctx->time_stop = nullptr;
   const bool fused = f16_fusable(jobs, n_jobs);
   const int groups = fused ? 1 : n_jobs;
+  const bool glu = glu_y != nullptr;
+  if (glu && (n_jobs != 2 || !gemm_f16_glu_ok(jobs[0], jobs[1]))) fail(MDMA_ERR_BACKEND, "gated GEMM: jobs not fusable");
   for (int g = 0; g < groups; g++) {
     const GemvJob *gj = fused ? jobs : jobs + g;
     const int nj = fused ? n_jobs : 1;
@@ -769,7 +812,7 @@ void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float
       F16Args a{xh + m0 * K, sx + m0 * nb, ph + m0 * nb, (uint32_t)(pl - ph), inv + m0, w.w, w.y + m0 * w.n_out,
                 (uint32_t)Mc, (uint32_t)w.n_out, (uint32_t)K, gfx950_row_bytes(w.dtype, K),
                 w.dots ? w.dots + m0 * w.n_out * (K / 32) : nullptr, sp.S > 1 ? part : nullptr,
-                sp.S > 1 ? cnt : nullptr, sp.sbs, (uint32_t)nj, {}, {}, {}, {}};
+                sp.S > 1 ? cnt : nullptr, sp.sbs, (uint32_t)nj, {}, {}, {}, {}, glu ? glu_y + m0 * w.n_out : nullptr};
       uint32_t first = 0;
       for (int j = 0; j < nj; j++) {
         a.jw[j] = gj[j].w;
@@ -778,12 +821,17 @@ void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float
         a.jt[j] = first;
         first += (uint32_t)((gj[j].n_out + TN - 1) / TN);
       }
+      // (A gated launch has the same number of column tiles: 64 rows of
+      // both weights each, N a multiple of 128.)
       const dim3 grid((uint32_t)ct, (uint32_t)((Mc + TM - 1) / TM), sp.S), block(256);
       // Timing events bracket the calls' GEMM launches (not the prologue).
       const hipEvent_t e0 = g == 0 && m0 == 0 ? t0 : nullptr, e1 = g == groups - 1 && m0 + Mc >= M ? t1 : nullptr;
       if (w.dtype == DT_Q6_K) {
         if (e0 || e1) hipExtLaunchKernelGGL(gemm_f16_q6_kernel, grid, block, 0, ctx->stream, e0, e1, 0, a);
         else gemm_f16_q6_kernel<<<grid, block, 0, ctx->stream>>>(a);
+      } else if (glu) {
+        if (e0 || e1) hipExtLaunchKernelGGL(gemm_f16_kernel<DT_Q4_K, false, true>, grid, block, 0, ctx->stream, e0, e1, 0, a);
+        else gemm_f16_kernel<DT_Q4_K, false, true><<<grid, block, 0, ctx->stream>>>(a);
       } else if (a.dots) gemm_f16_kernel<DT_Q4_K, true><<<grid, block, 0, ctx->stream>>>(a);
       else if (e0 || e1) hipExtLaunchKernelGGL(gemm_f16_kernel<DT_Q4_K>, grid, block, 0, ctx->stream, e0, e1, 0, a);
       else gemm_f16_kernel<DT_Q4_K><<<grid, block, 0, ctx->stream>>>(a);

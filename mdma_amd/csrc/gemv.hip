@@ -894,8 +894,11 @@ void launch_gemv_f32_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up
 // (quantized once for every job sharing x). Returns false when a job is not
 // covered. Q4_K and Q6_K jobs take the f16-path GEMM unless the context asks
 // for the int8 one, or its inputs do not fit where they must go (a
-// capture's fixed-size scratch, an allocation-free call's buffer).
-static bool try_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t T) {
+// capture's fixed-size scratch, an allocation-free call's buffer). glu_y:
+// a gated call whose two jobs (gate, up) run as one gated launch writing
+// silu(gate) * up there.
+static bool try_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t T,
+                         float *glu_y = nullptr) {
   if (ctx->prefill_kernel != MDMA_PREFILL_AUTO) return false;
   for (int i = 0; i < n_jobs; i++)
     if (!gemm_f16_supported(jobs[i].dtype, jobs[i].layout, jobs[i].n_in, jobs[i].n_out) ||
@@ -916,7 +919,7 @@ static bool try_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const f
   }
   uint32_t *cnt = pb && nc ? gemm_counters(ctx, nc) : nullptr;
   launch_gemm_f16(ctx, jobs, n_jobs, x, T, s, cnt ? reinterpret_cast<float *>(s + need) : nullptr, cnt ? pb : 0, cnt,
-                  cnt ? nc : 0);
+                  cnt ? nc : 0, glu_y);
   return true;
 }
 
@@ -1008,6 +1011,8 @@ void launch_gemv_i8(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float 
 void launch_gemv_i8_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up, const float *x, uint64_t T,
                           float *y) {
   const GemvJob gu[2] = {gate, up};
+  // Q4_K gate and up on the f16-path GEMM: the SiLU product in its epilogue.
+  if (T >= GEMM_MIN_TOKENS && gemm_f16_glu_ok(gate, up) && try_gemm_f16(ctx, gu, 2, x, T, y)) return;
   if (try_gemm_i8(ctx, gu, 2, x, T)) {
     launch_silu_mul(ctx, gate.y, up.y, y, T * gate.n_out);
     return;

@@ -332,8 +332,11 @@ uint64_t gemm_f16_input_bytes(uint64_t M, uint64_t K);
 // Split-K partials the f16-path launches of these jobs over M tokens take
 // (bytes; 0 = unsplit) and the arrival counters they need (*tiles).
 uint64_t gemm_f16_split_bytes(const mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, uint64_t M, uint64_t *tiles);
+// glu_y: jobs are (gate, up) passing gemm_f16_glu_ok; one gated launch
+// writes silu(gate) * up to glu_y (the jobs' own outputs are not written).
+bool gemm_f16_glu_ok(const GemvJob &gate, const GemvJob &up);
 void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t M, char *scratch,
-                     float *part, uint64_t part_bytes, uint32_t *cnt, uint64_t counters);
+                     float *part, uint64_t part_bytes, uint32_t *cnt, uint64_t counters, float *glu_y = nullptr);
 void launch_quantize_act(mdma_ctx *ctx, const float *x, uint64_t n, uint64_t group, int8_t *q,
                          float *d, int32_t *sum16);
 void launch_block_dot(mdma_ctx *ctx, const GemvJob &w, const int8_t *qx, uint64_t T, int32_t *out);

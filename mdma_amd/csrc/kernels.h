@@ -53,6 +53,16 @@ __device__ __forceinline__ void lds_dma4(const void *base, uint32_t off, const v
 }
 __device__ __forceinline__ void lds_wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// silu_mul of one element (cpu.rs:447-458): (g / (1 + exp(-g))) * u, each
+// operation rounded on its own (no contraction), the device expf. The
+// elementwise kernel and the prefill GEMM's fused gate/up epilogue share it,
+// so both give the same bits.
+__device__ __forceinline__ float silu_mul1(float g, float u) {
+#pragma clang fp contract(off)
+  const float s = g / (1.0f + expf(-g));
+  return s * u;
+}
+
 __device__ __forceinline__ float h2f(uint32_t bits16) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits16 & 0xffff));
 }

@@ -235,12 +235,8 @@ __global__ void add_kernel(const float *__restrict__ a, const float *__restrict_
 // silu_mul (cpu.rs:447-458): y = (g / (1 + exp(-g))) * u.
 __global__ void silu_mul_kernel(const float *__restrict__ g, const float *__restrict__ u, float *__restrict__ y,
                                 size_t n) {
-#pragma clang fp contract(off)
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
-    const float gv = g[i];
-    const float s = gv / (1.0f + expf(-gv));
-    y[i] = s * u[i];
-  }
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    y[i] = silu_mul1(g[i], u[i]);
 }
 
 // Interleaved-pair rotation (apply_rope, cpu.rs:68-84) of one pair.

@@ -889,6 +889,59 @@ def q6k_full_scale_cases(backend, kind):
         w.buf.close(), xb.close(), yb.close()
 
 
+@pytest.mark.parametrize("shape", [(200, 768, 256), (64, 512, 384), (130, 512, 128)])
+def test_prefill_gated_gemm_equals_separate(backend, shape):
+    """Q4_K ffn_gate_up at prefill size runs one gated GEMM launch whose
+    epilogue writes silu(gate) * up. Each output's arithmetic is that of the
+    separate GEMMs (K under 1024 columns: no launch splits K), and the SiLU
+    is silu_mul's, so the result equals qmatmul(gate), qmatmul(up), then
+    silu_mul, bit for bit."""
+    T, k, n = shape
+    backend.set_act_mode(1)
+    try:
+        raws = [synth.weight(Q4K, n, k, 530 + i) for i in range(2)]
+        ws = [backend.upload_weight(r, Q4K, (n, k)) for r in raws]
+        xb = backend.f32_buf(synth.normal_f32(T * k, 540 + T))
+        gs, us, y = (backend.alloc(T * n * 4) for _ in range(3))
+        backend.ffn_gate_up(ws[0], ws[1], xb, gs, us, y)
+        got = backend.download_f32(y)
+        og, ou, y2 = (backend.alloc(T * n * 4) for _ in range(3))
+        backend.qmatmul(ws[0], xb, og)
+        backend.qmatmul(ws[1], xb, ou)
+        backend.silu_mul(og, ou, y2)
+        want = backend.download_f32(y2)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), \
+            f"gated GEMM differs from separate GEMMs + silu_mul at {shape}: {np.sum(got != want)} elements"
+    finally:
+        backend.set_act_mode(0)
+
+
+@pytest.mark.parametrize("shape", [(64, 4096, 1024), (70, 512, 320), (300, 2048, 256)])
+def test_prefill_gated_gemm_matches_oracle(backend, shape):
+    """The gated launch against the oracle's silu(gate) * up where K is
+    split over workgroups (64 x 4096 -> 1024: 16 column tiles) and over
+    ragged token counts; 320 rows (not a multiple of 128) take the unfused
+    GEMMs and silu_mul."""
+    T, k, n = shape
+    backend.set_act_mode(1)
+    try:
+        raws = [synth.weight(Q4K, n, k, 550 + i) for i in range(2)]
+        ws = [backend.upload_weight(r, Q4K, (n, k)) for r in raws]
+        x = synth.normal_f32(T * k, 560 + n)
+        xb = backend.f32_buf(x)
+        gs, us = backend.alloc(T * n * 4), backend.alloc(T * n * 4)
+        y = backend.f32_buf(np.full(T * n + 16, CANARY, np.float32))
+        backend.ffn_gate_up(ws[0], ws[1], xb, gs, us, y)
+        out = backend.download_f32(y)
+        assert np.all(out[T * n:] == CANARY)
+        g = oracle_i8_32(Q4K, raws[0], n, k, x)[0].astype(np.float32)
+        u = oracle_i8_32(Q4K, raws[1], n, k, x)[0].astype(np.float32)
+        want = ffi.silu_mul(g.reshape(-1), u.reshape(-1))
+        np.testing.assert_allclose(out[:T * n], want, rtol=2e-3, atol=1e-3)
+    finally:
+        backend.set_act_mode(0)
+
+
 @pytest.mark.parametrize("dtype", [Q8, Q4K, Q6K])
 def test_prefill_gemm_fused_calls(backend, dtype):
     backend.set_act_mode(1)
