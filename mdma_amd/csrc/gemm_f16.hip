@@ -211,13 +211,16 @@ __device__ __forceinline__ void q4_f16(uint32_t q, h2 sa, h2 na, h2 sb, h2 nb_, 
 // (possibly on different XCDs, whose L2s are not coherent with each other)
 // only through device-scope stores and loads; each wave waits for its
 // stores before the barrier that precedes the counter's device-scope add.
+// NT: the workgroup's threads (a tile of NT * 64 outputs).
+template <int NT = 256>
 __device__ bool f16_split_merge(float (&acc)[4][4][4], const F16Args &a) {
   __shared__ uint32_t last;
+  constexpr uint32_t TILE = NT * 64;
   const uint32_t tile = blockIdx.y * gridDim.x + blockIdx.x, S = gridDim.z, z = blockIdx.z, tid = threadIdx.x;
-  float *pt = a.part + (size_t)tile * S * (TM * TN) + tid;
+  float *pt = a.part + (size_t)tile * S * TILE + tid;
 #pragma unroll
   for (int k = 0; k < 64; k++)
-    __hip_atomic_store(pt + (size_t)z * (TM * TN) + 256 * k, acc[k >> 4][(k >> 2) & 3][k & 3], __ATOMIC_RELAXED,
+    __hip_atomic_store(pt + (size_t)z * TILE + NT * k, acc[k >> 4][(k >> 2) & 3][k & 3], __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
@@ -236,11 +239,11 @@ __device__ bool f16_split_merge(float (&acc)[4][4][4], const F16Args &a) {
 #pragma unroll
   for (int k = 0; k < 64; k++) sum[k] = 0.f;
   for (uint32_t y = 0; y < S; y++) {
-    const float *py = pt + (size_t)y * (TM * TN);
+    const float *py = pt + (size_t)y * TILE;
 #pragma unroll
     for (int k = 0; k < 64; k++)
       sum[k] += y == z ? acc[k >> 4][(k >> 2) & 3][k & 3]
-                       : __hip_atomic_load(py + 256 * k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                       : __hip_atomic_load(py + NT * k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 #pragma unroll
   for (int k = 0; k < 64; k++) acc[k >> 4][(k >> 2) & 3][k & 3] = sum[k];
@@ -703,6 +706,202 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_q6_kernel(F16Args a) {
   }
 }
 
+// Q6_K with 256 tokens per workgroup: 512 threads (8 waves of 64 rows x 64
+// tokens), one workgroup per CU (148 KB of LDS). The same arithmetic per
+// output as gemm_f16_q6_kernel; what changes is the schedule: the operands
+// A1 / A2 are double-buffered like gemm_f16_kernel's (one barrier per
+// stage: stage st + 1 is converted while stage st's MFMAs run), each
+// stage's weight conversion serves 256 tokens instead of 128, and it is
+// split over all 8 waves (block 0 of the stage on waves 0-3, block 1 on
+// waves 4-7). Between a wave's wait for its own DMAs and the barrier it
+// reads only what it loaded itself: waves 0-3 load plane A, waves 4-7
+// plane B, each half its own copy of plane Q and of the scales, and waves
+// 0-1 the d of the rows they convert.
+constexpr int TMW = 256;
+
+__global__ __launch_bounds__(512, 1) void gemm_f16_q6w_kernel(F16Args a) {
+  __shared__ __attribute__((aligned(16))) _Float16 ws[2][TN][SK];    // A1, by stage parity
+  __shared__ __attribute__((aligned(16))) _Float16 ws2[2][TN][SK];   // A2
+  __shared__ __attribute__((aligned(16))) _Float16 xs[2][TMW][SK];   // activations, f16 int8 values
+  // Planes A and B, then plane Q twice (for waves 0-3 and 4-7), of thread
+  // (row, h'); the scales twice.
+  __shared__ __attribute__((aligned(16))) uint8_t wraw[4][256][16];
+  __shared__ __attribute__((aligned(16))) uint32_t wsc[2][256];     // the unit's 4 scales
+  __shared__ __attribute__((aligned(16))) uint32_t dvr[TN];          // the dword holding d, then d (f32)
+  __shared__ __attribute__((aligned(16))) float sxs[2][2][TMW];
+  // Per stage parity and wave: some A2 of the wave's conversion is not zero
+  // (each wave writes its own byte, so nothing needs clearing).
+  __shared__ __attribute__((aligned(8))) uint8_t need2w[2][8];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const F16Job J = f16_job(a);
+  const uint32_t bn = J.bn, bm = blockIdx.y * TMW;
+  const int wn = (wave & 1) * 64, wm = (wave >> 1) * 64;
+  const int l16 = lane & 15, lq = lane >> 4;
+  const uint32_t K = a.K, nb = K / 32, nst = K / SK, U = K / 64, rb = (uint32_t)a.row_bytes;
+
+  uint32_t xo[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int row = 32 * wave + 8 * i + (lane >> 3);
+    xo[i] = 2 * (min(bm + row, a.M - 1) * K + 8 * swz(row, lane & 7));
+  }
+  const int s_tok = tid & (TMW - 1), s_blk = tid >> 8;
+  const uint32_t so = 4 * (min(bm + s_tok, a.M - 1) * nb + s_blk);
+  // Quant planes: thread pt = tid % 256 = (row pt / 2, unit h' = pt % 2)
+  // converts the stage's block wh = tid / 256 from plane wh and plane Q.
+  const int pt = tid & 255, w_row = pt >> 1, w_h = pt & 1, wh = tid >> 8;
+  const uint32_t wrow = min(bn + w_row, J.N - 1) * rb;
+  // d: waves 0 and 1 load and convert rows 64 w + lane.
+  const uint32_t drow = min(bn + 64 * (wave & 1) + lane, J.N - 1) * rb + 52 * U;
+  const uint32_t whs = wave >> 2;  // the wave's half: planes A or B (uniform)
+
+  auto gload = [&](uint32_t st) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) lds_dma16(a.xh, xo[i] + 128 * st, &xs[st & 1][32 * wave + 8 * i][0]);
+    lds_dma4(a.sx, so + 8 * st, &sxs[st & 1][0][64 * wave]);
+    if (st % 2 == 0) {  // the half super-block's planes serve both its stages
+      const uint32_t u = 2 * (st / 2) + w_h, q = 64 * (wave & 3);
+      lds_dma16(J.w, wrow + 16 * (whs * U + u), &wraw[whs][q][0]);
+      lds_dma16(J.w, wrow + 16 * (2 * U + u), &wraw[2 + whs][q][0]);
+      lds_dma4(J.w, wrow + 48 * U + 4 * u, &wsc[whs][q]);
+    }
+    // A super-block's d goes in with its second stage (the previous
+    // super-block's epilogue, at its last stage, has read dvr by then).
+    if (st % 4 == 1 && wave < 2) lds_dma4(J.w, (drow + 2 * (st / 4)) & ~3u, &dvr[64 * wave]);
+  };
+  // Stage st's operands into buffer st % 2: this thread's 16 columns of
+  // block wh.
+  auto wstore = [&](uint32_t st) {
+    const uint4 P = *reinterpret_cast<const uint4 *>(&wraw[wh][pt][0]);
+    const uint4 Q = *reinterpret_cast<const uint4 *>(&wraw[2 + wh][pt][0]);
+    const uint32_t sc4 = wsc[wh][pt];
+    const int qp = st & 1, qq = 2 * qp + wh, b = st & 1;
+    const uint32_t pv[4] = {P.x, P.y, P.z, P.w}, hv[4] = {Q.x, Q.y, Q.z, Q.w};
+    const _Float16 fs = (_Float16)(float)(int8_t)(sc4 >> (8 * qq));
+    const h2 sc2 = {fs, fs};
+    const int c0 = 4 * wh + 2 * w_h;
+    uint32_t any = 0;
+#pragma unroll
+    for (int d = 0; d < 4; d++) {  // columns 4d..4d+3 of the thread's 16: half of chunk c0 + d / 2
+      const uint32_t nib = qp ? (pv[d] >> 4) & 0x0F0F0F0Fu : pv[d] & 0x0F0F0F0Fu;
+      const uint32_t v = nib | (((hv[d] >> (2 * qq)) & 0x03030303u) << 4);
+      uint32_t a1[2], a2[2];
+      q6_pair_f16(v, sc2, a1[0], a2[0], 0);
+      q6_pair_f16(v, sc2, a1[1], a2[1], 1);
+      any |= (a2[0] | a2[1]) & 0x7FFF7FFFu;
+      const int col = 8 * swz(w_row, c0 + (d >> 1)) + 4 * (d & 1);
+      *reinterpret_cast<uint2 *>(&ws[b][w_row][col]) = make_uint2(a1[0], a1[1]);
+      *reinterpret_cast<uint2 *>(&ws2[b][w_row][col]) = make_uint2(a2[0], a2[1]);
+    }
+    const bool nz = __builtin_amdgcn_ballot_w64(any != 0) != 0;
+    if (lane == 0) need2w[b][wave] = nz ? 1 : 0;
+  };
+  // Super-block sb's d (the half of the aligned dword holding it) as f32,
+  // in place, rows 0..127 (threads 0..127: waves 0 and 1, which loaded them).
+  auto hstore = [&](uint32_t sb) {
+    if (tid < TN) {
+      const uint32_t w = dvr[tid];
+      dvr[tid] = __builtin_bit_cast(uint32_t, h2f(sb & 1 ? w >> 16 : w));
+    }
+  };
+
+  float acc[4][4][4], part[4][4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) acc[i][j][r] = 0.f, part[i][j][r] = 0.f;
+
+  const uint32_t st0 = blockIdx.z * a.sb_split * 4, st1 = min(st0 + a.sb_split * 4, nst);
+  gload(st0);
+  lds_wait_dma();
+  lds_barrier();
+  wstore(st0);
+  lds_barrier();
+  for (uint32_t st = st0; st < st1; st++) {
+    // Stage st + 1's loads in flight over this stage's MFMAs, into buffers
+    // last read by stage st - 1 (before the barrier). Each wave waits for
+    // its own before converting what they brought (lds_wait_dma below).
+    if (st + 1 < st1) gload(st + 1);
+    const int buf = st & 1;
+    const bool n2 = *reinterpret_cast<const uint64_t *>(&need2w[buf][0]) != 0;
+    auto block = [&](int h, auto first) {
+      v8h A[4], A2[4], B[4];
+      float s[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int r = wn + 16 * i + l16;
+        A[i] = *reinterpret_cast<const v8h *>(&ws[buf][r][8 * swz(r, 4 * h + lq)]);
+        if (n2) A2[i] = *reinterpret_cast<const v8h *>(&ws2[buf][r][8 * swz(r, 4 * h + lq)]);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int r = wm + 16 * j + l16;
+        B[j] = *reinterpret_cast<const v8h *>(&xs[buf][r][8 * swz(r, 4 * h + lq)]);
+        s[j] = sxs[buf][h][r];
+      }
+      auto dot = [&](int t) {
+        v4f c = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[t >> 2], B[t & 3], v4f{}, 0, 0, 0);
+        if (n2) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(A2[t >> 2], B[t & 3], c, 0, 0, 0);
+        return c;
+      };
+      v4f c[3];
+      c[0] = dot(0);
+      c[1] = dot(1);
+#pragma unroll
+      for (int t = 0; t < 16; t++) {
+        if (t + 2 < 16) c[(t + 2) % 3] = dot(t + 2);
+        const int i = t >> 2, j = t & 3;
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          part[i][j][r] = first ? s[j] * c[t % 3][r] : fmaf(s[j], c[t % 3][r], part[i][j][r]);
+      }
+    };
+    if (st % 4 == 0) block(0, std::true_type{});
+    else block(0, std::false_type{});
+    block(1, std::false_type{});
+    if (st % 4 == 3) {  // the super-block's last stage: acc += d * part
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float4 d4 = *reinterpret_cast<const float4 *>(&dvr[wn + 16 * i + 4 * lq]);
+        const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) acc[i][j][r] = fmaf(dv[r], part[i][j][r], acc[i][j][r]);
+      }
+    }
+    lds_wait_dma();
+    if (st + 1 < st1) {
+      wstore(st + 1);
+      if ((st + 1) % 4 == 1) hstore((st + 1) / 4);
+    }
+    lds_barrier();
+  }
+  if (gridDim.z > 1 && !f16_split_merge<512>(acc, a)) return;
+  const bool vec = (J.N & 3) == 0;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint32_t m = bm + wm + 16 * j + l16;
+    if (m >= a.M) continue;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t n = bn + wn + 16 * i + 4 * lq;
+      float *yp = J.y + (size_t)m * J.N + n;
+      if (vec && n + 3 < J.N) {
+        *reinterpret_cast<float4 *>(yp) = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+          if (n + t < J.N) yp[t] = acc[i][j][t];
+      }
+    }
+  }
+}
+
 }  // namespace
 
 bool gemm_f16_supported(int32_t dtype, int layout, uint64_t n_in, uint64_t n_out) {
@@ -734,6 +933,37 @@ F16Split f16_plan(const mdma_ctx *ctx, uint64_t tiles, uint64_t K) {
   return F16Split{(uint32_t)((nsb + sbs - 1) / sbs), (uint32_t)sbs};
 }
 uint64_t rows_per_launch(uint64_t K) { return ((1ull << 31) / K) / TM * TM; }
+
+// A launch's kernel: the wide Q6_K kernel (256 tokens per workgroup, one
+// workgroup per CU) for Q6_K over more than 128 tokens, else 128 x 128
+// tiles, two workgroups per CU.
+struct F16Shape {
+  bool wide;
+  uint64_t tm;
+};
+F16Shape f16_shape(const GemvJob &w, uint64_t Mc) {
+  const bool wide = w.dtype == DT_Q6_K && !w.dots && Mc > (uint64_t)TM;
+  return F16Shape{wide, wide ? (uint64_t)TMW : (uint64_t)TM};
+}
+// The wide kernel's splits: its launches have half the tiles with one
+// resident workgroup per CU, so the count keeps the launch's length lowest
+// -- rounds of workgroups times a workgroup's super-blocks, plus one for a
+// split's partial tile and merge, the fewer splits on a tie (3 splits of
+// 96 tiles would be 288 workgroups on 256 CUs: a second round as long as
+// the first).
+F16Split f16_plan_for(const mdma_ctx *ctx, bool wide, uint64_t tiles, uint64_t K) {
+  if (!wide) return f16_plan(ctx, tiles, K);
+  const uint64_t cus = ctx->cu_count ? ctx->cu_count : 256, nsb = K / 256;
+  F16Split best{1, (uint32_t)nsb};
+  if (tiles >= cus || nsb < 4) return best;
+  uint64_t best_cost = (tiles + cus - 1) / cus * nsb;
+  for (uint64_t s = 2; s <= std::min<uint64_t>(nsb / 2, 16); s++) {
+    const uint64_t sbs = (nsb + s - 1) / s, S = (nsb + sbs - 1) / sbs;
+    const uint64_t cost = (tiles * S + cus - 1) / cus * (sbs + 1);
+    if (cost < best_cost) best_cost = cost, best = F16Split{(uint32_t)S, (uint32_t)sbs};
+  }
+  return best;
+}
 }  // namespace
 
 namespace {
@@ -753,15 +983,17 @@ uint64_t col_tiles(const GemvJob *jobs, int n) {
 }  // namespace
 
 uint64_t gemm_f16_split_bytes(const mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, uint64_t M, uint64_t *tiles) {
-  const uint64_t K = jobs[0].n_in, Mc = std::min(M, rows_per_launch(K)), mt = (Mc + TM - 1) / TM;
+  const uint64_t K = jobs[0].n_in, Mc = std::min(M, rows_per_launch(K));
   const int groups = f16_fusable(jobs, n_jobs) ? 1 : n_jobs;
   uint64_t bytes = 0;
   *tiles = 0;
   for (int g = 0; g < groups; g++) {
-    const uint64_t t = (groups == 1 ? col_tiles(jobs, n_jobs) : col_tiles(jobs + g, 1)) * mt;
-    const F16Split sp = f16_plan(ctx, t, K);
+    const GemvJob *gj = groups == 1 ? jobs : jobs + g;
+    const F16Shape sh = f16_shape(gj[0], Mc);
+    const uint64_t t = col_tiles(gj, groups == 1 ? n_jobs : 1) * ((Mc + sh.tm - 1) / sh.tm);
+    const F16Split sp = f16_plan_for(ctx, sh.wide, t, K);
     if (sp.S > 1) {
-      bytes = std::max(bytes, t * sp.S * (uint64_t)(TM * TN) * 4);
+      bytes = std::max(bytes, t * sp.S * sh.tm * TN * 4);
       *tiles = std::max(*tiles, t);
     }
   }
@@ -804,10 +1036,10 @@ void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float
       const uint64_t Mc = M - m0 < rows ? M - m0 : rows;
       // Split K when the launch has few tiles and the partials fit (not for
       // the block-dot capture, whose dots are stored by the one split).
-      const uint64_t ct = col_tiles(gj, nj), tiles = ct * ((Mc + TM - 1) / TM);
-      F16Split sp = f16_plan(ctx, tiles, K);
-      if (sp.S > 1 && (w.dots || !part || !cnt || tiles > counters ||
-                       tiles * sp.S * (uint64_t)(TM * TN) * 4 > part_bytes))
+      const F16Shape sh = f16_shape(w, Mc);
+      const uint64_t ct = col_tiles(gj, nj), mt = (Mc + sh.tm - 1) / sh.tm, tiles = ct * mt;
+      F16Split sp = f16_plan_for(ctx, sh.wide, tiles, K);
+      if (sp.S > 1 && (w.dots || !part || !cnt || tiles > counters || tiles * sp.S * sh.tm * TN * 4 > part_bytes))
         sp = F16Split{1, (uint32_t)(K / 256)};
       F16Args a{xh + m0 * K, sx + m0 * nb, ph + m0 * nb, (uint32_t)(pl - ph), inv + m0, w.w, w.y + m0 * w.n_out,
                 (uint32_t)Mc, (uint32_t)w.n_out, (uint32_t)K, gfx950_row_bytes(w.dtype, K),
@@ -823,10 +1055,13 @@ void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float
       }
       // (A gated launch has the same number of column tiles: 64 rows of
       // both weights each, N a multiple of 128.)
-      const dim3 grid((uint32_t)ct, (uint32_t)((Mc + TM - 1) / TM), sp.S), block(256);
+      const dim3 grid((uint32_t)ct, (uint32_t)mt, sp.S), block(sh.wide ? 512 : 256);
       // Timing events bracket the calls' GEMM launches (not the prologue).
       const hipEvent_t e0 = g == 0 && m0 == 0 ? t0 : nullptr, e1 = g == groups - 1 && m0 + Mc >= M ? t1 : nullptr;
-      if (w.dtype == DT_Q6_K) {
+      if (w.dtype == DT_Q6_K && sh.wide) {
+        if (e0 || e1) hipExtLaunchKernelGGL(gemm_f16_q6w_kernel, grid, block, 0, ctx->stream, e0, e1, 0, a);
+        else gemm_f16_q6w_kernel<<<grid, block, 0, ctx->stream>>>(a);
+      } else if (w.dtype == DT_Q6_K) {
         if (e0 || e1) hipExtLaunchKernelGGL(gemm_f16_q6_kernel, grid, block, 0, ctx->stream, e0, e1, 0, a);
         else gemm_f16_q6_kernel<<<grid, block, 0, ctx->stream>>>(a);
       } else if (glu) {

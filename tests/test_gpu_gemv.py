@@ -782,7 +782,7 @@ def gemm_cases(f):
 
 
 @pytest.mark.parametrize("shape", [(64, 256, 64), (97, 512, 200), (130, 1024, 257), (64, 4096, 384),
-                                   (300, 768, 130)])
+                                   (300, 768, 130), (300, 4096, 384), (520, 1024, 520)])
 @gemm_cases
 def test_prefill_gemm_i8(backend, dtype, prefill_kernel, shape):
     T, k, rows = shape
@@ -887,6 +887,41 @@ def q6k_full_scale_cases(backend, kind):
             assert_parity(y[tok, r0:r0 + 16].reshape(-1), cpu, exact, 1e-3, abs_sum=absum,
                           what=f"gemm q6k full scales kind={kind} T={T} rows {r0}..")
         w.buf.close(), xb.close(), yb.close()
+
+
+@pytest.mark.parametrize("shape", [(512, 4096, 1024), (300, 14336, 256)])
+def test_prefill_gemm_q6k_wide_repeatable(backend, shape):
+    """The Q6_K f16-path GEMM over more than 128 tokens (256 tokens per
+    workgroup, split K at these row counts) gives the same bits on every
+    call, with full-range sub-block scales (A2 terms present) and the
+    oracle's values on sampled rows: a read of LDS another wave's loads have
+    not filled would show as call-to-call differences."""
+    T, k, rows = shape
+    backend.set_act_mode(1)
+    try:
+        raw = q6k_full_scale_range(synth.weight(Q6K, rows, k, 620 + T), rows, k, 621)
+        x = synth.normal_f32(T * k, 622 + T)
+        w = backend.upload_weight(raw, Q6K, (rows, k))
+        xb = backend.f32_buf(x)
+        outs = []
+        for _ in range(6):
+            yb = backend.alloc(T * rows * 4)
+            backend.qmatmul_i8(w, xb, yb)
+            outs.append(backend.download_f32(yb))
+            yb.close()
+        for o in outs[1:]:
+            assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)), f"wide Q6_K GEMM not repeatable at {shape}"
+        y = outs[0].reshape(T, rows)
+        rb = len(raw) // rows
+        for r0 in (0, rows - 16):
+            sl = raw[r0 * rb:(r0 + 16) * rb]
+            tok = np.unique(np.r_[0:4, 255:259, T - 4:T])
+            cpu, exact, absum = oracle_i8_32(Q6K, sl, 16, k, x.reshape(T, k)[tok].reshape(-1))
+            assert_parity(y[tok, r0:r0 + 16].reshape(-1), cpu, exact, 1e-3, abs_sum=absum,
+                          what=f"wide q6k T={T} k={k} rows {r0}..")
+        w.buf.close(), xb.close()
+    finally:
+        backend.set_act_mode(0)
 
 
 @pytest.mark.parametrize("shape", [(200, 768, 256), (64, 512, 384), (130, 512, 128)])
