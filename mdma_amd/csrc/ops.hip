@@ -416,6 +416,15 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q, 
 //     keys) split into f16 hi and lo as it is read; V goes to LDS
 //     transposed (dims x keys), so an operand's 8 keys are one 16-byte read.
 // s = (q.k) * scale and p = expf(s - m) in f32, the output O / l.
+// Key chunks (ct > 0): a query block's tiles are split into chunks of ct
+// tiles, one workgroup each (blockIdx.z), so the long blocks at the end of
+// a causal prompt no longer set the launch's length alone and more
+// workgroups share each CU. Each chunk leaves its rows' (m, l, O) in part
+// [slot][value][thread]; the chunk that arrives last at the block's
+// counter merges all chunks in chunk order (the same result whatever the
+// arrival order) and writes O / l. Chunk 0 holds key 0, which every row
+// sees, so the merged maximum is finite; a later chunk's fully masked row
+// contributes nothing.
 constexpr uint32_t ATT_PREFILL_MIN = 64;
 
 typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
@@ -450,7 +459,8 @@ template <int G, int HD>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restrict__ q, const uint16_t *__restrict__ K,
                                                            const uint16_t *__restrict__ V, float *__restrict__ o,
                                                            uint32_t n_q, uint32_t prefix, uint32_t n_q_heads,
-                                                           uint32_t n_kv_heads, float scale) {
+                                                           uint32_t n_kv_heads, float scale, uint32_t ct,
+                                                           float *__restrict__ part, uint32_t *__restrict__ cnt) {
   constexpr int QT = 64 / G;             // queries per workgroup
   constexpr int NC = HD / 32;            // 32-dim K steps of S
   constexpr int ND = HD / 16;            // 16-dim blocks of O
@@ -489,7 +499,12 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
       }
     }
   };
-  gload(0);
+  // This workgroup's tiles: all of the block's, or chunk blockIdx.z of ct.
+  const uint32_t n_tiles = (prefix + min(q0 + QT, n_q) - 1) / 64 + 1;
+  const uint32_t n_ch = ct ? (n_tiles + ct - 1) / ct : 1, ch = blockIdx.z;
+  if (ch >= n_ch) return;  // (uniform: this block has fewer chunks)
+  const uint32_t t_begin = ct ? ch * ct : 0, t_end = ct ? min(t_begin + ct, n_tiles) : n_tiles;
+  gload(t_begin);
 
   // This lane's Q operand row (16 wave + l16) as f16 hi + mid + lo, dims
   // 32c + 8lq (each remainder is exact in f32).
@@ -523,10 +538,9 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
   for (int j = 0; j < 4; j++) m[j] = -INFINITY, l[j] = 0.f;
 #pragma unroll
   for (int n = 0; n < ND; n++) O[n] = v4f_t{0.f, 0.f, 0.f, 0.f};
-  const uint32_t n_tiles = (prefix + min(q0 + QT, n_q) - 1) / 64 + 1;
   float *pwf = pw[wave];
 
-  for (uint32_t t = 0; t < n_tiles; t++) {
+  for (uint32_t t = t_begin; t < t_end; t++) {
     lds_barrier();  // the previous tile's reads of ks and vt are done
 #pragma unroll
     for (int i = 0; i < IT; i++) {
@@ -546,7 +560,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
       }
     }
     lds_barrier();
-    if (t + 1 < n_tiles) gload(t + 1);  // in flight over this tile's arithmetic
+    if (t + 1 < t_end) gload(t + 1);  // in flight over this tile's arithmetic
 
     // ---- S = Q K^T: 16 rows x 64 keys per wave ----
     v4f_t S[4];
@@ -577,12 +591,14 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
         s[kb] = key <= vis[j] ? S[kb][j] * scale : -INFINITY;
         mx = fmaxf(mx, s[kb]);
       }
-      const float mn = fmaxf(m[j], row16_max(mx));  // finite: key 0 is every row's
-      const float alpha = expf(m[j] - mn);          // 0 on the first tile (m = -inf)
+      // mn is finite once a visible key has been seen (the first tile of
+      // chunk 0 holds key 0); a later chunk's row may see none yet.
+      const float mn = fmaxf(m[j], row16_max(mx));
+      const float alpha = mn == -INFINITY ? 1.f : expf(m[j] - mn);  // 0 on the first visible tile (m = -inf)
       float ps = 0.f;
 #pragma unroll
       for (int kb = 0; kb < 4; kb++) {
-        const float p = expf(s[kb] - mn);  // 0 for masked keys
+        const float p = s[kb] == -INFINITY ? 0.f : expf(s[kb] - mn);  // 0 for masked keys
         ps += p;
         pwf[(4 * lq + j) * PP + 16 * kb + l16] = p;
       }
@@ -612,6 +628,74 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
 #pragma unroll
       for (int n = 0; n < ND; n++) O[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, B[n], O[n], 0, 0, 0);
     }
+  }
+  if (n_ch > 1) {
+    // Leave this chunk's (m, l, O), then the last chunk to arrive merges.
+    constexpr int NV = 8 + 4 * ND;
+    __shared__ uint32_t last;
+    const size_t blk = (size_t)kvh * gridDim.y + blockIdx.y;
+    float *pb = part + blk * gridDim.z * (NV * 256) + tid;
+    {
+      float *pc = pb + (size_t)ch * (NV * 256);
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        __hip_atomic_store(pc + 256 * j, m[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pc + 256 * (4 + j), l[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+#pragma unroll
+      for (int n = 0; n < ND; n++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          __hip_atomic_store(pc + 256 * (8 + 4 * n + j), O[n][j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t prev = __hip_atomic_fetch_add(cnt + blk * CNT_STRIDE, 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+      last = prev == n_ch - 1;
+      if (last) __hip_atomic_store(cnt + blk * CNT_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last) return;
+    float M[4], L[4];
+    v4f_t OA[ND];
+    for (uint32_t c = 0; c < n_ch; c++) {
+      const float *pc = pb + (size_t)c * (NV * 256);
+      float mc[4], lc[4];
+      v4f_t Oc[ND];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        mc[j] = c == ch ? m[j] : __hip_atomic_load(pc + 256 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        lc[j] = c == ch ? l[j] : __hip_atomic_load(pc + 256 * (4 + j), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+#pragma unroll
+      for (int n = 0; n < ND; n++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          Oc[n][j] = c == ch ? O[n][j]
+                             : __hip_atomic_load(pc + 256 * (8 + 4 * n + j), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (c == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) M[j] = mc[j], L[j] = lc[j];
+#pragma unroll
+        for (int n = 0; n < ND; n++) OA[n] = Oc[n];
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const float mn = fmaxf(M[j], mc[j]);  // finite: chunk 0's M is
+          const float a = expf(M[j] - mn), b = mc[j] == -INFINITY ? 0.f : expf(mc[j] - mn);
+          L[j] = L[j] * a + lc[j] * b;
+#pragma unroll
+          for (int n = 0; n < ND; n++) OA[n][j] = OA[n][j] * a + Oc[n][j] * b;
+          M[j] = mn;
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) l[j] = L[j];
+#pragma unroll
+    for (int n = 0; n < ND; n++) O[n] = OA[n];
   }
 #pragma unroll
   for (int j = 0; j < 4; j++) {
@@ -1302,12 +1386,30 @@ bool attn_impl(mdma_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t
       n_kv_heads && GP * n_kv_heads == n_q_heads && (GP == 1 || GP == 2 || GP == 4 || GP == 8) &&
       kv_len * n_kv_heads * hd < (1ull << 32) && n_kv_heads < 65536) {
     // A prompt's causal attention on the matrix cores (attn_prefill_kernel).
-    const dim3 grid((uint32_t)n_kv_heads, (uint32_t)((n_q + 64 / GP - 1) / (64 / GP)));
+    const uint64_t QT = 64 / GP, nqb = (n_q + QT - 1) / QT;
     const float sc = 1.0f / sqrtf((float)hd);
     const uint32_t pre = (uint32_t)(kv_len - n_q);
+    // Key chunks of ct tiles: about two workgroups per CU (what stays
+    // resident) over the prompt's tile work, at least two tiles each; none
+    // when no block has more than ct tiles, under stream capture or in a
+    // fixed scratch.
+    uint64_t units = 0, max_t = 0;
+    for (uint64_t b = 0; b < nqb; b++) {
+      const uint64_t t = (pre + std::min((b + 1) * QT, n_q) - 1) / 64 + 1;
+      units += t;
+      max_t = std::max(max_t, t);
+    }
+    units *= n_kv_heads;
+    const uint64_t cus = ctx->cu_count ? ctx->cu_count : 256;
+    uint64_t ct = std::max<uint64_t>(2, (units + 2 * cus - 1) / (2 * cus)), n_ch = (max_t + ct - 1) / ct;
+    const uint64_t NV = 8 + 4 * (hd / 16), pbytes = n_kv_heads * nqb * n_ch * NV * 256 * 4;
+    if (n_ch < 2 || ctx->capturing || ctx->fixed_scratch || pbytes > (256ull << 20)) ct = 0, n_ch = 1;
+    float *part = ct ? reinterpret_cast<float *>(scratch(ctx, pbytes)) : nullptr;
+    uint32_t *cnt = ct ? attn_counters(ctx, n_kv_heads * nqb) : nullptr;
+    const dim3 grid((uint32_t)n_kv_heads, (uint32_t)nqb, (uint32_t)n_ch);
 #define MDMA_ATTP(GG, HH)                                                                                          \
   attn_prefill_kernel<GG, HH><<<grid, dim3(256), 0, ctx->stream>>>(q, k, v, o, (uint32_t)n_q, pre, (uint32_t)n_q_heads, \
-                                                                   (uint32_t)n_kv_heads, sc)
+                                                                   (uint32_t)n_kv_heads, sc, (uint32_t)ct, part, cnt)
     if (hd == 128) {
       if (GP == 1) MDMA_ATTP(1, 128);
       else if (GP == 2) MDMA_ATTP(2, 128);
