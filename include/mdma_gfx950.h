@@ -152,8 +152,10 @@ int mdma_gfx950_set_act_mode(mdma_ctx *ctx, int mode);
 int mdma_gfx950_set_norm_fusion(mdma_ctx *ctx, int on);
 /* Extra: the int8 mode's prefill GEMM kernel (calls of 64 or more tokens).
  * AUTO (default) takes the f16-path GEMM where it covers the weight (Q4_K
- * rows of whole 256-column blocks) and the int8 MFMA GEMM elsewhere; I8
- * forces the int8 MFMA GEMM (for A/B measurement and parity of both).
+ * and Q6_K rows of whole 256-column blocks; a Q4_K gate/up pair as one
+ * launch with the SiLU product in its epilogue) and the int8 MFMA GEMM
+ * elsewhere (Q8_0); I8 forces the int8 MFMA GEMM (for A/B measurement and
+ * parity of both).
  * Both compute the per-32-quantized product of the reference's
  * qmatmul_i8 (src/backend/rocm.rs:1759-1918). */
 typedef enum { MDMA_PREFILL_AUTO = 0, MDMA_PREFILL_I8 = 1 } mdma_prefill_kernel;
