@@ -483,7 +483,14 @@ constexpr int nbuf() {
 #ifndef MDMA_PRO4_TEAMS
 #define MDMA_PRO4_TEAMS 2
 #endif
-constexpr int team_wg(int pro, int tw) { return pro == 4 ? 64 * tw * MDMA_PRO4_TEAMS : WG; }
+// Threads of a workgroup staging quantized x (PRO 3): its waves share one
+// staged copy.
+#ifndef MDMA_PRO3_WG
+#define MDMA_PRO3_WG 256
+#endif
+constexpr int team_wg(int pro, int tw) {
+  return pro == 4 ? 64 * tw * MDMA_PRO4_TEAMS : (pro == 3 ? MDMA_PRO3_WG : WG);
+}
 
 // CAP: the block-dot capture instantiation (TeamJob::dots set), which also
 // stores each int32 sub-block dot; the production instantiations have none
@@ -878,7 +885,11 @@ void launch_iters(mdma_ctx *ctx, TeamSet ts, int tw, int pl, const float *xf, co
   }
   constexpr bool PRO_OK = !F32 && TT == 1 && !std::is_same<F, Q8G>::value;
   const bool pro4 = PRO_OK && ts.pro && tw > 1 && pl == 1;
-  const int wg = pro4 ? 64 * tw * MDMA_PRO4_TEAMS : WG, tpw = wg / 64 / tw;
+  // Staging x (PRO 3) pays for the fused gate/up and for Q4_K rows; the
+  // Q6_K one-wave launches measured faster with per-lane loads.
+  constexpr bool STAGE_OK = !F32 && TT == 1 && ITERS == 1 && (GATED || std::is_same<F, Q4G>::value);
+  const bool pro3 = STAGE_OK && !(PRO_OK && ts.pro) && !ts.nsum && tw == 1 && pl == 1;
+  const int wg = pro4 ? 64 * tw * MDMA_PRO4_TEAMS : (pro3 ? MDMA_PRO3_WG : WG), tpw = wg / 64 / tw;
   const dim3 grid((uint32_t)((teams + tpw - 1) / tpw)), block(wg);
   if (ts.ssq && grid.x > ts.ssq_cap) {  // one sum-of-squares partial per workgroup: no room, no launch
     ctx->team_grid = 0;
@@ -889,9 +900,6 @@ void launch_iters(mdma_ctx *ctx, TeamSet ts, int tw, int pl, const float *xf, co
   // duration, as a profiler measures it); they apply to one launch.
   hipEvent_t t0 = ctx->time_start, t1 = ctx->time_stop;
   ctx->time_start = ctx->time_stop = nullptr;
-  // Staging x through LDS pays for the fused gate/up and for Q4_K rows; the
-  // Q6_K one-wave launches measured faster with per-lane loads.
-  constexpr bool STAGE_OK = !F32 && TT == 1 && ITERS == 1 && (GATED || std::is_same<F, Q4G>::value);
   constexpr bool NORM_OK = !F32 && TT == 1 && !GATED && !std::is_same<F, Q8G>::value;
 #define MDMA_TEAM_GO(TW_, PL_, PRO_)                                                                              \
   do {                                                                                                            \
