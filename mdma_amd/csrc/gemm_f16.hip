@@ -176,26 +176,10 @@ __device__ __forceinline__ F16Job f16_job(const F16Args &a, uint32_t bx) {
   return F16Job{a.w, a.y, a.N, bx * TN};
 }
 
-// The workgroup's output tile (column tile x, token tile y). Workgroups go
-// to the 8 XCDs, each with its own L2, round-robin by dispatch index
-// d = y * nx + x (the same for every split z when nx * ny is a multiple of
-// 8). XCD j = d % 8 takes the tiles [j P, (j + 1) P), P = nx ny / 8, of an
-// order that walks MDMA_F16_GT token tiles for each column tile, so the
-// workgroups on one XCD share few token tiles' activations instead of
-// reading every token tile once per column tile they hold.
+// Token tiles walked per column tile in the XCD-aware tile order.
 #ifndef MDMA_F16_GT
 #define MDMA_F16_GT 4
 #endif
-struct F16Tile {
-  uint32_t x, y;
-};
-__device__ __forceinline__ F16Tile f16_tile() {
-  const uint32_t nx = gridDim.x, ny = gridDim.y, n = nx * ny;
-  if (MDMA_F16_GT == 0 || ny < 2 || n % 8) return F16Tile{blockIdx.x, blockIdx.y};
-  const uint32_t d = blockIdx.y * nx + blockIdx.x, l = (d % 8) * (n / 8) + d / 8;
-  const uint32_t gt = MDMA_F16_GT, g = l / (gt * nx), y0 = g * gt, gn = min(gt, ny - y0), r = l - y0 * nx;
-  return F16Tile{r / gn, y0 + r % gn};
-}
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
@@ -290,7 +274,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
   __shared__ float invs[TM];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const F16Tile tl = f16_tile();
+  const GridTile tl = grid_tile(MDMA_F16_GT);
   const F16Job J = f16_job(a, tl.x);
   const uint32_t bn = GLU ? tl.x * (TN / 2) : J.bn, bm = tl.y * TM, N = GLU ? a.N : J.N;
   const int wn = (wave & 1) * 64, wm = (wave >> 1) * 64;
@@ -557,7 +541,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_q6_kernel(F16Args a) {
   __shared__ uint32_t need2[2];  // per stage parity: some A2 of the stage is not zero
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const F16Tile tl = f16_tile();
+  const GridTile tl = grid_tile(MDMA_F16_GT);
   const F16Job J = f16_job(a, tl.x);
   const uint32_t bn = J.bn, bm = tl.y * TM;
   const int wn = (wave & 1) * 64, wm = (wave >> 1) * 64;
@@ -757,7 +741,7 @@ __global__ __launch_bounds__(512, 1) void gemm_f16_q6w_kernel(F16Args a) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const F16Tile tl = f16_tile();
+  const GridTile tl = grid_tile(MDMA_F16_GT);
   const F16Job J = f16_job(a, tl.x);
   const uint32_t bn = J.bn, bm = tl.y * TMW;
   const int wn = (wave & 1) * 64, wm = (wave >> 1) * 64;

@@ -35,6 +35,10 @@ namespace mdma {
 namespace {
 
 constexpr int BM = 64, BN = 128, BK = 128, KB = BK / 32, LDR = 48;
+// Token tiles walked per column tile in the XCD-aware tile order.
+#ifndef MDMA_I8_GT
+#define MDMA_I8_GT 16
+#endif
 
 // Q6_K: the 6-bit values of quarter r (0..3) of a unit from its ql bytes a
 // (quarters 0, 2), b (quarters 1, 3) and qh bytes h, four per dword, and
@@ -78,7 +82,8 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(16))) float d6[BN];         // Q6_K: d
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t bm = blockIdx.y * BM, bn = blockIdx.x * BN;
+  const GridTile tl = grid_tile(MDMA_I8_GT);
+  const uint32_t bm = tl.y * BM, bn = tl.x * BN;
   const int wm = (wave >> 1) * 32, wn = (wave & 1) * 64;
   const uint32_t K = a.K, nk32 = K / 32;
   // This workgroup's columns: split blockIdx.z of the K range.

@@ -53,6 +53,26 @@ __device__ __forceinline__ void lds_dma4(const void *base, uint32_t off, const v
 }
 __device__ __forceinline__ void lds_wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// A GEMM workgroup's output tile (column tile x, token tile y) on a grid of
+// nx column tiles by ny token tiles. Workgroups go to the 8 XCDs, each with
+// its own L2, round-robin by dispatch index d = y * nx + x (the same for
+// every split z when nx * ny is a multiple of 8). XCD j = d % 8 takes the
+// tiles [j P, (j + 1) P), P = nx ny / 8, of an order that walks gt token
+// tiles for each column tile, so the workgroups on one XCD share a few token
+// tiles' activations instead of reading every token tile once per column
+// tile they hold. Grids whose tile count is not a multiple of 8 keep the
+// dispatch order.
+struct GridTile {
+  uint32_t x, y;
+};
+__device__ __forceinline__ GridTile grid_tile(uint32_t gt) {
+  const uint32_t nx = gridDim.x, ny = gridDim.y, n = nx * ny;
+  if (gt == 0 || ny < 2 || n % 8) return GridTile{blockIdx.x, blockIdx.y};
+  const uint32_t d = blockIdx.y * nx + blockIdx.x, l = (d % 8) * (n / 8) + d / 8;
+  const uint32_t g = l / (gt * nx), y0 = g * gt, gn = min(gt, ny - y0), r = l - y0 * nx;
+  return GridTile{r / gn, y0 + r % gn};
+}
+
 // silu_mul of one element (cpu.rs:447-458): (g / (1 + exp(-g))) * u, each
 // operation rounded on its own (no contraction), the device expf. The
 // elementwise kernel and the prefill GEMM's fused gate/up epilogue share it,
