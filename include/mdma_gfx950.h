@@ -146,9 +146,12 @@ int mdma_gfx950_buffer_usage(mdma_ctx *ctx, int domain, uint64_t *used, uint64_t
 int mdma_gfx950_set_act_mode(mdma_ctx *ctx, int mode);
 /* Extra: in the int8 mode's one-token decode, fuse each layer's attention
  * RMSNorm into the GEMVs around it (the down projection stores the residual
- * stream and sums of squares, the QKV GEMV normalizes in its prologue).
- * Default on; off runs the separate norm kernel (for A/B measurement and
- * the parity test of the fused path). */
+ * stream and sums of squares, the QKV GEMV normalizes in its prologue); in
+ * the Llama driver's prefill (64 tokens and up), have the RMSNorms ahead of
+ * the QKV and gate/up GEMMs write those GEMMs' input, so the GEMMs skip
+ * their own quantization pass (the same bits). Default on; off runs the
+ * separate kernels (for A/B measurement and the parity tests of the fused
+ * paths). */
 int mdma_gfx950_set_norm_fusion(mdma_ctx *ctx, int on);
 /* Extra: the int8 mode's prefill GEMM kernel (calls of 64 or more tokens).
  * AUTO (default) takes the f16-path GEMM where it covers the weight (Q4_K

@@ -412,9 +412,15 @@ uint32_t *gemm_counters(mdma_ctx *ctx, uint64_t n) {
 
 void q8_invalidate_range(mdma_ctx *ctx, const void *p, uint64_t bytes) {
   if (!ctx->tiled.empty()) drop_tiles(ctx, p, bytes);  // an op output over a weight's bytes
-  if (!ctx->q8_valid) return;
-  const char *a = static_cast<const char *>(p), *x = reinterpret_cast<const char *>(ctx->q8_x);
-  if (a < x + ctx->q8_n * 4 && x < a + bytes) ctx->q8_valid = false;
+  const char *a = static_cast<const char *>(p);
+  auto over = [&](const void *q, uint64_t n) {
+    const char *b = static_cast<const char *>(q);
+    return a < b + n && b < a + bytes;
+  };
+  if (ctx->q8_valid && over(ctx->q8_x, ctx->q8_n * 4)) ctx->q8_valid = false;
+  if (ctx->a16_valid && (over(ctx->a16_x, ctx->a16_n * 4) ||
+                         over(ctx->a16_buf, gemm_f16_input_bytes(ctx->a16_n / ctx->a16_n_in, ctx->a16_n_in))))
+    ctx->a16_valid = false;
 }
 
 const float *rope_table(mdma_ctx *ctx, uint64_t max_pos, uint64_t hd, float theta) {

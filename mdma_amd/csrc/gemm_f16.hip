@@ -56,7 +56,6 @@ namespace mdma {
 namespace {
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int TN = 128, TM = 128, SK = 64, MAX_BLOCKS = 16384 / 32;
@@ -926,6 +925,33 @@ uint64_t gemm_f16_input_bytes(uint64_t M, uint64_t K) {
   return r256(M * K * 2) + r256(M * (K / 32) * 4) + 2 * r256(M * (K / 32) * 2) + r256(M * 4);
 }
 
+F16In gemm_f16_input_at(char *s, uint64_t M, uint64_t K) {
+  const uint64_t nb = K / 32;
+  F16In in;
+  in.xh = reinterpret_cast<_Float16 *>(s);
+  s += r256(M * K * 2);
+  in.sx = reinterpret_cast<float *>(s);
+  s += r256(M * nb * 4);
+  in.ph = reinterpret_cast<_Float16 *>(s);
+  s += r256(M * nb * 2);
+  in.pl = reinterpret_cast<_Float16 *>(s);
+  s += r256(M * nb * 2);
+  in.inv = reinterpret_cast<float *>(s);
+  return in;
+}
+
+void a16_mark(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in, char *buf) {
+  ctx->a16_valid = true;
+  ctx->a16_x = x;
+  ctx->a16_buf = buf;
+  ctx->a16_n = T * n_in;
+  ctx->a16_n_in = n_in;
+}
+
+bool a16_holds(const mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in) {
+  return ctx->a16_valid && ctx->a16_x == x && ctx->a16_n == T * n_in && ctx->a16_n_in == n_in;
+}
+
 namespace {
 // Splits of K for a launch of few output tiles (few weight rows): enough
 // workgroups for two per CU, whole super-blocks, at least two per split.
@@ -1014,19 +1040,16 @@ bool gemm_f16_glu_ok(const GemvJob &gate, const GemvJob &up) {
 }
 
 void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t M, char *s,
-                     float *part, uint64_t part_bytes, uint32_t *cnt, uint64_t counters, float *glu_y) {
+                     float *part, uint64_t part_bytes, uint32_t *cnt, uint64_t counters, float *glu_y,
+                     bool have_input) {
   const uint64_t K = jobs[0].n_in, nb = K / 32;
-  _Float16 *xh = reinterpret_cast<_Float16 *>(s);
-  s += r256(M * K * 2);
-  float *sx = reinterpret_cast<float *>(s);
-  s += r256(M * nb * 4);
-  _Float16 *ph = reinterpret_cast<_Float16 *>(s);
-  s += r256(M * nb * 2);
-  _Float16 *pl = reinterpret_cast<_Float16 *>(s);
-  s += r256(M * nb * 2);
-  float *inv = reinterpret_cast<float *>(s);
-  gemm_act_kernel<<<dim3((uint32_t)M), dim3(256), 0, ctx->stream>>>(x, (uint32_t)K, xh, sx, ph, pl, inv);
-  hip_check(hipGetLastError(), "gemm activation launch");
+  const F16In in = gemm_f16_input_at(s, M, K);
+  _Float16 *xh = in.xh, *ph = in.ph, *pl = in.pl;
+  float *sx = in.sx, *inv = in.inv;
+  if (!have_input) {
+    gemm_act_kernel<<<dim3((uint32_t)M), dim3(256), 0, ctx->stream>>>(x, (uint32_t)K, xh, sx, ph, pl, inv);
+    hip_check(hipGetLastError(), "gemm activation launch");
+  }
   // Token rows per launch: activation offsets are 32-bit inside the kernel.
   const uint64_t rows = rows_per_launch(K);
   hipEvent_t t0 = ctx->time_start, t1 = ctx->time_stop;

@@ -904,7 +904,9 @@ static bool try_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const f
     if (!gemm_f16_supported(jobs[i].dtype, jobs[i].layout, jobs[i].n_in, jobs[i].n_out) ||
         jobs[i].n_in != jobs[0].n_in || (jobs[i].dtype == DT_Q6_K && jobs[i].dots))
       return false;  // (Q6_K block-dot capture: the int8 GEMM's per-16 dots)
-  const uint64_t need = (gemm_f16_input_bytes(T, jobs[0].n_in) + 255) / 256 * 256;
+  // x's input already written by a fused rmsnorm (launch_rmsnorm_a16)?
+  const bool pre = !ctx->fixed_scratch && a16_holds(ctx, x, T, jobs[0].n_in);
+  const uint64_t need = pre ? 0 : (gemm_f16_input_bytes(T, jobs[0].n_in) + 255) / 256 * 256;
   // Split-K partials (launches run one after another and share them).
   uint64_t nc = 0, pb = gemm_f16_split_bytes(ctx, jobs, n_jobs, T, &nc);
   char *s;
@@ -918,8 +920,8 @@ static bool try_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const f
     s = scratch(ctx, need + pb);
   }
   uint32_t *cnt = pb && nc ? gemm_counters(ctx, nc) : nullptr;
-  launch_gemm_f16(ctx, jobs, n_jobs, x, T, s, cnt ? reinterpret_cast<float *>(s + need) : nullptr, cnt ? pb : 0, cnt,
-                  cnt ? nc : 0, glu_y);
+  launch_gemm_f16(ctx, jobs, n_jobs, x, T, pre ? ctx->a16_buf : s, cnt ? reinterpret_cast<float *>(s + need) : nullptr,
+                  cnt ? pb : 0, cnt, cnt ? nc : 0, glu_y, pre);
   return true;
 }
 

@@ -95,6 +95,12 @@ struct mdma_ctx {
   bool q8_valid = false;
   const float *q8_x = nullptr;
   uint64_t q8_n = 0, q8_n_in = 0;
+  // The f16-path GEMM's input for x [a16_n / a16_n_in, a16_n_in], written by
+  // a fused prefill rmsnorm into a16_buf (a caller's buffer), while valid.
+  bool a16_valid = false;
+  const float *a16_x = nullptr;
+  char *a16_buf = nullptr;
+  uint64_t a16_n = 0, a16_n_in = 0;
   // Device RoPE cos/sin table: [positions][head_dim/2] for one (head_dim, theta).
   float *rope_tab = nullptr;
   uint64_t rope_bytes = 0;
@@ -195,7 +201,7 @@ uint32_t *attn_counters(mdma_ctx *ctx, uint64_t n);
 uint32_t *gemm_counters(mdma_ctx *ctx, uint64_t n);
 // Forget the cached int8 activations: every entry point that writes device
 // memory calls this (a qmatmul only when its output overlaps the cached x).
-inline void q8_invalidate(mdma_ctx *ctx) { ctx->q8_valid = false; }
+inline void q8_invalidate(mdma_ctx *ctx) { ctx->q8_valid = ctx->a16_valid = false; }
 void q8_invalidate_range(mdma_ctx *ctx, const void *p, uint64_t bytes);
 // Device pointer to a cos/sin table covering positions [0, max_pos] for (hd, theta).
 const float *rope_table(mdma_ctx *ctx, uint64_t max_pos, uint64_t hd, float theta);
@@ -329,14 +335,31 @@ constexpr uint64_t GEMM_MIN_TOKENS = 64;
 // launch (quantization prologue, then each job's GEMM) with that scratch.
 bool gemm_f16_supported(int32_t dtype, int layout, uint64_t n_in, uint64_t n_out);
 uint64_t gemm_f16_input_bytes(uint64_t M, uint64_t K);
+// The input's parts in gemm_f16_input_bytes(M, K) bytes at s: the int8
+// values as f16 [M, K], per-32 scales [M, K/32], P's f16 halves [M, K/32]
+// each, and each row's 2^-e [M].
+struct F16In {
+  _Float16 *xh;
+  float *sx;
+  _Float16 *ph, *pl;
+  float *inv;
+};
+F16In gemm_f16_input_at(char *s, uint64_t M, uint64_t K);
+// The context's record of a fused rmsnorm's f16-path GEMM input for x, and
+// whether it holds x [T, n_in].
+void a16_mark(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in, char *buf);
+bool a16_holds(const mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in);
 // Split-K partials the f16-path launches of these jobs over M tokens take
 // (bytes; 0 = unsplit) and the arrival counters they need (*tiles).
 uint64_t gemm_f16_split_bytes(const mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, uint64_t M, uint64_t *tiles);
 // glu_y: jobs are (gate, up) passing gemm_f16_glu_ok; one gated launch
 // writes silu(gate) * up to glu_y (the jobs' own outputs are not written).
 bool gemm_f16_glu_ok(const GemvJob &gate, const GemvJob &up);
+// have_input: scratch already holds x's input (gemm_f16_input_at), so the
+// quantization prologue is not launched.
 void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t M, char *scratch,
-                     float *part, uint64_t part_bytes, uint32_t *cnt, uint64_t counters, float *glu_y = nullptr);
+                     float *part, uint64_t part_bytes, uint32_t *cnt, uint64_t counters, float *glu_y = nullptr,
+                     bool have_input = false);
 void launch_quantize_act(mdma_ctx *ctx, const float *x, uint64_t n, uint64_t group, int8_t *q,
                          float *d, int32_t *sum16);
 void launch_block_dot(mdma_ctx *ctx, const GemvJob &w, const int8_t *qx, uint64_t T, int32_t *out);
@@ -352,6 +375,13 @@ void launch_rmsnorm(mdma_ctx *ctx, const float *w, uint64_t dim, const float *a,
 // whole groups of 256 or exceeds 16384.
 bool launch_rmsnorm_q8(mdma_ctx *ctx, const float *w, uint64_t dim, const float *a, const float *b, float *sum,
                        float *y, uint64_t rows, float eps);
+// rmsnorm that also writes the f16-path GEMM's input for y (the bits its
+// quantization prologue would write) into buf and records it, so the GEMM
+// that reads y next skips that prologue. False, launching nothing, when dim
+// is not whole blocks of 32, exceeds 16384, or buf is smaller than
+// gemm_f16_input_bytes(rows, dim).
+bool launch_rmsnorm_a16(mdma_ctx *ctx, const float *w, uint64_t dim, const float *a, const float *b, float *sum,
+                        float *y, uint64_t rows, float eps, char *buf, uint64_t buf_bytes);
 void launch_add(mdma_ctx *ctx, const float *a, const float *b, float *y, uint64_t n);
 void launch_silu_mul(mdma_ctx *ctx, const float *g, const float *u, float *y, uint64_t n);
 // pos_dev (a captured decode step, one position): the position is read from

@@ -73,6 +73,8 @@ __device__ __forceinline__ GridTile grid_tile(uint32_t gt) {
   return GridTile{r / gn, y0 + r % gn};
 }
 
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+
 // silu_mul of one element (cpu.rs:447-458): (g / (1 + exp(-g))) * u, each
 // operation rounded on its own (no contraction), the device expf. The
 // elementwise kernel and the prefill GEMM's fused gate/up epilogue share it,

@@ -424,9 +424,25 @@ void run_layers(mdma_session *s, uint64_t T, uint32_t pos, uint64_t seq, bool ba
   // rmsnorm that produces them (prefill-sized ones go to the int8 GEMM,
   // which quantizes per 32 itself).
   const bool fuse_q8 = ctx->act_mode == MDMA_ACT_I8 && T < GEMM_MIN_TOKENS;
-  auto norm = [&](const mdma_buf *w, const float *a, const float *b, float *sum) {
+  // Prefill rows in the int8 mode whose GEMMs (cons) run on the f16 path:
+  // the rmsnorm also writes those GEMMs' input, into attn_out (not in use
+  // from the norm to the GEMMs that read it), and the GEMMs skip their own
+  // quantization pass.
+  auto a16_for = [&](const GemvJob *cons, int n) {
+    if (!cons || !ctx->norm_fusion || ctx->act_mode != MDMA_ACT_I8 || ctx->prefill_kernel != MDMA_PREFILL_AUTO ||
+        T < GEMM_MIN_TOKENS || ctx->fixed_scratch || ctx->capturing)
+      return false;
+    for (int i = 0; i < n; i++)
+      if (!gemm_f16_supported(cons[i].dtype, cons[i].layout, cons[i].n_in, cons[i].n_out)) return false;
+    return true;
+  };
+  auto norm = [&](const mdma_buf *w, const float *a, const float *b, float *sum, const GemvJob *cons = nullptr,
+                  int n_cons = 0) {
     q8_invalidate(ctx);
     if (fuse_q8 && launch_rmsnorm_q8(ctx, fp(w), E, a, b, sum, fp(s->normed), T, c.rms_eps)) return true;
+    if (a16_for(cons, n_cons) && launch_rmsnorm_a16(ctx, fp(w), E, a, b, sum, fp(s->normed), T, c.rms_eps,
+                                                    s->attn_out->ptr, s->attn_out->len))
+      return true;
     rmsnorm(ctx, fp(w), E, a, b, sum, fp(s->normed), T, c.rms_eps);
     return false;
   };
@@ -466,13 +482,13 @@ void run_layers(mdma_session *s, uint64_t T, uint32_t pos, uint64_t seq, bool ba
     GemvJob qkv[3] = {L.wq.job(fp(s->q)), L.wk.job(fp(s->k)), L.wv.job(fp(s->v))};
     bool qkv_done = false;
     if (i == 0) {
-      fresh = norm(L.attn_norm, fp(x), nullptr, nullptr);
+      fresh = norm(L.attn_norm, fp(x), nullptr, nullptr, qkv, 3);
     } else if (n_part) {
       q8_invalidate(ctx);
       qkv_done = launch_gemv_i8_normed(ctx, qkv, 3, fp(x), fp(L.attn_norm), n_part, c.rms_eps);
-      if (!qkv_done) fresh = norm(L.attn_norm, fp(x), nullptr, nullptr);
+      if (!qkv_done) fresh = norm(L.attn_norm, fp(x), nullptr, nullptr, qkv, 3);
     } else {
-      fresh = norm(L.attn_norm, fp(x), fp(s->proj), fp(x_alt));
+      fresh = norm(L.attn_norm, fp(x), fp(s->proj), fp(x_alt), qkv, 3);
       std::swap(x, x_alt);
     }
     if (!qkv_done) gemv(ctx, qkv, 3, fp(s->normed), T, fresh);
@@ -502,9 +518,10 @@ void run_layers(mdma_session *s, uint64_t T, uint32_t pos, uint64_t seq, bool ba
     }
     GemvJob wo = L.wo.job(fp(s->proj));
     gemv(ctx, &wo, 1, fp(s->attn_out), T, fresh);
-    fresh = norm(L.ffn_norm, fp(x), fp(s->proj), fp(x_alt));
+    const GemvJob gu[2] = {L.gate.job(fp(s->gate)), L.up.job(fp(s->up))};
+    fresh = norm(L.ffn_norm, fp(x), fp(s->proj), fp(x_alt), gu, 2);
     std::swap(x, x_alt);
-    gemv_gated(ctx, L.gate.job(fp(s->gate)), L.up.job(fp(s->up)), fp(s->normed), T, fp(s->act), fresh);
+    gemv_gated(ctx, gu[0], gu[1], fp(s->normed), T, fp(s->act), fresh);
     n_part = 0;
     if (fuse_norm) {
       // y = x + W act into the other residual buffer (the new stream).

@@ -154,13 +154,16 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ 
 // == 0) it also writes y's int8 form for the int8-activation GEMV: groups of
 // 256 (one wave each), d = amax/127, q = round-half-away(y*127/amax), exact
 // sums of 16 -- the arithmetic of quantize_act_kernel, so the result is the
-// same bit for bit.
-template <bool QUANT>
+// same bit for bit. With A16 (dim % 32 == 0) it writes instead the f16-path
+// GEMM's input for y, with gemm_act_kernel's arithmetic (the same bits): per
+// 32 columns (8 lanes) the int8 values as f16 and s = amax/127, and P = s *
+// their sum as f16 halves scaled by 2^e, e from the row's largest |P|.
+template <bool QUANT, bool A16 = false>
 __global__ __launch_bounds__(1024) void rmsnorm_row_kernel(const float *__restrict__ w, uint32_t dim,
                                                            const float *__restrict__ a, const float *__restrict__ b,
                                                            float *__restrict__ sum, float *__restrict__ y, float eps,
                                                            int8_t *__restrict__ q, float *__restrict__ qd,
-                                                           int32_t *__restrict__ qs16) {
+                                                           int32_t *__restrict__ qs16, F16In in = {}) {
 #pragma clang fp contract(off)
   __shared__ double sh[16];
   const size_t base = (size_t)blockIdx.x * dim;
@@ -168,6 +171,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_row_kernel(const float *__restri
   float v[4][4];
   float4 wv[4];
   double ss = 0.0;
+  float pc[4] = {0.f, 0.f, 0.f, 0.f}, pmax = 0.f;  // A16: each block's P, their maximum |P|
 #pragma unroll
   for (int c = 0; c < 4; c++) {
     const uint32_t i = 4 * t + 4096 * c;
@@ -224,6 +228,55 @@ __global__ __launch_bounds__(1024) void rmsnorm_row_kernel(const float *__restri
       if ((lane & 3) == 0) qs16[(base + i) / 16] = sm;
       if (lane == 0) qd[(base + i) / 256] = amax / 127.0f;
     }
+    if (A16) {  // 8 lanes hold a 32-column block
+      float am = fmaxf(fmaxf(fabsf(r[0]), fabsf(r[1])), fmaxf(fabsf(r[2]), fabsf(r[3])));
+      am = dpp_max<0xB1, 0xF>(am);
+      am = dpp_max<0x4E, 0xF>(am);
+      am = dpp_max<0x141, 0xF>(am);
+      const float iv = am == 0.f ? 0.f : 127.0f / am;
+      int qi[4], sm = 0;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        qi[k] = q8_quant(r[k], iv);
+        sm += qi[k];
+      }
+      sm += (int)dpp_u32<0xB1, 0xF>((uint32_t)sm);
+      sm += (int)dpp_u32<0x4E, 0xF>((uint32_t)sm);
+      sm += (int)dpp_u32<0x141, 0xF>((uint32_t)sm);
+      const float s = am / 127.0f;
+      pc[c] = s * (float)sm;
+      pmax = fmaxf(pmax, fabsf(pc[c]));
+      const v4h h = {(_Float16)(float)qi[0], (_Float16)(float)qi[1], (_Float16)(float)qi[2], (_Float16)(float)qi[3]};
+      *reinterpret_cast<v4h *>(in.xh + base + i) = h;
+      if ((lane & 7) == 0) in.sx[(base + i) / 32] = s;
+    }
+  }
+  if (A16) {
+    // e brings the row's largest |P| into [512, 1024).
+    __shared__ float pw[16];
+    pmax = wave_max_all(pmax);
+    if (lane == 0) pw[wave] = pmax;
+    __syncthreads();
+    float pm = 0.f;
+    for (int k = 0; k < 16; k++) pm = fmaxf(pm, pw[k]);
+    int e = 0;
+    if (pm > 0.f) {
+      int ex;
+      frexpf(pm, &ex);
+      e = min(max(10 - ex, -100), 100);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const uint32_t i = 4 * t + 4096 * c;
+      if (i >= dim) break;
+      if ((lane & 7) == 0) {
+        const float pe = ldexpf(pc[c], e);
+        const _Float16 hi = (_Float16)pe;
+        in.ph[(base + i) / 32] = hi;
+        in.pl[(base + i) / 32] = (_Float16)(pe - (float)hi);
+      }
+    }
+    if (t == 0) in.inv[blockIdx.x] = ldexpf(1.0f, -e);
   }
 }
 
@@ -1315,6 +1368,17 @@ void launch_rmsnorm(mdma_ctx *ctx, const float *w, uint64_t dim, const float *a,
   else
     rmsnorm_kernel<<<dim3((uint32_t)rows), dim3(256), 0, ctx->stream>>>(w, (uint32_t)dim, a, b, sum, y, eps);
   hip_check(hipGetLastError(), "rmsnorm launch");
+}
+
+bool launch_rmsnorm_a16(mdma_ctx *ctx, const float *w, uint64_t dim, const float *a, const float *b, float *sum,
+                        float *y, uint64_t rows, float eps, char *buf, uint64_t buf_bytes) {
+  if (dim % 32 || dim > 16384 || !buf || buf_bytes < gemm_f16_input_bytes(rows, dim)) return false;
+  const F16In in = gemm_f16_input_at(buf, rows, dim);
+  rmsnorm_row_kernel<false, true><<<dim3((uint32_t)rows), dim3(1024), 0, ctx->stream>>>(
+      w, (uint32_t)dim, a, b, sum, y, eps, nullptr, nullptr, nullptr, in);
+  hip_check(hipGetLastError(), "rmsnorm launch");
+  a16_mark(ctx, y, rows, dim, buf);
+  return true;
 }
 
 bool launch_rmsnorm_q8(mdma_ctx *ctx, const float *w, uint64_t dim, const float *a, const float *b, float *sum,

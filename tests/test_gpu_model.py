@@ -181,6 +181,33 @@ def test_int8_decode_norm_fusion_matches_separate_norm(backend, gqa):
     assert np.array_equal(fused.argmax(axis=1), sep.argmax(axis=1))
 
 
+def test_int8_prefill_norm_fusion_same_bits(backend, gqa_long):
+    """Prefill rows of 64 tokens and more in the int8 mode: the rmsnorms ahead
+    of the QKV and gate/up GEMMs also write those GEMMs' f16-path input (the
+    per-32 int8 values as f16, their scales and P halves), and the GEMMs
+    take it instead of quantizing the normed rows themselves. The rmsnorm
+    computes it with the quantization pass's arithmetic, so the prefill
+    logits with the fusion on are those with it off, bit for bit, over a
+    prompt that spans two token tiles."""
+    backend.set_act_mode(ACT_I8)
+    p = synth.tokens(200, 2048, 2200)
+    runs = []
+    try:
+        m = Model(backend, gqa_long)
+        for fused in (True, False):
+            backend.set_norm_fusion(fused)
+            s = m.session(208, 1, 200)
+            runs.append(s.prefill(p, 0))
+            s.close()
+        m.close()
+    finally:
+        backend.set_norm_fusion(True)
+        backend.set_act_mode(ACT_F32)
+    fused, sep = runs
+    assert np.all(np.isfinite(fused))
+    assert np.array_equal(fused.view(np.uint32), sep.view(np.uint32))
+
+
 # int8 mode end to end. The oracle runs the same int8 activation mode (x
 # requantized before every GEMV the device quantizes for; the reference's
 # "requantize, then CPU qmatmul" pattern, src/backend/rocm/decode/tests.rs:68-77).
