@@ -148,10 +148,10 @@ int mdma_gfx950_set_act_mode(mdma_ctx *ctx, int mode);
  * RMSNorm into the GEMVs around it (the down projection stores the residual
  * stream and sums of squares, the QKV GEMV normalizes in its prologue); in
  * the Llama driver's prefill (64 tokens and up), have the RMSNorms ahead of
- * the QKV and gate/up GEMMs write those GEMMs' input, so the GEMMs skip
- * their own quantization pass (the same bits). Default on; off runs the
- * separate kernels (for A/B measurement and the parity tests of the fused
- * paths). */
+ * the QKV and gate/up GEMMs, and the gated GEMM ahead of a Q6_K down
+ * projection, write those GEMMs' input, so the GEMMs skip their own
+ * quantization pass (the same bits). Default on; off runs the separate
+ * kernels (for A/B measurement and the parity tests of the fused paths). */
 int mdma_gfx950_set_norm_fusion(mdma_ctx *ctx, int on);
 /* Extra: the int8 mode's prefill GEMM kernel (calls of 64 or more tokens).
  * AUTO (default) takes the f16-path GEMM where it covers the weight (Q4_K

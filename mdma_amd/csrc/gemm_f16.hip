@@ -158,8 +158,12 @@ struct F16Args {
   float *jy[3];
   uint32_t jn[3], jt[3];
   // Gated launch (gemm_f16_kernel's GLU instantiation): jw[0] gate, jw[1]
-  // up, both N rows; glu_y [M, N] receives silu(gate) * up.
+  // up, both N rows; glu_y [M, N] receives silu(gate) * up. glu_in.xh set:
+  // the epilogue also writes the f16-path GEMM input of that output for a
+  // GEMM that reads no min-term sums (Q6_K): per 32 columns the int8
+  // values as f16 and the scale (xh, sx; gemm_act_kernel's arithmetic).
   float *glu_y;
+  F16In glu_in;
 };
 
 // The workgroup's weight of a fused launch (static indices: the values
@@ -468,17 +472,41 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
   }
   if (gridDim.z > 1 && !f16_split_merge(acc, a)) return;
   if constexpr (GLU) {  // silu(gate) * up; the launcher keeps N a multiple of 128
+    // A token's (lane l16's) 32 columns bn + wn / 2 + [0, 32) are one
+    // quantization block: 8 values in each of the lanes l16 + 16 lq.
+    const bool q = a.glu_in.xh != nullptr;  // uniform
+    const uint32_t n0 = bn + (wn >> 1);
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       const uint32_t m = bm + wm + 16 * j + l16;
-      if (m >= a.M) continue;
+      float h[2][4];
 #pragma unroll
       for (int i = 0; i < 2; i++) {
-        const uint32_t n = bn + (wn >> 1) + 16 * i + 4 * lq;
-        float h[4];
+        const uint32_t n = n0 + 16 * i + 4 * lq;
 #pragma unroll
-        for (int r = 0; r < 4; r++) h[r] = silu_mul1(acc[i][j][r], acc[i + 2][j][r]);
-        *reinterpret_cast<float4 *>(a.glu_y + (size_t)m * N + n) = make_float4(h[0], h[1], h[2], h[3]);
+        for (int r = 0; r < 4; r++) h[i][r] = silu_mul1(acc[i][j][r], acc[i + 2][j][r]);
+        if (m < a.M)
+          *reinterpret_cast<float4 *>(a.glu_y + (size_t)m * N + n) = make_float4(h[i][0], h[i][1], h[i][2], h[i][3]);
+      }
+      if (q) {
+#pragma clang fp contract(off)
+        float am = 0.f;
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) am = fmaxf(am, fabsf(h[i][r]));
+        am = fmaxf(am, __shfl_xor(am, 16));
+        am = fmaxf(am, __shfl_xor(am, 32));
+        const float iv = am == 0.f ? 0.f : 127.0f / am;
+        if (m < a.M) {
+#pragma unroll
+          for (int i = 0; i < 2; i++) {
+            const v4h hv = {(_Float16)(float)q8_quant(h[i][0], iv), (_Float16)(float)q8_quant(h[i][1], iv),
+                            (_Float16)(float)q8_quant(h[i][2], iv), (_Float16)(float)q8_quant(h[i][3], iv)};
+            *reinterpret_cast<v4h *>(a.glu_in.xh + (size_t)m * N + n0 + 16 * i + 4 * lq) = hv;
+          }
+          if (lq == 0) a.glu_in.sx[(size_t)m * (N / 32) + n0 / 32] = am / 127.0f;
+        }
       }
     }
     return;
@@ -940,8 +968,9 @@ F16In gemm_f16_input_at(char *s, uint64_t M, uint64_t K) {
   return in;
 }
 
-void a16_mark(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in, char *buf) {
+void a16_mark(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in, char *buf, bool with_p) {
   ctx->a16_valid = true;
+  ctx->a16_p = with_p;
   ctx->a16_x = x;
   ctx->a16_buf = buf;
   ctx->a16_n = T * n_in;
@@ -1058,6 +1087,10 @@ void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float
   const int groups = fused ? 1 : n_jobs;
   const bool glu = glu_y != nullptr;
   if (glu && (n_jobs != 2 || !gemm_f16_glu_ok(jobs[0], jobs[1]))) fail(MDMA_ERR_BACKEND, "gated GEMM: jobs not fusable");
+  // A request (a16_want) for the gated output's GEMM input (no min-term
+  // sums) in the caller's buffer.
+  const bool want = glu && ctx->a16_want_y == glu_y && ctx->a16_want_bytes >= gemm_f16_input_bytes(M, jobs[0].n_out);
+  const F16In want_in = want ? gemm_f16_input_at(ctx->a16_want_buf, M, jobs[0].n_out) : F16In{};
   for (int g = 0; g < groups; g++) {
     const GemvJob *gj = fused ? jobs : jobs + g;
     const int nj = fused ? n_jobs : 1;
@@ -1075,6 +1108,11 @@ void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float
                 (uint32_t)Mc, (uint32_t)w.n_out, (uint32_t)K, gfx950_row_bytes(w.dtype, K),
                 w.dots ? w.dots + m0 * w.n_out * (K / 32) : nullptr, sp.S > 1 ? part : nullptr,
                 sp.S > 1 ? cnt : nullptr, sp.sbs, (uint32_t)nj, {}, {}, {}, {}, glu ? glu_y + m0 * w.n_out : nullptr};
+      if (glu && want) {
+        a.glu_in = want_in;
+        a.glu_in.xh += m0 * w.n_out;
+        a.glu_in.sx += m0 * (w.n_out / 32);
+      }
       uint32_t first = 0;
       for (int j = 0; j < nj; j++) {
         a.jw[j] = gj[j].w;
@@ -1103,6 +1141,7 @@ void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float
       hip_check(hipGetLastError(), "gemm f16 launch");
     }
   }
+  if (want) a16_mark(ctx, glu_y, M, jobs[0].n_out, ctx->a16_want_buf, false);
 }
 
 }  // namespace mdma

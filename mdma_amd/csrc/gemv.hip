@@ -905,7 +905,9 @@ static bool try_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const f
         jobs[i].n_in != jobs[0].n_in || (jobs[i].dtype == DT_Q6_K && jobs[i].dots))
       return false;  // (Q6_K block-dot capture: the int8 GEMM's per-16 dots)
   // x's input already written by a fused rmsnorm (launch_rmsnorm_a16)?
-  const bool pre = !ctx->fixed_scratch && a16_holds(ctx, x, T, jobs[0].n_in);
+  bool pre = !ctx->fixed_scratch && a16_holds(ctx, x, T, jobs[0].n_in);
+  for (int i = 0; i < n_jobs && pre; i++)
+    if (jobs[i].dtype == DT_Q4_K && !ctx->a16_p) pre = false;  // the min term reads P
   const uint64_t need = pre ? 0 : (gemm_f16_input_bytes(T, jobs[0].n_in) + 255) / 256 * 256;
   // Split-K partials (launches run one after another and share them).
   uint64_t nc = 0, pb = gemm_f16_split_bytes(ctx, jobs, n_jobs, T, &nc);

@@ -97,10 +97,16 @@ struct mdma_ctx {
   uint64_t q8_n = 0, q8_n_in = 0;
   // The f16-path GEMM's input for x [a16_n / a16_n_in, a16_n_in], written by
   // a fused prefill rmsnorm into a16_buf (a caller's buffer), while valid.
-  bool a16_valid = false;
+  // a16_p: with the Q4_K min term's P halves and row exponents.
+  bool a16_valid = false, a16_p = false;
   const float *a16_x = nullptr;
   char *a16_buf = nullptr;
   uint64_t a16_n = 0, a16_n_in = 0;
+  // A request to the gated prefill GEMM producing a16_want_y: also write
+  // its output's input for a Q6_K GEMM into a16_want_buf (and record it).
+  const float *a16_want_y = nullptr;
+  char *a16_want_buf = nullptr;
+  uint64_t a16_want_bytes = 0;
   // Device RoPE cos/sin table: [positions][head_dim/2] for one (head_dim, theta).
   float *rope_tab = nullptr;
   uint64_t rope_bytes = 0;
@@ -347,7 +353,7 @@ struct F16In {
 F16In gemm_f16_input_at(char *s, uint64_t M, uint64_t K);
 // The context's record of a fused rmsnorm's f16-path GEMM input for x, and
 // whether it holds x [T, n_in].
-void a16_mark(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in, char *buf);
+void a16_mark(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in, char *buf, bool with_p);
 bool a16_holds(const mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in);
 // Split-K partials the f16-path launches of these jobs over M tokens take
 // (bytes; 0 = unsplit) and the arrival counters they need (*tiles).

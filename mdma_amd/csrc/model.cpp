@@ -521,7 +521,16 @@ void run_layers(mdma_session *s, uint64_t T, uint32_t pos, uint64_t seq, bool ba
     const GemvJob gu[2] = {L.gate.job(fp(s->gate)), L.up.job(fp(s->up))};
     fresh = norm(L.ffn_norm, fp(x), fp(s->proj), fp(x_alt), gu, 2);
     std::swap(x, x_alt);
+    // A Q6_K down projection on the f16 path: the gated GEMM also writes its
+    // input, into the gate buffer (the gated launch does not write it).
+    const GemvJob dn_next = L.down.job(fp(s->proj));
+    if (a16_for(&dn_next, 1) && dn_next.dtype == DT_Q6_K) {
+      ctx->a16_want_y = fp(s->act);
+      ctx->a16_want_buf = s->gate->ptr;
+      ctx->a16_want_bytes = s->gate->len;
+    }
     gemv_gated(ctx, gu[0], gu[1], fp(s->normed), T, fp(s->act), fresh);
+    ctx->a16_want_y = nullptr;
     n_part = 0;
     if (fuse_norm) {
       // y = x + W act into the other residual buffer (the new stream).
@@ -531,7 +540,7 @@ void run_layers(mdma_session *s, uint64_t T, uint32_t pos, uint64_t seq, bool ba
     }
     if (!n_part) {
       GemvJob dn = L.down.job(fp(s->proj));
-      gemv(ctx, &dn, 1, fp(s->act), T);
+      gemv(ctx, &dn, 1, fp(s->act), T, a16_holds(ctx, fp(s->act), T, c.n_ff));
     }
   }
   // The head GEMV quantizes the final-normed rows itself when it needs

@@ -1377,7 +1377,7 @@ bool launch_rmsnorm_a16(mdma_ctx *ctx, const float *w, uint64_t dim, const float
   rmsnorm_row_kernel<false, true><<<dim3((uint32_t)rows), dim3(1024), 0, ctx->stream>>>(
       w, (uint32_t)dim, a, b, sum, y, eps, nullptr, nullptr, nullptr, in);
   hip_check(hipGetLastError(), "rmsnorm launch");
-  a16_mark(ctx, y, rows, dim, buf);
+  a16_mark(ctx, y, rows, dim, buf, true);
   return true;
 }
 
