@@ -514,10 +514,19 @@ void run_layers(mdma_session *s, uint64_t T, uint32_t pos, uint64_t seq, bool ba
       uint16_t *ks = kb + seq * cache_stride, *vs = vb + seq * cache_stride;
       launch_rope_kv_write(ctx, fp(s->q), c.n_heads, fp(s->k), fp(s->v), c.n_kv_heads, hd, T, tab, pos,
                            ks + pos * kvw, vs + pos * kvw);
+      // A prompt's attention can also write a Q6_K output projection's
+      // f16-path input, into up (free until the gate/up GEMM).
+      const GemvJob wo_in = L.wo.job(fp(s->proj));
+      if (a16_for(&wo_in, 1) && wo_in.dtype == DT_Q6_K) {
+        ctx->a16_want_y = fp(s->attn_out);
+        ctx->a16_want_buf = s->up->ptr;
+        ctx->a16_want_bytes = s->up->len;
+      }
       attend(ks, vs, T, pos + T, 0);
+      ctx->a16_want_y = nullptr;
     }
     GemvJob wo = L.wo.job(fp(s->proj));
-    gemv(ctx, &wo, 1, fp(s->attn_out), T, fresh);
+    gemv(ctx, &wo, 1, fp(s->attn_out), T, fresh || a16_holds(ctx, fp(s->attn_out), T, c.n_heads * hd));
     const GemvJob gu[2] = {L.gate.job(fp(s->gate)), L.up.job(fp(s->up))};
     fresh = norm(L.ffn_norm, fp(x), fp(s->proj), fp(x_alt), gu, 2);
     std::swap(x, x_alt);

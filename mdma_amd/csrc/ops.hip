@@ -478,6 +478,9 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q, 
 // arrival order) and writes O / l. Chunk 0 holds key 0, which every row
 // sees, so the merged maximum is finite; a later chunk's fully masked row
 // contributes nothing.
+// in.xh set: the writer of O / l also writes the output projection's
+// f16-path input (per 32 dims of a row the int8 values as f16 and
+// amax / 127, the gemm_f16 quantization pass's arithmetic), no P halves.
 constexpr uint32_t ATT_PREFILL_MIN = 64;
 
 typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
@@ -513,7 +516,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
                                                            const uint16_t *__restrict__ V, float *__restrict__ o,
                                                            uint32_t n_q, uint32_t prefix, uint32_t n_q_heads,
                                                            uint32_t n_kv_heads, float scale, uint32_t ct,
-                                                           float *__restrict__ part, uint32_t *__restrict__ cnt) {
+                                                           float *__restrict__ part, uint32_t *__restrict__ cnt,
+                                                           F16In in) {
   constexpr int QT = 64 / G;             // queries per workgroup
   constexpr int NC = HD / 32;            // 32-dim K steps of S
   constexpr int ND = HD / 16;            // 16-dim blocks of O
@@ -750,13 +754,34 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
 #pragma unroll
     for (int n = 0; n < ND; n++) O[n] = OA[n];
   }
+  const bool qo = in.xh != nullptr;  // uniform
+  const uint32_t KO = n_q_heads * HD;
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     const uint32_t r = 16 * wave + 4 * lq + j, qi = q0 + r / G, h = kvh * G + r % G;
+    float val[ND];
+#pragma unroll
+    for (int n = 0; n < ND; n++) val[n] = O[n][j] / l[j];
+    if (qo) {
+      // The output projection's f16-path input (gemm_act_kernel's arithmetic):
+      // dims 32 b + [0, 32) of row (qi, h) are one quantization block, dims
+      // 2 b and 2 b + 1 of the 16 lanes that hold the row.
+#pragma unroll
+      for (int b = 0; b < ND / 2; b++) {
+        const float am = row16_max(fmaxf(fabsf(val[2 * b]), fabsf(val[2 * b + 1])));
+        const float iv = am == 0.f ? 0.f : 127.0f / am;
+        if (qi < n_q) {
+          _Float16 *xr = in.xh + (size_t)qi * KO + h * HD + 32 * b + l16;
+          xr[0] = (_Float16)(float)q8_quant(val[2 * b], iv);
+          xr[16] = (_Float16)(float)q8_quant(val[2 * b + 1], iv);
+          if (l16 == 0) in.sx[(size_t)qi * (KO / 32) + h * (HD / 32) + b] = am / 127.0f;
+        }
+      }
+    }
     if (qi >= n_q) continue;
     float *orow = o + ((size_t)qi * n_q_heads + h) * HD + l16;
 #pragma unroll
-    for (int n = 0; n < ND; n++) orow[16 * n] = O[n][j] / l[j];
+    for (int n = 0; n < ND; n++) orow[16 * n] = val[n];
   }
 }
 
@@ -1470,10 +1495,16 @@ bool attn_impl(mdma_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t
     if (n_ch < 2 || ctx->capturing || ctx->fixed_scratch || pbytes > (256ull << 20)) ct = 0, n_ch = 1;
     float *part = ct ? reinterpret_cast<float *>(scratch(ctx, pbytes)) : nullptr;
     uint32_t *cnt = ct ? attn_counters(ctx, n_kv_heads * nqb) : nullptr;
+    // Asked for (a16_want_y == o): also the output projection's f16-path
+    // input, into the caller's buffer.
+    const uint64_t KO = n_q_heads * hd;
+    const bool want = ctx->a16_want_y == o && ctx->a16_want_bytes >= gemm_f16_input_bytes(n_q, KO);
+    const F16In fin = want ? gemm_f16_input_at(ctx->a16_want_buf, n_q, KO) : F16In{};
     const dim3 grid((uint32_t)n_kv_heads, (uint32_t)nqb, (uint32_t)n_ch);
 #define MDMA_ATTP(GG, HH)                                                                                          \
   attn_prefill_kernel<GG, HH><<<grid, dim3(256), 0, ctx->stream>>>(q, k, v, o, (uint32_t)n_q, pre, (uint32_t)n_q_heads, \
-                                                                   (uint32_t)n_kv_heads, sc, (uint32_t)ct, part, cnt)
+                                                                   (uint32_t)n_kv_heads, sc, (uint32_t)ct, part, cnt, \
+                                                                   fin)
     if (hd == 128) {
       if (GP == 1) MDMA_ATTP(1, 128);
       else if (GP == 2) MDMA_ATTP(2, 128);
@@ -1487,6 +1518,7 @@ bool attn_impl(mdma_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t
     }
 #undef MDMA_ATTP
     hip_check(hipGetLastError(), "attn prefill launch");
+    if (want) a16_mark(ctx, o, n_q, KO, ctx->a16_want_buf, false);
     return true;
   }
   const AttnRope *rope = rope_in && rope_in->k ? rope_in : nullptr;

@@ -184,9 +184,10 @@ def test_int8_decode_norm_fusion_matches_separate_norm(backend, gqa):
 def test_int8_prefill_norm_fusion_same_bits(backend, gqa_long):
     """Prefill rows of 64 tokens and more in the int8 mode: the rmsnorms ahead
     of the QKV and gate/up GEMMs also write those GEMMs' f16-path input (the
-    per-32 int8 values as f16, their scales and P halves), and the GEMMs
-    take it instead of quantizing the normed rows themselves. The rmsnorm
-    computes it with the quantization pass's arithmetic, so the prefill
+    per-32 int8 values as f16, their scales and P halves), the gated GEMM and
+    the attention that of the Q6_K down and output projections (this model's
+    mixture), and the GEMMs take it instead of quantizing their input rows
+    themselves. The writers use the quantization pass's arithmetic, so the prefill
     logits with the fusion on are those with it off, bit for bit, over a
     prompt that spans two token tiles."""
     backend.set_act_mode(ACT_I8)
