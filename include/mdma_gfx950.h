@@ -150,8 +150,9 @@ int mdma_gfx950_set_act_mode(mdma_ctx *ctx, int mode);
  * the Llama driver's prefill (64 tokens and up), have the RMSNorms ahead of
  * the QKV and gate/up GEMMs, the gated GEMM ahead of a Q6_K down projection
  * and the attention ahead of a Q6_K output projection, write those GEMMs'
- * input, so the GEMMs skip their own
- * quantization pass (the same bits). Default on; off runs the separate
+ * input, so the GEMMs skip their own quantization pass, and have a Q6_K QKV
+ * GEMM apply RoPE and write the K/V cache rows (the same bits). Default on;
+ * off runs the separate
  * kernels (for A/B measurement and the parity tests of the fused paths). */
 int mdma_gfx950_set_norm_fusion(mdma_ctx *ctx, int on);
 /* Extra: the int8 mode's prefill GEMM kernel (calls of 64 or more tokens).

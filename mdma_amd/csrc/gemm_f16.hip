@@ -164,6 +164,16 @@ struct F16Args {
   // values as f16 and the scale (xh, sx; gemm_act_kernel's arithmetic).
   float *glu_y;
   F16In glu_in;
+  // Fused QKV of a prompt (rope.tab set; the Q6_K wide kernel): q (job 0)
+  // rotated before its store, k (job 1) rotated and v (job 2) stored as f16
+  // cache rows of token m at m * kv_stride, position pos + m (rope_kv_kernel's
+  // arithmetic), in place of k's and v's f32 outputs.
+  struct {
+    const float *tab;  // [position][hd / 2] (cos, sin)
+    uint16_t *dk, *dv;
+    uint32_t pos, hd;
+    uint64_t kv_stride;
+  } rope;
 };
 
 // The workgroup's weight of a fused launch (static indices: the values
@@ -917,6 +927,8 @@ __global__ __launch_bounds__(512, 1) void gemm_f16_q6w_kernel(F16Args a) {
   }
   if (gridDim.z > 1 && !f16_split_merge<512>(acc, a)) return;
   const bool vec = (J.N & 3) == 0;
+  // The rope epilogue's job: 0 q, 1 k, 2 v; 3 none (uniform).
+  const uint32_t rj = !a.rope.tab ? 3 : J.y == a.jy[0] ? 0 : J.y == a.jy[1] ? 1 : 2;
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     const uint32_t m = bm + wm + 16 * j + l16;
@@ -925,6 +937,25 @@ __global__ __launch_bounds__(512, 1) void gemm_f16_q6w_kernel(F16Args a) {
     for (int i = 0; i < 4; i++) {
       const uint32_t n = bn + wn + 16 * i + 4 * lq;
       float *yp = J.y + (size_t)m * J.N + n;
+      if (rj < 3) {  // N a multiple of hd, hd of 4: the 4 columns are 2 pairs of one head
+        if (n >= J.N) continue;
+        float r[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+        if (rj < 2) {
+          const uint32_t half = a.rope.hd / 2;
+          const float4 cs =
+              *reinterpret_cast<const float4 *>(a.rope.tab + 2 * ((size_t)(a.rope.pos + m) * half + (n % a.rope.hd) / 2));
+          rot(r[0], r[1], cs.x, cs.y);
+          rot(r[2], r[3], cs.z, cs.w);
+        }
+        if (rj == 0) {
+          *reinterpret_cast<float4 *>(yp) = make_float4(r[0], r[1], r[2], r[3]);
+        } else {
+          uint16_t *d = (rj == 1 ? a.rope.dk : a.rope.dv) + (size_t)m * a.rope.kv_stride + n;
+          const v4h h = {(_Float16)r[0], (_Float16)r[1], (_Float16)r[2], (_Float16)r[3]};
+          *reinterpret_cast<v4h *>(d) = h;
+        }
+        continue;
+      }
       if (vec && n + 3 < J.N) {
         *reinterpret_cast<float4 *>(yp) = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
       } else {
@@ -1091,6 +1122,14 @@ void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float
   // sums) in the caller's buffer.
   const bool want = glu && ctx->a16_want_y == glu_y && ctx->a16_want_bytes >= gemm_f16_input_bytes(M, jobs[0].n_out);
   const F16In want_in = want ? gemm_f16_input_at(ctx->a16_want_buf, M, jobs[0].n_out) : F16In{};
+  // A request (rope_want) for RoPE and the K/V cache write in the fused QKV
+  // launch: Q6_K q, k, v in one wide launch per row chunk.
+  const uint32_t rhd = ctx->rope_want_hd;
+  bool rope = fused && n_jobs == 3 && ctx->rope_want_q == jobs[0].y && rhd && rhd % 4 == 0 &&
+              ctx->rope_want_stride % 4 == 0 && jobs[1].n_out == jobs[2].n_out && jobs[1].n_out <= ctx->rope_want_stride;
+  for (int j = 0; rope && j < 3; j++)
+    rope = jobs[j].dtype == DT_Q6_K && !jobs[j].dots && jobs[j].n_out % rhd == 0;
+  for (uint64_t m0 = 0; rope && m0 < M; m0 += rows) rope = f16_shape(jobs[0], std::min(M - m0, rows)).wide;
   for (int g = 0; g < groups; g++) {
     const GemvJob *gj = fused ? jobs : jobs + g;
     const int nj = fused ? n_jobs : 1;
@@ -1108,6 +1147,14 @@ void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float
                 (uint32_t)Mc, (uint32_t)w.n_out, (uint32_t)K, gfx950_row_bytes(w.dtype, K),
                 w.dots ? w.dots + m0 * w.n_out * (K / 32) : nullptr, sp.S > 1 ? part : nullptr,
                 sp.S > 1 ? cnt : nullptr, sp.sbs, (uint32_t)nj, {}, {}, {}, {}, glu ? glu_y + m0 * w.n_out : nullptr};
+      if (rope) {
+        a.rope.tab = ctx->rope_want_tab;
+        a.rope.dk = ctx->rope_want_dk + m0 * ctx->rope_want_stride;
+        a.rope.dv = ctx->rope_want_dv + m0 * ctx->rope_want_stride;
+        a.rope.pos = ctx->rope_want_pos + (uint32_t)m0;
+        a.rope.hd = rhd;
+        a.rope.kv_stride = ctx->rope_want_stride;
+      }
       if (glu && want) {
         a.glu_in = want_in;
         a.glu_in.xh += m0 * w.n_out;
@@ -1142,6 +1189,7 @@ void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float
     }
   }
   if (want) a16_mark(ctx, glu_y, M, jobs[0].n_out, ctx->a16_want_buf, false);
+  if (rope) ctx->rope_done = true;
 }
 
 }  // namespace mdma

@@ -107,6 +107,15 @@ struct mdma_ctx {
   const float *a16_want_y = nullptr;
   char *a16_want_buf = nullptr;
   uint64_t a16_want_bytes = 0;
+  // A request to the fused QKV GEMM of a prompt writing q into rope_want_q:
+  // RoPE on q and k and the k / v cache rows in its epilogue (rope_done set
+  // when a launch took it).
+  const float *rope_want_q = nullptr;
+  const float *rope_want_tab = nullptr;
+  uint16_t *rope_want_dk = nullptr, *rope_want_dv = nullptr;
+  uint32_t rope_want_pos = 0, rope_want_hd = 0;
+  uint64_t rope_want_stride = 0;
+  bool rope_done = false;
   // Device RoPE cos/sin table: [positions][head_dim/2] for one (head_dim, theta).
   float *rope_tab = nullptr;
   uint64_t rope_bytes = 0;

@@ -227,5 +227,13 @@ __device__ __forceinline__ double fma4(uint32_t w, const double *x, double acc) 
   return acc;
 }
 
+// Interleaved-pair rotation (apply_rope, cpu.rs:68-84) of one pair.
+__device__ __forceinline__ void rot(float &x0, float &x1, float c, float s) {
+#pragma clang fp contract(off)
+  const float a = x0 * c, bb = x1 * s, cc = x0 * s, d = x1 * c;
+  x0 = a - bb;
+  x1 = cc + d;
+}
+
 }  // namespace
 }  // namespace mdma

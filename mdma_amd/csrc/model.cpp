@@ -491,9 +491,21 @@ void run_layers(mdma_session *s, uint64_t T, uint32_t pos, uint64_t seq, bool ba
       fresh = norm(L.attn_norm, fp(x), fp(s->proj), fp(x_alt), qkv, 3);
       std::swap(x, x_alt);
     }
-    if (!qkv_done) gemv(ctx, qkv, 3, fp(s->normed), T, fresh);
     // KvCache::rope_write (src/kv_cache.rs:212-244): rotate q, store rotated k and v.
     uint16_t *kb = reinterpret_cast<uint16_t *>(s->kc[i]->ptr), *vb = reinterpret_cast<uint16_t *>(s->vc[i]->ptr);
+    // A prompt's fused QKV GEMM can do that in its epilogue (rope_done).
+    ctx->rope_done = false;
+    if (!qkv_done && !batched && !cpu_order && !pos_dev && T > 1 && a16_for(qkv, 3)) {
+      ctx->rope_want_q = fp(s->q);
+      ctx->rope_want_tab = tab;
+      ctx->rope_want_dk = kb + seq * cache_stride + pos * kvw;
+      ctx->rope_want_dv = vb + seq * cache_stride + pos * kvw;
+      ctx->rope_want_pos = pos;
+      ctx->rope_want_hd = (uint32_t)hd;
+      ctx->rope_want_stride = kvw;
+    }
+    if (!qkv_done) gemv(ctx, qkv, 3, fp(s->normed), T, fresh);
+    ctx->rope_want_q = nullptr;
     if (cpu_order) {
       // The CPU's order: RoPE and the cache write, then attention; a
       // captured step reads the position from device memory in both.
@@ -512,8 +524,9 @@ void run_layers(mdma_session *s, uint64_t T, uint32_t pos, uint64_t seq, bool ba
       attend(kb, vb, T, pos + 1, cache_stride);
     } else {
       uint16_t *ks = kb + seq * cache_stride, *vs = vb + seq * cache_stride;
-      launch_rope_kv_write(ctx, fp(s->q), c.n_heads, fp(s->k), fp(s->v), c.n_kv_heads, hd, T, tab, pos,
-                           ks + pos * kvw, vs + pos * kvw);
+      if (!ctx->rope_done)
+        launch_rope_kv_write(ctx, fp(s->q), c.n_heads, fp(s->k), fp(s->v), c.n_kv_heads, hd, T, tab, pos,
+                             ks + pos * kvw, vs + pos * kvw);
       // A prompt's attention can also write a Q6_K output projection's
       // f16-path input, into up (free until the gate/up GEMM).
       const GemvJob wo_in = L.wo.job(fp(s->proj));

@@ -292,14 +292,6 @@ __global__ void silu_mul_kernel(const float *__restrict__ g, const float *__rest
     y[i] = silu_mul1(g[i], u[i]);
 }
 
-// Interleaved-pair rotation (apply_rope, cpu.rs:68-84) of one pair.
-__device__ __forceinline__ void rot(float &x0, float &x1, float c, float s) {
-#pragma clang fp contract(off)
-  const float a = x0 * c, bb = x1 * s, cc = x0 * s, d = x1 * c;
-  x0 = a - bb;
-  x1 = cc + d;
-}
-
 // x: [n_tokens, heads, hd]; tab: [pos][hd/2] (cos, sin). pos_dev (a
 // captured decode step): the position is read from there.
 __global__ void rope_kernel(float *__restrict__ x, uint32_t heads, uint32_t hd, uint64_t pairs,

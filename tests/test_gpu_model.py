@@ -187,9 +187,11 @@ def test_int8_prefill_norm_fusion_same_bits(backend, gqa_long):
     per-32 int8 values as f16, their scales and P halves), the gated GEMM and
     the attention that of the Q6_K down and output projections (this model's
     mixture), and the GEMMs take it instead of quantizing their input rows
-    themselves. The writers use the quantization pass's arithmetic, so the prefill
-    logits with the fusion on are those with it off, bit for bit, over a
-    prompt that spans two token tiles."""
+    themselves; the fused Q6_K QKV GEMM also applies RoPE and writes the K/V
+    cache rows. The writers use the separate kernels' arithmetic, so the
+    prefill logits with the fusion on are those with it off, bit for bit,
+    over a prompt that spans two token tiles, and so are the next decode
+    steps' (which read the cache the prefill wrote)."""
     backend.set_act_mode(ACT_I8)
     p = synth.tokens(200, 2048, 2200)
     runs = []
@@ -198,7 +200,10 @@ def test_int8_prefill_norm_fusion_same_bits(backend, gqa_long):
         for fused in (True, False):
             backend.set_norm_fusion(fused)
             s = m.session(208, 1, 200)
-            runs.append(s.prefill(p, 0))
+            lg = [s.prefill(p, 0)]
+            for k in range(3):
+                lg.append(s.forward(int(np.argmax(lg[-1])), 200 + k))
+            runs.append(np.stack(lg))
             s.close()
         m.close()
     finally:
