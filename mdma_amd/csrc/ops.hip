@@ -757,15 +757,20 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
     if (qo) {
       // The output projection's f16-path input (gemm_act_kernel's arithmetic):
       // dims 32 b + [0, 32) of row (qi, h) are one quantization block, dims
-      // 2 b and 2 b + 1 of the 16 lanes that hold the row.
+      // 2 b and 2 b + 1 of the 16 lanes that hold the row. Lane pairs swap
+      // halves so that each lane stores one pair of adjacent dims: an even
+      // lane dims l16, l16 + 1, an odd lane dims 15 + l16, 16 + l16.
 #pragma unroll
       for (int b = 0; b < ND / 2; b++) {
         const float am = row16_max(fmaxf(fabsf(val[2 * b]), fabsf(val[2 * b + 1])));
         const float iv = am == 0.f ? 0.f : 127.0f / am;
+        const uint32_t ha = __builtin_bit_cast(uint16_t, (_Float16)(float)q8_quant(val[2 * b], iv));
+        const uint32_t hb = __builtin_bit_cast(uint16_t, (_Float16)(float)q8_quant(val[2 * b + 1], iv));
+        const uint32_t na = dpp_u32<0xB1, 0xF>(ha), nb = dpp_u32<0xB1, 0xF>(hb);  // lane l16 ^ 1's
         if (qi < n_q) {
-          _Float16 *xr = in.xh + (size_t)qi * KO + h * HD + 32 * b + l16;
-          xr[0] = (_Float16)(float)q8_quant(val[2 * b], iv);
-          xr[16] = (_Float16)(float)q8_quant(val[2 * b + 1], iv);
+          const bool ev = (l16 & 1) == 0;
+          _Float16 *xr = in.xh + (size_t)qi * KO + h * HD + 32 * b + (ev ? l16 : 15 + l16);
+          *reinterpret_cast<uint32_t *>(xr) = ev ? ha | na << 16 : nb | hb << 16;
           if (l16 == 0) in.sx[(size_t)qi * (KO / 32) + h * (HD / 32) + b] = am / 127.0f;
         }
       }
