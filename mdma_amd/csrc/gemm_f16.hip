@@ -164,6 +164,7 @@ struct F16Args {
   // values as f16 and the scale (xh, sx; gemm_act_kernel's arithmetic).
   float *glu_y;
   F16In glu_in;
+  uint32_t glu_no_y;  // with glu_in: glu_y's f32 rows are not stored
   // Fused QKV of a prompt (rope.tab set; the Q6_K wide kernel): q (job 0)
   // rotated before its store, k (job 1) rotated and v (job 2) stored as f16
   // cache rows of token m at m * kv_stride, position pos + m (rope_kv_kernel's
@@ -495,7 +496,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(F16Args a) {
         const uint32_t n = n0 + 16 * i + 4 * lq;
 #pragma unroll
         for (int r = 0; r < 4; r++) h[i][r] = silu_mul1(acc[i][j][r], acc[i + 2][j][r]);
-        if (m < a.M)
+        if (m < a.M && !a.glu_no_y)
           *reinterpret_cast<float4 *>(a.glu_y + (size_t)m * N + n) = make_float4(h[i][0], h[i][1], h[i][2], h[i][3]);
       }
       if (q) {
@@ -1002,6 +1003,7 @@ F16In gemm_f16_input_at(char *s, uint64_t M, uint64_t K) {
 void a16_mark(mdma_ctx *ctx, const float *x, uint64_t T, uint64_t n_in, char *buf, bool with_p) {
   ctx->a16_valid = true;
   ctx->a16_p = with_p;
+  ctx->a16_noy = false;
   ctx->a16_x = x;
   ctx->a16_buf = buf;
   ctx->a16_n = T * n_in;
@@ -1156,6 +1158,7 @@ void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float
         a.rope.kv_stride = ctx->rope_want_stride;
       }
       if (glu && want) {
+        a.glu_no_y = ctx->a16_want_input_only;
         a.glu_in = want_in;
         a.glu_in.xh += m0 * w.n_out;
         a.glu_in.sx += m0 * (w.n_out / 32);
@@ -1188,7 +1191,10 @@ void launch_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float
       hip_check(hipGetLastError(), "gemm f16 launch");
     }
   }
-  if (want) a16_mark(ctx, glu_y, M, jobs[0].n_out, ctx->a16_want_buf, false);
+  if (want) {
+    a16_mark(ctx, glu_y, M, jobs[0].n_out, ctx->a16_want_buf, false);
+    ctx->a16_noy = ctx->a16_want_input_only;
+  }
   if (rope) ctx->rope_done = true;
 }
 

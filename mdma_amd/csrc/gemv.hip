@@ -899,15 +899,22 @@ void launch_gemv_f32_gated(mdma_ctx *ctx, const GemvJob &gate, const GemvJob &up
 // silu(gate) * up there.
 static bool try_gemm_f16(mdma_ctx *ctx, const GemvJob *jobs, int n_jobs, const float *x, uint64_t T,
                          float *glu_y = nullptr) {
-  if (ctx->prefill_kernel != MDMA_PREFILL_AUTO) return false;
+  // x's f32 rows never stored (a16_noy): this call must take the record.
+  const bool noy = ctx->a16_noy && a16_holds(ctx, x, T, jobs[0].n_in);
+  auto decline = [&]() {
+    if (noy) fail(MDMA_ERR_BACKEND, "GEMM input without its f32 rows cannot serve this call");
+    return false;
+  };
+  if (ctx->prefill_kernel != MDMA_PREFILL_AUTO) return decline();
   for (int i = 0; i < n_jobs; i++)
     if (!gemm_f16_supported(jobs[i].dtype, jobs[i].layout, jobs[i].n_in, jobs[i].n_out) ||
         jobs[i].n_in != jobs[0].n_in || (jobs[i].dtype == DT_Q6_K && jobs[i].dots))
-      return false;  // (Q6_K block-dot capture: the int8 GEMM's per-16 dots)
+      return decline();  // (Q6_K block-dot capture: the int8 GEMM's per-16 dots)
   // x's input already written by a fused rmsnorm (launch_rmsnorm_a16)?
   bool pre = !ctx->fixed_scratch && a16_holds(ctx, x, T, jobs[0].n_in);
   for (int i = 0; i < n_jobs && pre; i++)
     if (jobs[i].dtype == DT_Q4_K && !ctx->a16_p) pre = false;  // the min term reads P
+  if (!pre) decline();
   const uint64_t need = pre ? 0 : (gemm_f16_input_bytes(T, jobs[0].n_in) + 255) / 256 * 256;
   // Split-K partials (launches run one after another and share them).
   uint64_t nc = 0, pb = gemm_f16_split_bytes(ctx, jobs, n_jobs, T, &nc);

@@ -107,6 +107,9 @@ struct mdma_ctx {
   const float *a16_want_y = nullptr;
   char *a16_want_buf = nullptr;
   uint64_t a16_want_bytes = 0;
+  // With the request: the caller reads a16_want_y only through that input,
+  // so its f32 rows are not stored (a16_noy marks such a record).
+  bool a16_want_input_only = false, a16_noy = false;
   // A request to the fused QKV GEMM of a prompt writing q into rope_want_q:
   // RoPE on q and k and the k / v cache rows in its epilogue (rope_done set
   // when a launch took it).

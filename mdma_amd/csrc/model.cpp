@@ -550,9 +550,12 @@ void run_layers(mdma_session *s, uint64_t T, uint32_t pos, uint64_t seq, bool ba
       ctx->a16_want_y = fp(s->act);
       ctx->a16_want_buf = s->gate->ptr;
       ctx->a16_want_bytes = s->gate->len;
+      // The down GEMM below reads act only through that input.
+      ctx->a16_want_input_only = !dn_next.dots;
     }
     gemv_gated(ctx, gu[0], gu[1], fp(s->normed), T, fp(s->act), fresh);
     ctx->a16_want_y = nullptr;
+    ctx->a16_want_input_only = false;
     n_part = 0;
     if (fuse_norm) {
       // y = x + W act into the other residual buffer (the new stream).
